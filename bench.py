@@ -1,0 +1,221 @@
+#!/usr/bin/env python3
+"""Benchmark of the LoGo query-sparse attention hot path on one MI355X.
+
+Metric: ``sq_full_attn`` forward+backward effective TFLOP/s at
+T=32768, H=16, D=128 with a 25% global ratio.  A step is one user-level call
+``o = sq_full_attn(q, k, v, selection, cu_seqlens=cu)`` plus its backward
+(compaction, forward, delta, dq, dk/dv), on synthetic inputs already resident
+in HBM.  Effective FLOPs count selected rows only:
+``F = 3.5 * 4 * D * HQ * sum over selected rows of (p + 1)``.
+
+Prints ONE JSON line.  Per-kernel durations come from HIP events recorded on
+the launch stream around every C-ABI launch inside the timed region; the
+dominant kernel's roofline is its algorithmic FLOPs over that duration.  The
+CPU baseline times the reference's CPU formulation (dense causal attention per
+segment, then row masking, torch fp32 autograd) on a bounded sample of heads.
+"""
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+import torch
+
+MFMA_BF16_PEAK_TFLOPS = 2516.6  # dense bf16 MFMA, 256 CU x 2.4 GHz x 4096 FLOP/clk
+HBM_PEAK_GBS = 8000.0
+
+# Matmul FLOPs per visible (query, key) pair and head dim, per kernel: the
+# forward does QK^T and PV; dq recomputes S and dP and forms dQ; dk/dv
+# recompute S and dP and form dV and dK.
+KERNEL_FLOPS_PER_PAIR_D = {
+    "logo_sq_fwd": 4,
+    "logo_sq_bwd_dq": 6,
+    "logo_sq_bwd_dkv": 8,
+}
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--seq-len", type=int, default=32768)
+    ap.add_argument("--heads", type=int, default=16)
+    ap.add_argument("--head-dim", type=int, default=128)
+    ap.add_argument("--ratio", type=float, default=0.25)
+    ap.add_argument("--cpu-heads", type=int, default=8, help="heads in the CPU-baseline sample")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--seed", type=int, default=2)
+    return ap.parse_args()
+
+
+def markov_mask(n, ratio, mean_run, gen):
+    """Selection correlated in spans: two-state Markov chain with mean run of
+    ones `mean_run` and stationary ratio `ratio` (initial state stationary)."""
+    p10 = 1.0 / mean_run
+    p01 = ratio * p10 / (1.0 - ratio)
+    u = torch.rand(n, generator=gen).numpy()
+    out = np.empty(n, dtype=bool)
+    state = u[0] < ratio
+    out[0] = state
+    for i in range(1, n):
+        state = (u[i] >= p10) if state else (u[i] < p01)
+        out[i] = state
+    return out
+
+
+class EventTimer:
+    """Launch hook: HIP events around each C-ABI launch on the current stream."""
+
+    def __init__(self):
+        self.pending = {}
+        self.pairs = {}
+        self.enabled = False
+
+    def __call__(self, name, phase):
+        if not self.enabled:
+            return
+        ev = torch.cuda.Event(enable_timing=True)
+        ev.record(torch.cuda.current_stream())
+        if phase == "start":
+            self.pending[name] = ev
+        else:
+            self.pairs.setdefault(name, []).append((self.pending.pop(name), ev))
+
+    def averages_ms(self):
+        return {k: float(np.mean([a.elapsed_time(b) for a, b in v])) for k, v in self.pairs.items()}
+
+    def counts(self):
+        return {k: len(v) for k, v in self.pairs.items()}
+
+
+def cpu_baseline(q, k, v, sel_np, cu, do, heads, flops_per_head):
+    from oracle.cpu_path import time_fwd_bwd
+
+    threads = min(16, len(os.sched_getaffinity(0)))
+    qs = q[:, :heads].float().cpu()
+    ks = k[:, :heads].float().cpu()
+    vs = v[:, :heads].float().cpu()
+    ds = do[:, :heads].float().cpu()
+    sel = torch.from_numpy(sel_np)
+    secs = time_fwd_bwd(qs, ks, vs, sel, cu, ds, threads)
+    return {
+        "value": round(flops_per_head * heads / secs / 1e12, 4),
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"reference CPU formulation (logo/ops/dense_full_attn.py:30-69 dense causal SDPA per "
+                   f"segment, then selection mask) in torch fp32 autograd fwd+bwd on {heads} of "
+                   f"{q.shape[1]} heads of the same T={q.shape[0]} workload; {secs:.2f} s; effective "
+                   f"FLOPs on selected rows as for the GPU value"),
+    }
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (collectives, sharding) and "
+              "each box has a single MI355X; run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    from logo_amd import _lib
+    from logo_amd.ops import sq_full_attn
+
+    dev = torch.device("cuda", 0)
+    T, H, D = args.seq_len, args.heads, args.head_dim
+    gen = torch.Generator()
+    gen.manual_seed(args.seed)
+    sel_np = markov_mask(T, args.ratio, 8, gen)
+    sel_np[0] = True
+    q = (torch.randn(T, H, D, generator=gen) * 0.5).to(torch.bfloat16)
+    k = (torch.randn(T, H, D, generator=gen) * 0.5).to(torch.bfloat16)
+    v = (torch.randn(T, H, D, generator=gen) * 0.5).to(torch.bfloat16)
+    do = torch.randn(T, H, D, generator=gen).to(torch.bfloat16)
+    pos = np.flatnonzero(sel_np)
+    pairs_per_head = float((pos + 1).sum())  # single sequence: p = token index
+    f_fwd = 4.0 * D * H * pairs_per_head
+    f_step = 3.5 * f_fwd
+
+    qg = q.to(dev)[None].requires_grad_()
+    kg = k.to(dev)[None].requires_grad_()
+    vg = v.to(dev)[None].requires_grad_()
+    dog = do.to(dev)[None]
+    selg = torch.from_numpy(sel_np).to(dev)[None]
+    cu = torch.tensor([0, T], dtype=torch.int32, device=dev)
+
+    def step():
+        o = sq_full_attn(qg, kg, vg, selg, cu_seqlens=cu)
+        torch.autograd.grad(o, (qg, kg, vg), dog)
+
+    timer = EventTimer()
+    _lib.set_launch_hook(timer)
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    timer.enabled = True
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    timer.enabled = False
+    _lib.set_launch_hook(None)
+
+    ms_per_step = elapsed * 1e3 / args.steps
+    value = f_step / (ms_per_step * 1e-3) / 1e12
+    kern_ms = timer.averages_ms()
+    flop_kernels = {n: ms for n, ms in kern_ms.items() if n in KERNEL_FLOPS_PER_PAIR_D}
+    dom = max(flop_kernels, key=flop_kernels.get)
+    dom_flops = KERNEL_FLOPS_PER_PAIR_D[dom] * D * H * pairs_per_head
+    achieved = dom_flops / (kern_ms[dom] * 1e-3) / 1e12
+    roofline = {
+        "kernel": dom,
+        "bound": "mfma",
+        "achieved": round(achieved, 2),
+        "peak": MFMA_BF16_PEAK_TFLOPS,
+        "unit": "TFLOP/s",
+        "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4),
+        "traffic": None,
+        "flops_per_launch": dom_flops,
+        "avg_launch_ms": round(kern_ms[dom], 4),
+    }
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(q, k, v, sel_np, [0, T], do, min(args.cpu_heads, H), f_step / H)
+
+    line = {
+        "metric": "sq_full_attn fwd+bwd effective TFLOP/s @T=32K, 25% global; decode tok/s",
+        "value": round(value, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "sq_full_attn fwd+bwd, single sequence, selection Markov spans (mean run 8)",
+            "T": T, "HQ": H, "H": H, "D": D,
+            "global_ratio": round(float(sel_np.mean()), 4),
+            "effective_tflop_per_step": round(f_step / 1e12, 4),
+            "seed": args.seed,
+        },
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "kernel_ms": {k_: round(v_, 4) for k_, v_ in sorted(kern_ms.items())},
+        "kernel_tflops": {n: round(KERNEL_FLOPS_PER_PAIR_D[n] * D * H * pairs_per_head / (ms * 1e-3) / 1e12, 2)
+                          for n, ms in flop_kernels.items()},
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,148 @@
+/*
+ * logo_hip.h -- C ABI of the MI355X (gfx950) LoGo attention hot path.
+ *
+ * Every entry point takes raw device pointers, element counts and a HIP
+ * stream (passed as void*), launches asynchronously on that stream, and
+ * returns LOGO_OK or an error code; logo_last_error() gives the message of
+ * the calling thread's last failure.  No entry point allocates device memory:
+ * the caller passes every output and workspace buffer.
+ *
+ * Tensor layouts follow the reference's packed varlen convention with the
+ * batch axis (B = 1) dropped (logo/ops/selected_full_attn.py:505-514):
+ *   q [N, HQ, D], k [N, H, D], v [N, H, D], o [N, HQ, D]  (bf16, contiguous)
+ *   selection: uint8 [N] (shared by all heads, the reference API) or
+ *              uint8 [N, HQ] (per-(token, head) extension); "lanes" = 1 or HQ.
+ *   cu: int32 [nseq + 1], cu[0] = 0, cu[nseq] = N, non-decreasing.
+ *
+ * Compaction metadata ("meta"), int32, one block of LOGO_META_STRIDE(nseq)
+ * per lane:
+ *   [0] Sq   selected rows           [1] NTq  query tiles of LOGO_BQ rows
+ *   [2] NTk  key tiles of LOGO_BKV   [3] N    [4] nseq   [5..7] reserved
+ *   [8 ...]                      cu_q  [nseq+1]  (logo/ops/common.py:94-96)
+ *   [8 +   (nseq+1) ...]         prefix of ceil(count_s / LOGO_BQ)
+ *   [8 + 2*(nseq+1) ...]         prefix of ceil(len_s / LOGO_BKV)
+ * Row lists: q_idx int64 [lanes, N], pos int32 [lanes, N]; entries
+ * [0, Sq) of each lane are valid (logo/ops/common.py:90-93).
+ * lse / delta: float32 [HQ, N] indexed by compacted row (log2 domain lse,
+ * logo/ops/selected_full_attn.py:118-119).
+ */
+#ifndef LOGO_HIP_H_
+#define LOGO_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LOGO_OK 0
+#define LOGO_EINVAL 1
+#define LOGO_EHIP 2
+
+#define LOGO_BQ 128
+#define LOGO_BKV 128
+#define LOGO_META_HDR 8
+#define LOGO_META_STRIDE(nseq) (LOGO_META_HDR + 3 * ((nseq) + 1))
+
+#define LOGO_DTYPE_BF16 0
+
+/* Message of the calling thread's last error ("" if none). */
+const char* logo_last_error(void);
+
+/* ABI version of this library. */
+int logo_abi_version(void);
+
+/* Bytes of workspace logo_compact needs. */
+size_t logo_compact_workspace_bytes(int64_t n_tokens, int lanes);
+
+/*
+ * Row compaction (wavefront ballot + prefix sum): selected rows per lane in
+ * ascending token order, their positions inside their segment, cu_q, and the
+ * tile prefixes in `meta`.  Bit-exact restatement of build_selection,
+ * logo/ops/common.py:71-107 (q_idx :90, seg :92, pos_ids :93, cu_q :94-96).
+ */
+int logo_compact(const uint8_t* selection, int64_t n_tokens, int lanes,
+                 const int32_t* cu, int nseq, int64_t* q_idx, int32_t* pos,
+                 int32_t* meta, void* workspace, void* stream);
+
+/*
+ * Metadata for dense attention over every row (cu_q = cu, Sq = N), used by
+ * the sliding-window branch and the all-ones ("flash") global branch
+ * (logo/layers/utils.py:107-234, logo/ops/dense_full_attn.py:12-22).
+ */
+int logo_dense_meta(const int32_t* cu, int nseq, int64_t n_tokens, int32_t* meta,
+                    void* stream);
+
+/*
+ * (sequence id, block id) tile list for blocks of `chunk` rows over cu, in
+ * order; *count receives NT.  Restates prepare_chunk_indices,
+ * logo/ops/common.py:110-124.  `out` holds max_tiles pairs; `workspace`
+ * holds nseq + 1 int32.
+ */
+int logo_chunk_indices(const int32_t* cu, int nseq, int chunk, int32_t* out,
+                       int64_t max_tiles, int32_t* count, int32_t* workspace,
+                       void* stream);
+
+/*
+ * First compacted-query block of each key block: for tile t = (s, j) of
+ * `chunks`, (lower_bound(pos[cu_q[s]:cu_q[s+1]], j*block) - 0) / block.
+ * Restates _compute_q_start_blk, logo/ops/selected_full_attn.py:374-402.
+ */
+int logo_q_start_blk(const int32_t* pos, const int32_t* cu_q, const int32_t* chunks,
+                     const int32_t* count, int64_t max_tiles, int block, int32_t* out,
+                     void* stream);
+
+/*
+ * Query-sparse causal attention forward on selected rows
+ * (sq_full_attn_fwd_kernel + _fwd, logo/ops/selected_full_attn.py:33-121,
+ * :340-362, with the q gather :461 and output scatter :469-471 fused).
+ * Writes o[t] for selected rows t only (the caller zero-fills o) and lse per
+ * compacted row.  q_idx/pos == NULL selects dense mode (every row, meta from
+ * logo_dense_meta).  window < 0: full causal; window >= 0: keys
+ * [p - window, p] (logo/layers/utils.py:144-147).
+ */
+int logo_sq_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
+                const int64_t* q_idx, const int32_t* pos, const int32_t* meta,
+                const int32_t* cu, int64_t n_tokens, int nseq, int hq, int h, int d,
+                int lanes, float scale, int window, int dtype, void* stream);
+
+/*
+ * Backward (logo/ops/selected_full_attn.py:124-138 delta, :141-228 dq,
+ * :231-337 dk/dv, :444-445 GQA sum), with the dO gather (:483) and dq scatter
+ * (:487-488) fused.  o and dout are [N, HQ, D]; writes dq rows of selected
+ * tokens (caller zero-fills dq), every row of dk and dv [N, H, D], and delta
+ * [HQ, N] (workspace the caller provides).
+ */
+int logo_sq_bwd(const void* q, const void* k, const void* v, const void* o,
+                const void* dout, const float* lse, float* delta, void* dq, void* dk,
+                void* dv, const int64_t* q_idx, const int32_t* pos, const int32_t* meta,
+                const int32_t* cu, int64_t n_tokens, int nseq, int hq, int h, int d,
+                int lanes, float scale, int window, int dtype, void* stream);
+
+/*
+ * The three backward phases of logo_sq_bwd as separate launches, same
+ * arguments: delta only (:124-138, :365-371), dq only (:141-228, :424-432),
+ * dk/dv only (:231-337, :433-445).  Callers time or overlap them one by one.
+ */
+int logo_sq_bwd_delta(const void* q, const void* k, const void* v, const void* o,
+                      const void* dout, const float* lse, float* delta, void* dq, void* dk,
+                      void* dv, const int64_t* q_idx, const int32_t* pos, const int32_t* meta,
+                      const int32_t* cu, int64_t n_tokens, int nseq, int hq, int h, int d,
+                      int lanes, float scale, int window, int dtype, void* stream);
+int logo_sq_bwd_dq(const void* q, const void* k, const void* v, const void* o,
+                   const void* dout, const float* lse, float* delta, void* dq, void* dk,
+                   void* dv, const int64_t* q_idx, const int32_t* pos, const int32_t* meta,
+                   const int32_t* cu, int64_t n_tokens, int nseq, int hq, int h, int d,
+                   int lanes, float scale, int window, int dtype, void* stream);
+int logo_sq_bwd_dkv(const void* q, const void* k, const void* v, const void* o,
+                    const void* dout, const float* lse, float* delta, void* dq, void* dk,
+                    void* dv, const int64_t* q_idx, const int32_t* pos, const int32_t* meta,
+                    const int32_t* cu, int64_t n_tokens, int nseq, int hq, int h, int d,
+                    int lanes, float scale, int window, int dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LOGO_HIP_H_ */

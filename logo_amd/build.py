@@ -1,0 +1,76 @@
+"""Build recipe for ``logo_amd/liblogo_hip.so`` (gfx950 only).
+
+Compiles every ``csrc/*.hip`` and ``csrc/*.cpp`` with ``hipcc`` into one
+C-ABI shared library next to this file.  Packed-FP32 instructions are disabled
+for all device code (``-Xclang -target-feature -Xclang -packed-fp32-ops``).
+
+Usage: ``python -m logo_amd.build`` (or ``__graft_entry__.build()``).
+"""
+
+import os
+import subprocess
+import sys
+import tempfile
+from concurrent.futures import ThreadPoolExecutor
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+CSRC = os.path.join(HERE, "csrc")
+LIB = os.path.join(HERE, "liblogo_hip.so")
+ARCH = "gfx950"
+
+COMMON_FLAGS = [
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    f"--offload-arch={ARCH}",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wno-unused-result",
+]
+
+
+def _hipcc():
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc"):
+        if cand and os.path.exists(cand):
+            return cand
+    return "hipcc"
+
+
+def sources():
+    out = []
+    for name in sorted(os.listdir(CSRC)):
+        if name.endswith((".hip", ".cpp")):
+            out.append(os.path.join(CSRC, name))
+    return out
+
+
+def build(verbose: bool = False, jobs: int = 8) -> str:
+    """Compile all sources and link ``liblogo_hip.so``; returns its path."""
+    hipcc = _hipcc()
+    srcs = sources()
+    with tempfile.TemporaryDirectory(prefix="logo_build_") as tmp:
+        def compile_one(src):
+            obj = os.path.join(tmp, os.path.basename(src) + ".o")
+            cmd = [hipcc, *COMMON_FLAGS, "-I", os.path.join(HERE, "..", "include"), "-c", src, "-o", obj]
+            if verbose:
+                print(" ".join(cmd), flush=True)
+            res = subprocess.run(cmd, capture_output=True, text=True)
+            if res.returncode != 0:
+                raise RuntimeError(f"hipcc failed for {src}:\n{res.stderr}")
+            return obj
+
+        with ThreadPoolExecutor(max_workers=max(1, min(jobs, len(srcs)))) as ex:
+            objs = list(ex.map(compile_one, srcs))
+        tmp_lib = LIB + ".tmp"
+        cmd = [hipcc, "-shared", "-fPIC", f"--offload-arch={ARCH}", *objs, "-o", tmp_lib]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        res = subprocess.run(cmd, capture_output=True, text=True)
+        if res.returncode != 0:
+            raise RuntimeError(f"link failed:\n{res.stderr}")
+        os.replace(tmp_lib, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    path = build(verbose="-v" in sys.argv)
+    print(path)

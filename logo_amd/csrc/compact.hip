@@ -1,0 +1,302 @@
+// Row compaction for query-sparse attention (gfx950).
+//
+// Bit-exact restatement of build_selection (logo/ops/common.py:71-107):
+// q_idx = nonzero(selection) in ascending order, pos = q_idx - cu[seg],
+// cu_q = exclusive prefix of per-sequence counts; plus the tile prefixes the
+// attention kernels use to map a workgroup to (sequence, block), which replace
+// prepare_chunk_indices (logo/ops/common.py:110-124) and its host sync.
+//
+// Three launches, none of them synchronising with the host:
+//   count    : per 4096-token chunk and lane, popcount of wave ballots
+//   scatter  : chunk prefix + wave prefix (LDS) + mbcnt rank -> q_idx, pos
+//   finalize : Sq, cu_q by binary search over q_idx, tile prefixes by block scan
+#include "capi.hpp"
+#include "common.hpp"
+
+namespace logo {
+
+constexpr int kChunk = 4096;  // tokens per workgroup: 4 waves x 16 ballots x 64 lanes
+
+__device__ __forceinline__ bool sel_on(const uint8_t* sel, int64_t n, int lanes, int lane, int64_t t) {
+  return t < n && sel[t * lanes + lane] != 0;
+}
+
+__global__ __launch_bounds__(256) void compact_count(const uint8_t* __restrict__ sel, int64_t n,
+                                                     int lanes, int32_t* __restrict__ counts,
+                                                     int nchunk) {
+  const int lane = blockIdx.y;
+  const int64_t base = (int64_t)blockIdx.x * kChunk;
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+  int cnt = 0;
+#pragma unroll 4
+  for (int s = 0; s < 16; ++s) {
+    const int64_t t = base + w * 1024 + s * 64 + l;
+    cnt += __popcll(__ballot(sel_on(sel, n, lanes, lane, t)));
+  }
+  __shared__ int wc[4];
+  if (l == 0) wc[w] = cnt;
+  __syncthreads();
+  if (threadIdx.x == 0) counts[lane * nchunk + blockIdx.x] = wc[0] + wc[1] + wc[2] + wc[3];
+}
+
+__device__ __forceinline__ int block_sum(int v, int* red) {
+  // 256-thread sum through LDS; red holds 4 ints.
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+  const int w = threadIdx.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[w] = v;
+  __syncthreads();
+  return red[0] + red[1] + red[2] + red[3];
+}
+
+__global__ __launch_bounds__(256) void compact_scatter(const uint8_t* __restrict__ sel, int64_t n,
+                                                       int lanes, const int32_t* __restrict__ cu,
+                                                       int nseq, const int32_t* __restrict__ counts,
+                                                       int nchunk, int64_t* __restrict__ q_idx,
+                                                       int32_t* __restrict__ pos) {
+  __shared__ int red[4];
+  __shared__ int wc[4];
+  const int lane = blockIdx.y;
+  const int chunk = blockIdx.x;
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+
+  int part = 0;
+  for (int c = threadIdx.x; c < chunk; c += 256) part += counts[lane * nchunk + c];
+  const int prefix = block_sum(part, red);
+
+  const int64_t base = (int64_t)chunk * kChunk + w * 1024;
+  uint64_t masks[16];
+  int cnt = 0;
+#pragma unroll
+  for (int s = 0; s < 16; ++s) {
+    masks[s] = __ballot(sel_on(sel, n, lanes, lane, base + s * 64 + l));
+    cnt += __popcll(masks[s]);
+  }
+  if (l == 0) wc[w] = cnt;
+  __syncthreads();
+  int run = prefix;
+  for (int i = 0; i < w; ++i) run += wc[i];
+
+  int64_t* qi = q_idx + (int64_t)lane * n;
+  int32_t* ps = pos + (int64_t)lane * n;
+  const uint64_t below = (l == 0) ? 0ull : (~0ull >> (64 - l));
+#pragma unroll
+  for (int s = 0; s < 16; ++s) {
+    const uint64_t m = masks[s];
+    if ((m >> l) & 1ull) {
+      const int rank = run + __popcll(m & below);
+      const int64_t t = base + s * 64 + l;
+      const int sg = seg_of(cu, nseq, t);
+      qi[rank] = t;
+      ps[rank] = (int32_t)(t - cu[sg]);
+    }
+    run += __popcll(m);
+  }
+}
+
+// Exclusive scan over 256 threads; returns this thread's exclusive prefix and
+// writes the block total to *total.
+__device__ __forceinline__ int block_exscan(int v, int* buf, int* total) {
+  const int tid = threadIdx.x;
+  buf[tid] = v;
+  __syncthreads();
+  for (int off = 1; off < 256; off <<= 1) {
+    int add = tid >= off ? buf[tid - off] : 0;
+    __syncthreads();
+    buf[tid] += add;
+    __syncthreads();
+  }
+  const int inc = buf[tid];
+  *total = buf[255];
+  __syncthreads();
+  return inc - v;
+}
+
+// One workgroup per lane.  dense != 0: cu_q = cu and Sq = n (no q_idx).
+__global__ __launch_bounds__(256) void compact_finalize(const int32_t* __restrict__ cu, int nseq,
+                                                        int64_t n, const int32_t* __restrict__ counts,
+                                                        int nchunk, const int64_t* __restrict__ q_idx,
+                                                        int32_t* __restrict__ meta, int dense) {
+  __shared__ int red[4];
+  __shared__ int buf[256];
+  const int lane = blockIdx.x;
+  const int stride = LOGO_META_STRIDE(nseq);
+  int32_t* m = meta + (int64_t)lane * stride;
+  int32_t* cu_q = m + kMetaHdr;
+  int32_t* cu_tq = cu_q + (nseq + 1);
+  int32_t* cu_tk = cu_tq + (nseq + 1);
+
+  int sq;
+  if (dense) {
+    sq = (int)n;
+  } else {
+    int part = 0;
+    for (int c = threadIdx.x; c < nchunk; c += 256) part += counts[lane * nchunk + c];
+    sq = block_sum(part, red);
+  }
+  const int64_t* qi = q_idx + (int64_t)lane * n;
+  for (int s = threadIdx.x; s <= nseq; s += 256) {
+    int v;
+    if (dense) {
+      v = cu[s];
+    } else {
+      // cu_q[s] = number of selected rows before token cu[s].
+      int lo = 0, hi = sq;
+      const int64_t key = cu[s];
+      while (lo < hi) {
+        int mid = (lo + hi) >> 1;
+        if (qi[mid] < key) lo = mid + 1; else hi = mid;
+      }
+      v = lo;
+    }
+    cu_q[s] = v;
+  }
+  __syncthreads();
+
+  int carry_q = 0, carry_k = 0;
+  for (int s0 = 0; s0 < nseq; s0 += 256) {
+    const int s = s0 + threadIdx.x;
+    int bq = 0, bk = 0;
+    if (s < nseq) {
+      const int cq = cu_q[s + 1] - cu_q[s];
+      const int ck = cu[s + 1] - cu[s];
+      bq = (cq + LOGO_BQ - 1) / LOGO_BQ;
+      bk = (ck + LOGO_BKV - 1) / LOGO_BKV;
+    }
+    int tq, tk;
+    const int eq = block_exscan(bq, buf, &tq);
+    const int ek = block_exscan(bk, buf, &tk);
+    if (s < nseq) {
+      cu_tq[s] = carry_q + eq;
+      cu_tk[s] = carry_k + ek;
+    }
+    carry_q += tq;
+    carry_k += tk;
+  }
+  if (threadIdx.x == 0) {
+    cu_tq[nseq] = carry_q;
+    cu_tk[nseq] = carry_k;
+    m[0] = sq;
+    m[1] = carry_q;
+    m[2] = carry_k;
+    m[3] = (int)n;
+    m[4] = nseq;
+    m[5] = m[6] = m[7] = 0;
+  }
+}
+
+// prepare_chunk_indices for an arbitrary chunk size (parity helper).
+__global__ __launch_bounds__(256) void chunk_prefix_kernel(const int32_t* __restrict__ cu, int nseq,
+                                                           int chunk, int32_t* __restrict__ prefix,
+                                                           int32_t* __restrict__ count) {
+  __shared__ int buf[256];
+  int carry = 0;
+  for (int s0 = 0; s0 < nseq; s0 += 256) {
+    const int s = s0 + threadIdx.x;
+    const int b = s < nseq ? (cu[s + 1] - cu[s] + chunk - 1) / chunk : 0;
+    int tot;
+    const int e = block_exscan(b, buf, &tot);
+    if (s < nseq) prefix[s] = carry + e;
+    carry += tot;
+  }
+  if (threadIdx.x == 0) {
+    prefix[nseq] = carry;
+    *count = carry;
+  }
+}
+
+__global__ __launch_bounds__(256) void chunk_list_kernel(const int32_t* __restrict__ prefix, int nseq,
+                                                         int32_t* __restrict__ out, int64_t max_tiles) {
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int nt = prefix[nseq];
+  if (t >= nt || t >= max_tiles) return;
+  const int s = seg_of(prefix, nseq, t);
+  out[2 * t] = s;
+  out[2 * t + 1] = (int32_t)(t - prefix[s]);
+}
+
+__global__ __launch_bounds__(256) void q_start_kernel(const int32_t* __restrict__ pos,
+                                                      const int32_t* __restrict__ cu_q,
+                                                      const int32_t* __restrict__ chunks,
+                                                      const int32_t* __restrict__ count,
+                                                      int64_t max_tiles, int block,
+                                                      int32_t* __restrict__ out) {
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t >= *count || t >= max_tiles) return;
+  const int s = chunks[2 * t], j = chunks[2 * t + 1];
+  const int lo = cu_q[s], hi = cu_q[s + 1];
+  const int first = lower_bound_i32(pos, lo, hi, j * block);
+  out[t] = (first - lo) / block;
+}
+
+}  // namespace logo
+
+using namespace logo;
+
+extern "C" size_t logo_compact_workspace_bytes(int64_t n_tokens, int lanes) {
+  const int64_t nchunk = (n_tokens + kChunk - 1) / kChunk;
+  return (size_t)(nchunk > 0 ? nchunk : 1) * (size_t)(lanes > 0 ? lanes : 1) * sizeof(int32_t);
+}
+
+extern "C" int logo_compact(const uint8_t* selection, int64_t n_tokens, int lanes, const int32_t* cu,
+                            int nseq, int64_t* q_idx, int32_t* pos, int32_t* meta, void* workspace,
+                            void* stream) {
+  LOGO_REQUIRE(n_tokens >= 0 && n_tokens < (int64_t)1 << 31, "n_tokens out of range: %lld",
+               (long long)n_tokens);
+  LOGO_REQUIRE(lanes >= 1 && nseq >= 1, "lanes (%d) and nseq (%d) must be >= 1", lanes, nseq);
+  LOGO_REQUIRE(cu && meta && workspace, "null pointer argument");
+  LOGO_REQUIRE(n_tokens == 0 || (selection && q_idx && pos), "null selection/q_idx/pos");
+  hipStream_t st = as_stream(stream);
+  const int nchunk = (int)((n_tokens + kChunk - 1) / kChunk);
+  int32_t* counts = static_cast<int32_t*>(workspace);
+  if (nchunk > 0) {
+    dim3 grid(nchunk, lanes);
+    hipLaunchKernelGGL(compact_count, grid, dim3(256), 0, st, selection, n_tokens, lanes, counts, nchunk);
+    LOGO_LAUNCH_CHECK("compact_count");
+    hipLaunchKernelGGL(compact_scatter, grid, dim3(256), 0, st, selection, n_tokens, lanes, cu, nseq,
+                       counts, nchunk, q_idx, pos);
+    LOGO_LAUNCH_CHECK("compact_scatter");
+  }
+  hipLaunchKernelGGL(compact_finalize, dim3(lanes), dim3(256), 0, st, cu, nseq, n_tokens, counts,
+                     nchunk, q_idx, meta, 0);
+  LOGO_LAUNCH_CHECK("compact_finalize");
+  return LOGO_OK;
+}
+
+extern "C" int logo_dense_meta(const int32_t* cu, int nseq, int64_t n_tokens, int32_t* meta,
+                               void* stream) {
+  LOGO_REQUIRE(n_tokens >= 0 && n_tokens < (int64_t)1 << 31, "n_tokens out of range");
+  LOGO_REQUIRE(nseq >= 1 && cu && meta, "bad arguments");
+  hipLaunchKernelGGL(compact_finalize, dim3(1), dim3(256), 0, as_stream(stream), cu, nseq, n_tokens,
+                     (const int32_t*)nullptr, 0, (const int64_t*)nullptr, meta, 1);
+  LOGO_LAUNCH_CHECK("compact_finalize(dense)");
+  return LOGO_OK;
+}
+
+extern "C" int logo_chunk_indices(const int32_t* cu, int nseq, int chunk, int32_t* out,
+                                  int64_t max_tiles, int32_t* count, int32_t* workspace,
+                                  void* stream) {
+  LOGO_REQUIRE(nseq >= 1 && chunk >= 1 && cu && out && count && workspace, "bad arguments");
+  hipStream_t st = as_stream(stream);
+  hipLaunchKernelGGL(chunk_prefix_kernel, dim3(1), dim3(256), 0, st, cu, nseq, chunk, workspace, count);
+  LOGO_LAUNCH_CHECK("chunk_prefix_kernel");
+  if (max_tiles > 0) {
+    const int64_t nb = (max_tiles + 255) / 256;
+    hipLaunchKernelGGL(chunk_list_kernel, dim3((unsigned)nb), dim3(256), 0, st, workspace, nseq, out,
+                       max_tiles);
+    LOGO_LAUNCH_CHECK("chunk_list_kernel");
+  }
+  return LOGO_OK;
+}
+
+extern "C" int logo_q_start_blk(const int32_t* pos, const int32_t* cu_q, const int32_t* chunks,
+                                const int32_t* count, int64_t max_tiles, int block, int32_t* out,
+                                void* stream) {
+  LOGO_REQUIRE(block >= 1 && cu_q && chunks && count && out, "bad arguments");
+  if (max_tiles <= 0) return LOGO_OK;
+  const int64_t nb = (max_tiles + 255) / 256;
+  hipLaunchKernelGGL(q_start_kernel, dim3((unsigned)nb), dim3(256), 0, as_stream(stream), pos, cu_q,
+                     chunks, count, max_tiles, block, out);
+  LOGO_LAUNCH_CHECK("q_start_kernel");
+  return LOGO_OK;
+}

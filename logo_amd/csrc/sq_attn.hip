@@ -1,0 +1,719 @@
+// Query-sparse causal attention, forward and backward, for gfx950.
+//
+// Semantics follow logo/ops/selected_full_attn.py: selected ("compacted")
+// query rows attend causally to every key of their own packed segment up to
+// their real position (:33-121); the backward recomputes P from the stored
+// log2-domain LSE (:141-228 dq, :231-337 dk/dv) with delta = rowsum(o * dO)
+// (:124-138); dk/dv of a GQA group are summed over its query heads (:444-445).
+// Differences in structure, not in results:
+//   * q / dO rows are gathered and o / dq rows scattered inside the kernels
+//     (the reference materialises q_sel / do_sel / o_sel, :461 :469 :483 :487);
+//   * the tile -> (sequence, block) map comes from device-side prefixes built
+//     by the compaction kernels (no host list, :348 :413-414);
+//   * the dk/dv kernel starts each key block at its exact first visible query
+//     (the reference rounds down to a block, :374-402) and accumulates the GQA
+//     sum in registers, storing bf16 once (no fp32 [N, HQ, D] buffers);
+//   * an optional sliding window (keys [p - w, p]) turns the same kernels into
+//     the local SWA branch (logo/layers/utils.py:144-147).
+//
+// Tiling (32x32x16 bf16 MFMA, wave64, 4 waves per workgroup):
+//   fwd / dq : 128 compacted rows per workgroup (32 per wave, Q and dO held in
+//              registers as B operands), K/V streamed in 64-key LDS tiles.
+//              S^T = K Q^T puts one query per lane pair, so the softmax row
+//              statistics need a single cross-lane exchange (lane ^ 32).
+//   dk/dv    : 128 keys per workgroup (32 per wave, K and V in registers),
+//              compacted query rows streamed in 64-row LDS tiles, GQA heads
+//              looped inside the workgroup.
+#include <math.h>
+
+#include "capi.hpp"
+#include "common.hpp"
+
+namespace logo {
+
+struct AttnArgs {
+  const bf16* q;
+  const bf16* k;
+  const bf16* v;
+  bf16* o;
+  float* lse;
+  const bf16* dout;
+  float* delta;
+  bf16* dq;
+  bf16* dk;
+  bf16* dv;
+  const int64_t* q_idx;
+  const int32_t* pos;
+  const int32_t* meta;
+  const int32_t* cu;
+  int64_t n;
+  int nseq;
+  int hq;
+  int h;
+  int g;
+  int lanes;
+  int meta_stride;
+  float scale;
+  float scale_log2;
+  int window;
+};
+
+// Per-lane view of the compaction metadata.
+template <bool SPARSE>
+struct RowView {
+  const int64_t* qi;
+  const int32_t* ps;
+  int bos;
+  __device__ __forceinline__ int64_t token(int r) const { return SPARSE ? qi[r] : (int64_t)r; }
+  __device__ __forceinline__ int posn(int r) const { return SPARSE ? ps[r] : r - bos; }
+};
+
+template <bool SPARSE>
+__device__ __forceinline__ RowView<SPARSE> row_view(const AttnArgs& a, int lane_sel, int bos) {
+  RowView<SPARSE> v;
+  v.qi = SPARSE ? a.q_idx + (int64_t)lane_sel * a.n : nullptr;
+  v.ps = SPARSE ? a.pos + (int64_t)lane_sel * a.n : nullptr;
+  v.bos = bos;
+  return v;
+}
+
+extern __shared__ __attribute__((aligned(16))) char logo_smem[];
+__device__ __forceinline__ bf16* dyn_smem() { return reinterpret_cast<bf16*>(logo_smem); }
+
+__device__ __forceinline__ float wave_pair_max(float x) { return fmaxf(x, __shfl_xor(x, 32)); }
+
+// ---------------------------------------------------------------------------
+// Forward
+// ---------------------------------------------------------------------------
+template <int D, bool SPARSE, bool WINDOW>
+__global__ __launch_bounds__(256) void sq_fwd_kernel(const AttnArgs a) {
+  using TL = Tile64<D>;
+  constexpr int RS = TL::RS, TS = TL::TS, DS = D / 16, DT = D / 32;
+  bf16* const smem = dyn_smem();
+  // [K tile 0][K tile 1][V^T tile 0][V^T tile 1]
+  auto sK = [&](int b) { return smem + b * (64 * RS); };
+  auto sVt = [&](int b) { return smem + 128 * RS + b * (D * TS); };
+
+  int rank, hq;
+  xcd_remap(blockIdx.x, a.hq, rank, hq);
+  const int lane_sel = a.lanes > 1 ? hq : 0;
+  const int32_t* meta = a.meta + (int64_t)lane_sel * a.meta_stride;
+  const int nt = meta[1];
+  if (rank >= nt) return;
+  const int tile = nt - 1 - rank;  // heaviest (latest) blocks first
+  const int32_t* cu_q = meta + kMetaHdr;
+  const int32_t* cu_tq = cu_q + (a.nseq + 1);
+  const int s = seg_of(cu_tq, a.nseq, tile);
+  const int r0 = cu_q[s] + (tile - cu_tq[s]) * kBQ;
+  const int r_end = min(r0 + kBQ, cu_q[s + 1]);
+  const int bos = a.cu[s];
+  const int seqlen = a.cu[s + 1] - bos;
+  const int h = hq / a.g;
+  const RowView<SPARSE> rv = row_view<SPARSE>(a, lane_sel, bos);
+
+  const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63, i = l & 31, g = l >> 5;
+  const int rw0 = r0 + 32 * wave;
+  const bool wave_active = rw0 < r_end;
+  const int pmin = wave_active ? rv.posn(rw0) : 0;
+  const int pmax = wave_active ? rv.posn(min(rw0 + 31, r_end - 1)) : -1;
+  const int r = rw0 + i;
+  const bool valid = r < r_end;
+  const int64_t t = valid ? rv.token(r) : 0;
+  const int p = valid ? rv.posn(r) : -1;
+  const int W = a.window;
+  const int kv_lo = WINDOW ? (max(0, rv.posn(r0) - W) & ~63) : 0;
+  const int kv_hi = rv.posn(r_end - 1) + 1;
+
+  bf16x8 qreg[DS];
+  {
+    const bf16* qrow = a.q + (t * a.hq + hq) * D + 8 * g;
+#pragma unroll
+    for (int ds = 0; ds < DS; ++ds)
+      qreg[ds] = valid ? *reinterpret_cast<const bf16x8*>(qrow + 16 * ds) : bf16x8{};
+  }
+
+  f32x16 oacc[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) oacc[dt] = f32x16{};
+  float m_run = -INFINITY, l_run = 0.f;
+  const float c = a.scale_log2;
+
+  const int64_t rstride = (int64_t)a.h * D;
+  const bf16* kbase = a.k + ((int64_t)bos * a.h + h) * D;
+  const bf16* vbase = a.v + ((int64_t)bos * a.h + h) * D;
+  TL kt, vt;
+  auto load_tile = [&](int j0) {
+    kt.load(tid, [&](int rr) -> const bf16* { return j0 + rr < seqlen ? kbase + (j0 + rr) * rstride : nullptr; });
+    vt.load(tid, [&](int rr) -> const bf16* { return j0 + rr < seqlen ? vbase + (j0 + rr) * rstride : nullptr; });
+  };
+
+  load_tile(kv_lo);
+  kt.store_rows(sK(0), tid);
+  vt.store_cols(sVt(0), tid);
+  __syncthreads();
+  int buf = 0;
+  for (int j0 = kv_lo; j0 < kv_hi; j0 += 64) {
+    const bool has_next = j0 + 64 < kv_hi;
+    if (has_next) load_tile(j0 + 64);
+
+    const bool skip = !wave_active || j0 > pmax || (WINDOW && j0 + 63 < pmin - W);
+    if (!skip) {
+      const bool need_mask = (j0 + 63 > pmin) || (WINDOW && j0 < pmax - W);
+      const bf16* kb = sK(buf);
+      const bf16* vb = sVt(buf);
+      f32x16 sacc[2];
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        sacc[kk] = f32x16{};
+#pragma unroll
+        for (int ds = 0; ds < DS; ++ds) sacc[kk] = mfma32(read_row_op<RS>(kb, 32 * kk + i, ds, g), qreg[ds], sacc[kk]);
+      }
+      if (need_mask) {
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+          for (int jj = 0; jj < 16; ++jj) {
+            const int key = j0 + 32 * kk + rowmap(g, jj);
+            bool vis = key <= p;
+            if (WINDOW) vis = vis && key >= p - W;
+            if (!vis) sacc[kk][jj] = -INFINITY;
+          }
+      }
+      float mx = -INFINITY;
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+        for (int jj = 0; jj < 16; ++jj) mx = fmaxf(mx, sacc[kk][jj]);
+      mx = wave_pair_max(mx);
+      const float m_new = fmaxf(m_run, mx);
+      const float base = (m_new == -INFINITY) ? 0.f : m_new * c;
+      const float alpha = fast_exp2(m_run * c - base);
+      float psum = 0.f;
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+        for (int jj = 0; jj < 16; ++jj) {
+          const float pv = fast_exp2(fmaf(sacc[kk][jj], c, -base));
+          sacc[kk][jj] = pv;
+          psum += pv;
+        }
+      l_run = l_run * alpha + psum;
+      m_run = m_new;
+      if (__ballot(alpha != 1.f)) {
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) oacc[dt] *= alpha;
+      }
+      bf16x8 pb[4];
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) pb[ks] = acc_to_bf16(sacc[ks >> 1], ks & 1);
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) oacc[dt] = mfma32(read_perm_k<TS>(vb, 32 * dt + i, ks, g), pb[ks], oacc[dt]);
+    }
+    if (has_next) {
+      kt.store_rows(sK(buf ^ 1), tid);
+      vt.store_cols(sVt(buf ^ 1), tid);
+    }
+    __syncthreads();
+    buf ^= 1;
+  }
+
+  const float l_tot = l_run + __shfl_xor(l_run, 32);
+  if (valid) {
+    const float inv = 1.f / l_tot;
+    bf16* orow = a.o + (t * a.hq + hq) * D;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        bf16x4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = (bf16)(oacc[dt][4 * q4 + e] * inv);
+        *reinterpret_cast<bf16x4*>(orow + 32 * dt + 8 * q4 + 4 * g) = v;
+      }
+    if (g == 0) a.lse[(int64_t)hq * a.n + r] = m_run * c + log2f(l_tot);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Backward preprocess: delta = rowsum(o * dO) per compacted row (fp32).
+// ---------------------------------------------------------------------------
+template <int D, bool SPARSE>
+__global__ __launch_bounds__(256) void sq_delta_kernel(const AttnArgs a) {
+  constexpr int LPR = D / 8;          // lanes per row
+  constexpr int RPB = 256 / LPR;      // rows per workgroup
+  const int hq = blockIdx.y;
+  const int lane_sel = a.lanes > 1 ? hq : 0;
+  const int32_t* meta = a.meta + (int64_t)lane_sel * a.meta_stride;
+  const int sq = meta[0];
+  const int r = blockIdx.x * RPB + threadIdx.x / LPR;
+  const int c = threadIdx.x % LPR;
+  float acc = 0.f;
+  if (r < sq) {
+    const int64_t t = SPARSE ? a.q_idx[(int64_t)lane_sel * a.n + r] : (int64_t)r;
+    const int64_t off = (t * a.hq + hq) * D + 8 * c;
+    const bf16x8 ov = *reinterpret_cast<const bf16x8*>(a.o + off);
+    const bf16x8 dv = *reinterpret_cast<const bf16x8*>(a.dout + off);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc = fmaf((float)ov[e], (float)dv[e], acc);
+  }
+#pragma unroll
+  for (int off = LPR / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
+  if (r < sq && c == 0) a.delta[(int64_t)hq * a.n + r] = acc;
+}
+
+// ---------------------------------------------------------------------------
+// Backward dq
+// ---------------------------------------------------------------------------
+template <int D, bool SPARSE, bool WINDOW>
+__global__ __launch_bounds__(256) void sq_dq_kernel(const AttnArgs a) {
+  using TL = Tile64<D>;
+  constexpr int RS = TL::RS, TS = TL::TS, DS = D / 16, DT = D / 32;
+  bf16* sK = dyn_smem();
+  bf16* sV = sK + 64 * RS;
+  bf16* sKt = sV + 64 * RS;
+
+  int rank, hq;
+  xcd_remap(blockIdx.x, a.hq, rank, hq);
+  const int lane_sel = a.lanes > 1 ? hq : 0;
+  const int32_t* meta = a.meta + (int64_t)lane_sel * a.meta_stride;
+  const int nt = meta[1];
+  if (rank >= nt) return;
+  const int tile = nt - 1 - rank;
+  const int32_t* cu_q = meta + kMetaHdr;
+  const int32_t* cu_tq = cu_q + (a.nseq + 1);
+  const int s = seg_of(cu_tq, a.nseq, tile);
+  const int r0 = cu_q[s] + (tile - cu_tq[s]) * kBQ;
+  const int r_end = min(r0 + kBQ, cu_q[s + 1]);
+  const int bos = a.cu[s];
+  const int seqlen = a.cu[s + 1] - bos;
+  const int h = hq / a.g;
+  const RowView<SPARSE> rv = row_view<SPARSE>(a, lane_sel, bos);
+
+  const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63, i = l & 31, g = l >> 5;
+  const int rw0 = r0 + 32 * wave;
+  const bool wave_active = rw0 < r_end;
+  const int pmin = wave_active ? rv.posn(rw0) : 0;
+  const int pmax = wave_active ? rv.posn(min(rw0 + 31, r_end - 1)) : -1;
+  const int r = rw0 + i;
+  const bool valid = r < r_end;
+  const int64_t t = valid ? rv.token(r) : 0;
+  const int p = valid ? rv.posn(r) : -1;
+  const int W = a.window;
+  const int kv_lo = WINDOW ? (max(0, rv.posn(r0) - W) & ~63) : 0;
+  const int kv_hi = rv.posn(r_end - 1) + 1;
+
+  bf16x8 qreg[DS], doreg[DS];
+  {
+    const int64_t off = (t * a.hq + hq) * D + 8 * g;
+#pragma unroll
+    for (int ds = 0; ds < DS; ++ds) {
+      qreg[ds] = valid ? *reinterpret_cast<const bf16x8*>(a.q + off + 16 * ds) : bf16x8{};
+      doreg[ds] = valid ? *reinterpret_cast<const bf16x8*>(a.dout + off + 16 * ds) : bf16x8{};
+    }
+  }
+  const float lse_q = valid ? a.lse[(int64_t)hq * a.n + r] : 0.f;
+  const float delta_q = valid ? a.delta[(int64_t)hq * a.n + r] : 0.f;
+  const float c = a.scale_log2;
+
+  f32x16 dqacc[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) dqacc[dt] = f32x16{};
+
+  const int64_t rstride = (int64_t)a.h * D;
+  const bf16* kbase = a.k + ((int64_t)bos * a.h + h) * D;
+  const bf16* vbase = a.v + ((int64_t)bos * a.h + h) * D;
+  TL kt, vt;
+  auto load_tile = [&](int j0) {
+    kt.load(tid, [&](int rr) -> const bf16* { return j0 + rr < seqlen ? kbase + (j0 + rr) * rstride : nullptr; });
+    vt.load(tid, [&](int rr) -> const bf16* { return j0 + rr < seqlen ? vbase + (j0 + rr) * rstride : nullptr; });
+  };
+
+  load_tile(kv_lo);
+  kt.store_rows(sK, tid);
+  kt.store_cols(sKt, tid);
+  vt.store_rows(sV, tid);
+  __syncthreads();
+  for (int j0 = kv_lo; j0 < kv_hi; j0 += 64) {
+    const bool has_next = j0 + 64 < kv_hi;
+    if (has_next) load_tile(j0 + 64);
+
+    const bool skip = !wave_active || j0 > pmax || (WINDOW && j0 + 63 < pmin - W);
+    if (!skip) {
+      const bool need_mask = (j0 + 63 > pmin) || (WINDOW && j0 < pmax - W);
+      f32x16 sacc[2], pacc[2];
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        sacc[kk] = f32x16{};
+        pacc[kk] = f32x16{};
+#pragma unroll
+        for (int ds = 0; ds < DS; ++ds) {
+          sacc[kk] = mfma32(read_row_op<RS>(sK, 32 * kk + i, ds, g), qreg[ds], sacc[kk]);
+          pacc[kk] = mfma32(read_row_op<RS>(sV, 32 * kk + i, ds, g), doreg[ds], pacc[kk]);
+        }
+      }
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+        for (int jj = 0; jj < 16; ++jj) {
+          float pv = fast_exp2(fmaf(sacc[kk][jj], c, -lse_q));
+          if (need_mask) {
+            const int key = j0 + 32 * kk + rowmap(g, jj);
+            bool vis = key <= p;
+            if (WINDOW) vis = vis && key >= p - W;
+            if (!vis) pv = 0.f;
+          }
+          sacc[kk][jj] = pv * (pacc[kk][jj] - delta_q);
+        }
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+          dqacc[dt] = mfma32(read_perm_k<TS>(sKt, 32 * dt + i, ks, g), acc_to_bf16(sacc[ks >> 1], ks & 1), dqacc[dt]);
+    }
+    __syncthreads();
+    if (has_next) {
+      kt.store_rows(sK, tid);
+      kt.store_cols(sKt, tid);
+      vt.store_rows(sV, tid);
+    }
+    __syncthreads();
+  }
+
+  if (valid) {
+    bf16* dqrow = a.dq + (t * a.hq + hq) * D;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        bf16x4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = (bf16)(dqacc[dt][4 * q4 + e] * a.scale);
+        *reinterpret_cast<bf16x4*>(dqrow + 32 * dt + 8 * q4 + 4 * g) = v;
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Backward dk / dv
+// ---------------------------------------------------------------------------
+template <int D, bool SPARSE, bool WINDOW>
+__global__ __launch_bounds__(256) void sq_dkv_kernel(const AttnArgs a) {
+  using TL = Tile64<D>;
+  constexpr int RS = TL::RS, TS = TL::TS, DS = D / 16, DT = D / 32;
+  bf16* sQ = dyn_smem();
+  bf16* sO = sQ + 64 * RS;
+  bf16* sQt = sO + 64 * RS;
+  bf16* sOt = sQt + D * TS;
+  float* sLse = reinterpret_cast<float*>(sOt + D * TS);
+  float* sDelta = sLse + 64;
+  int* sPos = reinterpret_cast<int*>(sDelta + 64);
+
+  int rank, h;
+  xcd_remap(blockIdx.x, a.h, rank, h);
+  const int32_t* meta0 = a.meta;
+  const int ntk = meta0[2];
+  if (rank >= ntk) return;
+  const int tile = rank;  // early key blocks (most queries) first
+  const int32_t* cu_tk = meta0 + kMetaHdr + 2 * (a.nseq + 1);
+  const int s = seg_of(cu_tk, a.nseq, tile);
+  const int k0 = (tile - cu_tk[s]) * kBKV;
+  const int bos = a.cu[s];
+  const int seqlen = a.cu[s + 1] - bos;
+  const int k_last = min(k0 + kBKV, seqlen) - 1;
+
+  const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63, i = l & 31, g = l >> 5;
+  const int kw0 = k0 + 32 * wave;
+  const bool wave_active = kw0 < seqlen;
+  const int kw_last = min(kw0 + 31, seqlen - 1);
+  const int key = kw0 + i;
+  const bool valid_k = key < seqlen;
+  const int W = a.window;
+  const float c = a.scale_log2;
+
+  bf16x8 kreg[DS], vreg[DS];
+  {
+    const int64_t off = ((int64_t)(bos + key) * a.h + h) * D + 8 * g;
+#pragma unroll
+    for (int ds = 0; ds < DS; ++ds) {
+      kreg[ds] = valid_k ? *reinterpret_cast<const bf16x8*>(a.k + off + 16 * ds) : bf16x8{};
+      vreg[ds] = valid_k ? *reinterpret_cast<const bf16x8*>(a.v + off + 16 * ds) : bf16x8{};
+    }
+  }
+  f32x16 dkacc[DT], dvacc[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) {
+    dkacc[dt] = f32x16{};
+    dvacc[dt] = f32x16{};
+  }
+
+  TL qt, ot;
+  for (int gg = 0; gg < a.g; ++gg) {
+    const int hq = h * a.g + gg;
+    const int lane_sel = a.lanes > 1 ? hq : 0;
+    const int32_t* cu_q = a.meta + (int64_t)lane_sel * a.meta_stride + kMetaHdr;
+    const RowView<SPARSE> rv = row_view<SPARSE>(a, lane_sel, bos);
+    const int q_lo = cu_q[s], q_hi = cu_q[s + 1];
+    int rq0, rq_end;
+    if (SPARSE) {
+      rq0 = lower_bound_i32(rv.ps, q_lo, q_hi, k0);
+      rq_end = WINDOW ? lower_bound_i32(rv.ps, rq0, q_hi, k_last + W + 1) : q_hi;
+    } else {
+      rq0 = min(q_lo + k0, q_hi);
+      rq_end = WINDOW ? min(q_hi, q_lo + k_last + W + 1) : q_hi;
+    }
+    const int64_t qoff = (int64_t)hq * D;
+    const int64_t qstride = (int64_t)a.hq * D;
+    auto load_tile = [&](int rt) {
+      qt.load(tid, [&](int rr) -> const bf16* {
+        return rt + rr < rq_end ? a.q + rv.token(rt + rr) * qstride + qoff : nullptr;
+      });
+      ot.load(tid, [&](int rr) -> const bf16* {
+        return rt + rr < rq_end ? a.dout + rv.token(rt + rr) * qstride + qoff : nullptr;
+      });
+    };
+    if (rq0 < rq_end) load_tile(rq0);
+    for (int rt = rq0; rt < rq_end; rt += 64) {
+      const bool has_next = rt + 64 < rq_end;
+      __syncthreads();  // previous tile fully consumed
+      qt.store_rows(sQ, tid);
+      qt.store_cols(sQt, tid);
+      ot.store_rows(sO, tid);
+      ot.store_cols(sOt, tid);
+      if (tid < 64) {
+        const int rr = rt + tid;
+        const bool ok = rr < rq_end;
+        sLse[tid] = ok ? a.lse[(int64_t)hq * a.n + rr] : 0.f;
+        sDelta[tid] = ok ? a.delta[(int64_t)hq * a.n + rr] : 0.f;
+        sPos[tid] = ok ? rv.posn(rr) : -1;
+      }
+      __syncthreads();
+      if (has_next) load_tile(rt + 64);
+
+      const int last = min(rt + 63, rq_end - 1);
+      const int p_first = sPos[0];
+      const int p_last = sPos[last - rt];
+      const bool skip = !wave_active || p_last < kw0 || (WINDOW && p_first > kw_last + W);
+      if (!skip) {
+        const bool need_mask = WINDOW || (p_first < kw_last) || (rt + 64 > rq_end);
+        f32x16 sacc[2], pacc[2];
+#pragma unroll
+        for (int qq = 0; qq < 2; ++qq) {
+          sacc[qq] = f32x16{};
+          pacc[qq] = f32x16{};
+#pragma unroll
+          for (int ds = 0; ds < DS; ++ds) {
+            sacc[qq] = mfma32(read_row_op<RS>(sQ, 32 * qq + i, ds, g), kreg[ds], sacc[qq]);
+            pacc[qq] = mfma32(read_row_op<RS>(sO, 32 * qq + i, ds, g), vreg[ds], pacc[qq]);
+          }
+        }
+#pragma unroll
+        for (int qq = 0; qq < 2; ++qq)
+#pragma unroll
+          for (int jj = 0; jj < 16; ++jj) {
+            const int qr = 32 * qq + rowmap(g, jj);
+            float pv = fast_exp2(fmaf(sacc[qq][jj], c, -sLse[qr]));
+            if (need_mask) {
+              const int pq = sPos[qr];
+              bool vis = key <= pq;
+              if (WINDOW) vis = vis && key >= pq - W;
+              if (!vis) pv = 0.f;
+            }
+            sacc[qq][jj] = pv;
+            pacc[qq][jj] = pv * (pacc[qq][jj] - sDelta[qr]);
+          }
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+          const bf16x8 pb = acc_to_bf16(sacc[ks >> 1], ks & 1);
+          const bf16x8 db = acc_to_bf16(pacc[ks >> 1], ks & 1);
+#pragma unroll
+          for (int dt = 0; dt < DT; ++dt) {
+            dvacc[dt] = mfma32(read_perm_k<TS>(sOt, 32 * dt + i, ks, g), pb, dvacc[dt]);
+            dkacc[dt] = mfma32(read_perm_k<TS>(sQt, 32 * dt + i, ks, g), db, dkacc[dt]);
+          }
+        }
+      }
+    }
+  }
+
+  if (valid_k) {
+    const int64_t off = ((int64_t)(bos + key) * a.h + h) * D;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        bf16x4 kv, vv;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          kv[e] = (bf16)(dkacc[dt][4 * q4 + e] * a.scale);
+          vv[e] = (bf16)dvacc[dt][4 * q4 + e];
+        }
+        *reinterpret_cast<bf16x4*>(a.dk + off + 32 * dt + 8 * q4 + 4 * g) = kv;
+        *reinterpret_cast<bf16x4*>(a.dv + off + 32 * dt + 8 * q4 + 4 * g) = vv;
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host launchers
+// ---------------------------------------------------------------------------
+template <int D>
+constexpr size_t fwd_smem() { return (size_t)(2 * 64 * (D + 8) + 2 * D * 68) * sizeof(bf16); }
+template <int D>
+constexpr size_t dq_smem() { return (size_t)(2 * 64 * (D + 8) + D * 68) * sizeof(bf16); }
+template <int D>
+constexpr size_t dkv_smem() { return (size_t)(2 * 64 * (D + 8) + 2 * D * 68) * sizeof(bf16) + 3 * 64 * 4; }
+
+template <typename K>
+static hipError_t allow_smem(K kernel, size_t bytes) {
+  return hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+}
+
+static int check_common(int64_t n, int nseq, int hq, int h, int d, int lanes, int dtype) {
+  LOGO_REQUIRE(n > 0 && n < ((int64_t)1 << 31), "n_tokens out of range: %lld", (long long)n);
+  LOGO_REQUIRE(nseq >= 1, "nseq must be >= 1");
+  LOGO_REQUIRE(h >= 1 && hq >= h && hq % h == 0, "HQ (%d) must be a multiple of H (%d)", hq, h);
+  LOGO_REQUIRE(d == 64 || d == 128, "head dim %d unsupported (64 or 128)", d);
+  LOGO_REQUIRE(lanes == 1 || lanes == hq, "lanes must be 1 or HQ");
+  LOGO_REQUIRE(dtype == LOGO_DTYPE_BF16, "only bf16 tensors are supported");
+  return LOGO_OK;
+}
+
+template <int D, bool SPARSE, bool WINDOW>
+static int launch_fwd(const AttnArgs& a, hipStream_t st) {
+  const int64_t ntmax = (a.n + kBQ - 1) / kBQ + a.nseq;
+  const int64_t nblk = ntmax * a.hq;
+  LOGO_REQUIRE(nblk < ((int64_t)1 << 31), "grid too large");
+  auto kern = sq_fwd_kernel<D, SPARSE, WINDOW>;
+  LOGO_HIP_CHECK(allow_smem(kern, fwd_smem<D>()));
+  hipLaunchKernelGGL(kern, dim3((unsigned)nblk), dim3(256), fwd_smem<D>(), st, a);
+  LOGO_LAUNCH_CHECK("sq_fwd_kernel");
+  return LOGO_OK;
+}
+
+// Backward phases: 0 = delta, 1 = dq, 2 = dk/dv, -1 = all three in order.
+template <int D, bool SPARSE, bool WINDOW>
+static int launch_bwd_phase(const AttnArgs& a, hipStream_t st, int phase) {
+  if (phase < 0 || phase == 0) {
+    constexpr int RPB = 256 / (D / 8);
+    dim3 grid((unsigned)((a.n + RPB - 1) / RPB), a.hq);
+    hipLaunchKernelGGL((sq_delta_kernel<D, SPARSE>), grid, dim3(256), 0, st, a);
+    LOGO_LAUNCH_CHECK("sq_delta_kernel");
+  }
+  if (phase < 0 || phase == 1) {
+    const int64_t ntmax = (a.n + kBQ - 1) / kBQ + a.nseq;
+    auto kern = sq_dq_kernel<D, SPARSE, WINDOW>;
+    LOGO_HIP_CHECK(allow_smem(kern, dq_smem<D>()));
+    hipLaunchKernelGGL(kern, dim3((unsigned)(ntmax * a.hq)), dim3(256), dq_smem<D>(), st, a);
+    LOGO_LAUNCH_CHECK("sq_dq_kernel");
+  }
+  if (phase < 0 || phase == 2) {
+    const int64_t ntmax = (a.n + kBKV - 1) / kBKV + a.nseq;
+    auto kern = sq_dkv_kernel<D, SPARSE, WINDOW>;
+    LOGO_HIP_CHECK(allow_smem(kern, dkv_smem<D>()));
+    hipLaunchKernelGGL(kern, dim3((unsigned)(ntmax * a.h)), dim3(256), dkv_smem<D>(), st, a);
+    LOGO_LAUNCH_CHECK("sq_dkv_kernel");
+  }
+  return LOGO_OK;
+}
+
+template <int D, bool SPARSE, bool WINDOW>
+static int launch_bwd(const AttnArgs& a, hipStream_t st) { return launch_bwd_phase<D, SPARSE, WINDOW>(a, st, -1); }
+template <int D, bool SPARSE, bool WINDOW>
+static int launch_bwd_delta(const AttnArgs& a, hipStream_t st) { return launch_bwd_phase<D, SPARSE, WINDOW>(a, st, 0); }
+template <int D, bool SPARSE, bool WINDOW>
+static int launch_bwd_dq(const AttnArgs& a, hipStream_t st) { return launch_bwd_phase<D, SPARSE, WINDOW>(a, st, 1); }
+template <int D, bool SPARSE, bool WINDOW>
+static int launch_bwd_dkv(const AttnArgs& a, hipStream_t st) { return launch_bwd_phase<D, SPARSE, WINDOW>(a, st, 2); }
+
+static AttnArgs make_args(const void* q, const void* k, const void* v, const int64_t* q_idx,
+                          const int32_t* pos, const int32_t* meta, const int32_t* cu, int64_t n,
+                          int nseq, int hq, int h, int lanes, float scale, int window) {
+  AttnArgs a{};
+  a.q = static_cast<const bf16*>(q);
+  a.k = static_cast<const bf16*>(k);
+  a.v = static_cast<const bf16*>(v);
+  a.q_idx = q_idx;
+  a.pos = pos;
+  a.meta = meta;
+  a.cu = cu;
+  a.n = n;
+  a.nseq = nseq;
+  a.hq = hq;
+  a.h = h;
+  a.g = hq / h;
+  a.lanes = lanes;
+  a.meta_stride = LOGO_META_STRIDE(nseq);
+  a.scale = scale;
+  a.scale_log2 = scale * 1.4426950408889634f;
+  a.window = window;
+  return a;
+}
+
+#define LOGO_DISPATCH(FN, a, st, d, sparse, window)                                   \
+  ((d) == 128 ? ((sparse) ? ((window) ? FN<128, true, true>(a, st) : FN<128, true, false>(a, st))   \
+                          : ((window) ? FN<128, false, true>(a, st) : FN<128, false, false>(a, st))) \
+              : ((sparse) ? ((window) ? FN<64, true, true>(a, st) : FN<64, true, false>(a, st))     \
+                          : ((window) ? FN<64, false, true>(a, st) : FN<64, false, false>(a, st))))
+
+}  // namespace logo
+
+using namespace logo;
+
+extern "C" int logo_sq_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
+                           const int64_t* q_idx, const int32_t* pos, const int32_t* meta,
+                           const int32_t* cu, int64_t n_tokens, int nseq, int hq, int h, int d,
+                           int lanes, float scale, int window, int dtype, void* stream) {
+  int rc = check_common(n_tokens, nseq, hq, h, d, lanes, dtype);
+  if (rc != LOGO_OK) return rc;
+  LOGO_REQUIRE(q && k && v && o && lse && meta && cu, "null pointer argument");
+  LOGO_REQUIRE((q_idx == nullptr) == (pos == nullptr), "q_idx and pos must both be set or both be null");
+  AttnArgs a = make_args(q, k, v, q_idx, pos, meta, cu, n_tokens, nseq, hq, h, lanes, scale, window);
+  a.o = static_cast<bf16*>(o);
+  a.lse = lse;
+  const bool sparse = q_idx != nullptr;
+  const bool win = window >= 0;
+  return LOGO_DISPATCH(launch_fwd, a, as_stream(stream), d, sparse, win);
+}
+
+#define LOGO_BWD_PARAMS                                                                       \
+  const void *q, const void *k, const void *v, const void *o, const void *dout, const float *lse, \
+      float *delta, void *dq, void *dk, void *dv, const int64_t *q_idx, const int32_t *pos,          \
+      const int32_t *meta, const int32_t *cu, int64_t n_tokens, int nseq, int hq, int h, int d,      \
+      int lanes, float scale, int window, int dtype, void *stream
+
+#define LOGO_BWD_ARGS                                                                             \
+  q, k, v, o, dout, lse, delta, dq, dk, dv, q_idx, pos, meta, cu, n_tokens, nseq, hq, h, d, lanes, \
+      scale, window, dtype, stream
+
+static int bwd_entry(LOGO_BWD_PARAMS, int phase) {
+  int rc = check_common(n_tokens, nseq, hq, h, d, lanes, dtype);
+  if (rc != LOGO_OK) return rc;
+  LOGO_REQUIRE(q && k && v && o && dout && lse && delta && meta && cu, "null pointer argument");
+  LOGO_REQUIRE(phase == 0 || (dq && dk && dv), "null gradient pointer");
+  LOGO_REQUIRE((q_idx == nullptr) == (pos == nullptr), "q_idx and pos must both be set or both be null");
+  AttnArgs a = make_args(q, k, v, q_idx, pos, meta, cu, n_tokens, nseq, hq, h, lanes, scale, window);
+  a.o = const_cast<bf16*>(static_cast<const bf16*>(o));
+  a.dout = static_cast<const bf16*>(dout);
+  a.lse = const_cast<float*>(lse);
+  a.delta = delta;
+  a.dq = static_cast<bf16*>(dq);
+  a.dk = static_cast<bf16*>(dk);
+  a.dv = static_cast<bf16*>(dv);
+  const bool sparse = q_idx != nullptr;
+  const bool win = window >= 0;
+  hipStream_t st = as_stream(stream);
+  switch (phase) {
+    case 0: return LOGO_DISPATCH(launch_bwd_delta, a, st, d, sparse, win);
+    case 1: return LOGO_DISPATCH(launch_bwd_dq, a, st, d, sparse, win);
+    case 2: return LOGO_DISPATCH(launch_bwd_dkv, a, st, d, sparse, win);
+    default: return LOGO_DISPATCH(launch_bwd, a, st, d, sparse, win);
+  }
+}
+
+extern "C" int logo_sq_bwd(LOGO_BWD_PARAMS) { return bwd_entry(LOGO_BWD_ARGS, -1); }
+extern "C" int logo_sq_bwd_delta(LOGO_BWD_PARAMS) { return bwd_entry(LOGO_BWD_ARGS, 0); }
+extern "C" int logo_sq_bwd_dq(LOGO_BWD_PARAMS) { return bwd_entry(LOGO_BWD_ARGS, 1); }
+extern "C" int logo_sq_bwd_dkv(LOGO_BWD_PARAMS) { return bwd_entry(LOGO_BWD_ARGS, 2); }

@@ -1,0 +1,180 @@
+"""Query-sparse causal attention (``sq_full_attn``) on the HIP kernels.
+
+Drop-in for logo/ops/selected_full_attn.py:495-527: same signature, the same
+``AssertionError`` checks (:518-522), default ``scale = K ** -0.5`` (:523-524),
+zero output rows for unselected tokens (:469-471) and gradients for q, k, v
+only (:492).  The same kernels, in dense mode with a window, give the local
+sliding-window branch (``swa_attn``) and the dense causal global branch
+(``dense_causal_attn``).
+"""
+
+import functools
+from typing import Optional
+
+import torch
+
+from .. import _lib
+from .common import DeviceSelection, compact_selection, dense_selection
+
+__all__ = ["sq_full_attn", "swa_attn", "dense_causal_attn", "SQFullAttentionFunction"]
+
+_custom_fwd = functools.partial(torch.amp.custom_fwd, device_type="cuda")
+_custom_bwd = functools.partial(torch.amp.custom_bwd, device_type="cuda")
+
+
+def _to_kernel_dtype(t: torch.Tensor) -> torch.Tensor:
+    # The kernels compute in bf16 with fp32 accumulation; fp16/fp32 inputs are
+    # rounded to bf16 (the reference's Triton path likewise runs its dots at
+    # reduced precision).
+    return t.contiguous() if t.dtype == torch.bfloat16 else t.to(torch.bfloat16).contiguous()
+
+
+def _fwd(q, k, v, dsel: DeviceSelection, scale: float, window: int):
+    n, hq, d = q.shape
+    h = k.shape[1]
+    o = torch.zeros(n, hq, d, dtype=torch.bfloat16, device=q.device)
+    lse = torch.empty(hq, n, dtype=torch.float32, device=q.device)
+    lib = _lib.lib()
+    _lib.launch("logo_sq_fwd", lib.logo_sq_fwd,
+                _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(o), _lib.ptr(lse),
+                _lib.ptr(dsel.q_idx), _lib.ptr(dsel.pos), _lib.ptr(dsel.meta), _lib.ptr(dsel.cu),
+                n, dsel.nseq, hq, h, d, dsel.lanes, float(scale), int(window), _lib.DTYPE_BF16,
+                _lib.stream_of(q))
+    return o, lse
+
+
+def _bwd(q, k, v, o, lse, do, dsel: DeviceSelection, scale: float, window: int):
+    n, hq, d = q.shape
+    h = k.shape[1]
+    dq = torch.zeros_like(q)
+    dk = torch.empty_like(k)
+    dv = torch.empty_like(v)
+    delta = torch.empty(hq, n, dtype=torch.float32, device=q.device)
+    lib = _lib.lib()
+    args = (_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(o), _lib.ptr(do), _lib.ptr(lse),
+            _lib.ptr(delta), _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(dv),
+            _lib.ptr(dsel.q_idx), _lib.ptr(dsel.pos), _lib.ptr(dsel.meta), _lib.ptr(dsel.cu),
+            n, dsel.nseq, hq, h, d, dsel.lanes, float(scale), int(window), _lib.DTYPE_BF16,
+            _lib.stream_of(q))
+    _lib.launch("logo_sq_bwd_delta", lib.logo_sq_bwd_delta, *args)
+    _lib.launch("logo_sq_bwd_dq", lib.logo_sq_bwd_dq, *args)
+    _lib.launch("logo_sq_bwd_dkv", lib.logo_sq_bwd_dkv, *args)
+    return dq, dk, dv
+
+
+class SQFullAttentionFunction(torch.autograd.Function):
+    """Autograd wrapper (logo/ops/selected_full_attn.py:449-492)."""
+
+    @staticmethod
+    @_custom_fwd
+    def forward(ctx, q, k, v, scale, dsel: DeviceSelection, window: int = -1):
+        B, T, HQ, K = q.shape
+        H = k.shape[2]
+        V = v.shape[3]
+        in_dtypes = (q.dtype, k.dtype, v.dtype)
+        qf = _to_kernel_dtype(q).view(B * T, HQ, K)
+        kf = _to_kernel_dtype(k).view(B * T, H, K)
+        vf = _to_kernel_dtype(v).view(B * T, H, V)
+        o, lse = _fwd(qf, kf, vf, dsel, scale, window)
+        ctx.save_for_backward(qf, kf, vf, o, lse)
+        ctx.dsel = dsel
+        ctx.scale = scale
+        ctx.window = window
+        ctx.shapes = (B, T, HQ, H, K, V)
+        ctx.in_dtypes = in_dtypes
+        out = o.view(B, T, HQ, V)
+        return out if q.dtype == torch.bfloat16 else out.to(q.dtype)
+
+    @staticmethod
+    @_custom_bwd
+    def backward(ctx, do):
+        qf, kf, vf, o, lse = ctx.saved_tensors
+        B, T, HQ, H, K, V = ctx.shapes
+        dof = _to_kernel_dtype(do).view(B * T, HQ, V)
+        dq, dk, dv = _bwd(qf, kf, vf, o, lse, dof, ctx.dsel, ctx.scale, ctx.window)
+        tq, tk, tv = ctx.in_dtypes
+        dq = dq.view(B, T, HQ, K).to(tq)
+        dk = dk.view(B, T, H, K).to(tk)
+        dv = dv.view(B, T, H, V).to(tv)
+        return dq, dk, dv, None, None, None
+
+
+def _check_qkv(q, k, v):
+    assert q.dim() == 4 and k.dim() == 4 and v.dim() == 4, "q/k/v must be [B, T, H, D]"
+    B, T, HQ, K = q.shape
+    H = k.shape[2]
+    assert HQ % H == 0, "HQ must be a multiple of H (GQA)"
+    assert K <= 256, "K must fit in a single block (<=256)"
+    _lib.require_gpu(q, k, v)
+    return B, T, HQ, H, K
+
+
+def sq_full_attn(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    selection: torch.Tensor,
+    scale: Optional[float] = None,
+    cu_seqlens: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    r"""Selected-query full causal attention.
+
+    Args:
+        q: queries `[1, total_tokens, HQ, K]`.
+        k: keys    `[1, total_tokens, H, K]` (GQA when HQ % H == 0).
+        v: values  `[1, total_tokens, H, V]`.
+        selection: per-token bool mask `[1, total_tokens]`, or the per-head
+            extension `[1, total_tokens, HQ]`.
+        scale: attention scale; defaults to `K ** -0.5`.
+        cu_seqlens: required `[Nseq+1]` int tensor for packed varlen input.
+
+    Returns:
+        o: `[1, total_tokens, HQ, V]`; rows for unselected query tokens are 0.
+    """
+    B, T, HQ, K = q.shape
+    H = k.shape[2]
+    assert q.dim() == 4 and k.dim() == 4 and v.dim() == 4, "q/k/v must be [B, T, H, D]"
+    assert HQ % H == 0, "HQ must be a multiple of H (GQA)"
+    per_head = selection.dim() == 3
+    assert selection.dtype == torch.bool and (
+        selection.shape == (B, T) or (per_head and selection.shape == (B, T, HQ))
+    ), "selection must be a bool mask [B, T]"
+    assert B == 1, "sq_full_attn only supports B=1 packed-varlen input"
+    assert cu_seqlens is not None, "sq_full_attn requires explicit cu_seqlens"
+    assert K <= 256, "K must fit in a single block (<=256)"
+    if scale is None:
+        scale = K ** -0.5
+    _lib.require_gpu(q, k, v, selection)
+    if T == 0:
+        return q.new_zeros(B, T, HQ, v.shape[3])
+    dsel = compact_selection(selection.reshape(B * T, *selection.shape[2:]), cu_seqlens)
+    dsel.B, dsel.T = B, T
+    return SQFullAttentionFunction.apply(q, k, v, scale, dsel, -1)
+
+
+def swa_attn(q, k, v, cu_seqlens: torch.Tensor, window: int = 128,
+             scale: Optional[float] = None) -> torch.Tensor:
+    """Causal sliding-window attention over every row: keys ``[p - window, p]``
+    of the row's own segment (flash-attn ``window_size=(w, w)``, ``causal=True``
+    as used by logo/layers/utils.py:144-147, :166-178).  ``q [1, N, HQ, D]``."""
+    B, T, HQ, H, K = _check_qkv(q, k, v)
+    assert B == 1, "swa_attn takes packed [1, N, H, D] input"
+    if scale is None:
+        scale = K ** -0.5
+    if T == 0:
+        return q.new_zeros(B, T, HQ, v.shape[3])
+    dsel = dense_selection(cu_seqlens, B * T, q.device)
+    return SQFullAttentionFunction.apply(q, k, v, scale, dsel, int(window))
+
+
+def dense_causal_attn(q, k, v, cu_seqlens: torch.Tensor, scale: Optional[float] = None) -> torch.Tensor:
+    """Dense causal attention over every row (the ``"flash"`` global branch,
+    logo/layers/logo.py:211-224), on the same kernels without compaction."""
+    B, T, HQ, H, K = _check_qkv(q, k, v)
+    assert B == 1, "dense_causal_attn takes packed [1, N, H, D] input"
+    if scale is None:
+        scale = K ** -0.5
+    if T == 0:
+        return q.new_zeros(B, T, HQ, v.shape[3])
+    dsel = dense_selection(cu_seqlens, B * T, q.device)
+    return SQFullAttentionFunction.apply(q, k, v, scale, dsel, -1)

@@ -1,0 +1,167 @@
+"""GPU parity of the HIP query-sparse attention against the oracle.
+
+Small and mid sizes compare with oracle.attn (numpy, CPU); the full-size
+cases use the fp32 torch reference of tests/helpers.py (pinned against the
+oracle in tests/test_oracle_attn.py).  Tolerance: bf16
+outputs and gradients within max-abs 2e-2 and mean-abs 2e-3 of the fp32
+reference.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from logo_amd.ops import dense_causal_attn, sq_full_attn, sq_full_attn_dense_ref, swa_attn
+from oracle import attn
+from tests.helpers import (assert_within, cu_from_lengths, gen, markov_selection, randn,
+                           torch_sq_attn, varlen_lengths)
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(q, k, v, sel, cu, dev, do=None, scale=None):
+    qg, kg, vg = (x.to(dev).requires_grad_(do is not None) for x in (q, k, v))
+    o = sq_full_attn(qg[None], kg[None], vg[None], sel.to(dev)[None], scale=scale, cu_seqlens=cu.to(dev))[0]
+    if do is None:
+        return o, None
+    o.backward(do.to(dev))
+    return o, (qg.grad, kg.grad, vg.grad)
+
+
+def _oracle(q, k, v, sel, cu, do=None, scale=None, window=None, dtype=np.float64):
+    qn, kn, vn = (x.float().numpy() for x in (q, k, v))
+    o, lse = attn.sq_attn_fwd(qn, kn, vn, None if sel is None else sel.numpy(), cu.numpy(), scale=scale,
+                              window=window, dtype=dtype)
+    if do is None:
+        return o, None
+    grads = attn.sq_attn_bwd(qn, kn, vn, o, do.float().numpy(), None if sel is None else sel.numpy(),
+                             cu.numpy(), scale=scale, window=window, dtype=dtype)
+    return o, grads
+
+
+@pytest.mark.parametrize("n,hq,h,d,ratio,cu,per_head", [
+    (512, 4, 4, 64, 0.5, [0, 512], True),            # cfg1 shape, per-head extension
+    (512, 4, 4, 64, 0.5, [0, 512], False),           # cfg1 shape, reference API
+    (700, 4, 2, 128, 0.4, [0, 1, 1, 200, 700], False),  # GQA, zero/single-token segments
+    (1000, 2, 2, 128, 1.0, [0, 333, 1000], False),   # all selected
+    (300, 2, 1, 64, 0.1, [0, 150, 300], True),       # sparse per-head GQA
+])
+def test_fwd_bwd_matches_oracle(gpu, n, hq, h, d, ratio, cu, per_head):
+    g = gen(n + hq)
+    q, k, v = randn((n, hq, d), g), randn((n, h, d), g), randn((n, h, d), g)
+    do = randn((n, hq, d), g)
+    sel = torch.rand((n, hq) if per_head else (n,), generator=g) < ratio
+    cu = torch.tensor(cu, dtype=torch.int32)
+    print(f"fwd/bwd n={n} hq={hq} h={h} d={d} ratio={ratio} per_head={per_head}", flush=True)
+    o, (dq, dk, dv) = _run(q, k, v, sel, cu, gpu, do)
+    ro, (rdq, rdk, rdv) = _oracle(q, k, v, sel, cu, do)
+    assert_within("o", o, ro)
+    assert_within("dq", dq, rdq)
+    assert_within("dk", dk, rdk)
+    assert_within("dv", dv, rdv)
+    rows_off = ~sel if sel.dim() == 1 else ~sel
+    if sel.dim() == 1:
+        assert torch.all(o[rows_off.to(gpu)] == 0) and torch.all(dq[rows_off.to(gpu)] == 0)
+
+
+def test_cfg2_forward_per_head(gpu):
+    """cfg2: bf16, T=8192, H=16, D=128, per-(head, token) Bernoulli(0.5), token 0 on."""
+    n, hq, d = 8192, 16, 128
+    g = gen(1)
+    q, k, v = (randn((n, hq, d), g, 0.5) for _ in range(3))
+    sel = torch.rand(n, hq, generator=g) < 0.5
+    sel[0, :] = True
+    cu = torch.tensor([0, n], dtype=torch.int32)
+    print("cfg2 forward", flush=True)
+    o, _ = _run(q, k, v, sel, cu, gpu)
+    ro, _ = _oracle(q, k, v, sel, cu, dtype=np.float32)
+    assert_within("o", o, ro)
+
+
+def test_cfg3_varlen_fwd_bwd_full_size(gpu):
+    """cfg3: packed varlen ~32K tokens, Markov selection ratio 0.25, dO ~ N(0,1)."""
+    g = gen(2)
+    lens = varlen_lengths(g)
+    n = sum(lens)
+    hq = h = 16
+    d = 128
+    sel = markov_selection(n, g)
+    q, k, v = (randn((n, hq, d), g, 0.5) for _ in range(3))
+    do = randn((n, hq, d), g)
+    cu = cu_from_lengths(lens)
+    print(f"cfg3 lens={lens} ratio={sel.float().mean():.3f}", flush=True)
+    o, (dq, dk, dv) = _run(q, k, v, sel, cu, gpu, do)
+    ro, (rdq, rdk, rdv) = torch_sq_attn(q.to(gpu), k.to(gpu), v.to(gpu), sel.to(gpu), cu,
+                                        do=do.to(gpu))
+    assert_within("o", o, ro)
+    assert_within("dq", dq, rdq)
+    assert_within("dk", dk, rdk)
+    assert_within("dv", dv, rdv)
+
+
+def test_empty_selection(gpu):
+    n, hq, d = 300, 2, 128
+    g = gen(5)
+    q, k, v = (randn((n, hq, d), g) for _ in range(3))
+    do = randn((n, hq, d), g)
+    sel = torch.zeros(n, dtype=torch.bool)
+    o, (dq, dk, dv) = _run(q, k, v, sel, torch.tensor([0, 100, 300], dtype=torch.int32), gpu, do)
+    assert torch.all(o == 0) and torch.all(dq == 0) and torch.all(dk == 0) and torch.all(dv == 0)
+
+
+def test_dense_paths_and_dense_ref(gpu):
+    n, hq, d = 1100, 4, 128
+    g = gen(6)
+    q, k, v = (randn((n, hq, d), g) for _ in range(3))
+    cu = torch.tensor([0, 100, 1100], dtype=torch.int32)
+    ro, _ = _oracle(q, k, v, None, cu)
+    o1 = sq_full_attn_dense_ref(q[None].to(gpu), k[None].to(gpu), v[None].to(gpu), cu_seqlens=cu.to(gpu))[0]
+    o2 = dense_causal_attn(q[None].to(gpu), k[None].to(gpu), v[None].to(gpu), cu.to(gpu))[0]
+    assert_within("dense_ref", o1, ro)
+    assert_within("dense", o2, ro)
+
+
+@pytest.mark.parametrize("window", [128, 16])
+def test_swa_fwd_bwd_matches_oracle(gpu, window):
+    n, hq, h, d = 900, 4, 2, 128
+    g = gen(7 + window)
+    q, k, v = randn((n, hq, d), g), randn((n, h, d), g), randn((n, h, d), g)
+    do = randn((n, hq, d), g)
+    cu = torch.tensor([0, 50, 51, 900], dtype=torch.int32)
+    qg, kg, vg = (x.to(gpu).requires_grad_() for x in (q, k, v))
+    o = swa_attn(qg[None], kg[None], vg[None], cu.to(gpu), window=window)[0]
+    o.backward(do.to(gpu))
+    ro, (rdq, rdk, rdv) = _oracle(q, k, v, None, cu, do=do, window=window)
+    assert_within("o", o, ro)
+    assert_within("dq", qg.grad, rdq)
+    assert_within("dk", kg.grad, rdk)
+    assert_within("dv", vg.grad, rdv)
+
+
+def test_noncontiguous_and_fp32_inputs(gpu):
+    n, hq, d = 256, 2, 64
+    g = gen(9)
+    base = randn((n, d, hq), g).float()
+    q = base.transpose(1, 2)  # non-contiguous view [n, hq, d]
+    k = randn((n, hq, d), g).float()
+    v = randn((n, hq, d), g).float()
+    sel = torch.rand(n, generator=g) < 0.5
+    cu = torch.tensor([0, n], dtype=torch.int32)
+    o = sq_full_attn(q[None].to(gpu), k[None].to(gpu), v[None].to(gpu), sel[None].to(gpu), cu_seqlens=cu.to(gpu))
+    assert o.dtype == torch.float32
+    ro, _ = _oracle(q.bfloat16(), k.bfloat16(), v.bfloat16(), sel, cu)
+    assert_within("o", o[0], ro)
+
+
+def test_deterministic(gpu):
+    n, hq, d = 2048, 4, 128
+    g = gen(10)
+    q, k, v = (randn((n, hq, d), g) for _ in range(3))
+    do = randn((n, hq, d), g)
+    sel = torch.rand(n, generator=g) < 0.3
+    cu = torch.tensor([0, 1000, 2048], dtype=torch.int32)
+    a = _run(q, k, v, sel, cu, gpu, do)
+    b = _run(q, k, v, sel, cu, gpu, do)
+    assert torch.equal(a[0], b[0])
+    for x, y in zip(a[1], b[1]):
+        assert torch.equal(x, y)
