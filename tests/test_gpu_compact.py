@@ -117,4 +117,7 @@ def test_compaction_is_deterministic(gpu):
     cu = torch.tensor([0, 20000, 50000], dtype=torch.int32)
     a = compact_selection(mask, cu)
     b = compact_selection(mask, cu)
-    assert torch.equal(a.q_idx, b.q_idx) and torch.equal(a.pos, b.pos) and torch.equal(a.meta, b.meta)
+    sq = a.sq()
+    assert sq == int(mask.sum().item())
+    assert torch.equal(a.meta, b.meta)
+    assert torch.equal(a.q_idx[:, :sq], b.q_idx[:, :sq]) and torch.equal(a.pos[:, :sq], b.pos[:, :sq])
