@@ -77,6 +77,17 @@ __device__ __forceinline__ RowView<SPARSE> row_view(const AttnArgs& a, int lane_
   return v;
 }
 
+// Waves per SIMD each kernel is compiled for (caps VGPRs at 512 / waves).
+#ifndef LOGO_OCC_FWD
+#define LOGO_OCC_FWD __attribute__((amdgpu_waves_per_eu(2, 2)))
+#endif
+#ifndef LOGO_OCC_DQ
+#define LOGO_OCC_DQ __attribute__((amdgpu_waves_per_eu(2, 2)))
+#endif
+#ifndef LOGO_OCC_DKV
+#define LOGO_OCC_DKV __attribute__((amdgpu_waves_per_eu(1, 1)))
+#endif
+
 extern __shared__ __attribute__((aligned(16))) char logo_smem[];
 __device__ __forceinline__ bf16* dyn_smem() { return reinterpret_cast<bf16*>(logo_smem); }
 
@@ -86,7 +97,7 @@ __device__ __forceinline__ float wave_pair_max(float x) { return fmaxf(x, __shfl
 // Forward
 // ---------------------------------------------------------------------------
 template <int D, bool SPARSE, bool WINDOW>
-__global__ __launch_bounds__(256) void sq_fwd_kernel(const AttnArgs a) {
+__global__ __launch_bounds__(256) LOGO_OCC_FWD void sq_fwd_kernel(const AttnArgs a) {
   using TL = Tile64<D>;
   constexpr int RS = TL::RS, TS = TL::TS, DS = D / 16, DT = D / 32;
   bf16* const smem = dyn_smem();
@@ -267,7 +278,7 @@ __global__ __launch_bounds__(256) void sq_delta_kernel(const AttnArgs a) {
 // Backward dq
 // ---------------------------------------------------------------------------
 template <int D, bool SPARSE, bool WINDOW>
-__global__ __launch_bounds__(256) void sq_dq_kernel(const AttnArgs a) {
+__global__ __launch_bounds__(256) LOGO_OCC_DQ void sq_dq_kernel(const AttnArgs a) {
   using TL = Tile64<D>;
   constexpr int RS = TL::RS, TS = TL::TS, DS = D / 16, DT = D / 32;
   bf16* sK = dyn_smem();
@@ -342,35 +353,34 @@ __global__ __launch_bounds__(256) void sq_dq_kernel(const AttnArgs a) {
     const bool skip = !wave_active || j0 > pmax || (WINDOW && j0 + 63 < pmin - W);
     if (!skip) {
       const bool need_mask = (j0 + 63 > pmin) || (WINDOW && j0 < pmax - W);
-      f32x16 sacc[2], pacc[2];
+      // Two 32-key halves in turn keep only one S / dP accumulator pair live.
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
-        sacc[kk] = f32x16{};
-        pacc[kk] = f32x16{};
+        f32x16 sacc{}, pacc{};
 #pragma unroll
         for (int ds = 0; ds < DS; ++ds) {
-          sacc[kk] = mfma32(read_row_op<RS>(sK, 32 * kk + i, ds, g), qreg[ds], sacc[kk]);
-          pacc[kk] = mfma32(read_row_op<RS>(sV, 32 * kk + i, ds, g), doreg[ds], pacc[kk]);
+          sacc = mfma32(read_row_op<RS>(sK, 32 * kk + i, ds, g), qreg[ds], sacc);
+          pacc = mfma32(read_row_op<RS>(sV, 32 * kk + i, ds, g), doreg[ds], pacc);
         }
-      }
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
         for (int jj = 0; jj < 16; ++jj) {
-          float pv = fast_exp2(fmaf(sacc[kk][jj], c, -lse_q));
+          float pv = fast_exp2(fmaf(sacc[jj], c, -lse_q));
           if (need_mask) {
             const int key = j0 + 32 * kk + rowmap(g, jj);
             bool vis = key <= p;
             if (WINDOW) vis = vis && key >= p - W;
             if (!vis) pv = 0.f;
           }
-          sacc[kk][jj] = pv * (pacc[kk][jj] - delta_q);
+          sacc[jj] = pv * (pacc[jj] - delta_q);
         }
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt)
+        for (int hh = 0; hh < 2; ++hh) {
+          const bf16x8 db = acc_to_bf16(sacc, hh);
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks)
-          dqacc[dt] = mfma32(read_perm_k<TS>(sKt, 32 * dt + i, ks, g), acc_to_bf16(sacc[ks >> 1], ks & 1), dqacc[dt]);
+          for (int dt = 0; dt < DT; ++dt)
+            dqacc[dt] = mfma32(read_perm_k<TS>(sKt, 32 * dt + i, 2 * kk + hh, g), db, dqacc[dt]);
+        }
+      }
     }
     __syncthreads();
     if (has_next) {
@@ -399,7 +409,7 @@ __global__ __launch_bounds__(256) void sq_dq_kernel(const AttnArgs a) {
 // Backward dk / dv
 // ---------------------------------------------------------------------------
 template <int D, bool SPARSE, bool WINDOW>
-__global__ __launch_bounds__(256) void sq_dkv_kernel(const AttnArgs a) {
+__global__ __launch_bounds__(256) LOGO_OCC_DKV void sq_dkv_kernel(const AttnArgs a) {
   using TL = Tile64<D>;
   constexpr int RS = TL::RS, TS = TL::TS, DS = D / 16, DT = D / 32;
   bf16* sQ = dyn_smem();
@@ -497,40 +507,38 @@ __global__ __launch_bounds__(256) void sq_dkv_kernel(const AttnArgs a) {
       const bool skip = !wave_active || p_last < kw0 || (WINDOW && p_first > kw_last + W);
       if (!skip) {
         const bool need_mask = WINDOW || (p_first < kw_last) || (rt + 64 > rq_end);
-        f32x16 sacc[2], pacc[2];
+        // Two 32-row halves of the query tile in turn keep one S / dP pair live.
 #pragma unroll
         for (int qq = 0; qq < 2; ++qq) {
-          sacc[qq] = f32x16{};
-          pacc[qq] = f32x16{};
+          f32x16 sacc{}, pacc{};
 #pragma unroll
           for (int ds = 0; ds < DS; ++ds) {
-            sacc[qq] = mfma32(read_row_op<RS>(sQ, 32 * qq + i, ds, g), kreg[ds], sacc[qq]);
-            pacc[qq] = mfma32(read_row_op<RS>(sO, 32 * qq + i, ds, g), vreg[ds], pacc[qq]);
+            sacc = mfma32(read_row_op<RS>(sQ, 32 * qq + i, ds, g), kreg[ds], sacc);
+            pacc = mfma32(read_row_op<RS>(sO, 32 * qq + i, ds, g), vreg[ds], pacc);
           }
-        }
-#pragma unroll
-        for (int qq = 0; qq < 2; ++qq)
 #pragma unroll
           for (int jj = 0; jj < 16; ++jj) {
             const int qr = 32 * qq + rowmap(g, jj);
-            float pv = fast_exp2(fmaf(sacc[qq][jj], c, -sLse[qr]));
+            float pv = fast_exp2(fmaf(sacc[jj], c, -sLse[qr]));
             if (need_mask) {
               const int pq = sPos[qr];
               bool vis = key <= pq;
               if (WINDOW) vis = vis && key >= pq - W;
               if (!vis) pv = 0.f;
             }
-            sacc[qq][jj] = pv;
-            pacc[qq][jj] = pv * (pacc[qq][jj] - sDelta[qr]);
+            sacc[jj] = pv;
+            pacc[jj] = pv * (pacc[jj] - sDelta[qr]);
           }
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-          const bf16x8 pb = acc_to_bf16(sacc[ks >> 1], ks & 1);
-          const bf16x8 db = acc_to_bf16(pacc[ks >> 1], ks & 1);
+          for (int hh = 0; hh < 2; ++hh) {
+            const int ks = 2 * qq + hh;
+            const bf16x8 pb = acc_to_bf16(sacc, hh);
+            const bf16x8 db = acc_to_bf16(pacc, hh);
 #pragma unroll
-          for (int dt = 0; dt < DT; ++dt) {
-            dvacc[dt] = mfma32(read_perm_k<TS>(sOt, 32 * dt + i, ks, g), pb, dvacc[dt]);
-            dkacc[dt] = mfma32(read_perm_k<TS>(sQt, 32 * dt + i, ks, g), db, dkacc[dt]);
+            for (int dt = 0; dt < DT; ++dt) {
+              dvacc[dt] = mfma32(read_perm_k<TS>(sOt, 32 * dt + i, ks, g), pb, dvacc[dt]);
+              dkacc[dt] = mfma32(read_perm_k<TS>(sQt, 32 * dt + i, ks, g), db, dkacc[dt]);
+            }
           }
         }
       }
