@@ -109,37 +109,40 @@ int logo_sq_fwd(const void* q, const void* k, const void* v, void* o, float* lse
 
 /*
  * Backward (logo/ops/selected_full_attn.py:124-138 delta, :141-228 dq,
- * :231-337 dk/dv, :444-445 GQA sum), with the dO gather (:483) and dq scatter
- * (:487-488) fused.  o and dout are [N, HQ, D]; writes dq rows of selected
- * tokens (caller zero-fills dq), every row of dk and dv [N, H, D], and delta
- * [HQ, N] (workspace the caller provides).
+ * :231-337 dk/dv, :444-445 GQA sum).  o and dout are [N, HQ, D]; writes dq
+ * rows of selected tokens (caller zero-fills dq; the scatter :487-488 is
+ * fused), every row of dk and dv [N, H, D], and the workspaces delta [HQ, N]
+ * fp32 and, in sparse mode, q_sel / do_sel [HQ, N, D] bf16: compacted copies
+ * of the selected q and dO rows (the reference's q_sel / do_sel, :461 :483),
+ * filled by the delta phase.  Dense mode ignores q_sel / do_sel.
  */
 int logo_sq_bwd(const void* q, const void* k, const void* v, const void* o,
-                const void* dout, const float* lse, float* delta, void* dq, void* dk,
-                void* dv, const int64_t* q_idx, const int32_t* pos, const int32_t* meta,
-                const int32_t* cu, int64_t n_tokens, int nseq, int hq, int h, int d,
-                int lanes, float scale, int window, int dtype, void* stream);
+    const void* dout, const float* lse, float* delta, void* q_sel, void* do_sel,
+    void* dq, void* dk, void* dv, const int64_t* q_idx, const int32_t* pos,
+    const int32_t* meta, const int32_t* cu, int64_t n_tokens, int nseq, int hq,
+    int h, int d, int lanes, float scale, int window, int dtype, void* stream);
 
 /*
  * The three backward phases of logo_sq_bwd as separate launches, same
- * arguments: delta only (:124-138, :365-371), dq only (:141-228, :424-432),
- * dk/dv only (:231-337, :433-445).  Callers time or overlap them one by one.
+ * arguments: delta and the q_sel / do_sel copies (:124-138, :365-371), dq
+ * (:141-228, :424-432), dk/dv (:231-337, :433-445).  Callers time or overlap
+ * them one by one; dq and dk/dv read what the delta phase wrote.
  */
 int logo_sq_bwd_delta(const void* q, const void* k, const void* v, const void* o,
-                      const void* dout, const float* lse, float* delta, void* dq, void* dk,
-                      void* dv, const int64_t* q_idx, const int32_t* pos, const int32_t* meta,
-                      const int32_t* cu, int64_t n_tokens, int nseq, int hq, int h, int d,
-                      int lanes, float scale, int window, int dtype, void* stream);
+    const void* dout, const float* lse, float* delta, void* q_sel, void* do_sel,
+    void* dq, void* dk, void* dv, const int64_t* q_idx, const int32_t* pos,
+    const int32_t* meta, const int32_t* cu, int64_t n_tokens, int nseq, int hq,
+    int h, int d, int lanes, float scale, int window, int dtype, void* stream);
 int logo_sq_bwd_dq(const void* q, const void* k, const void* v, const void* o,
-                   const void* dout, const float* lse, float* delta, void* dq, void* dk,
-                   void* dv, const int64_t* q_idx, const int32_t* pos, const int32_t* meta,
-                   const int32_t* cu, int64_t n_tokens, int nseq, int hq, int h, int d,
-                   int lanes, float scale, int window, int dtype, void* stream);
+    const void* dout, const float* lse, float* delta, void* q_sel, void* do_sel,
+    void* dq, void* dk, void* dv, const int64_t* q_idx, const int32_t* pos,
+    const int32_t* meta, const int32_t* cu, int64_t n_tokens, int nseq, int hq,
+    int h, int d, int lanes, float scale, int window, int dtype, void* stream);
 int logo_sq_bwd_dkv(const void* q, const void* k, const void* v, const void* o,
-                    const void* dout, const float* lse, float* delta, void* dq, void* dk,
-                    void* dv, const int64_t* q_idx, const int32_t* pos, const int32_t* meta,
-                    const int32_t* cu, int64_t n_tokens, int nseq, int hq, int h, int d,
-                    int lanes, float scale, int window, int dtype, void* stream);
+    const void* dout, const float* lse, float* delta, void* q_sel, void* do_sel,
+    void* dq, void* dk, void* dv, const int64_t* q_idx, const int32_t* pos,
+    const int32_t* meta, const int32_t* cu, int64_t n_tokens, int nseq, int hq,
+    int h, int d, int lanes, float scale, int window, int dtype, void* stream);
 
 #ifdef __cplusplus
 }

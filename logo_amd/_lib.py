@@ -32,7 +32,7 @@ SIGNATURES = {
     "logo_q_start_blk": ([_P, _P, _P, _P, _I64, _I, _P, _P], _I),
     "logo_sq_fwd": ([_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I, _I, _I, _I, _I, _F, _I, _I, _P], _I),
 }
-_BWD = ([_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I, _I, _I, _I, _I, _F, _I, _I, _P], _I)
+_BWD = ([_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I, _I, _I, _I, _I, _F, _I, _I, _P], _I)
 for _name in ("logo_sq_bwd", "logo_sq_bwd_delta", "logo_sq_bwd_dq", "logo_sq_bwd_dkv"):
     SIGNATURES[_name] = _BWD
 

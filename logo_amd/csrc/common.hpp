@@ -8,7 +8,7 @@
 // The hardware's k ordering inside Kset(g) only has to agree between A and B,
 // so operands built from an accumulator (P, dS) use the accumulator's own row
 // order as their k order and the matching operand is read from LDS in that
-// order (see read_perm_k).
+// order (see read_tr_op).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -26,7 +26,6 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 // Library-wide tile constants (must match include/logo_hip.h).
 constexpr int kBQ = 128;   // compacted query rows per workgroup (fwd, dq)
-constexpr int kBK = 64;    // keys per LDS tile (fwd, dq) / query rows per LDS tile (dkv)
 constexpr int kBKV = 128;  // keys per workgroup (dkv)
 constexpr int kMetaHdr = 8;
 
@@ -48,24 +47,14 @@ __device__ __forceinline__ bf16x8 acc_to_bf16(const f32x16& a, int h) {
   return r;
 }
 
-// Pack two bf16 from two dwords: lo halves (even element) or hi halves (odd).
-__device__ __forceinline__ uint32_t pack_lo(uint32_t a, uint32_t b) {
-  return __builtin_amdgcn_perm(b, a, 0x05040100u);
-}
-__device__ __forceinline__ uint32_t pack_hi(uint32_t a, uint32_t b) {
-  return __builtin_amdgcn_perm(b, a, 0x07060302u);
-}
-
-// A 64-row x D-column bf16 tile moved global -> registers -> LDS by 256
-// threads.  Thread tid owns the 16-byte column chunk c = tid % CH of rows
-// rg*RPT .. rg*RPT+RPT-1 (rg = tid / CH), so every group of CH lanes reads
-// one contiguous row.
-template <int D>
+// A 64-row x D-column bf16 tile moved global -> registers -> LDS (row-major,
+// row stride RS elements) by 256 threads.  Thread tid owns the 16-byte column
+// chunk c = tid % CH of rows rg*RPT .. rg*RPT+RPT-1 (rg = tid / CH), so every
+// group of CH lanes reads one contiguous row.
+template <int D, int RS>
 struct Tile64 {
   static constexpr int CH = D / 8;
   static constexpr int RPT = (64 * CH) / 256;  // rows per thread: D/32
-  static constexpr int RS = D + 8;             // row-major LDS stride (elements)
-  static constexpr int TS = 64 + 4;            // transposed LDS stride (elements)
   static_assert(RPT == 2 || RPT == 4, "head dim must be 64 or 128");
   u32x4 r[RPT];
 
@@ -83,31 +72,20 @@ struct Tile64 {
     }
   }
 
-  // Row-major store: lds[row * RS + col].
-  __device__ __forceinline__ void store_rows(bf16* lds, int tid) const {
+  __device__ __forceinline__ void store(bf16* lds, int tid) const {
     const int c = chunk(tid), r0 = row0(tid);
 #pragma unroll
     for (int i = 0; i < RPT; ++i) *reinterpret_cast<u32x4*>(lds + (r0 + i) * RS + 8 * c) = r[i];
   }
-
-  // Transposed store: lds[col * TS + row].
-  __device__ __forceinline__ void store_cols(bf16* lds, int tid) const {
-    const int c = chunk(tid), r0 = row0(tid);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int w = e >> 1;
-      bf16* dst = lds + (8 * c + e) * TS + r0;
-      if constexpr (RPT == 4) {
-        u32x2 v;
-        v[0] = (e & 1) ? pack_hi(r[0][w], r[1][w]) : pack_lo(r[0][w], r[1][w]);
-        v[1] = (e & 1) ? pack_hi(r[2][w], r[3][w]) : pack_lo(r[2][w], r[3][w]);
-        *reinterpret_cast<u32x2*>(dst) = v;
-      } else {
-        *reinterpret_cast<uint32_t*>(dst) = (e & 1) ? pack_hi(r[0][w], r[1][w]) : pack_lo(r[0][w], r[1][w]);
-      }
-    }
-  }
 };
+
+// LDS row strides (elements).  Tiles read only with ds_read_b128 along rows
+// use D + 8 (row starts 4 banks apart: conflict-free for 16 lanes reading 16
+// rows); tiles also read with the transposing ds_read_b64_tr_b16 use D + 16
+// (row starts 8 banks apart: the 4 rows x 4 chunks of a 16-lane group hit 32
+// distinct banks).
+template <int D> constexpr int kRowStride = D + 8;
+template <int D> constexpr int kTrStride = D + 16;
 
 // Row-major operand: 8 consecutive columns 16*ks + 8*g of row `row`.
 template <int RS>
@@ -115,15 +93,22 @@ __device__ __forceinline__ bf16x8 read_row_op(const bf16* lds, int row, int ks, 
   return *reinterpret_cast<const bf16x8*>(lds + row * RS + 16 * ks + 8 * g);
 }
 
-// Transposed operand whose k order matches acc_to_bf16(acc, ks & 1) of the
-// 32-row accumulator tile ks >> 1: columns 16*ks + {4g..4g+3, 8+4g..8+4g+3}.
-template <int TS>
-__device__ __forceinline__ bf16x8 read_perm_k(const bf16* lds, int row, int ks, int g) {
-  const bf16* p = lds + row * TS + 16 * ks + 4 * g;
-  u32x2 lo = *reinterpret_cast<const u32x2*>(p);
-  u32x2 hi = *reinterpret_cast<const u32x2*>(p + 8);
-  u32x4 v{lo[0], lo[1], hi[0], hi[1]};
-  return as_bf16x8(v);
+typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
+
+// Transposed operand from a row-major tile T (row stride RS): lane (i, g)
+// receives T[r0 + 4g + e][c0 + i] for e = 0..3 followed by
+// T[r0 + 8 + 4g + e][c0 + i], the k order acc_to_bf16(acc, ks & 1) produces
+// for r0 = 16*ks.  ds_read_b64_tr_b16 gives lane 16G + 4a + b element b of the
+// 8-byte chunks addressed by lanes 16G + a + 4e (e = 0..3), so lane 16G + j
+// addresses row r0 + 4g + j/4, column c0 + 16(G & 1) + 4(j & 3).
+template <int RS>
+__device__ __forceinline__ bf16x8 read_tr_op(const bf16* lds, int r0, int c0) {
+  const int l = threadIdx.x & 63;
+  const int G = l >> 4, j = l & 15;
+  const bf16* p = lds + (r0 + 4 * (G >> 1) + (j >> 2)) * RS + c0 + 16 * (G & 1) + 4 * (j & 3);
+  const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(p));
+  const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(p + 8 * RS));
+  return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
 // Largest s in [0, n) with arr[s] <= x (arr ascending, arr[0] <= x).

@@ -6,8 +6,11 @@
 // log2-domain LSE (:141-228 dq, :231-337 dk/dv) with delta = rowsum(o * dO)
 // (:124-138); dk/dv of a GQA group are summed over its query heads (:444-445).
 // Differences in structure, not in results:
-//   * q / dO rows are gathered and o / dq rows scattered inside the kernels
-//     (the reference materialises q_sel / do_sel / o_sel, :461 :469 :483 :487);
+//   * the forward gathers q rows and scatters o rows inside the kernel (the
+//     reference materialises q_sel / o_sel, :461 :469); the backward's delta
+//     pass writes compacted, head-major copies of q and dO ([HQ, N, D]) so the
+//     dq and dk/dv loops read contiguous rows (the reference's q_sel / do_sel,
+//     :461 :483), and the dq kernel scatters dq rows itself (:487);
 //   * the tile -> (sequence, block) map comes from device-side prefixes built
 //     by the compaction kernels (no host list, :348 :413-414);
 //   * the dk/dv kernel starts each key block at its exact first visible query
@@ -18,11 +21,15 @@
 //
 // Tiling (32x32x16 bf16 MFMA, wave64, 4 waves per workgroup):
 //   fwd / dq : 128 compacted rows per workgroup (32 per wave, Q and dO held in
-//              registers as B operands), K/V streamed in 64-key LDS tiles.
-//              S^T = K Q^T puts one query per lane pair, so the softmax row
-//              statistics need a single cross-lane exchange (lane ^ 32).
+//              registers as B operands), K/V streamed in double-buffered
+//              64-key row-major LDS tiles.  S^T = K Q^T puts one query per lane
+//              pair, so the softmax row statistics need a single cross-lane
+//              exchange (lane ^ 32).  The transposed operands V^T (fwd) and
+//              K^T (dq) come from the same row-major tiles through
+//              ds_read_b64_tr_b16.
 //   dk/dv    : 128 keys per workgroup (32 per wave, K and V in registers),
-//              compacted query rows streamed in 64-row LDS tiles, GQA heads
+//              compacted query rows streamed in double-buffered 64-row LDS
+//              tiles (Q^T and dO^T again by transposing reads), GQA heads
 //              looped inside the workgroup.
 #include <math.h>
 
@@ -42,6 +49,8 @@ struct AttnArgs {
   bf16* dq;
   bf16* dk;
   bf16* dv;
+  bf16* q_sel;   // [HQ, N, D] compacted q rows (sparse backward)
+  bf16* do_sel;  // [HQ, N, D] compacted dO rows (sparse backward)
   const int64_t* q_idx;
   const int32_t* pos;
   const int32_t* meta;
@@ -77,6 +86,20 @@ __device__ __forceinline__ RowView<SPARSE> row_view(const AttnArgs& a, int lane_
   return v;
 }
 
+// Query-side rows (q or dO) of head hq as the backward reads them: compacted
+// head-major copies [HQ, N, D] in sparse mode, the [N, HQ, D] inputs in dense
+// mode (where the compacted row index is the token).
+template <int D, bool SPARSE>
+struct QSide {
+  const bf16* base;
+  int64_t stride;
+  __device__ __forceinline__ QSide(const AttnArgs& a, const bf16* sel_buf, const bf16* full, int hq) {
+    base = SPARSE ? sel_buf + (int64_t)hq * a.n * D : full + (int64_t)hq * D;
+    stride = SPARSE ? (int64_t)D : (int64_t)a.hq * D;
+  }
+  __device__ __forceinline__ const bf16* row(int r) const { return base + (int64_t)r * stride; }
+};
+
 // Waves per SIMD each kernel is compiled for (caps VGPRs at 512 / waves).
 #ifndef LOGO_OCC_FWD
 #define LOGO_OCC_FWD __attribute__((amdgpu_waves_per_eu(2, 2)))
@@ -93,54 +116,72 @@ __device__ __forceinline__ bf16* dyn_smem() { return reinterpret_cast<bf16*>(log
 
 __device__ __forceinline__ float wave_pair_max(float x) { return fmaxf(x, __shfl_xor(x, 32)); }
 
+// Shared front matter of the fwd and dq kernels: which compacted rows this
+// workgroup and this lane own.  Returns false for a workgroup past the last
+// tile (the grid is sized for the worst case).
+template <bool SPARSE>
+struct QTile {
+  int hq, h, lane_sel, s, r0, r_end, bos, seqlen;
+  int pmin, pmax, r, p, kv_lo, kv_hi;
+  bool wave_active, valid;
+  int64_t t;
+  RowView<SPARSE> rv;
+
+  __device__ __forceinline__ bool init(const AttnArgs& a, int wave, int i, bool window) {
+    int rank;
+    xcd_remap(blockIdx.x, a.hq, rank, hq);
+    lane_sel = a.lanes > 1 ? hq : 0;
+    const int32_t* meta = a.meta + (int64_t)lane_sel * a.meta_stride;
+    const int nt = meta[1];
+    if (rank >= nt) return false;
+    const int tile = nt - 1 - rank;  // heaviest (latest) blocks first
+    const int32_t* cu_q = meta + kMetaHdr;
+    const int32_t* cu_tq = cu_q + (a.nseq + 1);
+    s = seg_of(cu_tq, a.nseq, tile);
+    r0 = cu_q[s] + (tile - cu_tq[s]) * kBQ;
+    r_end = min(r0 + kBQ, cu_q[s + 1]);
+    bos = a.cu[s];
+    seqlen = a.cu[s + 1] - bos;
+    h = hq / a.g;
+    rv = row_view<SPARSE>(a, lane_sel, bos);
+    const int rw0 = r0 + 32 * wave;
+    wave_active = rw0 < r_end;
+    pmin = wave_active ? rv.posn(rw0) : 0;
+    pmax = wave_active ? rv.posn(min(rw0 + 31, r_end - 1)) : -1;
+    r = rw0 + i;
+    valid = r < r_end;
+    t = valid ? rv.token(r) : 0;
+    p = valid ? rv.posn(r) : -1;
+    kv_lo = window ? (max(0, rv.posn(r0) - a.window) & ~63) : 0;
+    kv_hi = rv.posn(r_end - 1) + 1;
+    return true;
+  }
+};
+
 // ---------------------------------------------------------------------------
 // Forward
 // ---------------------------------------------------------------------------
 template <int D, bool SPARSE, bool WINDOW>
 __global__ __launch_bounds__(256) LOGO_OCC_FWD void sq_fwd_kernel(const AttnArgs a) {
-  using TL = Tile64<D>;
-  constexpr int RS = TL::RS, TS = TL::TS, DS = D / 16, DT = D / 32;
+  constexpr int RSK = kRowStride<D>, RSV = kTrStride<D>, DS = D / 16, DT = D / 32;
+  using TK = Tile64<D, RSK>;
+  using TV = Tile64<D, RSV>;
   bf16* const smem = dyn_smem();
-  // [K tile 0][K tile 1][V^T tile 0][V^T tile 1]
-  auto sK = [&](int b) { return smem + b * (64 * RS); };
-  auto sVt = [&](int b) { return smem + 128 * RS + b * (D * TS); };
-
-  int rank, hq;
-  xcd_remap(blockIdx.x, a.hq, rank, hq);
-  const int lane_sel = a.lanes > 1 ? hq : 0;
-  const int32_t* meta = a.meta + (int64_t)lane_sel * a.meta_stride;
-  const int nt = meta[1];
-  if (rank >= nt) return;
-  const int tile = nt - 1 - rank;  // heaviest (latest) blocks first
-  const int32_t* cu_q = meta + kMetaHdr;
-  const int32_t* cu_tq = cu_q + (a.nseq + 1);
-  const int s = seg_of(cu_tq, a.nseq, tile);
-  const int r0 = cu_q[s] + (tile - cu_tq[s]) * kBQ;
-  const int r_end = min(r0 + kBQ, cu_q[s + 1]);
-  const int bos = a.cu[s];
-  const int seqlen = a.cu[s + 1] - bos;
-  const int h = hq / a.g;
-  const RowView<SPARSE> rv = row_view<SPARSE>(a, lane_sel, bos);
+  // [K tile 0][K tile 1][V tile 0][V tile 1], all row-major
+  auto sK = [&](int b) { return smem + b * (64 * RSK); };
+  auto sV = [&](int b) { return smem + 2 * 64 * RSK + b * (64 * RSV); };
 
   const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63, i = l & 31, g = l >> 5;
-  const int rw0 = r0 + 32 * wave;
-  const bool wave_active = rw0 < r_end;
-  const int pmin = wave_active ? rv.posn(rw0) : 0;
-  const int pmax = wave_active ? rv.posn(min(rw0 + 31, r_end - 1)) : -1;
-  const int r = rw0 + i;
-  const bool valid = r < r_end;
-  const int64_t t = valid ? rv.token(r) : 0;
-  const int p = valid ? rv.posn(r) : -1;
-  const int W = a.window;
-  const int kv_lo = WINDOW ? (max(0, rv.posn(r0) - W) & ~63) : 0;
-  const int kv_hi = rv.posn(r_end - 1) + 1;
+  QTile<SPARSE> qt;
+  if (!qt.init(a, wave, i, WINDOW)) return;
+  const int hq = qt.hq, p = qt.p, W = a.window;
 
   bf16x8 qreg[DS];
   {
-    const bf16* qrow = a.q + (t * a.hq + hq) * D + 8 * g;
+    const bf16* qrow = a.q + (qt.t * a.hq + hq) * D + 8 * g;
 #pragma unroll
     for (int ds = 0; ds < DS; ++ds)
-      qreg[ds] = valid ? *reinterpret_cast<const bf16x8*>(qrow + 16 * ds) : bf16x8{};
+      qreg[ds] = qt.valid ? *reinterpret_cast<const bf16x8*>(qrow + 16 * ds) : bf16x8{};
   }
 
   f32x16 oacc[DT];
@@ -150,34 +191,36 @@ __global__ __launch_bounds__(256) LOGO_OCC_FWD void sq_fwd_kernel(const AttnArgs
   const float c = a.scale_log2;
 
   const int64_t rstride = (int64_t)a.h * D;
-  const bf16* kbase = a.k + ((int64_t)bos * a.h + h) * D;
-  const bf16* vbase = a.v + ((int64_t)bos * a.h + h) * D;
-  TL kt, vt;
+  const bf16* kbase = a.k + ((int64_t)qt.bos * a.h + qt.h) * D;
+  const bf16* vbase = a.v + ((int64_t)qt.bos * a.h + qt.h) * D;
+  const int seqlen = qt.seqlen;
+  TK kt;
+  TV vt;
   auto load_tile = [&](int j0) {
     kt.load(tid, [&](int rr) -> const bf16* { return j0 + rr < seqlen ? kbase + (j0 + rr) * rstride : nullptr; });
     vt.load(tid, [&](int rr) -> const bf16* { return j0 + rr < seqlen ? vbase + (j0 + rr) * rstride : nullptr; });
   };
 
-  load_tile(kv_lo);
-  kt.store_rows(sK(0), tid);
-  vt.store_cols(sVt(0), tid);
+  load_tile(qt.kv_lo);
+  kt.store(sK(0), tid);
+  vt.store(sV(0), tid);
   __syncthreads();
   int buf = 0;
-  for (int j0 = kv_lo; j0 < kv_hi; j0 += 64) {
-    const bool has_next = j0 + 64 < kv_hi;
+  for (int j0 = qt.kv_lo; j0 < qt.kv_hi; j0 += 64) {
+    const bool has_next = j0 + 64 < qt.kv_hi;
     if (has_next) load_tile(j0 + 64);
 
-    const bool skip = !wave_active || j0 > pmax || (WINDOW && j0 + 63 < pmin - W);
+    const bool skip = !qt.wave_active || j0 > qt.pmax || (WINDOW && j0 + 63 < qt.pmin - W);
     if (!skip) {
-      const bool need_mask = (j0 + 63 > pmin) || (WINDOW && j0 < pmax - W);
+      const bool need_mask = (j0 + 63 > qt.pmin) || (WINDOW && j0 < qt.pmax - W);
       const bf16* kb = sK(buf);
-      const bf16* vb = sVt(buf);
+      const bf16* vb = sV(buf);
       f32x16 sacc[2];
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
         sacc[kk] = f32x16{};
 #pragma unroll
-        for (int ds = 0; ds < DS; ++ds) sacc[kk] = mfma32(read_row_op<RS>(kb, 32 * kk + i, ds, g), qreg[ds], sacc[kk]);
+        for (int ds = 0; ds < DS; ++ds) sacc[kk] = mfma32(read_row_op<RSK>(kb, 32 * kk + i, ds, g), qreg[ds], sacc[kk]);
       }
       if (need_mask) {
 #pragma unroll
@@ -220,20 +263,20 @@ __global__ __launch_bounds__(256) LOGO_OCC_FWD void sq_fwd_kernel(const AttnArgs
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) oacc[dt] = mfma32(read_perm_k<TS>(vb, 32 * dt + i, ks, g), pb[ks], oacc[dt]);
+        for (int ks = 0; ks < 4; ++ks) oacc[dt] = mfma32(read_tr_op<RSV>(vb, 16 * ks, 32 * dt), pb[ks], oacc[dt]);
     }
     if (has_next) {
-      kt.store_rows(sK(buf ^ 1), tid);
-      vt.store_cols(sVt(buf ^ 1), tid);
+      kt.store(sK(buf ^ 1), tid);
+      vt.store(sV(buf ^ 1), tid);
     }
     __syncthreads();
     buf ^= 1;
   }
 
   const float l_tot = l_run + __shfl_xor(l_run, 32);
-  if (valid) {
+  if (qt.valid) {
     const float inv = 1.f / l_tot;
-    bf16* orow = a.o + (t * a.hq + hq) * D;
+    bf16* orow = a.o + (qt.t * a.hq + hq) * D;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
@@ -243,12 +286,13 @@ __global__ __launch_bounds__(256) LOGO_OCC_FWD void sq_fwd_kernel(const AttnArgs
         for (int e = 0; e < 4; ++e) v[e] = (bf16)(oacc[dt][4 * q4 + e] * inv);
         *reinterpret_cast<bf16x4*>(orow + 32 * dt + 8 * q4 + 4 * g) = v;
       }
-    if (g == 0) a.lse[(int64_t)hq * a.n + r] = m_run * c + log2f(l_tot);
+    if (g == 0) a.lse[(int64_t)hq * a.n + qt.r] = m_run * c + log2f(l_tot);
   }
 }
 
 // ---------------------------------------------------------------------------
-// Backward preprocess: delta = rowsum(o * dO) per compacted row (fp32).
+// Backward preprocess: delta = rowsum(o * dO) per compacted row (fp32); in
+// sparse mode also the compacted copies q_sel / do_sel.
 // ---------------------------------------------------------------------------
 template <int D, bool SPARSE>
 __global__ __launch_bounds__(256) void sq_delta_kernel(const AttnArgs a) {
@@ -268,6 +312,11 @@ __global__ __launch_bounds__(256) void sq_delta_kernel(const AttnArgs a) {
     const bf16x8 dv = *reinterpret_cast<const bf16x8*>(a.dout + off);
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc = fmaf((float)ov[e], (float)dv[e], acc);
+    if (SPARSE) {
+      const int64_t soff = ((int64_t)hq * a.n + r) * D + 8 * c;
+      *reinterpret_cast<bf16x8*>(a.do_sel + soff) = dv;
+      *reinterpret_cast<bf16x8*>(a.q_sel + soff) = *reinterpret_cast<const bf16x8*>(a.q + off);
+    }
   }
 #pragma unroll
   for (int off = LPR / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
@@ -279,53 +328,31 @@ __global__ __launch_bounds__(256) void sq_delta_kernel(const AttnArgs a) {
 // ---------------------------------------------------------------------------
 template <int D, bool SPARSE, bool WINDOW>
 __global__ __launch_bounds__(256) LOGO_OCC_DQ void sq_dq_kernel(const AttnArgs a) {
-  using TL = Tile64<D>;
-  constexpr int RS = TL::RS, TS = TL::TS, DS = D / 16, DT = D / 32;
-  bf16* sK = dyn_smem();
-  bf16* sV = sK + 64 * RS;
-  bf16* sKt = sV + 64 * RS;
-
-  int rank, hq;
-  xcd_remap(blockIdx.x, a.hq, rank, hq);
-  const int lane_sel = a.lanes > 1 ? hq : 0;
-  const int32_t* meta = a.meta + (int64_t)lane_sel * a.meta_stride;
-  const int nt = meta[1];
-  if (rank >= nt) return;
-  const int tile = nt - 1 - rank;
-  const int32_t* cu_q = meta + kMetaHdr;
-  const int32_t* cu_tq = cu_q + (a.nseq + 1);
-  const int s = seg_of(cu_tq, a.nseq, tile);
-  const int r0 = cu_q[s] + (tile - cu_tq[s]) * kBQ;
-  const int r_end = min(r0 + kBQ, cu_q[s + 1]);
-  const int bos = a.cu[s];
-  const int seqlen = a.cu[s + 1] - bos;
-  const int h = hq / a.g;
-  const RowView<SPARSE> rv = row_view<SPARSE>(a, lane_sel, bos);
+  constexpr int RSK = kTrStride<D>, RSV = kRowStride<D>, DS = D / 16, DT = D / 32;
+  using TK = Tile64<D, RSK>;
+  using TV = Tile64<D, RSV>;
+  bf16* const smem = dyn_smem();
+  auto sK = [&](int b) { return smem + b * (64 * RSK); };
+  auto sV = [&](int b) { return smem + 2 * 64 * RSK + b * (64 * RSV); };
 
   const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63, i = l & 31, g = l >> 5;
-  const int rw0 = r0 + 32 * wave;
-  const bool wave_active = rw0 < r_end;
-  const int pmin = wave_active ? rv.posn(rw0) : 0;
-  const int pmax = wave_active ? rv.posn(min(rw0 + 31, r_end - 1)) : -1;
-  const int r = rw0 + i;
-  const bool valid = r < r_end;
-  const int64_t t = valid ? rv.token(r) : 0;
-  const int p = valid ? rv.posn(r) : -1;
-  const int W = a.window;
-  const int kv_lo = WINDOW ? (max(0, rv.posn(r0) - W) & ~63) : 0;
-  const int kv_hi = rv.posn(r_end - 1) + 1;
+  QTile<SPARSE> qt;
+  if (!qt.init(a, wave, i, WINDOW)) return;
+  const int hq = qt.hq, p = qt.p, W = a.window;
 
   bf16x8 qreg[DS], doreg[DS];
   {
-    const int64_t off = (t * a.hq + hq) * D + 8 * g;
+    const QSide<D, SPARSE> qs(a, a.q_sel, a.q, hq), os(a, a.do_sel, a.dout, hq);
+    const bf16* qrow = qs.row(qt.r) + 8 * g;
+    const bf16* orow = os.row(qt.r) + 8 * g;
 #pragma unroll
     for (int ds = 0; ds < DS; ++ds) {
-      qreg[ds] = valid ? *reinterpret_cast<const bf16x8*>(a.q + off + 16 * ds) : bf16x8{};
-      doreg[ds] = valid ? *reinterpret_cast<const bf16x8*>(a.dout + off + 16 * ds) : bf16x8{};
+      qreg[ds] = qt.valid ? *reinterpret_cast<const bf16x8*>(qrow + 16 * ds) : bf16x8{};
+      doreg[ds] = qt.valid ? *reinterpret_cast<const bf16x8*>(orow + 16 * ds) : bf16x8{};
     }
   }
-  const float lse_q = valid ? a.lse[(int64_t)hq * a.n + r] : 0.f;
-  const float delta_q = valid ? a.delta[(int64_t)hq * a.n + r] : 0.f;
+  const float lse_q = qt.valid ? a.lse[(int64_t)hq * a.n + qt.r] : 0.f;
+  const float delta_q = qt.valid ? a.delta[(int64_t)hq * a.n + qt.r] : 0.f;
   const float c = a.scale_log2;
 
   f32x16 dqacc[DT];
@@ -333,34 +360,38 @@ __global__ __launch_bounds__(256) LOGO_OCC_DQ void sq_dq_kernel(const AttnArgs a
   for (int dt = 0; dt < DT; ++dt) dqacc[dt] = f32x16{};
 
   const int64_t rstride = (int64_t)a.h * D;
-  const bf16* kbase = a.k + ((int64_t)bos * a.h + h) * D;
-  const bf16* vbase = a.v + ((int64_t)bos * a.h + h) * D;
-  TL kt, vt;
+  const bf16* kbase = a.k + ((int64_t)qt.bos * a.h + qt.h) * D;
+  const bf16* vbase = a.v + ((int64_t)qt.bos * a.h + qt.h) * D;
+  const int seqlen = qt.seqlen;
+  TK kt;
+  TV vt;
   auto load_tile = [&](int j0) {
     kt.load(tid, [&](int rr) -> const bf16* { return j0 + rr < seqlen ? kbase + (j0 + rr) * rstride : nullptr; });
     vt.load(tid, [&](int rr) -> const bf16* { return j0 + rr < seqlen ? vbase + (j0 + rr) * rstride : nullptr; });
   };
 
-  load_tile(kv_lo);
-  kt.store_rows(sK, tid);
-  kt.store_cols(sKt, tid);
-  vt.store_rows(sV, tid);
+  load_tile(qt.kv_lo);
+  kt.store(sK(0), tid);
+  vt.store(sV(0), tid);
   __syncthreads();
-  for (int j0 = kv_lo; j0 < kv_hi; j0 += 64) {
-    const bool has_next = j0 + 64 < kv_hi;
+  int buf = 0;
+  for (int j0 = qt.kv_lo; j0 < qt.kv_hi; j0 += 64) {
+    const bool has_next = j0 + 64 < qt.kv_hi;
     if (has_next) load_tile(j0 + 64);
 
-    const bool skip = !wave_active || j0 > pmax || (WINDOW && j0 + 63 < pmin - W);
+    const bool skip = !qt.wave_active || j0 > qt.pmax || (WINDOW && j0 + 63 < qt.pmin - W);
     if (!skip) {
-      const bool need_mask = (j0 + 63 > pmin) || (WINDOW && j0 < pmax - W);
+      const bool need_mask = (j0 + 63 > qt.pmin) || (WINDOW && j0 < qt.pmax - W);
+      const bf16* kb = sK(buf);
+      const bf16* vb = sV(buf);
       // Two 32-key halves in turn keep only one S / dP accumulator pair live.
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
         f32x16 sacc{}, pacc{};
 #pragma unroll
         for (int ds = 0; ds < DS; ++ds) {
-          sacc = mfma32(read_row_op<RS>(sK, 32 * kk + i, ds, g), qreg[ds], sacc);
-          pacc = mfma32(read_row_op<RS>(sV, 32 * kk + i, ds, g), doreg[ds], pacc);
+          sacc = mfma32(read_row_op<RSK>(kb, 32 * kk + i, ds, g), qreg[ds], sacc);
+          pacc = mfma32(read_row_op<RSV>(vb, 32 * kk + i, ds, g), doreg[ds], pacc);
         }
 #pragma unroll
         for (int jj = 0; jj < 16; ++jj) {
@@ -378,21 +409,20 @@ __global__ __launch_bounds__(256) LOGO_OCC_DQ void sq_dq_kernel(const AttnArgs a
           const bf16x8 db = acc_to_bf16(sacc, hh);
 #pragma unroll
           for (int dt = 0; dt < DT; ++dt)
-            dqacc[dt] = mfma32(read_perm_k<TS>(sKt, 32 * dt + i, 2 * kk + hh, g), db, dqacc[dt]);
+            dqacc[dt] = mfma32(read_tr_op<RSK>(kb, 16 * (2 * kk + hh), 32 * dt), db, dqacc[dt]);
         }
       }
     }
-    __syncthreads();
     if (has_next) {
-      kt.store_rows(sK, tid);
-      kt.store_cols(sKt, tid);
-      vt.store_rows(sV, tid);
+      kt.store(sK(buf ^ 1), tid);
+      vt.store(sV(buf ^ 1), tid);
     }
     __syncthreads();
+    buf ^= 1;
   }
 
-  if (valid) {
-    bf16* dqrow = a.dq + (t * a.hq + hq) * D;
+  if (qt.valid) {
+    bf16* dqrow = a.dq + (qt.t * a.hq + hq) * D;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
@@ -408,17 +438,20 @@ __global__ __launch_bounds__(256) LOGO_OCC_DQ void sq_dq_kernel(const AttnArgs a
 // ---------------------------------------------------------------------------
 // Backward dk / dv
 // ---------------------------------------------------------------------------
+template <int D>
+constexpr int dkv_stage_bytes() { return 2 * 64 * kTrStride<D> * 2 + 3 * 64 * 4; }
+
 template <int D, bool SPARSE, bool WINDOW>
 __global__ __launch_bounds__(256) LOGO_OCC_DKV void sq_dkv_kernel(const AttnArgs a) {
-  using TL = Tile64<D>;
-  constexpr int RS = TL::RS, TS = TL::TS, DS = D / 16, DT = D / 32;
-  bf16* sQ = dyn_smem();
-  bf16* sO = sQ + 64 * RS;
-  bf16* sQt = sO + 64 * RS;
-  bf16* sOt = sQt + D * TS;
-  float* sLse = reinterpret_cast<float*>(sOt + D * TS);
-  float* sDelta = sLse + 64;
-  int* sPos = reinterpret_cast<int*>(sDelta + 64);
+  constexpr int RS = kTrStride<D>, DS = D / 16, DT = D / 32;
+  using TQ = Tile64<D, RS>;
+  char* const smem_b = logo_smem;
+  // stage b: [Q tile][dO tile][lse 64][delta 64][pos 64]
+  auto sQ = [&](int b) { return reinterpret_cast<bf16*>(smem_b + b * dkv_stage_bytes<D>()); };
+  auto sO = [&](int b) { return sQ(b) + 64 * RS; };
+  auto sLse = [&](int b) { return reinterpret_cast<float*>(sQ(b) + 2 * 64 * RS); };
+  auto sDelta = [&](int b) { return sLse(b) + 64; };
+  auto sPos = [&](int b) { return reinterpret_cast<int*>(sLse(b) + 128); };
 
   int rank, h;
   xcd_remap(blockIdx.x, a.h, rank, h);
@@ -458,12 +491,15 @@ __global__ __launch_bounds__(256) LOGO_OCC_DKV void sq_dkv_kernel(const AttnArgs
     dvacc[dt] = f32x16{};
   }
 
-  TL qt, ot;
+  TQ qtile, otile;
+  float lse_n = 0.f, delta_n = 0.f;
+  int pos_n = -1;
   for (int gg = 0; gg < a.g; ++gg) {
     const int hq = h * a.g + gg;
     const int lane_sel = a.lanes > 1 ? hq : 0;
     const int32_t* cu_q = a.meta + (int64_t)lane_sel * a.meta_stride + kMetaHdr;
     const RowView<SPARSE> rv = row_view<SPARSE>(a, lane_sel, bos);
+    const QSide<D, SPARSE> qs(a, a.q_sel, a.q, hq), os(a, a.do_sel, a.dout, hq);
     const int q_lo = cu_q[s], q_hi = cu_q[s + 1];
     int rq0, rq_end;
     if (SPARSE) {
@@ -473,37 +509,47 @@ __global__ __launch_bounds__(256) LOGO_OCC_DKV void sq_dkv_kernel(const AttnArgs
       rq0 = min(q_lo + k0, q_hi);
       rq_end = WINDOW ? min(q_hi, q_lo + k_last + W + 1) : q_hi;
     }
-    const int64_t qoff = (int64_t)hq * D;
-    const int64_t qstride = (int64_t)a.hq * D;
+    const float* lse_h = a.lse + (int64_t)hq * a.n;
+    const float* delta_h = a.delta + (int64_t)hq * a.n;
     auto load_tile = [&](int rt) {
-      qt.load(tid, [&](int rr) -> const bf16* {
-        return rt + rr < rq_end ? a.q + rv.token(rt + rr) * qstride + qoff : nullptr;
-      });
-      ot.load(tid, [&](int rr) -> const bf16* {
-        return rt + rr < rq_end ? a.dout + rv.token(rt + rr) * qstride + qoff : nullptr;
-      });
-    };
-    if (rq0 < rq_end) load_tile(rq0);
-    for (int rt = rq0; rt < rq_end; rt += 64) {
-      const bool has_next = rt + 64 < rq_end;
-      __syncthreads();  // previous tile fully consumed
-      qt.store_rows(sQ, tid);
-      qt.store_cols(sQt, tid);
-      ot.store_rows(sO, tid);
-      ot.store_cols(sOt, tid);
+      qtile.load(tid, [&](int rr) -> const bf16* { return rt + rr < rq_end ? qs.row(rt + rr) : nullptr; });
+      otile.load(tid, [&](int rr) -> const bf16* { return rt + rr < rq_end ? os.row(rt + rr) : nullptr; });
       if (tid < 64) {
         const int rr = rt + tid;
         const bool ok = rr < rq_end;
-        sLse[tid] = ok ? a.lse[(int64_t)hq * a.n + rr] : 0.f;
-        sDelta[tid] = ok ? a.delta[(int64_t)hq * a.n + rr] : 0.f;
-        sPos[tid] = ok ? rv.posn(rr) : -1;
+        lse_n = ok ? lse_h[rr] : 0.f;
+        delta_n = ok ? delta_h[rr] : 0.f;
+        pos_n = ok ? rv.posn(rr) : -1;
       }
-      __syncthreads();
+    };
+    auto store_tile = [&](int b) {
+      qtile.store(sQ(b), tid);
+      otile.store(sO(b), tid);
+      if (tid < 64) {
+        sLse(b)[tid] = lse_n;
+        sDelta(b)[tid] = delta_n;
+        sPos(b)[tid] = pos_n;
+      }
+    };
+
+    if (rq0 < rq_end) {
+      load_tile(rq0);
+      store_tile(0);
+    }
+    __syncthreads();
+    int buf = 0;
+    for (int rt = rq0; rt < rq_end; rt += 64) {
+      const bool has_next = rt + 64 < rq_end;
       if (has_next) load_tile(rt + 64);
 
+      const bf16* qb = sQ(buf);
+      const bf16* ob = sO(buf);
+      const float* lb = sLse(buf);
+      const float* dlb = sDelta(buf);
+      const int* pob = sPos(buf);
       const int last = min(rt + 63, rq_end - 1);
-      const int p_first = sPos[0];
-      const int p_last = sPos[last - rt];
+      const int p_first = pob[0];
+      const int p_last = pob[last - rt];
       const bool skip = !wave_active || p_last < kw0 || (WINDOW && p_first > kw_last + W);
       if (!skip) {
         const bool need_mask = WINDOW || (p_first < kw_last) || (rt + 64 > rq_end);
@@ -513,35 +559,38 @@ __global__ __launch_bounds__(256) LOGO_OCC_DKV void sq_dkv_kernel(const AttnArgs
           f32x16 sacc{}, pacc{};
 #pragma unroll
           for (int ds = 0; ds < DS; ++ds) {
-            sacc = mfma32(read_row_op<RS>(sQ, 32 * qq + i, ds, g), kreg[ds], sacc);
-            pacc = mfma32(read_row_op<RS>(sO, 32 * qq + i, ds, g), vreg[ds], pacc);
+            sacc = mfma32(read_row_op<RS>(qb, 32 * qq + i, ds, g), kreg[ds], sacc);
+            pacc = mfma32(read_row_op<RS>(ob, 32 * qq + i, ds, g), vreg[ds], pacc);
           }
 #pragma unroll
           for (int jj = 0; jj < 16; ++jj) {
             const int qr = 32 * qq + rowmap(g, jj);
-            float pv = fast_exp2(fmaf(sacc[jj], c, -sLse[qr]));
+            float pv = fast_exp2(fmaf(sacc[jj], c, -lb[qr]));
             if (need_mask) {
-              const int pq = sPos[qr];
+              const int pq = pob[qr];
               bool vis = key <= pq;
               if (WINDOW) vis = vis && key >= pq - W;
               if (!vis) pv = 0.f;
             }
             sacc[jj] = pv;
-            pacc[jj] = pv * (pacc[jj] - sDelta[qr]);
+            pacc[jj] = pv * (pacc[jj] - dlb[qr]);
           }
 #pragma unroll
           for (int hh = 0; hh < 2; ++hh) {
             const int ks = 2 * qq + hh;
-            const bf16x8 pb = acc_to_bf16(sacc, hh);
-            const bf16x8 db = acc_to_bf16(pacc, hh);
+            const bf16x8 pbf = acc_to_bf16(sacc, hh);
+            const bf16x8 dbf = acc_to_bf16(pacc, hh);
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) {
-              dvacc[dt] = mfma32(read_perm_k<TS>(sOt, 32 * dt + i, ks, g), pb, dvacc[dt]);
-              dkacc[dt] = mfma32(read_perm_k<TS>(sQt, 32 * dt + i, ks, g), db, dkacc[dt]);
+              dvacc[dt] = mfma32(read_tr_op<RS>(ob, 16 * ks, 32 * dt), pbf, dvacc[dt]);
+              dkacc[dt] = mfma32(read_tr_op<RS>(qb, 16 * ks, 32 * dt), dbf, dkacc[dt]);
             }
           }
         }
       }
+      if (has_next) store_tile(buf ^ 1);
+      __syncthreads();
+      buf ^= 1;
     }
   }
 
@@ -567,11 +616,11 @@ __global__ __launch_bounds__(256) LOGO_OCC_DKV void sq_dkv_kernel(const AttnArgs
 // Host launchers
 // ---------------------------------------------------------------------------
 template <int D>
-constexpr size_t fwd_smem() { return (size_t)(2 * 64 * (D + 8) + 2 * D * 68) * sizeof(bf16); }
+constexpr size_t fwd_smem() { return (size_t)(2 * 64 * kRowStride<D> + 2 * 64 * kTrStride<D>) * sizeof(bf16); }
 template <int D>
-constexpr size_t dq_smem() { return (size_t)(2 * 64 * (D + 8) + D * 68) * sizeof(bf16); }
+constexpr size_t dq_smem() { return (size_t)(2 * 64 * kTrStride<D> + 2 * 64 * kRowStride<D>) * sizeof(bf16); }
 template <int D>
-constexpr size_t dkv_smem() { return (size_t)(2 * 64 * (D + 8) + 2 * D * 68) * sizeof(bf16) + 3 * 64 * 4; }
+constexpr size_t dkv_smem() { return (size_t)2 * dkv_stage_bytes<D>(); }
 
 template <typename K>
 static hipError_t allow_smem(K kernel, size_t bytes) {
@@ -686,15 +735,15 @@ extern "C" int logo_sq_fwd(const void* q, const void* k, const void* v, void* o,
   return LOGO_DISPATCH(launch_fwd, a, as_stream(stream), d, sparse, win);
 }
 
-#define LOGO_BWD_PARAMS                                                                       \
+#define LOGO_BWD_PARAMS                                                                        \
   const void *q, const void *k, const void *v, const void *o, const void *dout, const float *lse, \
-      float *delta, void *dq, void *dk, void *dv, const int64_t *q_idx, const int32_t *pos,          \
-      const int32_t *meta, const int32_t *cu, int64_t n_tokens, int nseq, int hq, int h, int d,      \
-      int lanes, float scale, int window, int dtype, void *stream
+      float *delta, void *q_sel, void *do_sel, void *dq, void *dk, void *dv, const int64_t *q_idx, \
+      const int32_t *pos, const int32_t *meta, const int32_t *cu, int64_t n_tokens, int nseq,      \
+      int hq, int h, int d, int lanes, float scale, int window, int dtype, void *stream
 
 #define LOGO_BWD_ARGS                                                                             \
-  q, k, v, o, dout, lse, delta, dq, dk, dv, q_idx, pos, meta, cu, n_tokens, nseq, hq, h, d, lanes, \
-      scale, window, dtype, stream
+  q, k, v, o, dout, lse, delta, q_sel, do_sel, dq, dk, dv, q_idx, pos, meta, cu, n_tokens, nseq, hq, \
+      h, d, lanes, scale, window, dtype, stream
 
 static int bwd_entry(LOGO_BWD_PARAMS, int phase) {
   int rc = check_common(n_tokens, nseq, hq, h, d, lanes, dtype);
@@ -702,11 +751,14 @@ static int bwd_entry(LOGO_BWD_PARAMS, int phase) {
   LOGO_REQUIRE(q && k && v && o && dout && lse && delta && meta && cu, "null pointer argument");
   LOGO_REQUIRE(phase == 0 || (dq && dk && dv), "null gradient pointer");
   LOGO_REQUIRE((q_idx == nullptr) == (pos == nullptr), "q_idx and pos must both be set or both be null");
+  LOGO_REQUIRE(q_idx == nullptr || (q_sel && do_sel), "sparse backward needs q_sel and do_sel workspaces");
   AttnArgs a = make_args(q, k, v, q_idx, pos, meta, cu, n_tokens, nseq, hq, h, lanes, scale, window);
   a.o = const_cast<bf16*>(static_cast<const bf16*>(o));
   a.dout = static_cast<const bf16*>(dout);
   a.lse = const_cast<float*>(lse);
   a.delta = delta;
+  a.q_sel = static_cast<bf16*>(q_sel);
+  a.do_sel = static_cast<bf16*>(do_sel);
   a.dq = static_cast<bf16*>(dq);
   a.dk = static_cast<bf16*>(dk);
   a.dv = static_cast<bf16*>(dv);

@@ -50,9 +50,15 @@ def _bwd(q, k, v, o, lse, do, dsel: DeviceSelection, scale: float, window: int):
     dk = torch.empty_like(k)
     dv = torch.empty_like(v)
     delta = torch.empty(hq, n, dtype=torch.float32, device=q.device)
+    q_sel = do_sel = None
+    if not dsel.dense:
+        # compacted head-major copies of the selected q / dO rows, filled by
+        # the delta phase and streamed by the dq and dk/dv kernels
+        q_sel = torch.empty(hq, n, d, dtype=torch.bfloat16, device=q.device)
+        do_sel = torch.empty(hq, n, d, dtype=torch.bfloat16, device=q.device)
     lib = _lib.lib()
     args = (_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(o), _lib.ptr(do), _lib.ptr(lse),
-            _lib.ptr(delta), _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(dv),
+            _lib.ptr(delta), _lib.ptr(q_sel), _lib.ptr(do_sel), _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(dv),
             _lib.ptr(dsel.q_idx), _lib.ptr(dsel.pos), _lib.ptr(dsel.meta), _lib.ptr(dsel.cu),
             n, dsel.nseq, hq, h, d, dsel.lanes, float(scale), int(window), _lib.DTYPE_BF16,
             _lib.stream_of(q))
