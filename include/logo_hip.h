@@ -144,6 +144,57 @@ int logo_sq_bwd_dkv(const void* q, const void* k, const void* v, const void* o,
     const int32_t* meta, const int32_t* cu, int64_t n_tokens, int nseq, int hq,
     int h, int d, int lanes, float scale, int window, int dtype, void* stream);
 
+/*
+ * Fused epilogue forward: gate threshold, the two branch context RMSNorms
+ * (one [D] weight each, shared by all heads) and the gated fusion, with the
+ * reference's eager bf16 rounding points (logo/modules/layernorm.py:17-22;
+ * logo/layers/logo.py:180-181, :225-226, :256-258).  L, G: [N, H, D];
+ * gate: [N] (post-sigmoid); thres: one float on the device; w_l, w_g: [D];
+ * out: [N, H*D].
+ */
+int logo_epilogue_fwd(const void* L, const void* G, const void* gate, const float* thres,
+                      const void* w_l, const void* w_g, void* out, int64_t n_tokens,
+                      int heads, int d, float eps, int dtype, void* stream);
+
+/* Bytes of workspace logo_epilogue_bwd needs. */
+size_t logo_epilogue_bwd_workspace_bytes(int64_t n_tokens, int heads, int d);
+
+/*
+ * Fused epilogue backward (autograd of the same expression): dL, dG [N, H, D],
+ * dgate [N] (zero where gate < thres: the masked_fill at logo/layers/logo.py:256
+ * blocks it), dw_l, dw_g [D]; reductions are deterministic.
+ */
+int logo_epilogue_bwd(const void* L, const void* G, const void* gate, const float* thres,
+                      const void* w_l, const void* w_g, const void* dout, void* dL, void* dG,
+                      void* dgate, void* dw_l, void* dw_g, int64_t n_tokens, int heads, int d,
+                      float eps, void* workspace, int dtype, void* stream);
+
+/* Bytes of split-K workspace logo_decode_attn needs for rows of <= max_len keys. */
+size_t logo_decode_workspace_bytes(int batch, int hq, int d, int max_len);
+
+/*
+ * Gate-aware decode attention, one query token per sequence: for row b with
+ * gate[b] >= *thres (or every row when gate is NULL), out[b, hq] =
+ * softmax(scale * q[b, hq] K[b, h, 0:lens[b]]^T) V[b, h, 0:lens[b]]; rows
+ * whose gate fails get zeros and read no cache (the reference runs dense
+ * attention for all rows and masks, logo/layers/logo.py:228-249, :256-258).
+ * q, out: [B, HQ, D]; k_cache, v_cache: [B, H, t_cap, D] (logo/cache.py
+ * layout, preallocated); max_len >= every lens[b] (sizes the grid).
+ */
+int logo_decode_attn(const void* q, const void* k_cache, const void* v_cache, const int32_t* lens,
+                     const void* gate, const float* thres, void* out, void* workspace, int batch,
+                     int hq, int h, int d, int64_t t_cap, int max_len, float scale, int dtype,
+                     void* stream);
+
+/*
+ * Append one key/value row per (b, h) at position pos[b] of a preallocated
+ * cache [B, H, t_cap, D] (ring > 0: at pos[b] % ring, the local window),
+ * replacing the per-step torch.cat of logo/cache.py:97-118.
+ */
+int logo_cache_append(const void* k_new, const void* v_new, void* k_cache, void* v_cache,
+                      const int32_t* pos, int batch, int h, int d, int64_t t_cap, int ring,
+                      int dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,266 @@
+// Gate-aware decode attention for gfx950 (one new query token per sequence).
+//
+// The reference's decode step (logo/layers/logo.py:228-249) syncs the host on
+// active.any() and, if any row's gate passes, runs dense attention over the
+// whole global KV cache for every row, then masks the inactive rows to zero.
+// Here each (sequence, head) reads the cache only if its gate passes
+// (gate >= thres, decided on the device), so HBM traffic scales with the
+// number of active rows.  The same kernel serves the local branch over the
+// 129-slot window ring (all rows active).
+//
+// Cache layout is logo/cache.py's: K/V [B, H, T, D] per layer (preallocated to
+// T_cap instead of grown with torch.cat, logo/cache.py:115-118).
+//
+// Split-K: a 256-thread workgroup takes 256 keys of one (b, q-head); each wave
+// takes 64 of them with lane l owning key 4s + l/16 (s = 0..15) and the 16-byte
+// column chunk l % 16, so every K/V load is a contiguous 256-byte row per 16
+// lanes.  Waves merge through LDS into one (max, sum, o[D]) partial per
+// workgroup; a combine kernel merges the partials of a row and normalises.
+#include <math.h>
+
+#include "capi.hpp"
+#include "common.hpp"
+
+namespace logo {
+
+constexpr int kDecKeysPerWave = 64;
+constexpr int kDecKeysPerWG = 256;
+
+struct DecArgs {
+  const bf16* q;        // [B, HQ, D]
+  const bf16* k;        // [B, H, T_cap, D]
+  const bf16* v;
+  const int32_t* lens;  // [B] keys per row
+  const bf16* gate;     // [B] or null (all active)
+  const float* thres;
+  bf16* out;            // [B, HQ, D]
+  float* part;          // [B*HQ, nsplit, D + 2]
+  int batch, hq, h, g, nsplit;
+  int64_t t_cap;
+  float scale_log2;
+};
+
+__device__ __forceinline__ bool dec_active(const DecArgs& a, int b) {
+  return a.gate == nullptr || !((float)a.gate[b] < *a.thres);
+}
+
+template <int D>
+__global__ __launch_bounds__(256) void decode_split_kernel(const DecArgs a) {
+  constexpr int CH = D / 8;                 // 16-byte chunks per row
+  constexpr int KPS = 64 / CH;              // keys per load step (4 for D=128)
+  constexpr int STEPS = kDecKeysPerWave / KPS;
+  const int split = blockIdx.x;
+  const int bq = blockIdx.y;                // b * HQ + hq
+  const int b = bq / a.hq, hq = bq % a.hq, h = hq / a.g;
+  if (!dec_active(a, b)) return;
+  const int len = a.lens[b];
+  const int k0 = split * kDecKeysPerWG;
+  if (k0 >= len) return;
+  const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63;
+  const int c = l % CH, kk = l / CH;
+  const int kw = k0 + wave * kDecKeysPerWave;
+
+  float qv[8];
+  {
+    const bf16x8 q8 = *reinterpret_cast<const bf16x8*>(a.q + (int64_t)bq * D + 8 * c);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) qv[e] = (float)q8[e] * a.scale_log2;
+  }
+  const bf16* kb = a.k + ((int64_t)b * a.h + h) * a.t_cap * D + 8 * c;
+  const bf16* vb = a.v + ((int64_t)b * a.h + h) * a.t_cap * D + 8 * c;
+
+  bf16x8 kr[STEPS];
+#pragma unroll
+  for (int s = 0; s < STEPS; ++s) {
+    const int key = kw + KPS * s + kk;
+    kr[s] = key < len ? *reinterpret_cast<const bf16x8*>(kb + (int64_t)key * D) : bf16x8{};
+  }
+  bf16x8 vr[STEPS];
+#pragma unroll
+  for (int s = 0; s < STEPS; ++s) {
+    const int key = kw + KPS * s + kk;
+    vr[s] = key < len ? *reinterpret_cast<const bf16x8*>(vb + (int64_t)key * D) : bf16x8{};
+  }
+  float sc[STEPS];
+  float m = -INFINITY;
+#pragma unroll
+  for (int s = 0; s < STEPS; ++s) {
+    float part = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) part = fmaf(qv[e], (float)kr[s][e], part);
+#pragma unroll
+    for (int off = CH / 2; off > 0; off >>= 1) part += __shfl_xor(part, off);
+    const int key = kw + KPS * s + kk;
+    sc[s] = key < len ? part : -INFINITY;
+    m = fmaxf(m, sc[s]);
+  }
+#pragma unroll
+  for (int off = CH; off < 64; off <<= 1) m = fmaxf(m, __shfl_xor(m, off));
+  const float base = m == -INFINITY ? 0.f : m;
+  float lsum = 0.f;
+  float o[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = 0.f;
+#pragma unroll
+  for (int s = 0; s < STEPS; ++s) {
+    const float p = fast_exp2(sc[s] - base);
+    lsum += p;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = fmaf(p, (float)vr[s][e], o[e]);
+  }
+#pragma unroll
+  for (int off = CH; off < 64; off <<= 1) {
+    lsum += __shfl_xor(lsum, off);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] += __shfl_xor(o[e], off);
+  }
+
+  __shared__ float sm[4], sl[4];
+  __shared__ float so[4][D];
+  if (l < CH) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) so[wave][8 * c + e] = o[e];
+  }
+  if (l == 0) {
+    sm[wave] = m;
+    sl[wave] = lsum;
+  }
+  __syncthreads();
+  if (tid < D) {
+    float M = -INFINITY;
+    for (int w = 0; w < 4; ++w) M = fmaxf(M, sm[w]);
+    const float Mb = M == -INFINITY ? 0.f : M;
+    float L = 0.f, O = 0.f;
+    for (int w = 0; w < 4; ++w) {
+      const float f = fast_exp2(sm[w] - Mb);
+      L += f * sl[w];
+      O += f * so[w][tid];
+    }
+    float* pp = a.part + ((int64_t)bq * a.nsplit + split) * (D + 2);
+    pp[2 + tid] = O;
+    if (tid == 0) {
+      pp[0] = M;
+      pp[1] = L;
+    }
+  }
+}
+
+template <int D>
+__global__ __launch_bounds__(D) void decode_combine_kernel(const DecArgs a) {
+  const int bq = blockIdx.x;
+  const int b = bq / a.hq;
+  const int d = threadIdx.x;
+  bf16* out = a.out + (int64_t)bq * D;
+  if (!dec_active(a, b)) {
+    out[d] = (bf16)0.f;
+    return;
+  }
+  const int len = a.lens[b];
+  const int ns = min(a.nsplit, (len + kDecKeysPerWG - 1) / kDecKeysPerWG);
+  const float* pp = a.part + (int64_t)bq * a.nsplit * (D + 2);
+  float M = -INFINITY;
+  for (int s = 0; s < ns; ++s) M = fmaxf(M, pp[(int64_t)s * (D + 2)]);
+  const float Mb = M == -INFINITY ? 0.f : M;
+  float L = 0.f, O = 0.f;
+  for (int s = 0; s < ns; ++s) {
+    const float* ps = pp + (int64_t)s * (D + 2);
+    const float f = fast_exp2(ps[0] - Mb);
+    L += f * ps[1];
+    O += f * ps[2 + d];
+  }
+  out[d] = (bf16)(L > 0.f ? O / L : 0.f);
+}
+
+// Write one new key/value row per (b, h) at position pos[b] (mod ring if > 0).
+template <int D>
+__global__ __launch_bounds__(256) void cache_append_kernel(const bf16* kn, const bf16* vn, bf16* kc, bf16* vc,
+                                                           const int32_t* pos, int h, int64_t t_cap, int ring,
+                                                           int64_t rows) {
+  constexpr int CH = D / 8;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t r = idx / CH;  // b * H + head
+  const int c = idx % CH;
+  if (r >= rows) return;
+  const int b = (int)(r / h);
+  int p = pos[b];
+  if (ring > 0) p %= ring;
+  const int64_t dst = (r * t_cap + p) * D + 8 * c;
+  *reinterpret_cast<u32x4*>(kc + dst) = *reinterpret_cast<const u32x4*>(kn + r * D + 8 * c);
+  *reinterpret_cast<u32x4*>(vc + dst) = *reinterpret_cast<const u32x4*>(vn + r * D + 8 * c);
+}
+
+}  // namespace logo
+
+using namespace logo;
+
+static int dec_nsplit(int max_len) { return (max_len + kDecKeysPerWG - 1) / kDecKeysPerWG; }
+
+extern "C" size_t logo_decode_workspace_bytes(int batch, int hq, int d, int max_len) {
+  const int ns = dec_nsplit(max_len > 0 ? max_len : 1);
+  return (size_t)batch * hq * ns * (d + 2) * sizeof(float);
+}
+
+extern "C" int logo_decode_attn(const void* q, const void* k_cache, const void* v_cache, const int32_t* lens,
+                                const void* gate, const float* thres, void* out, void* workspace, int batch,
+                                int hq, int h, int d, int64_t t_cap, int max_len, float scale, int dtype,
+                                void* stream) {
+  LOGO_REQUIRE(batch >= 1 && h >= 1 && hq % h == 0, "bad batch / head counts");
+  LOGO_REQUIRE(d == 64 || d == 128, "head dim %d unsupported (64 or 128)", d);
+  LOGO_REQUIRE(dtype == LOGO_DTYPE_BF16, "only bf16 tensors are supported");
+  LOGO_REQUIRE(max_len >= 1 && max_len <= t_cap, "max_len must be in [1, t_cap]");
+  LOGO_REQUIRE(q && k_cache && v_cache && lens && out && workspace, "null pointer argument");
+  LOGO_REQUIRE(gate == nullptr || thres != nullptr, "gate needs thres");
+  DecArgs a{};
+  a.q = static_cast<const bf16*>(q);
+  a.k = static_cast<const bf16*>(k_cache);
+  a.v = static_cast<const bf16*>(v_cache);
+  a.lens = lens;
+  a.gate = static_cast<const bf16*>(gate);
+  a.thres = thres;
+  a.out = static_cast<bf16*>(out);
+  a.part = static_cast<float*>(workspace);
+  a.batch = batch;
+  a.hq = hq;
+  a.h = h;
+  a.g = hq / h;
+  a.nsplit = dec_nsplit(max_len);
+  a.t_cap = t_cap;
+  a.scale_log2 = scale * 1.4426950408889634f;
+  hipStream_t st = as_stream(stream);
+  dim3 grid(a.nsplit, batch * hq);
+  if (d == 128) {
+    hipLaunchKernelGGL(decode_split_kernel<128>, grid, dim3(256), 0, st, a);
+    LOGO_LAUNCH_CHECK("decode_split_kernel");
+    hipLaunchKernelGGL(decode_combine_kernel<128>, dim3(batch * hq), dim3(128), 0, st, a);
+  } else {
+    hipLaunchKernelGGL(decode_split_kernel<64>, grid, dim3(256), 0, st, a);
+    LOGO_LAUNCH_CHECK("decode_split_kernel");
+    hipLaunchKernelGGL(decode_combine_kernel<64>, dim3(batch * hq), dim3(64), 0, st, a);
+  }
+  LOGO_LAUNCH_CHECK("decode_combine_kernel");
+  return LOGO_OK;
+}
+
+extern "C" int logo_cache_append(const void* k_new, const void* v_new, void* k_cache, void* v_cache,
+                                 const int32_t* pos, int batch, int h, int d, int64_t t_cap, int ring,
+                                 int dtype, void* stream) {
+  LOGO_REQUIRE(batch >= 1 && h >= 1, "bad batch / head counts");
+  LOGO_REQUIRE(d == 64 || d == 128, "head dim %d unsupported (64 or 128)", d);
+  LOGO_REQUIRE(dtype == LOGO_DTYPE_BF16, "only bf16 tensors are supported");
+  LOGO_REQUIRE(ring >= 0 && (ring == 0 || ring <= t_cap), "ring must be 0 or <= t_cap");
+  LOGO_REQUIRE(k_new && v_new && k_cache && v_cache && pos, "null pointer argument");
+  const int64_t rows = (int64_t)batch * h;
+  const int64_t total = rows * (d / 8);
+  const unsigned nblk = (unsigned)((total + 255) / 256);
+  hipStream_t st = as_stream(stream);
+  if (d == 128)
+    hipLaunchKernelGGL(cache_append_kernel<128>, dim3(nblk), dim3(256), 0, st, static_cast<const bf16*>(k_new),
+                       static_cast<const bf16*>(v_new), static_cast<bf16*>(k_cache), static_cast<bf16*>(v_cache),
+                       pos, h, t_cap, ring, rows);
+  else
+    hipLaunchKernelGGL(cache_append_kernel<64>, dim3(nblk), dim3(256), 0, st, static_cast<const bf16*>(k_new),
+                       static_cast<const bf16*>(v_new), static_cast<bf16*>(k_cache), static_cast<bf16*>(v_cache),
+                       pos, h, t_cap, ring, rows);
+  LOGO_LAUNCH_CHECK("cache_append_kernel");
+  return LOGO_OK;
+}

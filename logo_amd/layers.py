@@ -1,0 +1,252 @@
+"""LoGo attention layer on the HIP hot path (caller side of ``sq_full_attn``).
+
+Counterpart of ``LoGoAttention`` (logo/layers/logo.py:34-262), with the same
+parameter names and config knobs, so a reference state dict loads unchanged.
+The hot path (local SWA, query-sparse or dense global attention, the fused
+gate / context-norm / fusion epilogue, gate-aware decode) runs on this
+package's HIP kernels; the projections, the global re-parameterisation and
+RoPE stay plain PyTorch glue.
+
+Differences in structure (not in results): tensors stay in ``[B, T, H, D]``
+(no ``transpose(1, 2).contiguous()`` round trips, :121-158); equal-length
+batches are packed into ``[1, B*T]`` for every branch, as the reference does
+for its sparse branch (:199-209); decode reads a preallocated ``LogoKVCache``.
+
+``sparse_full_attn_backend``: ``"triton"`` (the reference's name, kept so
+configs load) and ``"hip"`` select the query-sparse kernel; ``"flash"``
+selects dense causal global attention on the same kernels
+(logo/configuration_logo.py:170-173, logo/layers/logo.py:185-224).
+"""
+
+import math
+from dataclasses import dataclass, field
+from typing import List, Optional
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from .ops.decode import LogoKVCache, decode_attn
+from .ops.epilogue import logo_epilogue
+from .ops.sq_attn import dense_causal_attn, sq_full_attn, swa_attn
+
+__all__ = ["LoGoConfig", "LoGoAttention", "RMSNorm", "rope_cos_sin", "apply_rope"]
+
+SPARSE_BACKENDS = ("triton", "hip")
+
+
+@dataclass
+class LoGoConfig:
+    """The LoGo knobs of logo/configuration_logo.py:86-183 that this path uses."""
+
+    vocab_size: int = 32000
+    hidden_size: int = 2048
+    intermediate_size: int = 5632
+    num_hidden_layers: int = 24
+    num_attention_heads: int = 16
+    num_key_value_heads: Optional[int] = None
+    rms_norm_eps: float = 1e-5
+    rope_theta: float = 10000.0
+    attention_bias: bool = False
+    attention_out_bias: bool = False
+    initializer_range: float = 0.02
+    tie_word_embeddings: bool = True
+    attn_type_list: Optional[List[int]] = None
+    window_size: int = 128
+    global_qk_param: str = "linear_proj"
+    sparse_full_attn_backend: str = "hip"
+    gate_thres_init: float = 0.5
+    use_context_norm: bool = True
+
+    def __post_init__(self):
+        if self.num_key_value_heads is None:
+            self.num_key_value_heads = self.num_attention_heads
+        if self.attn_type_list is None:
+            self.attn_type_list = [0] * self.num_hidden_layers
+        if self.global_qk_param not in ("scale_offset", "linear_proj"):
+            raise ValueError(f"`global_qk_param` must be 'scale_offset' or 'linear_proj', got {self.global_qk_param!r}")
+        if self.sparse_full_attn_backend not in ("flash", "triton", "hip"):
+            raise ValueError("`sparse_full_attn_backend` must be 'flash', 'triton' or 'hip', "
+                             f"got {self.sparse_full_attn_backend!r}")
+        if len(self.attn_type_list) != self.num_hidden_layers:
+            raise ValueError("`attn_type_list` must have length num_hidden_layers")
+
+    @property
+    def head_dim(self) -> int:
+        return self.hidden_size // self.num_attention_heads
+
+
+class RMSNorm(nn.Module):
+    """RMSNorm with the reference's rounding order (logo/modules/layernorm.py:9-22)."""
+
+    def __init__(self, hidden_size: int, eps: float = 1e-6):
+        super().__init__()
+        self.weight = nn.Parameter(torch.ones(hidden_size))
+        self.variance_epsilon = eps
+
+    def forward(self, x):
+        dt = x.dtype
+        xf = x.to(torch.float32)
+        xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.variance_epsilon)
+        return self.weight * xf.to(dt)
+
+
+def rope_cos_sin(positions: torch.Tensor, head_dim: int, theta: float, dtype):
+    """cos/sin ``[..., head_dim]`` computed in fp32, cast to ``dtype``
+    (logo/modules/rotary.py:58-78, default rope type)."""
+    inv_freq = 1.0 / (theta ** (torch.arange(0, head_dim, 2, device=positions.device, dtype=torch.float32) / head_dim))
+    freqs = positions.to(torch.float32)[..., None] * inv_freq
+    emb = torch.cat((freqs, freqs), dim=-1)
+    return emb.cos().to(dtype), emb.sin().to(dtype)
+
+
+def apply_rope(x, cos, sin):
+    """``x [..., T, H, D]`` with ``cos/sin [..., T, D]`` (logo/modules/rotary.py:81-106)."""
+    cos = cos.unsqueeze(-2)
+    sin = sin.unsqueeze(-2)
+    half = x.shape[-1] // 2
+    rot = torch.cat((-x[..., half:], x[..., :half]), dim=-1)
+    return x * cos + rot * sin
+
+
+def _per_head_linear(x, w):
+    """``x [..., H, D] @ w [H, D, E]`` per head with 2-D GEMMs."""
+    return torch.stack([x[..., h, :] @ w[h] for h in range(w.shape[0])], dim=-2)
+
+
+class LoGoAttention(nn.Module):
+    """Token-level dynamic local-global attention (logo/layers/logo.py:34-262)."""
+
+    def __init__(self, config: LoGoConfig, layer_idx: int = 0):
+        super().__init__()
+        self.config = config
+        self.layer_idx = layer_idx
+        self.hidden_size = config.hidden_size
+        self.num_heads = config.num_attention_heads
+        self.num_key_value_heads = config.num_key_value_heads
+        self.head_dim = config.head_dim
+        self.q_proj = nn.Linear(self.hidden_size, self.num_heads * self.head_dim, bias=config.attention_bias)
+        self.k_proj = nn.Linear(self.hidden_size, self.num_key_value_heads * self.head_dim, bias=config.attention_bias)
+        self.v_proj = nn.Linear(self.hidden_size, self.num_key_value_heads * self.head_dim, bias=config.attention_bias)
+        self.o_proj = nn.Linear(self.hidden_size, self.hidden_size, bias=config.attention_out_bias)
+        self.local_window_size = config.window_size
+        self.global_qk_param = config.global_qk_param
+        H, HK, D = self.num_heads, self.num_key_value_heads, self.head_dim
+        if self.global_qk_param == "scale_offset":
+            self.q_global_scale = nn.Parameter(torch.ones(H * D))
+            self.q_global_offset = nn.Parameter(torch.zeros(H * D))
+            self.k_global_scale = nn.Parameter(torch.ones(HK * D))
+            self.k_global_offset = nn.Parameter(torch.zeros(HK * D))
+            self.v_global_scale = nn.Parameter(torch.ones(HK * D))
+            self.v_global_offset = nn.Parameter(torch.zeros(HK * D))
+        else:
+            eye = torch.eye(D)
+            self.q_global_proj = nn.Parameter(eye.repeat(H, 1, 1))
+            self.k_global_proj = nn.Parameter(eye.repeat(HK, 1, 1))
+            self.v_global_proj = nn.Parameter(eye.repeat(HK, 1, 1))
+        self.gate_proj = nn.Linear(self.hidden_size, 1, bias=False)
+        self.use_context_norm = config.use_context_norm
+        if self.use_context_norm:
+            self.context_norm_local = RMSNorm(D, eps=config.rms_norm_eps)
+            self.context_norm_global = RMSNorm(D, eps=config.rms_norm_eps)
+        self.sparse_full_attn_backend = config.sparse_full_attn_backend
+        self.register_buffer("gate_thres", torch.full((1,), config.gate_thres_init))
+        # counters kept in fp32 even in a bf16 model (the reference's become bf16
+        # and lose integer precision above 256, logo/layers/logo.py:74-76)
+        self.register_buffer("gate_avg", torch.zeros(1, dtype=torch.float32), persistent=False)
+        self.register_buffer("global_token_count", torch.zeros(1, dtype=torch.float32), persistent=False)
+        self.register_buffer("total_token_count", torch.zeros(1, dtype=torch.float32), persistent=False)
+
+    def _apply(self, fn, recurse=True):
+        out = super()._apply(fn, recurse)
+        for name in ("gate_avg", "global_token_count", "total_token_count"):
+            buf = getattr(self, name)
+            if buf.dtype != torch.float32:
+                setattr(self, name, buf.float())
+        return out
+
+    def _global_qkv(self, q, k, v):
+        """Global re-parameterisation on ``[B, T, H, D]`` (logo/layers/logo.py:80-94)."""
+        if self.global_qk_param == "scale_offset":
+            sh = lambda x, s, o: x * s.view(x.shape[-2], x.shape[-1]) + o.view(x.shape[-2], x.shape[-1])
+            return (sh(q, self.q_global_scale, self.q_global_offset),
+                    sh(k, self.k_global_scale, self.k_global_offset),
+                    sh(v, self.v_global_scale, self.v_global_offset))
+        return (_per_head_linear(q, self.q_global_proj), _per_head_linear(k, self.k_global_proj),
+                _per_head_linear(v, self.v_global_proj))
+
+    def _fuse(self, local, glob, gate):
+        """Context norms + gate mask + fusion; ``local/glob [B, T, H, D]``."""
+        if self.use_context_norm:
+            return logo_epilogue(local, glob, gate, self.gate_thres, self.context_norm_local.weight,
+                                 self.context_norm_global.weight, self.context_norm_local.variance_epsilon)
+        g = gate.masked_fill(gate < self.gate_thres, 0.0)
+        B, T = local.shape[:2]
+        return ((1 - g) * local.reshape(B, T, -1) + g * glob.reshape(B, T, -1))
+
+    def forward(self, hidden_states, position_ids=None, cu_seqlens=None,
+                past_key_value: Optional[LogoKVCache] = None, **kwargs):
+        B, T, _ = hidden_states.shape
+        H, HK, D = self.num_heads, self.num_key_value_heads, self.head_dim
+        q = self.q_proj(hidden_states).view(B, T, H, D)
+        k = self.k_proj(hidden_states).view(B, T, HK, D)
+        v = self.v_proj(hidden_states).view(B, T, HK, D)
+        gq, gk, gv = self._global_qkv(q, k, v)
+        gate = torch.sigmoid(self.gate_proj(hidden_states))  # [B, T, 1]
+
+        if position_ids is None:
+            dev = hidden_states.device
+            if cu_seqlens is not None:
+                # positions restart at every packed segment (logo/modeling_logo.py:207-222)
+                idx = torch.arange(B * T, device=dev)
+                cu64 = cu_seqlens.to(device=dev, dtype=torch.int64)
+                seg = torch.searchsorted(cu64, idx, right=True) - 1
+                position_ids = (idx - cu64[seg]).view(B, T)
+            else:
+                start = past_key_value.get_seq_length() if past_key_value is not None else 0
+                position_ids = torch.arange(start, start + T, device=dev)[None].expand(B, T)
+        cos, sin = rope_cos_sin(position_ids, D, self.config.rope_theta, q.dtype)
+        q, k = apply_rope(q, cos, sin), apply_rope(k, cos, sin)
+        gq, gk = apply_rope(gq, cos, sin), apply_rope(gk, cos, sin)
+
+        if past_key_value is not None and T == 1:
+            out = self._decode(q, k, v, gq, gk, gv, gate, past_key_value)
+        else:
+            if past_key_value is not None:
+                past_key_value.prefill(self.layer_idx, k.transpose(1, 2), v.transpose(1, 2),
+                                       gk.transpose(1, 2), gv.transpose(1, 2))
+            out = self._prefill(q, k, v, gq, gk, gv, gate, cu_seqlens)
+
+        if self.training:
+            with torch.no_grad():
+                self.gate_avg.add_(gate.sum().float())
+                self.global_token_count.add_((gate >= self.gate_thres).sum().float())
+                self.total_token_count.add_(gate.numel())
+        return self.o_proj(out), None, past_key_value
+
+    def _prefill(self, q, k, v, gq, gk, gv, gate, cu_seqlens):
+        B, T, H, D = q.shape
+        N = B * T
+        if cu_seqlens is None:
+            cu = torch.arange(0, (B + 1) * T, T, dtype=torch.int32, device=q.device)
+        else:
+            assert B == 1, "cu_seqlens requires packed [1, N] input"
+            cu = cu_seqlens.to(torch.int32)
+        pk = lambda x: x.reshape(1, N, x.shape[2], x.shape[3])
+        local = swa_attn(pk(q), pk(k), pk(v), cu, window=self.local_window_size)
+        if self.sparse_full_attn_backend in SPARSE_BACKENDS:
+            selection = (gate.reshape(1, N) >= self.gate_thres)
+            glob = sq_full_attn(pk(gq), pk(gk), pk(gv), selection, cu_seqlens=cu)
+        else:
+            glob = dense_causal_attn(pk(gq), pk(gk), pk(gv), cu)
+        return self._fuse(local.view(B, T, H, D), glob.view(B, T, H, D), gate.view(B, T))
+
+    def _decode(self, q, k, v, gq, gk, gv, gate, cache: LogoKVCache):
+        B, _, H, D = q.shape
+        cache.append(self.layer_idx, k[:, 0], v[:, 0], gk[:, 0], gv[:, 0])
+        len_g, len_l = cache.lengths()
+        local = decode_attn(q[:, 0], cache.local_k[self.layer_idx], cache.local_v[self.layer_idx], len_l,
+                            max_len=min(cache.seen + 1, cache.ring))
+        glob = decode_attn(gq[:, 0], cache.global_k[self.layer_idx], cache.global_v[self.layer_idx], len_g,
+                           gate.view(B), self.gate_thres, max_len=cache.seen + 1)
+        return self._fuse(local.view(B, 1, H, D), glob.view(B, 1, H, D), gate.view(B, 1))

@@ -1,0 +1,120 @@
+"""Gate-aware decode attention and a preallocated LoGo KV cache.
+
+``decode_attn`` replaces the decode branch of logo/layers/logo.py:228-249:
+rows whose gate fails read no cache and return zeros, and no host
+synchronisation decides it (the reference's ``active.any()`` at :230).
+
+``LogoKVCache`` keeps the logical layout of logo/cache.py (per layer: local
+K/V for the sliding window, global K/V ``[B, H, T, D]``) but preallocates the
+global buffers to the maximum length and keeps the local branch as a ring of
+``window + 1`` slots, so a decode step appends in place instead of
+``torch.cat``-ing the whole cache (logo/cache.py:97-118).
+"""
+
+from typing import Optional
+
+import torch
+
+from .. import _lib
+
+__all__ = ["decode_attn", "cache_append", "LogoKVCache"]
+
+
+def decode_attn(q, k_cache, v_cache, lens, gate=None, thres=None, max_len: Optional[int] = None,
+                scale: Optional[float] = None):
+    """``q [B, HQ, D]``; caches ``[B, H, T_cap, D]``; ``lens`` int32 ``[B]`` on the
+    device; ``gate [B]`` (post-sigmoid) with ``thres`` (device tensor) or
+    ``None`` for all rows.  ``max_len`` is a host-side bound on ``lens``
+    (defaults to ``T_cap``).  Returns ``[B, HQ, D]``."""
+    _lib.require_gpu(q, k_cache, v_cache, lens)
+    B, HQ, D = q.shape
+    H, t_cap = k_cache.shape[1], k_cache.shape[2]
+    if scale is None:
+        scale = D ** -0.5
+    if max_len is None:
+        max_len = t_cap
+    qc = q.contiguous()
+    out = torch.empty_like(qc)
+    lib = _lib.lib()
+    ws = torch.empty((lib.logo_decode_workspace_bytes(B, HQ, D, max_len) + 3) // 4, dtype=torch.float32,
+                     device=q.device)
+    th = None
+    if gate is not None:
+        gate = gate.contiguous().view(B)
+        th = thres.detach().reshape(1).to(torch.float32).contiguous()
+    _lib.launch("logo_decode_attn", lib.logo_decode_attn, _lib.ptr(qc), _lib.ptr(k_cache), _lib.ptr(v_cache),
+                _lib.ptr(lens), _lib.ptr(gate), _lib.ptr(th), _lib.ptr(out), _lib.ptr(ws), B, HQ, H, D, t_cap,
+                int(max_len), float(scale), _lib.DTYPE_BF16, _lib.stream_of(q))
+    return out
+
+
+def cache_append(k_new, v_new, k_cache, v_cache, pos, ring: int = 0):
+    """Write ``k_new/v_new [B, H, D]`` at position ``pos[b]`` (mod ``ring`` if > 0)."""
+    B, H, D = k_new.shape
+    lib = _lib.lib()
+    _lib.launch("logo_cache_append", lib.logo_cache_append, _lib.ptr(k_new.contiguous()),
+                _lib.ptr(v_new.contiguous()), _lib.ptr(k_cache), _lib.ptr(v_cache), _lib.ptr(pos), B, H, D,
+                k_cache.shape[2], int(ring), _lib.DTYPE_BF16, _lib.stream_of(k_new))
+
+
+class LogoKVCache:
+    """Preallocated per-layer cache: global ``[B, H, max_len, D]`` and a local ring
+    ``[B, H, window + 1, D]`` (all rows of a batch share one length)."""
+
+    def __init__(self, num_layers: int, batch: int, kv_heads: int, head_dim: int, max_len: int,
+                 window: int = 128, dtype=torch.bfloat16, device=None):
+        self.window = window
+        self.ring = window + 1
+        self.max_len = max_len
+        shape_g = (batch, kv_heads, max_len, head_dim)
+        shape_l = (batch, kv_heads, self.ring, head_dim)
+        self.global_k = [torch.empty(shape_g, dtype=dtype, device=device) for _ in range(num_layers)]
+        self.global_v = [torch.empty(shape_g, dtype=dtype, device=device) for _ in range(num_layers)]
+        self.local_k = [torch.empty(shape_l, dtype=dtype, device=device) for _ in range(num_layers)]
+        self.local_v = [torch.empty(shape_l, dtype=dtype, device=device) for _ in range(num_layers)]
+        self.seen = 0
+        self.batch = batch
+        self._pos = torch.zeros(batch, dtype=torch.int32, device=device)
+        self._len_g = torch.zeros(batch, dtype=torch.int32, device=device)
+        self._len_l = torch.zeros(batch, dtype=torch.int32, device=device)
+
+    def get_seq_length(self) -> int:
+        return self.seen
+
+    def prefill(self, layer: int, k_local, v_local, k_global, v_global):
+        """Store a prompt's K/V (``[B, H, T, D]``) for one layer."""
+        T = k_global.shape[2]
+        if T > self.max_len:
+            raise ValueError(f"prompt of {T} tokens exceeds the cache's {self.max_len}")
+        self.global_k[layer][:, :, :T].copy_(k_global)
+        self.global_v[layer][:, :, :T].copy_(v_global)
+        lo = max(0, T - self.ring)
+        for p0 in range(lo, T, self.ring):
+            p1 = min(T, p0 + self.ring)
+            s0 = p0 % self.ring
+            n = p1 - p0
+            first = min(n, self.ring - s0)
+            self.local_k[layer][:, :, s0:s0 + first].copy_(k_local[:, :, p0:p0 + first])
+            self.local_v[layer][:, :, s0:s0 + first].copy_(v_local[:, :, p0:p0 + first])
+            if first < n:
+                self.local_k[layer][:, :, :n - first].copy_(k_local[:, :, p0 + first:p1])
+                self.local_v[layer][:, :, :n - first].copy_(v_local[:, :, p0 + first:p1])
+
+    def set_length(self, seen: int):
+        """Record that ``seen`` tokens are cached (call once per step, after layer 0)."""
+        self.seen = seen
+        self._pos.fill_(seen)
+
+    def append(self, layer: int, k_local, v_local, k_global, v_global):
+        """Append the new token (``[B, H, D]`` each) at position ``seen``."""
+        if self.seen >= self.max_len:
+            raise ValueError("cache is full")
+        cache_append(k_global, v_global, self.global_k[layer], self.global_v[layer], self._pos)
+        cache_append(k_local, v_local, self.local_k[layer], self.local_v[layer], self._pos, ring=self.ring)
+
+    def lengths(self):
+        """(global length, local length) device tensors for the token at ``seen``."""
+        n = self.seen + 1
+        self._len_g.fill_(n)
+        self._len_l.fill_(min(n, self.ring))
+        return self._len_g, self._len_l
