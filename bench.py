@@ -49,6 +49,7 @@ def parse():
     ap.add_argument("--cpu-heads", type=int, default=8, help="heads in the CPU-baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seed", type=int, default=2)
+    ap.add_argument("--no-extra", action="store_true", help="skip the secondary measurements")
     return ap.parse_args()
 
 
@@ -112,6 +113,131 @@ def cpu_baseline(q, k, v, sel_np, cu, do, heads, flops_per_head):
                    f"{q.shape[1]} heads of the same T={q.shape[0]} workload; {secs:.2f} s; effective "
                    f"FLOPs on selected rows as for the GPU value"),
     }
+
+
+def _time_ms(fn, iters, warmup=2):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(iters):
+        fn()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / iters
+
+
+def extra_measurements(dev):
+    """Secondary rows: speed-up vs global ratio, cfg2 forward, cfg3 varlen
+    fwd+bwd, SWA and epilogue at cfg4 shapes, gate-aware decode at cfg5 shape.
+    All timings are HIP events around the op on the current stream."""
+    from logo_amd.ops import dense_causal_attn, sq_full_attn, swa_attn
+    from logo_amd.ops.decode import decode_attn
+    from logo_amd.ops.epilogue import logo_epilogue
+
+    out = {}
+    gen = torch.Generator()
+    gen.manual_seed(7)
+    T, H, D = 32768, 16, 128
+    q = (torch.randn(1, T, H, D, generator=gen) * 0.5).bfloat16().to(dev).requires_grad_()
+    k = (torch.randn(1, T, H, D, generator=gen) * 0.5).bfloat16().to(dev).requires_grad_()
+    v = (torch.randn(1, T, H, D, generator=gen) * 0.5).bfloat16().to(dev).requires_grad_()
+    do = torch.randn(1, T, H, D, generator=gen).bfloat16().to(dev)
+    cu = torch.tensor([0, T], dtype=torch.int32, device=dev)
+
+    # speed-up of the sparse path over dense causal attention vs the global ratio
+    def fb_dense():
+        o = dense_causal_attn(q, k, v, cu)
+        torch.autograd.grad(o, (q, k, v), do)
+    t_dense = _time_ms(fb_dense, 3)
+    sweep = {"dense_ms": round(t_dense, 3)}
+    for r in (0.5, 0.25, 0.125):
+        sel = torch.from_numpy(markov_mask(T, r, 8, gen)).to(dev)[None]
+
+        def fb_sparse():
+            o = sq_full_attn(q, k, v, sel, cu_seqlens=cu)
+            torch.autograd.grad(o, (q, k, v), do)
+        t = _time_ms(fb_sparse, 3)
+        sweep[f"r{r}"] = {"ms": round(t, 3), "speedup": round(t_dense / t, 2), "ideal": round(1 / r, 2)}
+    out["fwd_bwd_speedup_vs_dense_T32768"] = sweep
+
+    # cfg2: forward only, T=8192, per-(head, token) Bernoulli(0.5)
+    T2 = 8192
+    q2, k2, v2 = (x[:, :T2].detach() for x in (q, k, v))
+    sel2 = torch.rand(1, T2, H, generator=gen) < 0.5
+    sel2[:, 0, :] = True
+    pairs = float(sum((np.flatnonzero(sel2[0, :, h].numpy()) + 1).sum() for h in range(H)))
+    sel2 = sel2.to(dev)
+    cu2 = torch.tensor([0, T2], dtype=torch.int32, device=dev)
+    with torch.no_grad():
+        t2 = _time_ms(lambda: sq_full_attn(q2, k2, v2, sel2, cu_seqlens=cu2), 10)
+    out["cfg2_fwd_T8192_per_head_r0.5"] = {"ms": round(t2, 4), "tflops": round(4 * D * pairs / t2 / 1e9, 1)}
+
+    # cfg3: varlen fwd+bwd, ~32K tokens in 4 sequences, Markov ratio 0.25
+    lens = [7210, 12503, 2789, 9871]
+    cu3 = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int32, device=dev)
+    n3 = sum(lens)
+    sel3_np = markov_mask(n3, 0.25, 8, gen)
+    pos3 = np.concatenate([np.flatnonzero(sel3_np[c0:c0 + L]) for c0, L in zip(np.cumsum([0] + lens[:-1]), lens)])
+    sel3 = torch.from_numpy(sel3_np).to(dev)[None]
+    q3, k3, v3 = (x[:, :n3].detach().requires_grad_() for x in (q, k, v))
+
+    def fb3():
+        o = sq_full_attn(q3, k3, v3, sel3, cu_seqlens=cu3)
+        torch.autograd.grad(o, (q3, k3, v3), do[:, :n3])
+    t3 = _time_ms(fb3, 5)
+    f3 = 3.5 * 4 * D * H * float((pos3 + 1).sum())
+    out["cfg3_fwd_bwd_varlen"] = {"lens": lens, "ms": round(t3, 3), "tflops": round(f3 / t3 / 1e9, 1)}
+
+    # SWA (window 128) fwd+bwd at cfg4 shape: [1, 4*8192, 16, 128]
+    N4 = 4 * 8192
+    cu4 = torch.arange(0, N4 + 1, 8192, dtype=torch.int32, device=dev)
+    q4, k4, v4 = (x[:, :N4].detach().requires_grad_() for x in (q, k, v))
+    with torch.no_grad():
+        tsf = _time_ms(lambda: swa_attn(q4, k4, v4, cu4, window=128), 10)
+
+    def swa_fb():
+        o = swa_attn(q4, k4, v4, cu4, window=128)
+        torch.autograd.grad(o, (q4, k4, v4), do[:, :N4])
+    tsb = _time_ms(swa_fb, 5)
+    io = 4 * N4 * H * D * 2  # q, k, v read + o written, bf16
+    out["swa_w128_cfg4"] = {"fwd_ms": round(tsf, 4), "fwd_gbs": round(io / tsf / 1e6, 1),
+                            "fwd_bwd_ms": round(tsb, 4)}
+
+    # fused epilogue at cfg4 shape: L, G [32768, 16, 128], gate [32768]
+    L = (torch.randn(N4, H, D, generator=gen)).bfloat16().to(dev).requires_grad_()
+    G = (torch.randn(N4, H, D, generator=gen)).bfloat16().to(dev).requires_grad_()
+    gate = torch.sigmoid(torch.randn(N4, generator=gen)).bfloat16().to(dev).requires_grad_()
+    thres = torch.tensor([0.5], dtype=torch.bfloat16, device=dev)
+    wl = torch.ones(D, dtype=torch.bfloat16, device=dev, requires_grad=True)
+    wg = torch.ones(D, dtype=torch.bfloat16, device=dev, requires_grad=True)
+    dO = torch.randn(N4, H * D, generator=gen).bfloat16().to(dev)
+    with torch.no_grad():
+        tef = _time_ms(lambda: logo_epilogue(L, G, gate, thres, wl, wg, 1e-5), 20)
+    o_e = logo_epilogue(L, G, gate, thres, wl, wg, 1e-5)
+    teb = _time_ms(lambda: torch.autograd.grad(o_e, (L, G, gate, wl, wg), dO, retain_graph=True), 20)
+    elem = N4 * H * D * 2
+    out["epilogue_cfg4"] = {"fwd_ms": round(tef, 4), "fwd_gbs": round(3 * elem / tef / 1e6, 1),
+                            "bwd_ms": round(teb, 4), "bwd_gbs": round(5 * elem / teb / 1e6, 1)}
+    del L, G, o_e
+
+    # gate-aware decode attention at cfg5 shape: B=32, H=16, D=128, ctx 16384+1, r=0.5
+    B5, ctx = 32, 16385
+    kc = (torch.randn(B5, H, ctx, D, generator=gen) * 0.5).bfloat16().to(dev)
+    vc = torch.randn(B5, H, ctx, D, generator=gen).bfloat16().to(dev)
+    q5 = torch.randn(B5, H, D, generator=gen).bfloat16().to(dev)
+    gate5 = torch.tensor([0.75, 0.25] * (B5 // 2), dtype=torch.bfloat16, device=dev)
+    lens5 = torch.full((B5,), ctx, dtype=torch.int32, device=dev)
+    td = _time_ms(lambda: decode_attn(q5, kc, vc, lens5, gate5, thres, max_len=ctx), 20)
+    bytes_active = (B5 // 2) * H * ctx * D * 2 * 2
+    td_all = _time_ms(lambda: decode_attn(q5, kc, vc, lens5, max_len=ctx), 20)
+    out["decode_global_cfg5_layer"] = {
+        "active_rows": B5 // 2, "ms": round(td, 4), "gbs": round(bytes_active / td / 1e6, 1),
+        "all_rows_ms": round(td_all, 4), "all_rows_gbs": round(2 * bytes_active / td_all / 1e6, 1),
+        "hbm_peak_gbs": HBM_PEAK_GBS}
+    return out
 
 
 def main():
@@ -188,6 +314,8 @@ def main():
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(q, k, v, sel_np, [0, T], do, min(args.cpu_heads, H), f_step / H)
 
+    extra = None if args.no_extra else extra_measurements(dev)
+
     line = {
         "metric": "sq_full_attn fwd+bwd effective TFLOP/s @T=32K, 25% global; decode tok/s",
         "value": round(value, 3),
@@ -213,6 +341,7 @@ def main():
         "kernel_ms": {k_: round(v_, 4) for k_, v_ in sorted(kern_ms.items())},
         "kernel_tflops": {n: round(KERNEL_FLOPS_PER_PAIR_D[n] * D * H * pairs_per_head / (ms * 1e-3) / 1e12, 2)
                           for n, ms in flop_kernels.items()},
+        "extra": extra,
     }
     print(json.dumps(line), flush=True)
 
