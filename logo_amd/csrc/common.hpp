@@ -47,11 +47,40 @@ __device__ __forceinline__ bf16x8 acc_to_bf16(const f32x16& a, int h) {
   return r;
 }
 
-// A 64-row x D-column bf16 tile moved global -> registers -> LDS (row-major,
-// row stride RS elements) by 256 threads.  Thread tid owns the 16-byte column
-// chunk c = tid % CH of rows rg*RPT .. rg*RPT+RPT-1 (rg = tid / CH), so every
-// group of CH lanes reads one contiguous row.
-template <int D, int RS>
+// LDS tile layouts.  gfx950's LDS serves 64 four-byte banks per cycle:
+// ds_read_b128 16 lanes per cycle, ds_read_b64_tr_b16 32 lanes per cycle.
+//   kRow : rows padded to D + 8 elements (start 4 banks apart): 16 lanes
+//          reading one 16-byte chunk of 16 consecutive rows hit 64 distinct
+//          banks.  For tiles read only along rows.
+//   kTr  : rows padded to D + 32 (start 16 banks apart): a transposing read
+//          covers rows 4m..4m+3 x 32 consecutive columns, again 64 distinct
+//          banks.  For tiles read only through ds_read_b64_tr_b16.
+//   kSwz : no padding; the 16-byte chunk ch of row r is stored at chunk
+//          ch ^ swz(r), swz(r) = 4*(r & 3) | ((r >> 2) & 3): conflict-free
+//          for both read kinds (swz takes all 16 values on 16 aligned rows;
+//          on rows 4m..4m+3 times chunks C..C+3, (C | dc) ^ (4e + x) is
+//          distinct).  For tiles read both ways.
+// Row stores (16 lanes write the 16 chunks of one row) are conflict-free in
+// every layout.  D = 64 uses the low three swizzle bits (correct; the
+// conflict analysis above is for D = 128).
+enum TileKind { kRow = 0, kTr = 1, kSwz = 2 };
+
+template <int D, int KIND>
+struct TileGeom {
+  static constexpr int RS = KIND == kRow ? D + 8 : KIND == kTr ? D + 32 : D;  // row stride (elements)
+  static constexpr int ELEMS = 64 * RS;
+  __device__ __forceinline__ static int swz(int r) {
+    return KIND == kSwz ? ((((r & 3) << 2) | ((r >> 2) & 3)) & (D / 8 - 1)) : 0;
+  }
+  // element offset of (row r, logical 16-byte chunk ch)
+  __device__ __forceinline__ static int off(int r, int ch) { return r * RS + ((ch ^ swz(r)) << 3); }
+};
+
+// A 64-row x D-column bf16 tile moved global -> registers -> LDS by 256
+// threads.  Thread tid owns the 16-byte column chunk c = tid % CH of rows
+// rg*RPT .. rg*RPT+RPT-1 (rg = tid / CH), so every group of CH lanes reads one
+// contiguous row.
+template <int D>
 struct Tile64 {
   static constexpr int CH = D / 8;
   static constexpr int RPT = (64 * CH) / 256;  // rows per thread: D/32
@@ -61,55 +90,112 @@ struct Tile64 {
   __device__ __forceinline__ static int chunk(int tid) { return tid % CH; }
   __device__ __forceinline__ static int row0(int tid) { return (tid / CH) * RPT; }
 
-  // rowptr(row) returns the row's base pointer or nullptr for a zero row.
+  // rowptr(row) returns a valid row pointer for every tile row: callers
+  // clamp rows past the end of their range to a real row, whose (finite)
+  // values the attention mask then ignores, so the loads are unconditional.
   template <typename F>
   __device__ __forceinline__ void load(int tid, F rowptr) {
     const int c = chunk(tid), r0 = row0(tid);
 #pragma unroll
-    for (int i = 0; i < RPT; ++i) {
-      const bf16* p = rowptr(r0 + i);
-      r[i] = p ? *reinterpret_cast<const u32x4*>(p + 8 * c) : u32x4{0u, 0u, 0u, 0u};
-    }
+    for (int i = 0; i < RPT; ++i) r[i] = *reinterpret_cast<const u32x4*>(rowptr(r0 + i) + 8 * c);
   }
 
+  template <int KIND>
   __device__ __forceinline__ void store(bf16* lds, int tid) const {
     const int c = chunk(tid), r0 = row0(tid);
 #pragma unroll
-    for (int i = 0; i < RPT; ++i) *reinterpret_cast<u32x4*>(lds + (r0 + i) * RS + 8 * c) = r[i];
+    for (int i = 0; i < RPT; ++i) *reinterpret_cast<u32x4*>(lds + TileGeom<D, KIND>::off(r0 + i, c)) = r[i];
   }
 };
 
-// LDS row strides (elements).  Tiles read only with ds_read_b128 along rows
-// use D + 8 (row starts 4 banks apart: conflict-free for 16 lanes reading 16
-// rows); tiles also read with the transposing ds_read_b64_tr_b16 use D + 16
-// (row starts 8 banks apart: the 4 rows x 4 chunks of a 16-lane group hit 32
-// distinct banks).
-template <int D> constexpr int kRowStride = D + 8;
-template <int D> constexpr int kTrStride = D + 16;
+// Global -> LDS copy of a 64-row x D-column bf16 tile into the kSwz layout
+// with global_load_lds_dwordx4 (no register staging, no LDS store
+// instructions).  Each such load writes 64 lanes x 16 bytes = 1 KB contiguous
+// at a wave-uniform LDS address, i.e. RPB = 64 / CH whole rows; lane j fills
+// physical chunk j % CH of row (block row + j / CH), so it loads that row's
+// logical chunk (j % CH) ^ swz(row).  Wave w copies rows 16w .. 16w + 15.
+// The caller waits for the loads (s_waitcnt vmcnt) before the barrier that
+// publishes the tile.
+template <int D>
+struct TileDma {
+  static constexpr int CH = D / 8;
+  static constexpr int RPB = 64 / CH;
+  static constexpr int BLOCKS = 16 / RPB;
+  using Geo = TileGeom<D, kSwz>;
 
-// Row-major operand: 8 consecutive columns 16*ks + 8*g of row `row`.
-template <int RS>
-__device__ __forceinline__ bf16x8 read_row_op(const bf16* lds, int row, int ks, int g) {
-  return *reinterpret_cast<const bf16x8*>(lds + row * RS + 16 * ks + 8 * g);
-}
+  template <typename F>
+  __device__ __forceinline__ static void issue(bf16* tile, F rowptr) {
+    const int wave = threadIdx.x >> 6, j = threadIdx.x & 63;
+#pragma unroll
+    for (int b = 0; b < BLOCKS; ++b) {
+      const int rb = 16 * wave + RPB * b;
+      const int row = rb + j / CH;
+      const int ch = (j % CH) ^ Geo::swz(row);
+      __builtin_amdgcn_global_load_lds(rowptr(row) + 8 * ch,
+                                       (__attribute__((address_space(3))) void*)(tile + rb * D), 16, 0, 0);
+    }
+  }
+};
+
+// Wait for this wave's outstanding vector-memory operations (the tile copies
+// above) to land.
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0); }
 
 typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
 
-// Transposed operand from a row-major tile T (row stride RS): lane (i, g)
-// receives T[r0 + 4g + e][c0 + i] for e = 0..3 followed by
-// T[r0 + 8 + 4g + e][c0 + i], the k order acc_to_bf16(acc, ks & 1) produces
-// for r0 = 16*ks.  ds_read_b64_tr_b16 gives lane 16G + 4a + b element b of the
-// 8-byte chunks addressed by lanes 16G + a + 4e (e = 0..3), so lane 16G + j
-// addresses row r0 + 4g + j/4, column c0 + 16(G & 1) + 4(j & 3).
-template <int RS>
-__device__ __forceinline__ bf16x8 read_tr_op(const bf16* lds, int r0, int c0) {
-  const int l = threadIdx.x & 63;
-  const int G = l >> 4, j = l & 15;
-  const bf16* p = lds + (r0 + 4 * (G >> 1) + (j >> 2)) * RS + c0 + 16 * (G & 1) + 4 * (j & 3);
-  const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(p));
-  const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(p + 8 * RS));
-  return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-}
+// MFMA operand reads from a tile, with every lane-dependent part of the
+// address computed once (init) so that in the unrolled loops each read is a
+// lane register plus an immediate.
+//   row(tile, rbase, ks): lane (i, g) gets the 8 columns 16*ks + 8*g of row
+//     rbase + i (rbase a multiple of 16) -- the A/B operand whose m/n index
+//     is the tile row.
+//   tr(tile, r0, dt): lane (i, g) gets T[r0 + 4g + e][32*dt + i] for e = 0..3
+//     then T[r0 + 8 + 4g + e][32*dt + i] (r0 a multiple of 16), the k order
+//     acc_to_bf16(acc, ks & 1) produces for r0 = 16*ks.  ds_read_b64_tr_b16
+//     gives lane 16G + 4a + b element b of the 8-byte chunks addressed by
+//     lanes 16G + a + 4e (e = 0..3), so lane 16G + j addresses row
+//     r0 + 4g + j/4 (+ 8), column 32*dt + 16(G & 1) + 4(j & 3).
+template <int D, int KIND>
+struct TileReader {
+  using Geo = TileGeom<D, KIND>;
+  static constexpr int DS = D / 16, DT = D / 32;
+  static constexpr bool SWZ = KIND == kSwz;
+  int row_off[SWZ ? DS : 1];
+  int tr_off[SWZ ? 2 * DT : 1];
+
+  __device__ __forceinline__ void init() {
+    const int l = threadIdx.x & 63, i = l & 31, g = l >> 5;
+    const int G = l >> 4, j = l & 15;
+    if constexpr (SWZ) {
+#pragma unroll
+      for (int ks = 0; ks < DS; ++ks) row_off[ks] = Geo::off(i, 2 * ks + g);
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int row = 4 * g + (j >> 2) + 8 * h;
+          const int col = 32 * dt + 16 * (G & 1) + 4 * (j & 3);
+          tr_off[2 * dt + h] = Geo::off(row, col >> 3) + (col & 7);
+        }
+    } else {
+      row_off[0] = i * Geo::RS + 8 * g;
+      tr_off[0] = (4 * g + (j >> 2)) * Geo::RS + 16 * (G & 1) + 4 * (j & 3);
+    }
+  }
+
+  __device__ __forceinline__ bf16x8 row(const bf16* tile, int rbase, int ks) const {
+    const int o = SWZ ? rbase * Geo::RS + row_off[ks] : rbase * Geo::RS + 16 * ks + row_off[0];
+    return *reinterpret_cast<const bf16x8*>(tile + o);
+  }
+
+  __device__ __forceinline__ bf16x8 tr(const bf16* tile, int r0, int dt) const {
+    const int o0 = SWZ ? r0 * Geo::RS + tr_off[2 * dt] : r0 * Geo::RS + 32 * dt + tr_off[0];
+    const int o1 = SWZ ? r0 * Geo::RS + tr_off[2 * dt + 1] : o0 + 8 * Geo::RS;
+    const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(tile + o0));
+    const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(tile + o1));
+    return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+  }
+};
 
 // Largest s in [0, n) with arr[s] <= x (arr ascending, arr[0] <= x).
 __device__ __forceinline__ int seg_of(const int32_t* arr, int n, int64_t x) {

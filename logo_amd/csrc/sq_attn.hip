@@ -33,6 +33,8 @@
 //              looped inside the workgroup.
 #include <math.h>
 
+#include <type_traits>
+
 #include "capi.hpp"
 #include "common.hpp"
 
@@ -161,15 +163,17 @@ struct QTile {
 // ---------------------------------------------------------------------------
 // Forward
 // ---------------------------------------------------------------------------
+template <int B>
+using BufTag = std::integral_constant<int, B>;
+
 template <int D, bool SPARSE, bool WINDOW>
 __global__ __launch_bounds__(256) LOGO_OCC_FWD void sq_fwd_kernel(const AttnArgs a) {
-  constexpr int RSK = kRowStride<D>, RSV = kTrStride<D>, DS = D / 16, DT = D / 32;
-  using TK = Tile64<D, RSK>;
-  using TV = Tile64<D, RSV>;
+  constexpr int DS = D / 16, DT = D / 32;
+  using GT = TileGeom<D, kSwz>;
   bf16* const smem = dyn_smem();
-  // [K tile 0][K tile 1][V tile 0][V tile 1], all row-major
-  auto sK = [&](int b) { return smem + b * (64 * RSK); };
-  auto sV = [&](int b) { return smem + 2 * 64 * RSK + b * (64 * RSV); };
+  // [K tile 0][K tile 1][V tile 0][V tile 1], swizzled
+  auto tileK = [&](int b) { return smem + b * GT::ELEMS; };
+  auto tileV = [&](int b) { return smem + 2 * GT::ELEMS + b * GT::ELEMS; };
 
   const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63, i = l & 31, g = l >> 5;
   QTile<SPARSE> qt;
@@ -190,39 +194,37 @@ __global__ __launch_bounds__(256) LOGO_OCC_FWD void sq_fwd_kernel(const AttnArgs
   float m_run = -INFINITY, l_run = 0.f;
   const float c = a.scale_log2;
 
+  TileReader<D, kSwz> rd;  // K read along rows, V transposed
+  rd.init();
   const int64_t rstride = (int64_t)a.h * D;
   const bf16* kbase = a.k + ((int64_t)qt.bos * a.h + qt.h) * D;
   const bf16* vbase = a.v + ((int64_t)qt.bos * a.h + qt.h) * D;
   const int seqlen = qt.seqlen;
-  TK kt;
-  TV vt;
-  auto load_tile = [&](int j0) {
-    kt.load(tid, [&](int rr) -> const bf16* { return j0 + rr < seqlen ? kbase + (j0 + rr) * rstride : nullptr; });
-    vt.load(tid, [&](int rr) -> const bf16* { return j0 + rr < seqlen ? vbase + (j0 + rr) * rstride : nullptr; });
+  // rows past the sequence end are clamped to its last key: the causal mask
+  // hides every key > p, and p < seqlen
+  auto load_tile = [&](int j0, int b) {
+    TileDma<D>::issue(tileK(b), [&](int rr) -> const bf16* { return kbase + min(j0 + rr, seqlen - 1) * rstride; });
+    TileDma<D>::issue(tileV(b), [&](int rr) -> const bf16* { return vbase + min(j0 + rr, seqlen - 1) * rstride; });
   };
 
-  load_tile(qt.kv_lo);
-  kt.store(sK(0), tid);
-  vt.store(sV(0), tid);
-  __syncthreads();
-  int buf = 0;
-  for (int j0 = qt.kv_lo; j0 < qt.kv_hi; j0 += 64) {
+  // One 64-key tile on LDS buffer B while the next one streams into B ^ 1.
+  auto step = [&](auto buf_tag, int j0) {
+    constexpr int B = decltype(buf_tag)::value;
     const bool has_next = j0 + 64 < qt.kv_hi;
-    if (has_next) load_tile(j0 + 64);
-
-    const bool skip = !qt.wave_active || j0 > qt.pmax || (WINDOW && j0 + 63 < qt.pmin - W);
-    if (!skip) {
-      const bool need_mask = (j0 + 63 > qt.pmin) || (WINDOW && j0 < qt.pmax - W);
-      const bf16* kb = sK(buf);
-      const bf16* vb = sV(buf);
+    if (has_next) load_tile(j0 + 64, B ^ 1);
+    const bf16* kb = tileK(B);
+    const bf16* vb = tileV(B);
+    // one instantiation per masking mode: fully visible tiles carry no mask work
+    auto compute = [&](auto mask_tag) {
+      constexpr bool MASK = decltype(mask_tag)::value;
       f32x16 sacc[2];
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
         sacc[kk] = f32x16{};
 #pragma unroll
-        for (int ds = 0; ds < DS; ++ds) sacc[kk] = mfma32(read_row_op<RSK>(kb, 32 * kk + i, ds, g), qreg[ds], sacc[kk]);
+        for (int ds = 0; ds < DS; ++ds) sacc[kk] = mfma32(rd.row(kb, 32 * kk, ds), qreg[ds], sacc[kk]);
       }
-      if (need_mask) {
+      if constexpr (MASK) {
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
@@ -263,14 +265,24 @@ __global__ __launch_bounds__(256) LOGO_OCC_FWD void sq_fwd_kernel(const AttnArgs
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) oacc[dt] = mfma32(read_tr_op<RSV>(vb, 16 * ks, 32 * dt), pb[ks], oacc[dt]);
+        for (int ks = 0; ks < 4; ++ks) oacc[dt] = mfma32(rd.tr(vb, 16 * ks, dt), pb[ks], oacc[dt]);
+    };
+    const bool skip = !qt.wave_active || j0 > qt.pmax || (WINDOW && j0 + 63 < qt.pmin - W);
+    if (!skip) {
+      const bool need_mask = (j0 + 63 > qt.pmin) || (WINDOW && j0 < qt.pmax - W);
+      if (need_mask) compute(std::true_type{});
+      else compute(std::false_type{});
     }
-    if (has_next) {
-      kt.store(sK(buf ^ 1), tid);
-      vt.store(sV(buf ^ 1), tid);
-    }
+    wait_vmem();
     __syncthreads();
-    buf ^= 1;
+  };
+
+  load_tile(qt.kv_lo, 0);
+  wait_vmem();
+  __syncthreads();
+  for (int j0 = qt.kv_lo; j0 < qt.kv_hi; j0 += 128) {
+    step(BufTag<0>{}, j0);
+    if (j0 + 64 < qt.kv_hi) step(BufTag<1>{}, j0 + 64);
   }
 
   const float l_tot = l_run + __shfl_xor(l_run, 32);
@@ -328,12 +340,11 @@ __global__ __launch_bounds__(256) void sq_delta_kernel(const AttnArgs a) {
 // ---------------------------------------------------------------------------
 template <int D, bool SPARSE, bool WINDOW>
 __global__ __launch_bounds__(256) LOGO_OCC_DQ void sq_dq_kernel(const AttnArgs a) {
-  constexpr int RSK = kTrStride<D>, RSV = kRowStride<D>, DS = D / 16, DT = D / 32;
-  using TK = Tile64<D, RSK>;
-  using TV = Tile64<D, RSV>;
+  constexpr int DS = D / 16, DT = D / 32;
+  using GT = TileGeom<D, kSwz>;  // K read along rows (S) and transposed (dQ); V along rows
   bf16* const smem = dyn_smem();
-  auto sK = [&](int b) { return smem + b * (64 * RSK); };
-  auto sV = [&](int b) { return smem + 2 * 64 * RSK + b * (64 * RSV); };
+  auto tileK = [&](int b) { return smem + b * GT::ELEMS; };
+  auto tileV = [&](int b) { return smem + 2 * GT::ELEMS + b * GT::ELEMS; };
 
   const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63, i = l & 31, g = l >> 5;
   QTile<SPARSE> qt;
@@ -359,44 +370,49 @@ __global__ __launch_bounds__(256) LOGO_OCC_DQ void sq_dq_kernel(const AttnArgs a
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) dqacc[dt] = f32x16{};
 
+  TileReader<D, kSwz> rd;
+  rd.init();
   const int64_t rstride = (int64_t)a.h * D;
   const bf16* kbase = a.k + ((int64_t)qt.bos * a.h + qt.h) * D;
   const bf16* vbase = a.v + ((int64_t)qt.bos * a.h + qt.h) * D;
   const int seqlen = qt.seqlen;
-  TK kt;
-  TV vt;
-  auto load_tile = [&](int j0) {
-    kt.load(tid, [&](int rr) -> const bf16* { return j0 + rr < seqlen ? kbase + (j0 + rr) * rstride : nullptr; });
-    vt.load(tid, [&](int rr) -> const bf16* { return j0 + rr < seqlen ? vbase + (j0 + rr) * rstride : nullptr; });
+  auto load_tile = [&](int j0, int b) {
+    TileDma<D>::issue(tileK(b), [&](int rr) -> const bf16* { return kbase + min(j0 + rr, seqlen - 1) * rstride; });
+    TileDma<D>::issue(tileV(b), [&](int rr) -> const bf16* { return vbase + min(j0 + rr, seqlen - 1) * rstride; });
   };
 
-  load_tile(qt.kv_lo);
-  kt.store(sK(0), tid);
-  vt.store(sV(0), tid);
-  __syncthreads();
-  int buf = 0;
-  for (int j0 = qt.kv_lo; j0 < qt.kv_hi; j0 += 64) {
+  auto step = [&](auto buf_tag, int j0) {
+    constexpr int B = decltype(buf_tag)::value;
     const bool has_next = j0 + 64 < qt.kv_hi;
-    if (has_next) load_tile(j0 + 64);
-
-    const bool skip = !qt.wave_active || j0 > qt.pmax || (WINDOW && j0 + 63 < qt.pmin - W);
-    if (!skip) {
-      const bool need_mask = (j0 + 63 > qt.pmin) || (WINDOW && j0 < qt.pmax - W);
-      const bf16* kb = sK(buf);
-      const bf16* vb = sV(buf);
+    if (has_next) load_tile(j0 + 64, B ^ 1);
+    const bf16* kb = tileK(B);
+    const bf16* vb = tileV(B);
+    auto compute = [&](auto mask_tag) {
+      constexpr bool MASK = decltype(mask_tag)::value;
       // Two 32-key halves in turn keep only one S / dP accumulator pair live.
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
         f32x16 sacc{}, pacc{};
+        // operands fetched one step ahead; the fences keep the compiler from
+        // hoisting every LDS read of the tile (which overflows 256 VGPRs)
+        bf16x8 ka = rd.row(kb, 32 * kk, 0), va = rd.row(vb, 32 * kk, 0);
 #pragma unroll
         for (int ds = 0; ds < DS; ++ds) {
-          sacc = mfma32(read_row_op<RSK>(kb, 32 * kk + i, ds, g), qreg[ds], sacc);
-          pacc = mfma32(read_row_op<RSV>(vb, 32 * kk + i, ds, g), doreg[ds], pacc);
+          bf16x8 kn = ka, vn = va;
+          if (ds + 1 < DS) {
+            kn = rd.row(kb, 32 * kk, ds + 1);
+            vn = rd.row(vb, 32 * kk, ds + 1);
+          }
+          sacc = mfma32(ka, qreg[ds], sacc);
+          pacc = mfma32(va, doreg[ds], pacc);
+          ka = kn;
+          va = vn;
+          __builtin_amdgcn_sched_barrier(0);
         }
 #pragma unroll
         for (int jj = 0; jj < 16; ++jj) {
           float pv = fast_exp2(fmaf(sacc[jj], c, -lse_q));
-          if (need_mask) {
+          if constexpr (MASK) {
             const int key = j0 + 32 * kk + rowmap(g, jj);
             bool vis = key <= p;
             if (WINDOW) vis = vis && key >= p - W;
@@ -407,18 +423,34 @@ __global__ __launch_bounds__(256) LOGO_OCC_DQ void sq_dq_kernel(const AttnArgs a
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
           const bf16x8 db = acc_to_bf16(sacc, hh);
+          bf16x8 kt = rd.tr(kb, 16 * (2 * kk + hh), 0);
 #pragma unroll
-          for (int dt = 0; dt < DT; ++dt)
-            dqacc[dt] = mfma32(read_tr_op<RSK>(kb, 16 * (2 * kk + hh), 32 * dt), db, dqacc[dt]);
+          for (int dt = 0; dt < DT; ++dt) {
+            bf16x8 kn = kt;
+            if (dt + 1 < DT) kn = rd.tr(kb, 16 * (2 * kk + hh), dt + 1);
+            dqacc[dt] = mfma32(kt, db, dqacc[dt]);
+            kt = kn;
+            __builtin_amdgcn_sched_barrier(0);
+          }
         }
       }
+    };
+    const bool skip = !qt.wave_active || j0 > qt.pmax || (WINDOW && j0 + 63 < qt.pmin - W);
+    if (!skip) {
+      const bool need_mask = (j0 + 63 > qt.pmin) || (WINDOW && j0 < qt.pmax - W);
+      if (need_mask) compute(std::true_type{});
+      else compute(std::false_type{});
     }
-    if (has_next) {
-      kt.store(sK(buf ^ 1), tid);
-      vt.store(sV(buf ^ 1), tid);
-    }
+    wait_vmem();
     __syncthreads();
-    buf ^= 1;
+  };
+
+  load_tile(qt.kv_lo, 0);
+  wait_vmem();
+  __syncthreads();
+  for (int j0 = qt.kv_lo; j0 < qt.kv_hi; j0 += 128) {
+    step(BufTag<0>{}, j0);
+    if (j0 + 64 < qt.kv_hi) step(BufTag<1>{}, j0 + 64);
   }
 
   if (qt.valid) {
@@ -439,17 +471,17 @@ __global__ __launch_bounds__(256) LOGO_OCC_DQ void sq_dq_kernel(const AttnArgs a
 // Backward dk / dv
 // ---------------------------------------------------------------------------
 template <int D>
-constexpr int dkv_stage_bytes() { return 2 * 64 * kTrStride<D> * 2 + 3 * 64 * 4; }
+constexpr int dkv_stage_bytes() { return 2 * TileGeom<D, kSwz>::ELEMS * 2 + 3 * 64 * 4; }
 
 template <int D, bool SPARSE, bool WINDOW>
 __global__ __launch_bounds__(256) LOGO_OCC_DKV void sq_dkv_kernel(const AttnArgs a) {
-  constexpr int RS = kTrStride<D>, DS = D / 16, DT = D / 32;
-  using TQ = Tile64<D, RS>;
+  constexpr int DS = D / 16, DT = D / 32;
+  using GQ = TileGeom<D, kSwz>;  // Q and dO read along rows (S, dP) and transposed (dK, dV)
   char* const smem_b = logo_smem;
   // stage b: [Q tile][dO tile][lse 64][delta 64][pos 64]
   auto sQ = [&](int b) { return reinterpret_cast<bf16*>(smem_b + b * dkv_stage_bytes<D>()); };
-  auto sO = [&](int b) { return sQ(b) + 64 * RS; };
-  auto sLse = [&](int b) { return reinterpret_cast<float*>(sQ(b) + 2 * 64 * RS); };
+  auto sO = [&](int b) { return sQ(b) + GQ::ELEMS; };
+  auto sLse = [&](int b) { return reinterpret_cast<float*>(sQ(b) + 2 * GQ::ELEMS); };
   auto sDelta = [&](int b) { return sLse(b) + 64; };
   auto sPos = [&](int b) { return reinterpret_cast<int*>(sLse(b) + 128); };
 
@@ -491,7 +523,8 @@ __global__ __launch_bounds__(256) LOGO_OCC_DKV void sq_dkv_kernel(const AttnArgs
     dvacc[dt] = f32x16{};
   }
 
-  TQ qtile, otile;
+  TileReader<D, kSwz> rd;
+  rd.init();
   float lse_n = 0.f, delta_n = 0.f;
   int pos_n = -1;
   for (int gg = 0; gg < a.g; ++gg) {
@@ -511,20 +544,20 @@ __global__ __launch_bounds__(256) LOGO_OCC_DKV void sq_dkv_kernel(const AttnArgs
     }
     const float* lse_h = a.lse + (int64_t)hq * a.n;
     const float* delta_h = a.delta + (int64_t)hq * a.n;
-    auto load_tile = [&](int rt) {
-      qtile.load(tid, [&](int rr) -> const bf16* { return rt + rr < rq_end ? qs.row(rt + rr) : nullptr; });
-      otile.load(tid, [&](int rr) -> const bf16* { return rt + rr < rq_end ? os.row(rt + rr) : nullptr; });
+    auto load_tile = [&](int rt, int b) {
+      // rows past rq_end are clamped to a real row and masked (pos = -1)
+      TileDma<D>::issue(sQ(b), [&](int rr) -> const bf16* { return qs.row(min(rt + rr, rq_end - 1)); });
+      TileDma<D>::issue(sO(b), [&](int rr) -> const bf16* { return os.row(min(rt + rr, rq_end - 1)); });
       if (tid < 64) {
         const int rr = rt + tid;
         const bool ok = rr < rq_end;
-        lse_n = ok ? lse_h[rr] : 0.f;
-        delta_n = ok ? delta_h[rr] : 0.f;
+        const int rc = min(rr, rq_end - 1);
+        lse_n = lse_h[rc];
+        delta_n = delta_h[rc];
         pos_n = ok ? rv.posn(rr) : -1;
       }
     };
-    auto store_tile = [&](int b) {
-      qtile.store(sQ(b), tid);
-      otile.store(sO(b), tid);
+    auto store_stats = [&](int b) {
       if (tid < 64) {
         sLse(b)[tid] = lse_n;
         sDelta(b)[tid] = delta_n;
@@ -532,48 +565,51 @@ __global__ __launch_bounds__(256) LOGO_OCC_DKV void sq_dkv_kernel(const AttnArgs
       }
     };
 
-    if (rq0 < rq_end) {
-      load_tile(rq0);
-      store_tile(0);
-    }
-    __syncthreads();
-    int buf = 0;
-    for (int rt = rq0; rt < rq_end; rt += 64) {
+    auto step = [&](auto buf_tag, int rt) {
+      constexpr int B = decltype(buf_tag)::value;
       const bool has_next = rt + 64 < rq_end;
-      if (has_next) load_tile(rt + 64);
-
-      const bf16* qb = sQ(buf);
-      const bf16* ob = sO(buf);
-      const float* lb = sLse(buf);
-      const float* dlb = sDelta(buf);
-      const int* pob = sPos(buf);
+      if (has_next) load_tile(rt + 64, B ^ 1);
+      const bf16* qb = sQ(B);
+      const bf16* ob = sO(B);
+      const float* lb = sLse(B);
+      const float* dlb = sDelta(B);
+      const int* pob = sPos(B);
       const int last = min(rt + 63, rq_end - 1);
       const int p_first = pob[0];
       const int p_last = pob[last - rt];
-      const bool skip = !wave_active || p_last < kw0 || (WINDOW && p_first > kw_last + W);
-      if (!skip) {
-        const bool need_mask = WINDOW || (p_first < kw_last) || (rt + 64 > rq_end);
+      auto compute = [&](auto mask_tag) {
+        constexpr bool MASK = decltype(mask_tag)::value;
         // Two 32-row halves of the query tile in turn keep one S / dP pair live.
 #pragma unroll
         for (int qq = 0; qq < 2; ++qq) {
           f32x16 sacc{}, pacc{};
 #pragma unroll
           for (int ds = 0; ds < DS; ++ds) {
-            sacc = mfma32(read_row_op<RS>(qb, 32 * qq + i, ds, g), kreg[ds], sacc);
-            pacc = mfma32(read_row_op<RS>(ob, 32 * qq + i, ds, g), vreg[ds], pacc);
+            sacc = mfma32(rd.row(qb, 32 * qq, ds), kreg[ds], sacc);
+            pacc = mfma32(rd.row(ob, 32 * qq, ds), vreg[ds], pacc);
           }
+          // items 4m..4m+3 of this lane are the 4 consecutive query rows
+          // 32qq + 8m + 4g + (0..3): one 16-byte LDS read per statistic
 #pragma unroll
-          for (int jj = 0; jj < 16; ++jj) {
-            const int qr = 32 * qq + rowmap(g, jj);
-            float pv = fast_exp2(fmaf(sacc[jj], c, -lb[qr]));
-            if (need_mask) {
-              const int pq = pob[qr];
-              bool vis = key <= pq;
-              if (WINDOW) vis = vis && key >= pq - W;
-              if (!vis) pv = 0.f;
+          for (int m = 0; m < 4; ++m) {
+            const int qr = 32 * qq + 8 * m + 4 * g;
+            const f32x4 l4 = *reinterpret_cast<const f32x4*>(lb + qr);
+            const f32x4 d4 = *reinterpret_cast<const f32x4*>(dlb + qr);
+            int4 p4 = make_int4(0, 0, 0, 0);
+            if constexpr (MASK) p4 = *reinterpret_cast<const int4*>(pob + qr);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int jj = 4 * m + e;
+              float pv = fast_exp2(fmaf(sacc[jj], c, -l4[e]));
+              if constexpr (MASK) {
+                const int pq = e == 0 ? p4.x : e == 1 ? p4.y : e == 2 ? p4.z : p4.w;
+                bool vis = key <= pq;
+                if (WINDOW) vis = vis && key >= pq - W;
+                if (!vis) pv = 0.f;
+              }
+              sacc[jj] = pv;
+              pacc[jj] = pv * (pacc[jj] - d4[e]);
             }
-            sacc[jj] = pv;
-            pacc[jj] = pv * (pacc[jj] - dlb[qr]);
           }
 #pragma unroll
           for (int hh = 0; hh < 2; ++hh) {
@@ -582,15 +618,32 @@ __global__ __launch_bounds__(256) LOGO_OCC_DKV void sq_dkv_kernel(const AttnArgs
             const bf16x8 dbf = acc_to_bf16(pacc, hh);
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) {
-              dvacc[dt] = mfma32(read_tr_op<RS>(ob, 16 * ks, 32 * dt), pbf, dvacc[dt]);
-              dkacc[dt] = mfma32(read_tr_op<RS>(qb, 16 * ks, 32 * dt), dbf, dkacc[dt]);
+              dvacc[dt] = mfma32(rd.tr(ob, 16 * ks, dt), pbf, dvacc[dt]);
+              dkacc[dt] = mfma32(rd.tr(qb, 16 * ks, dt), dbf, dkacc[dt]);
             }
           }
         }
+      };
+      const bool skip = !wave_active || p_last < kw0 || (WINDOW && p_first > kw_last + W);
+      if (!skip) {
+        const bool need_mask = WINDOW || (p_first < kw_last) || (rt + 64 > rq_end);
+        if (need_mask) compute(std::true_type{});
+        else compute(std::false_type{});
       }
-      if (has_next) store_tile(buf ^ 1);
+      if (has_next) store_stats(B ^ 1);
+      wait_vmem();
       __syncthreads();
-      buf ^= 1;
+    };
+
+    if (rq0 < rq_end) {
+      load_tile(rq0, 0);
+      store_stats(0);
+    }
+    wait_vmem();
+    __syncthreads();
+    for (int rt = rq0; rt < rq_end; rt += 128) {
+      step(BufTag<0>{}, rt);
+      if (rt + 64 < rq_end) step(BufTag<1>{}, rt + 64);
     }
   }
 
@@ -616,9 +669,9 @@ __global__ __launch_bounds__(256) LOGO_OCC_DKV void sq_dkv_kernel(const AttnArgs
 // Host launchers
 // ---------------------------------------------------------------------------
 template <int D>
-constexpr size_t fwd_smem() { return (size_t)(2 * 64 * kRowStride<D> + 2 * 64 * kTrStride<D>) * sizeof(bf16); }
+constexpr size_t fwd_smem() { return (size_t)4 * TileGeom<D, kSwz>::ELEMS * sizeof(bf16); }
 template <int D>
-constexpr size_t dq_smem() { return (size_t)(2 * 64 * kTrStride<D> + 2 * 64 * kRowStride<D>) * sizeof(bf16); }
+constexpr size_t dq_smem() { return (size_t)4 * TileGeom<D, kSwz>::ELEMS * sizeof(bf16); }
 template <int D>
 constexpr size_t dkv_smem() { return (size_t)2 * dkv_stage_bytes<D>(); }
 
