@@ -24,6 +24,8 @@ COMMON_FLAGS = [
     "-fPIC",
     f"--offload-arch={ARCH}",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA results the VALU reads (S, dP) stay in VGPRs instead of AGPRs
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
     "-Wno-unused-result",
 ]
 

@@ -577,19 +577,54 @@ __global__ __launch_bounds__(256) LOGO_OCC_DKV void sq_dkv_kernel(const AttnArgs
       const int last = min(rt + 63, rq_end - 1);
       const int p_first = pob[0];
       const int p_last = pob[last - rt];
+      // Software-pipelined over the two 32-row halves of the tile, one wave per
+      // SIMD: S/dP MFMAs of half 1 run while the softmax / dS arithmetic of
+      // half 0 executes on the VALU, and the dV/dK MFMAs of half 0 while half
+      // 1's arithmetic runs; every phase's LDS operands are fetched one phase
+      // ahead.  sched_group_barrier fixes the MFMA / VALU / LDS interleave.
       auto compute = [&](auto mask_tag) {
         constexpr bool MASK = decltype(mask_tag)::value;
-        // Two 32-row halves of the query tile in turn keep one S / dP pair live.
-#pragma unroll
-        for (int qq = 0; qq < 2; ++qq) {
-          f32x16 sacc{}, pacc{};
+        bf16x8 opA[2][2][DS];      // [half][Q rows | dO rows][ds]
+        bf16x8 opC[2][2][2][DT];   // [half][dO^T | Q^T][hh][dt]
+        f32x16 sacc[2], pacc[2];
+        bf16x8 pbf[2][2], dbf[2][2];  // [half][hh]
+        auto loadA = [&](int qq) {
 #pragma unroll
           for (int ds = 0; ds < DS; ++ds) {
-            sacc = mfma32(rd.row(qb, 32 * qq, ds), kreg[ds], sacc);
-            pacc = mfma32(rd.row(ob, 32 * qq, ds), vreg[ds], pacc);
+            opA[qq][0][ds] = rd.row(qb, 32 * qq, ds);
+            opA[qq][1][ds] = rd.row(ob, 32 * qq, ds);
           }
-          // items 4m..4m+3 of this lane are the 4 consecutive query rows
-          // 32qq + 8m + 4g + (0..3): one 16-byte LDS read per statistic
+        };
+        auto mfmaA = [&](int qq) {
+          sacc[qq] = f32x16{};
+          pacc[qq] = f32x16{};
+#pragma unroll
+          for (int ds = 0; ds < DS; ++ds) {
+            sacc[qq] = mfma32(opA[qq][0][ds], kreg[ds], sacc[qq]);
+            pacc[qq] = mfma32(opA[qq][1][ds], vreg[ds], pacc[qq]);
+          }
+        };
+        auto loadC = [&](int qq) {
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+              opC[qq][0][hh][dt] = rd.tr(ob, 16 * (2 * qq + hh), dt);
+              opC[qq][1][hh][dt] = rd.tr(qb, 16 * (2 * qq + hh), dt);
+            }
+        };
+        auto mfmaC = [&](int qq) {
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+              dvacc[dt] = mfma32(opC[qq][0][hh][dt], pbf[qq][hh], dvacc[dt]);
+              dkacc[dt] = mfma32(opC[qq][1][hh][dt], dbf[qq][hh], dkacc[dt]);
+            }
+        };
+        // P = exp2(S*c - lse), dS = P * (dP - delta); items 4m..4m+3 of this
+        // lane are the consecutive query rows 32qq + 8m + 4g + (0..3)
+        auto softmax = [&](int qq) {
 #pragma unroll
           for (int m = 0; m < 4; ++m) {
             const int qr = 32 * qq + 8 * m + 4 * g;
@@ -600,29 +635,55 @@ __global__ __launch_bounds__(256) LOGO_OCC_DKV void sq_dkv_kernel(const AttnArgs
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
               const int jj = 4 * m + e;
-              float pv = fast_exp2(fmaf(sacc[jj], c, -l4[e]));
+              float pv = fast_exp2(fmaf(sacc[qq][jj], c, -l4[e]));
               if constexpr (MASK) {
                 const int pq = e == 0 ? p4.x : e == 1 ? p4.y : e == 2 ? p4.z : p4.w;
                 bool vis = key <= pq;
                 if (WINDOW) vis = vis && key >= pq - W;
                 if (!vis) pv = 0.f;
               }
-              sacc[jj] = pv;
-              pacc[jj] = pv * (pacc[jj] - d4[e]);
+              sacc[qq][jj] = pv;
+              pacc[qq][jj] = pv * (pacc[qq][jj] - d4[e]);
             }
           }
 #pragma unroll
           for (int hh = 0; hh < 2; ++hh) {
-            const int ks = 2 * qq + hh;
-            const bf16x8 pbf = acc_to_bf16(sacc, hh);
-            const bf16x8 dbf = acc_to_bf16(pacc, hh);
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt) {
-              dvacc[dt] = mfma32(rd.tr(ob, 16 * ks, dt), pbf, dvacc[dt]);
-              dkacc[dt] = mfma32(rd.tr(qb, 16 * ks, dt), dbf, dkacc[dt]);
-            }
+            pbf[qq][hh] = acc_to_bf16(sacc[qq], hh);
+            dbf[qq][hh] = acc_to_bf16(pacc[qq], hh);
           }
+        };
+        constexpr int kV = MASK ? 8 : 6;  // VALU per MFMA slot in the overlapped phases
+        loadA(0);
+        __builtin_amdgcn_sched_barrier(0);
+        loadA(1);
+        mfmaA(0);
+#pragma unroll
+        for (int k = 0; k < 2 * DS; ++k) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
         }
+        __builtin_amdgcn_sched_barrier(0);
+        loadC(0);
+        mfmaA(1);
+        softmax(0);
+#pragma unroll
+        for (int k = 0; k < 2 * DS; ++k) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);  // MFMA
+          __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);  // DS read
+          __builtin_amdgcn_sched_group_barrier(0x002, kV, 1); // VALU
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        loadC(1);
+        mfmaC(0);
+        softmax(1);
+#pragma unroll
+        for (int k = 0; k < 4 * DT; ++k) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 2);  // MFMA
+          __builtin_amdgcn_sched_group_barrier(0x100, 2, 2);  // DS read
+          __builtin_amdgcn_sched_group_barrier(0x002, kV, 2); // VALU
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        mfmaC(1);
       };
       const bool skip = !wave_active || p_last < kw0 || (WINDOW && p_first > kw_last + W);
       if (!skip) {
