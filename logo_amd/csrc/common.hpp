@@ -135,6 +135,21 @@ struct TileDma {
                                        (__attribute__((address_space(3))) void*)(tile + rb * D), 16, 0, 0);
     }
   }
+
+  // Rows evenly strided from a wave-uniform base; tile rows past last_row
+  // are clamped to it.  The address is the uniform base plus a 32-bit lane
+  // offset (the 64 rows of a tile span far less than 2^31 elements).
+  __device__ __forceinline__ static void issue_strided(bf16* tile, const bf16* base, int row_stride, int last_row) {
+    const int wave = threadIdx.x >> 6, j = threadIdx.x & 63;
+#pragma unroll
+    for (int b = 0; b < BLOCKS; ++b) {
+      const int rb = 16 * wave + RPB * b;
+      const int row = rb + j / CH;
+      const int ch = (j % CH) ^ Geo::swz(row);
+      __builtin_amdgcn_global_load_lds(base + (min(row, last_row) * row_stride + 8 * ch),
+                                       (__attribute__((address_space(3))) void*)(tile + rb * D), 16, 0, 0);
+    }
+  }
 };
 
 // Wait for this wave's outstanding vector-memory operations (the tile copies

@@ -203,8 +203,8 @@ __global__ __launch_bounds__(256) LOGO_OCC_FWD void sq_fwd_kernel(const AttnArgs
   // rows past the sequence end are clamped to its last key: the causal mask
   // hides every key > p, and p < seqlen
   auto load_tile = [&](int j0, int b) {
-    TileDma<D>::issue(tileK(b), [&](int rr) -> const bf16* { return kbase + min(j0 + rr, seqlen - 1) * rstride; });
-    TileDma<D>::issue(tileV(b), [&](int rr) -> const bf16* { return vbase + min(j0 + rr, seqlen - 1) * rstride; });
+    TileDma<D>::issue_strided(tileK(b), kbase + j0 * rstride, (int)rstride, seqlen - 1 - j0);
+    TileDma<D>::issue_strided(tileV(b), vbase + j0 * rstride, (int)rstride, seqlen - 1 - j0);
   };
 
   // One 64-key tile on LDS buffer B while the next one streams into B ^ 1.
@@ -225,13 +225,17 @@ __global__ __launch_bounds__(256) LOGO_OCC_FWD void sq_fwd_kernel(const AttnArgs
         for (int ds = 0; ds < DS; ++ds) sacc[kk] = mfma32(rd.row(kb, 32 * kk, ds), qreg[ds], sacc[kk]);
       }
       if constexpr (MASK) {
+        // key j0 + 32kk + rowmap(g, jj) is visible iff its offset from
+        // j0 + 4g (a compile-time constant per item) lies in [lo, hi]
+        const int hi = p - j0 - 4 * g;
+        const int lo = hi - W;
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
           for (int jj = 0; jj < 16; ++jj) {
-            const int key = j0 + 32 * kk + rowmap(g, jj);
-            bool vis = key <= p;
-            if (WINDOW) vis = vis && key >= p - W;
+            const int off = 32 * kk + 8 * (jj / 4) + (jj % 4);
+            bool vis = off <= hi;
+            if (WINDOW) vis = vis && off >= lo;
             if (!vis) sacc[kk][jj] = -INFINITY;
           }
       }
@@ -241,7 +245,11 @@ __global__ __launch_bounds__(256) LOGO_OCC_FWD void sq_fwd_kernel(const AttnArgs
 #pragma unroll
         for (int jj = 0; jj < 16; ++jj) mx = fmaxf(mx, sacc[kk][jj]);
       mx = wave_pair_max(mx);
-      const float m_new = fmaxf(m_run, mx);
+      // Lazy rescale: the reference max only moves when some row's max grew
+      // by more than 2^8 in the exp2 domain (or on the first visible key);
+      // otherwise p <= 2^8, exact in fp32 and bf16, and O, l keep their scale.
+      const bool grow = (mx - m_run) * c > 8.f;
+      const float m_new = __ballot(grow) ? fmaxf(m_run, mx) : m_run;
       const float base = (m_new == -INFINITY) ? 0.f : m_new * c;
       const float alpha = fast_exp2(m_run * c - base);
       float psum = 0.f;
@@ -377,8 +385,8 @@ __global__ __launch_bounds__(256) LOGO_OCC_DQ void sq_dq_kernel(const AttnArgs a
   const bf16* vbase = a.v + ((int64_t)qt.bos * a.h + qt.h) * D;
   const int seqlen = qt.seqlen;
   auto load_tile = [&](int j0, int b) {
-    TileDma<D>::issue(tileK(b), [&](int rr) -> const bf16* { return kbase + min(j0 + rr, seqlen - 1) * rstride; });
-    TileDma<D>::issue(tileV(b), [&](int rr) -> const bf16* { return vbase + min(j0 + rr, seqlen - 1) * rstride; });
+    TileDma<D>::issue_strided(tileK(b), kbase + j0 * rstride, (int)rstride, seqlen - 1 - j0);
+    TileDma<D>::issue_strided(tileV(b), vbase + j0 * rstride, (int)rstride, seqlen - 1 - j0);
   };
 
   auto step = [&](auto buf_tag, int j0) {
@@ -413,9 +421,11 @@ __global__ __launch_bounds__(256) LOGO_OCC_DQ void sq_dq_kernel(const AttnArgs a
         for (int jj = 0; jj < 16; ++jj) {
           float pv = fast_exp2(fmaf(sacc[jj], c, -lse_q));
           if constexpr (MASK) {
-            const int key = j0 + 32 * kk + rowmap(g, jj);
-            bool vis = key <= p;
-            if (WINDOW) vis = vis && key >= p - W;
+            // key j0 + 32kk + rowmap(g, jj) against the lane's [p - W, p]
+            const int off = 8 * (jj / 4) + (jj % 4);
+            const int hi = p - j0 - 32 * kk - 4 * g;
+            bool vis = off <= hi;
+            if (WINDOW) vis = vis && off >= hi - W;
             if (!vis) pv = 0.f;
           }
           sacc[jj] = pv * (pacc[jj] - delta_q);
@@ -546,8 +556,8 @@ __global__ __launch_bounds__(256) LOGO_OCC_DKV void sq_dkv_kernel(const AttnArgs
     const float* delta_h = a.delta + (int64_t)hq * a.n;
     auto load_tile = [&](int rt, int b) {
       // rows past rq_end are clamped to a real row and masked (pos = -1)
-      TileDma<D>::issue(sQ(b), [&](int rr) -> const bf16* { return qs.row(min(rt + rr, rq_end - 1)); });
-      TileDma<D>::issue(sO(b), [&](int rr) -> const bf16* { return os.row(min(rt + rr, rq_end - 1)); });
+      TileDma<D>::issue_strided(sQ(b), qs.row(rt), (int)qs.stride, rq_end - 1 - rt);
+      TileDma<D>::issue_strided(sO(b), os.row(rt), (int)os.stride, rq_end - 1 - rt);
       if (tid < 64) {
         const int rr = rt + tid;
         const bool ok = rr < rq_end;
