@@ -37,6 +37,26 @@ KERNEL_FLOPS_PER_PAIR_D = {
 }
 
 
+TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
+
+
+def measured_traffic(kernel, T, H, D, ratio, seed):
+    """HBM bytes per launch of ``kernel`` from the committed rocprofv3 counter
+    runs (FETCH_SIZE and WRITE_SIZE in KiB per dispatch, each scaled by what the
+    same counter reads for a 1 GiB copy), or None when this workload has not
+    been profiled."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            rec = json.load(f)
+    except (OSError, ValueError):
+        return None
+    wl = f"T{T}_H{H}_D{D}_r{ratio}_seed{seed}"
+    ent = rec.get("kernels", {}).get(kernel)
+    if rec.get("workload") != wl or ent is None:
+        return None
+    return ent["bytes_per_launch"]
+
+
 def parse():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -50,6 +70,9 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seed", type=int, default=2)
     ap.add_argument("--no-extra", action="store_true", help="skip the secondary measurements")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run one 1 GiB device-to-device copy before the workload (the reference kernel "
+                         "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters to bytes)")
     return ap.parse_args()
 
 
@@ -277,6 +300,14 @@ def main():
         o = sq_full_attn(qg, kg, vg, selg, cu_seqlens=cu)
         torch.autograd.grad(o, (qg, kg, vg), dog)
 
+    if args.copy_calibration:
+        src = torch.ones(1 << 29, dtype=torch.bfloat16, device=dev)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+
     timer = EventTimer()
     _lib.set_launch_hook(timer)
     for _ in range(args.warmup):
@@ -305,7 +336,7 @@ def main():
         "peak": MFMA_BF16_PEAK_TFLOPS,
         "unit": "TFLOP/s",
         "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4),
-        "traffic": None,
+        "traffic": measured_traffic(dom, T, H, D, args.ratio, args.seed),
         "flops_per_launch": dom_flops,
         "avg_launch_ms": round(kern_ms[dom], 4),
     }

@@ -14,6 +14,9 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+#include <utility>
+
 namespace logo {
 
 typedef __bf16 bf16;
@@ -28,6 +31,37 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 constexpr int kBQ = 128;   // compacted query rows per workgroup (fwd, dq)
 constexpr int kBKV = 128;  // keys per workgroup (dkv)
 constexpr int kMetaHdr = 8;
+
+// D += A * B (v_mfma_f32_32x32x16_bf16) with D held in AGPRs, for
+// accumulators that only MFMAs touch inside the loop (the other MFMAs of a
+// kernel built with VGPR-form results keep theirs in VGPRs).  The compiler
+// does not see inside the asm, so it supplies its own wait states: the
+// leading s_nop covers a VALU write of A, B or D just before it, and
+// agpr_acc_drain() must run before any other instruction reads D.
+__device__ __forceinline__ void mfma32_agpr(f32x16& d, const bf16x8& a, const bf16x8& b) {
+  asm volatile("s_nop 2\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(d) : "v"(a), "v"(b));
+}
+// Wait states between the last mfma32_agpr and a VALU read of its result
+// (an 8-pass MFMA needs fewer than 32).
+__device__ __forceinline__ void agpr_acc_drain() { asm volatile("s_nop 15\n\ts_nop 15"); }
+
+// Anchors a value at this point of the instruction stream (an empty asm
+// statement that reads and rewrites it): arithmetic on it cannot be hoisted
+// above, nor its producer sunk below, this point.  Used with scheduling
+// fences to lay out MFMA / VALU / LDS slots explicitly.
+template <typename T>
+__device__ __forceinline__ void pin(T& x) { asm volatile("" : "+v"(x)); }
+
+// Calls f(std::integral_constant<int, I>{}) for I = 0 .. N-1 (compile-time
+// indices, so per-slot register arrays stay in registers).
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
 
 __device__ __forceinline__ int rowmap(int g, int j) { return 8 * (j >> 2) + 4 * g + (j & 3); }
 
@@ -158,6 +192,20 @@ __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0); }
 
 typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
 
+// LDS reads through a restrict pointer: inlining gives the read
+// alias-scope metadata, without which the compiler's wait-count insertion
+// treats it as possibly reading LDS that an in-flight global->LDS copy (the
+// next tile, into the other buffer) writes, and stalls it on that copy.
+// The kernels order those copies against reads with explicit waits and
+// barriers.
+template <typename T>
+__device__ __attribute__((always_inline)) inline T lds_load(const T* __restrict__ p) {
+  return *p;
+}
+__device__ __attribute__((always_inline)) inline bf16x4 ds_read_tr(const lds_bf16x4* __restrict__ p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4bf16(const_cast<lds_bf16x4*>(p));
+}
+
 // MFMA operand reads from a tile, with every lane-dependent part of the
 // address computed once (init) so that in the unrolled loops each read is a
 // lane register plus an immediate.
@@ -200,14 +248,14 @@ struct TileReader {
 
   __device__ __forceinline__ bf16x8 row(const bf16* tile, int rbase, int ks) const {
     const int o = SWZ ? rbase * Geo::RS + row_off[ks] : rbase * Geo::RS + 16 * ks + row_off[0];
-    return *reinterpret_cast<const bf16x8*>(tile + o);
+    return lds_load(reinterpret_cast<const bf16x8*>(tile + o));
   }
 
   __device__ __forceinline__ bf16x8 tr(const bf16* tile, int r0, int dt) const {
     const int o0 = SWZ ? r0 * Geo::RS + tr_off[2 * dt] : r0 * Geo::RS + 32 * dt + tr_off[0];
     const int o1 = SWZ ? r0 * Geo::RS + tr_off[2 * dt + 1] : o0 + 8 * Geo::RS;
-    const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(tile + o0));
-    const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(tile + o1));
+    const bf16x4 lo = ds_read_tr((const lds_bf16x4*)(tile + o0));
+    const bf16x4 hi = ds_read_tr((const lds_bf16x4*)(tile + o1));
     return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
   }
 };

@@ -480,20 +480,26 @@ __global__ __launch_bounds__(256) LOGO_OCC_DQ void sq_dq_kernel(const AttnArgs a
 // ---------------------------------------------------------------------------
 // Backward dk / dv
 // ---------------------------------------------------------------------------
+// Query rows staged per LDS buffer (64-row sub-tiles; 128 would halve the
+// barriers but needs a second set of LDS address registers past 64 KB).
+constexpr int kDkvRows = 64;
 template <int D>
-constexpr int dkv_stage_bytes() { return 2 * TileGeom<D, kSwz>::ELEMS * 2 + 3 * 64 * 4; }
+constexpr int dkv_stage_bytes() { return 2 * kDkvRows * D * 2 + 3 * kDkvRows * 4; }
 
 template <int D, bool SPARSE, bool WINDOW>
 __global__ __launch_bounds__(256) LOGO_OCC_DKV void sq_dkv_kernel(const AttnArgs a) {
   constexpr int DS = D / 16, DT = D / 32;
   using GQ = TileGeom<D, kSwz>;  // Q and dO read along rows (S, dP) and transposed (dK, dV)
   char* const smem_b = logo_smem;
-  // stage b: [Q tile][dO tile][lse 64][delta 64][pos 64]
+  constexpr int RS = kDkvRows, NSUB = RS / 64;
+  static_assert(GQ::ELEMS == 64 * D, "64-row swizzled tiles");
+  // stage b: [Q rows][dO rows][lse][delta][pos], RS rows each; Q and dO as
+  // NSUB consecutive 64-row swizzled tiles
   auto sQ = [&](int b) { return reinterpret_cast<bf16*>(smem_b + b * dkv_stage_bytes<D>()); };
-  auto sO = [&](int b) { return sQ(b) + GQ::ELEMS; };
-  auto sLse = [&](int b) { return reinterpret_cast<float*>(sQ(b) + 2 * GQ::ELEMS); };
-  auto sDelta = [&](int b) { return sLse(b) + 64; };
-  auto sPos = [&](int b) { return reinterpret_cast<int*>(sLse(b) + 128); };
+  auto sO = [&](int b) { return sQ(b) + RS * D; };
+  auto sLse = [&](int b) { return reinterpret_cast<float*>(sQ(b) + 2 * RS * D); };
+  auto sDelta = [&](int b) { return sLse(b) + RS; };
+  auto sPos = [&](int b) { return reinterpret_cast<int*>(sLse(b) + 2 * RS); };
 
   int rank, h;
   xcd_remap(blockIdx.x, a.h, rank, h);
@@ -556,9 +562,14 @@ __global__ __launch_bounds__(256) LOGO_OCC_DKV void sq_dkv_kernel(const AttnArgs
     const float* delta_h = a.delta + (int64_t)hq * a.n;
     auto load_tile = [&](int rt, int b) {
       // rows past rq_end are clamped to a real row and masked (pos = -1)
-      TileDma<D>::issue_strided(sQ(b), qs.row(rt), (int)qs.stride, rq_end - 1 - rt);
-      TileDma<D>::issue_strided(sO(b), os.row(rt), (int)os.stride, rq_end - 1 - rt);
-      if (tid < 64) {
+      // (last_row may be negative for the second sub-tile: every row then
+      // reads row rq_end - 1)
+#pragma unroll
+      for (int u = 0; u < NSUB; ++u) {
+        TileDma<D>::issue_strided(sQ(b) + 64 * D * u, qs.row(rt + 64 * u), (int)qs.stride, rq_end - 1 - rt - 64 * u);
+        TileDma<D>::issue_strided(sO(b) + 64 * D * u, os.row(rt + 64 * u), (int)os.stride, rq_end - 1 - rt - 64 * u);
+      }
+      if (tid < RS) {
         const int rr = rt + tid;
         const bool ok = rr < rq_end;
         const int rc = min(rr, rq_end - 1);
@@ -568,7 +579,7 @@ __global__ __launch_bounds__(256) LOGO_OCC_DKV void sq_dkv_kernel(const AttnArgs
       }
     };
     auto store_stats = [&](int b) {
-      if (tid < 64) {
+      if (tid < RS) {
         sLse(b)[tid] = lse_n;
         sDelta(b)[tid] = delta_n;
         sPos(b)[tid] = pos_n;
@@ -577,127 +588,139 @@ __global__ __launch_bounds__(256) LOGO_OCC_DKV void sq_dkv_kernel(const AttnArgs
 
     auto step = [&](auto buf_tag, int rt) {
       constexpr int B = decltype(buf_tag)::value;
-      const bool has_next = rt + 64 < rq_end;
-      if (has_next) load_tile(rt + 64, B ^ 1);
+      const bool has_next = rt + RS < rq_end;
+      if (has_next) load_tile(rt + RS, B ^ 1);
       const bf16* qb = sQ(B);
       const bf16* ob = sO(B);
       const float* lb = sLse(B);
       const float* dlb = sDelta(B);
       const int* pob = sPos(B);
-      const int last = min(rt + 63, rq_end - 1);
+      const int last = min(rt + RS - 1, rq_end - 1);
       const int p_first = pob[0];
       const int p_last = pob[last - rt];
-      // Software-pipelined over the two 32-row halves of the tile, one wave per
-      // SIMD: S/dP MFMAs of half 1 run while the softmax / dS arithmetic of
-      // half 0 executes on the VALU, and the dV/dK MFMAs of half 0 while half
-      // 1's arithmetic runs; every phase's LDS operands are fetched one phase
-      // ahead.  sched_group_barrier fixes the MFMA / VALU / LDS interleave.
+      // Each 64-row sub-tile as two 32-row halves h0, h1 in four phases of NS
+      // MFMA slots (one wave per SIMD):
+      //   P0: S/dP MFMAs of h0
+      //   P1: S/dP MFMAs of h1  | P = exp2(S*c - lse), dS = P * (dP - delta) of h0
+      //   P2: dV/dK MFMAs of h0 | the same arithmetic for h1
+      //   P3: dV/dK MFMAs of h1
+      // A slot is one MFMA, one row's share of the arithmetic and the LDS reads
+      // of the operand used PF slots later (across sub-tiles too).  Scheduling
+      // fences between slots keep this order, so the VALU work issues under
+      // the MFMAs.
       auto compute = [&](auto mask_tag) {
         constexpr bool MASK = decltype(mask_tag)::value;
-        bf16x8 opA[2][2][DS];      // [half][Q rows | dO rows][ds]
-        bf16x8 opC[2][2][2][DT];   // [half][dO^T | Q^T][hh][dt]
+        constexpr int NS = 2 * DS;  // MFMAs per phase: S and dP over D / 16 k-steps
+        constexpr int SPT = 4 * NS; // slots per sub-tile
+        constexpr int PF = 6;       // operand prefetch distance, in slots
+        constexpr int IPS = 16 / NS;  // row items per slot
+        static_assert(IPS * NS == 16, "a half has 16 row items per lane");
         f32x16 sacc[2], pacc[2];
         bf16x8 pbf[2][2], dbf[2][2];  // [half][hh]
-        auto loadA = [&](int qq) {
-#pragma unroll
-          for (int ds = 0; ds < DS; ++ds) {
-            opA[qq][0][ds] = rd.row(qb, 32 * qq, ds);
-            opA[qq][1][ds] = rd.row(ob, 32 * qq, ds);
+        bf16x8 opA[NSUB * 2 * NS];    // S/dP operands: Q row (even) / dO row (odd)
+        bf16x8 opC[NSUB * 2 * NS];    // dV/dK operands: dO^T (even) / Q^T (odd)
+        f32x4 l4[NSUB][2][4], d4[NSUB][2][4];
+        int4 p4[NSUB][2][4];
+        // A operand a of sub-tile u: half a / NS, k-step (a % NS) / 2
+        auto load_a = [&](auto u_c, auto a_c) {
+          constexpr int U = decltype(u_c)::value, A = decltype(a_c)::value;
+          constexpr int QQ = A / NS, K = A % NS;
+          opA[U * 2 * NS + A] = rd.row(K % 2 ? ob : qb, 64 * U + 32 * QQ, K / 2);
+        };
+        // C operand c of sub-tile u: half c / NS, hh, dt
+        auto load_c = [&](auto u_c, auto c_c) {
+          constexpr int U = decltype(u_c)::value, C = decltype(c_c)::value;
+          constexpr int QQ = C / NS, K = C % NS, HH = K / (2 * DT), DTI = (K / 2) % DT;
+          opC[U * 2 * NS + C] = rd.tr(K % 2 ? qb : ob, 64 * U + 16 * (2 * QQ + HH), DTI);
+        };
+        // the operand first used at slot T
+        auto load_for_slot = [&](auto t_c) {
+          constexpr int T = decltype(t_c)::value, U = T / SPT, L = T % SPT;
+          if constexpr (L < 2 * NS) load_a(std::integral_constant<int, U>{}, std::integral_constant<int, L>{});
+          else load_c(std::integral_constant<int, U>{}, std::integral_constant<int, L - 2 * NS>{});
+        };
+        // lse / delta / positions of query rows 64u + 32qq + 8m + 4g + (0..3)
+        auto load_stats = [&](int u, int qq, int m) {
+          const int qr = 64 * u + 32 * qq + 8 * m + 4 * g;
+          l4[u][qq][m] = lds_load(reinterpret_cast<const f32x4*>(lb + qr));
+          d4[u][qq][m] = lds_load(reinterpret_cast<const f32x4*>(dlb + qr));
+          if constexpr (MASK) p4[u][qq][m] = lds_load(reinterpret_cast<const int4*>(pob + qr));
+        };
+        auto mfma_a = [&](auto u_c, auto a_c) {
+          constexpr int U = decltype(u_c)::value, A = decltype(a_c)::value;
+          constexpr int QQ = A / NS, K = A % NS;
+          bf16x8 op = opA[U * 2 * NS + A];
+          pin(op);
+          if constexpr (K % 2 == 0) {
+            sacc[QQ] = mfma32(op, kreg[K / 2], K == 0 ? f32x16{} : sacc[QQ]);
+          } else {
+            pacc[QQ] = mfma32(op, vreg[K / 2], K == 1 ? f32x16{} : pacc[QQ]);
           }
         };
-        auto mfmaA = [&](int qq) {
-          sacc[qq] = f32x16{};
-          pacc[qq] = f32x16{};
-#pragma unroll
-          for (int ds = 0; ds < DS; ++ds) {
-            sacc[qq] = mfma32(opA[qq][0][ds], kreg[ds], sacc[qq]);
-            pacc[qq] = mfma32(opA[qq][1][ds], vreg[ds], pacc[qq]);
+        auto mfma_c = [&](auto u_c, auto c_c) {
+          constexpr int U = decltype(u_c)::value, C = decltype(c_c)::value;
+          constexpr int QQ = C / NS, K = C % NS, HH = K / (2 * DT), DTI = (K / 2) % DT;
+          bf16x8 op = opC[U * 2 * NS + C];
+          pin(op);
+          if constexpr (K % 2 == 0) mfma32_agpr(dvacc[DTI], op, pbf[QQ][HH]);
+          else mfma32_agpr(dkacc[DTI], op, dbf[QQ][HH]);
+        };
+        // row item jj of half qq: items 4m..4m+3 are query rows 32qq + 8m + 4g + e
+        auto softmax_item = [&](auto u_c, int qq, auto jj_c) {
+          constexpr int U = decltype(u_c)::value, JJ = decltype(jj_c)::value;
+          constexpr int M = JJ / 4, E = JJ % 4;
+          float sv = sacc[qq][JJ], dpv = pacc[qq][JJ];
+          pin(sv);
+          pin(dpv);
+          float pv = fast_exp2(fmaf(sv, c, -l4[U][qq][M][E]));
+          if constexpr (MASK) {
+            const int pq = p4[U][qq][M][E];
+            bool vis = key <= pq;
+            if (WINDOW) vis = vis && key >= pq - W;
+            if (!vis) pv = 0.f;
+          }
+          float dsv = pv * (dpv - d4[U][qq][M][E]);
+          pin(pv);
+          pin(dsv);
+          if constexpr (JJ % 2 == 1) {
+            pbf[qq][JJ / 8][JJ % 8 - 1] = (bf16)sacc[qq][JJ - 1];
+            pbf[qq][JJ / 8][JJ % 8] = (bf16)pv;
+            dbf[qq][JJ / 8][JJ % 8 - 1] = (bf16)pacc[qq][JJ - 1];
+            dbf[qq][JJ / 8][JJ % 8] = (bf16)dsv;
+          } else {
+            sacc[qq][JJ] = pv;
+            pacc[qq][JJ] = dsv;
           }
         };
-        auto loadC = [&](int qq) {
+        // stats of (sub-tile u, half qq, group m) are read NS/2 slots before
+        // row item 4m
+        auto stats_slot = [](int u, int qq, int m) { return SPT * u + NS * (1 + qq) + 4 * m / IPS - NS / 2; };
+
+        static_for<PF>([&](auto t_c) { load_for_slot(t_c); });
+        static_for<NSUB * SPT>([&](auto s_c) {
+          constexpr int S = decltype(s_c)::value, U = S / SPT, L = S % SPT, PH = L / NS, K = L % NS;
+          using UC = std::integral_constant<int, U>;
+          __builtin_amdgcn_sched_barrier(0);
+          if constexpr (PH <= 1) mfma_a(UC{}, std::integral_constant<int, L>{});
+          else mfma_c(UC{}, std::integral_constant<int, L - 2 * NS>{});
+          if constexpr (S + PF < NSUB * SPT) load_for_slot(std::integral_constant<int, S + PF>{});
 #pragma unroll
-          for (int hh = 0; hh < 2; ++hh)
+          for (int u = 0; u < NSUB; ++u)
 #pragma unroll
-            for (int dt = 0; dt < DT; ++dt) {
-              opC[qq][0][hh][dt] = rd.tr(ob, 16 * (2 * qq + hh), dt);
-              opC[qq][1][hh][dt] = rd.tr(qb, 16 * (2 * qq + hh), dt);
-            }
-        };
-        auto mfmaC = [&](int qq) {
+            for (int qq = 0; qq < 2; ++qq)
 #pragma unroll
-          for (int hh = 0; hh < 2; ++hh)
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt) {
-              dvacc[dt] = mfma32(opC[qq][0][hh][dt], pbf[qq][hh], dvacc[dt]);
-              dkacc[dt] = mfma32(opC[qq][1][hh][dt], dbf[qq][hh], dkacc[dt]);
-            }
-        };
-        // P = exp2(S*c - lse), dS = P * (dP - delta); items 4m..4m+3 of this
-        // lane are the consecutive query rows 32qq + 8m + 4g + (0..3)
-        auto softmax = [&](int qq) {
-#pragma unroll
-          for (int m = 0; m < 4; ++m) {
-            const int qr = 32 * qq + 8 * m + 4 * g;
-            const f32x4 l4 = *reinterpret_cast<const f32x4*>(lb + qr);
-            const f32x4 d4 = *reinterpret_cast<const f32x4*>(dlb + qr);
-            int4 p4 = make_int4(0, 0, 0, 0);
-            if constexpr (MASK) p4 = *reinterpret_cast<const int4*>(pob + qr);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const int jj = 4 * m + e;
-              float pv = fast_exp2(fmaf(sacc[qq][jj], c, -l4[e]));
-              if constexpr (MASK) {
-                const int pq = e == 0 ? p4.x : e == 1 ? p4.y : e == 2 ? p4.z : p4.w;
-                bool vis = key <= pq;
-                if (WINDOW) vis = vis && key >= pq - W;
-                if (!vis) pv = 0.f;
-              }
-              sacc[qq][jj] = pv;
-              pacc[qq][jj] = pv * (pacc[qq][jj] - d4[e]);
-            }
-          }
-#pragma unroll
-          for (int hh = 0; hh < 2; ++hh) {
-            pbf[qq][hh] = acc_to_bf16(sacc[qq], hh);
-            dbf[qq][hh] = acc_to_bf16(pacc[qq], hh);
-          }
-        };
-        constexpr int kV = MASK ? 8 : 6;  // VALU per MFMA slot in the overlapped phases
-        loadA(0);
+              for (int m = 0; m < 4; ++m)
+                if (stats_slot(u, qq, m) == S) load_stats(u, qq, m);
+          if constexpr (PH == 1 || PH == 2)
+            static_for<IPS>([&](auto i_c) {
+              softmax_item(UC{}, PH - 1, std::integral_constant<int, K * IPS + decltype(i_c)::value>{});
+            });
+        });
         __builtin_amdgcn_sched_barrier(0);
-        loadA(1);
-        mfmaA(0);
-#pragma unroll
-        for (int k = 0; k < 2 * DS; ++k) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        loadC(0);
-        mfmaA(1);
-        softmax(0);
-#pragma unroll
-        for (int k = 0; k < 2 * DS; ++k) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);  // MFMA
-          __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);  // DS read
-          __builtin_amdgcn_sched_group_barrier(0x002, kV, 1); // VALU
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        loadC(1);
-        mfmaC(0);
-        softmax(1);
-#pragma unroll
-        for (int k = 0; k < 4 * DT; ++k) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 2);  // MFMA
-          __builtin_amdgcn_sched_group_barrier(0x100, 2, 2);  // DS read
-          __builtin_amdgcn_sched_group_barrier(0x002, kV, 2); // VALU
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        mfmaC(1);
       };
       const bool skip = !wave_active || p_last < kw0 || (WINDOW && p_first > kw_last + W);
       if (!skip) {
-        const bool need_mask = WINDOW || (p_first < kw_last) || (rt + 64 > rq_end);
+        const bool need_mask = WINDOW || (p_first < kw_last) || (rt + RS > rq_end);
         if (need_mask) compute(std::true_type{});
         else compute(std::false_type{});
       }
@@ -712,12 +735,13 @@ __global__ __launch_bounds__(256) LOGO_OCC_DKV void sq_dkv_kernel(const AttnArgs
     }
     wait_vmem();
     __syncthreads();
-    for (int rt = rq0; rt < rq_end; rt += 128) {
+    for (int rt = rq0; rt < rq_end; rt += 2 * RS) {
       step(BufTag<0>{}, rt);
-      if (rt + 64 < rq_end) step(BufTag<1>{}, rt + 64);
+      if (rt + RS < rq_end) step(BufTag<1>{}, rt + RS);
     }
   }
 
+  agpr_acc_drain();
   if (valid_k) {
     const int64_t off = ((int64_t)(bos + key) * a.h + h) * D;
 #pragma unroll
