@@ -45,6 +45,17 @@ __device__ __forceinline__ void mfma32_agpr(f32x16& d, const bf16x8& a, const bf
 // (an 8-pass MFMA needs fewer than 32).
 __device__ __forceinline__ void agpr_acc_drain() { asm volatile("s_nop 15\n\ts_nop 15"); }
 
+// Reductions over the lane pair (l, l ^ 32): v_permlane32_swap hands every
+// lane both values of its pair.
+__device__ __forceinline__ float pair_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // Anchors a value at this point of the instruction stream (an empty asm
 // statement that reads and rewrites it): arithmetic on it cannot be hoisted
 // above, nor its producer sunk below, this point.  Used with scheduling
@@ -147,14 +158,15 @@ struct Tile64 {
 // instructions).  Each such load writes 64 lanes x 16 bytes = 1 KB contiguous
 // at a wave-uniform LDS address, i.e. RPB = 64 / CH whole rows; lane j fills
 // physical chunk j % CH of row (block row + j / CH), so it loads that row's
-// logical chunk (j % CH) ^ swz(row).  Wave w copies rows 16w .. 16w + 15.
-// The caller waits for the loads (s_waitcnt vmcnt) before the barrier that
-// publishes the tile.
-template <int D>
+// logical chunk (j % CH) ^ swz(row).  With NW waves, wave w copies rows
+// (64 / NW) w .. (64 / NW)(w + 1) - 1.  The caller waits for the loads
+// (s_waitcnt vmcnt) before the barrier that publishes the tile.
+template <int D, int NW = 4>
 struct TileDma {
   static constexpr int CH = D / 8;
   static constexpr int RPB = 64 / CH;
-  static constexpr int BLOCKS = 16 / RPB;
+  static constexpr int RPW = 64 / NW;  // rows per wave
+  static constexpr int BLOCKS = RPW / RPB;
   using Geo = TileGeom<D, kSwz>;
 
   template <typename F>
@@ -162,10 +174,38 @@ struct TileDma {
     const int wave = threadIdx.x >> 6, j = threadIdx.x & 63;
 #pragma unroll
     for (int b = 0; b < BLOCKS; ++b) {
-      const int rb = 16 * wave + RPB * b;
+      const int rb = RPW * wave + RPB * b;
       const int row = rb + j / CH;
       const int ch = (j % CH) ^ Geo::swz(row);
       __builtin_amdgcn_global_load_lds(rowptr(row) + 8 * ch,
+                                       (__attribute__((address_space(3))) void*)(tile + rb * D), 16, 0, 0);
+    }
+  }
+
+  // Byte offsets, from a tile's first row, of the 16-byte chunks this lane
+  // copies for a fixed row stride (loop-invariant: computed once).
+  struct Offsets {
+    uint32_t o[BLOCKS];
+  };
+  __device__ __forceinline__ static Offsets offsets(int row_stride) {
+    Offsets r;
+    const int wave = threadIdx.x >> 6, j = threadIdx.x & 63;
+#pragma unroll
+    for (int b = 0; b < BLOCKS; ++b) {
+      const int row = RPW * wave + RPB * b + j / CH;
+      const int ch = (j % CH) ^ Geo::swz(row);
+      r.o[b] = (uint32_t)(row * row_stride + 8 * ch) * (uint32_t)sizeof(bf16);
+    }
+    return r;
+  }
+  // All 64 rows valid: a wave-uniform base plus the precomputed lane offsets
+  // (the scalar-base form of the load; no per-tile address arithmetic).
+  __device__ __forceinline__ static void issue_fast(bf16* tile, const bf16* base, const Offsets& off) {
+    const int wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int b = 0; b < BLOCKS; ++b) {
+      const int rb = RPW * wave + RPB * b;
+      __builtin_amdgcn_global_load_lds(reinterpret_cast<const char*>(base) + off.o[b],
                                        (__attribute__((address_space(3))) void*)(tile + rb * D), 16, 0, 0);
     }
   }
@@ -177,7 +217,7 @@ struct TileDma {
     const int wave = threadIdx.x >> 6, j = threadIdx.x & 63;
 #pragma unroll
     for (int b = 0; b < BLOCKS; ++b) {
-      const int rb = 16 * wave + RPB * b;
+      const int rb = RPW * wave + RPB * b;
       const int row = rb + j / CH;
       const int ch = (j % CH) ^ Geo::swz(row);
       __builtin_amdgcn_global_load_lds(base + (min(row, last_row) * row_stride + 8 * ch),

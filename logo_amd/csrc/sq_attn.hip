@@ -116,7 +116,6 @@ struct QSide {
 extern __shared__ __attribute__((aligned(16))) char logo_smem[];
 __device__ __forceinline__ bf16* dyn_smem() { return reinterpret_cast<bf16*>(logo_smem); }
 
-__device__ __forceinline__ float wave_pair_max(float x) { return fmaxf(x, __shfl_xor(x, 32)); }
 
 // Shared front matter of the fwd and dq kernels: which compacted rows this
 // workgroup and this lane own.  Returns false for a workgroup past the last
@@ -202,9 +201,15 @@ __global__ __launch_bounds__(256) LOGO_OCC_FWD void sq_fwd_kernel(const AttnArgs
   const int seqlen = qt.seqlen;
   // rows past the sequence end are clamped to its last key: the causal mask
   // hides every key > p, and p < seqlen
+  const auto dma_off = TileDma<D>::offsets((int)rstride);
   auto load_tile = [&](int j0, int b) {
-    TileDma<D>::issue_strided(tileK(b), kbase + j0 * rstride, (int)rstride, seqlen - 1 - j0);
-    TileDma<D>::issue_strided(tileV(b), vbase + j0 * rstride, (int)rstride, seqlen - 1 - j0);
+    if (j0 + 64 <= seqlen) {
+      TileDma<D>::issue_fast(tileK(b), kbase + j0 * rstride, dma_off);
+      TileDma<D>::issue_fast(tileV(b), vbase + j0 * rstride, dma_off);
+    } else {
+      TileDma<D>::issue_strided(tileK(b), kbase + j0 * rstride, (int)rstride, seqlen - 1 - j0);
+      TileDma<D>::issue_strided(tileV(b), vbase + j0 * rstride, (int)rstride, seqlen - 1 - j0);
+    }
   };
 
   // One 64-key tile on LDS buffer B while the next one streams into B ^ 1.
@@ -244,7 +249,7 @@ __global__ __launch_bounds__(256) LOGO_OCC_FWD void sq_fwd_kernel(const AttnArgs
       for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
         for (int jj = 0; jj < 16; ++jj) mx = fmaxf(mx, sacc[kk][jj]);
-      mx = wave_pair_max(mx);
+      mx = pair_max(mx);
       // Lazy rescale: the reference max only moves when some row's max grew
       // by more than 2^8 in the exp2 domain (or on the first visible key);
       // otherwise p <= 2^8, exact in fp32 and bf16, and O, l keep their scale.
@@ -293,7 +298,7 @@ __global__ __launch_bounds__(256) LOGO_OCC_FWD void sq_fwd_kernel(const AttnArgs
     if (j0 + 64 < qt.kv_hi) step(BufTag<1>{}, j0 + 64);
   }
 
-  const float l_tot = l_run + __shfl_xor(l_run, 32);
+  const float l_tot = pair_sum(l_run);
   if (qt.valid) {
     const float inv = 1.f / l_tot;
     bf16* orow = a.o + (qt.t * a.hq + hq) * D;
@@ -384,9 +389,15 @@ __global__ __launch_bounds__(256) LOGO_OCC_DQ void sq_dq_kernel(const AttnArgs a
   const bf16* kbase = a.k + ((int64_t)qt.bos * a.h + qt.h) * D;
   const bf16* vbase = a.v + ((int64_t)qt.bos * a.h + qt.h) * D;
   const int seqlen = qt.seqlen;
+  const auto dma_off = TileDma<D>::offsets((int)rstride);
   auto load_tile = [&](int j0, int b) {
-    TileDma<D>::issue_strided(tileK(b), kbase + j0 * rstride, (int)rstride, seqlen - 1 - j0);
-    TileDma<D>::issue_strided(tileV(b), vbase + j0 * rstride, (int)rstride, seqlen - 1 - j0);
+    if (j0 + 64 <= seqlen) {
+      TileDma<D>::issue_fast(tileK(b), kbase + j0 * rstride, dma_off);
+      TileDma<D>::issue_fast(tileV(b), vbase + j0 * rstride, dma_off);
+    } else {
+      TileDma<D>::issue_strided(tileK(b), kbase + j0 * rstride, (int)rstride, seqlen - 1 - j0);
+      TileDma<D>::issue_strided(tileV(b), vbase + j0 * rstride, (int)rstride, seqlen - 1 - j0);
+    }
   };
 
   auto step = [&](auto buf_tag, int j0) {
@@ -483,6 +494,7 @@ __global__ __launch_bounds__(256) LOGO_OCC_DQ void sq_dq_kernel(const AttnArgs a
 // Query rows staged per LDS buffer (64-row sub-tiles; 128 would halve the
 // barriers but needs a second set of LDS address registers past 64 KB).
 constexpr int kDkvRows = 64;
+constexpr int kDkvStages = 2;
 template <int D>
 constexpr int dkv_stage_bytes() { return 2 * kDkvRows * D * 2 + 3 * kDkvRows * 4; }
 
@@ -541,6 +553,8 @@ __global__ __launch_bounds__(256) LOGO_OCC_DKV void sq_dkv_kernel(const AttnArgs
 
   TileReader<D, kSwz> rd;
   rd.init();
+  // q / dO rows: stride D (compacted copies) or HQ * D (dense inputs)
+  const auto dma_off = TileDma<D>::offsets(SPARSE ? D : a.hq * D);
   float lse_n = 0.f, delta_n = 0.f;
   int pos_n = -1;
   for (int gg = 0; gg < a.g; ++gg) {
@@ -561,14 +575,6 @@ __global__ __launch_bounds__(256) LOGO_OCC_DKV void sq_dkv_kernel(const AttnArgs
     const float* lse_h = a.lse + (int64_t)hq * a.n;
     const float* delta_h = a.delta + (int64_t)hq * a.n;
     auto load_tile = [&](int rt, int b) {
-      // rows past rq_end are clamped to a real row and masked (pos = -1)
-      // (last_row may be negative for the second sub-tile: every row then
-      // reads row rq_end - 1)
-#pragma unroll
-      for (int u = 0; u < NSUB; ++u) {
-        TileDma<D>::issue_strided(sQ(b) + 64 * D * u, qs.row(rt + 64 * u), (int)qs.stride, rq_end - 1 - rt - 64 * u);
-        TileDma<D>::issue_strided(sO(b) + 64 * D * u, os.row(rt + 64 * u), (int)os.stride, rq_end - 1 - rt - 64 * u);
-      }
       if (tid < RS) {
         const int rr = rt + tid;
         const bool ok = rr < rq_end;
@@ -576,6 +582,19 @@ __global__ __launch_bounds__(256) LOGO_OCC_DKV void sq_dkv_kernel(const AttnArgs
         lse_n = lse_h[rc];
         delta_n = delta_h[rc];
         pos_n = ok ? rv.posn(rr) : -1;
+      }
+      // rows past rq_end are clamped to a real row and masked (pos = -1)
+      // (last_row may be negative for the second sub-tile: every row then
+      // reads row rq_end - 1)
+#pragma unroll
+      for (int u = 0; u < NSUB; ++u) {
+        if (rt + 64 * (u + 1) <= rq_end) {
+          TileDma<D>::issue_fast(sQ(b) + 64 * D * u, qs.row(rt + 64 * u), dma_off);
+          TileDma<D>::issue_fast(sO(b) + 64 * D * u, os.row(rt + 64 * u), dma_off);
+        } else {
+          TileDma<D>::issue_strided(sQ(b) + 64 * D * u, qs.row(rt + 64 * u), (int)qs.stride, rq_end - 1 - rt - 64 * u);
+          TileDma<D>::issue_strided(sO(b) + 64 * D * u, os.row(rt + 64 * u), (int)os.stride, rq_end - 1 - rt - 64 * u);
+        }
       }
     };
     auto store_stats = [&](int b) {
@@ -586,6 +605,8 @@ __global__ __launch_bounds__(256) LOGO_OCC_DKV void sq_dkv_kernel(const AttnArgs
       }
     };
 
+    // Two LDS stages: step t computes from stage t % 2 while the copy for
+    // step t + 1 lands in the other.
     auto step = [&](auto buf_tag, int rt) {
       constexpr int B = decltype(buf_tag)::value;
       const bool has_next = rt + RS < rq_end;
@@ -768,7 +789,7 @@ constexpr size_t fwd_smem() { return (size_t)4 * TileGeom<D, kSwz>::ELEMS * size
 template <int D>
 constexpr size_t dq_smem() { return (size_t)4 * TileGeom<D, kSwz>::ELEMS * sizeof(bf16); }
 template <int D>
-constexpr size_t dkv_smem() { return (size_t)2 * dkv_stage_bytes<D>(); }
+constexpr size_t dkv_smem() { return (size_t)kDkvStages * dkv_stage_bytes<D>(); }
 
 template <typename K>
 static hipError_t allow_smem(K kernel, size_t bytes) {
