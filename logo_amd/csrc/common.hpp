@@ -56,6 +56,16 @@ __device__ __forceinline__ float pair_sum(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// max(a, b, c) as one v_max3_f32, kept at its place in the instruction
+// stream.  (fmaxf on values that come out of an asm anchor would first be
+// canonicalised, one extra v_max per operand.)  NaN handling is not needed:
+// the attention scores it reduces are finite or -inf.
+__device__ __forceinline__ float max3_f32(float a, float b, float c) {
+  float r;
+  asm volatile("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+
 // Anchors a value at this point of the instruction stream (an empty asm
 // statement that reads and rewrites it): arithmetic on it cannot be hoisted
 // above, nor its producer sunk below, this point.  Used with scheduling
@@ -222,6 +232,73 @@ struct TileDma {
       const int ch = (j % CH) ^ Geo::swz(row);
       __builtin_amdgcn_global_load_lds(base + (min(row, last_row) * row_stride + 8 * ch),
                                        (__attribute__((address_space(3))) void*)(tile + rb * D), 16, 0, 0);
+    }
+  }
+};
+
+// The same tile copy through buffer_load_dwordx4 ... lds: a scalar buffer
+// descriptor based at the tile's first row, a scalar byte offset and one
+// 32-bit lane offset per 1 KB block (loop-invariant for full tiles).  The
+// descriptor's extent is the 64 rows of the tile, so the hardware returns
+// zeros for any read past them instead of touching memory outside the tile.
+constexpr int kBufRsrcWord3 = 0x00020000;  // raw, untyped 32-bit buffer (gfx9 family)
+
+// One buffer_load_dwordx4 ... lds: 64 lanes x 16 bytes to LDS at `lds`
+// (wave-uniform).  A non-template wrapper: clang's host pass drops the host
+// stubs of later kernel instantiations when this builtin sits directly in a
+// template.
+__device__ __forceinline__ void buf_load_lds16(__amdgpu_buffer_rsrc_t r, bf16* lds, uint32_t voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, 0, 0, 0);
+}
+
+template <int D, int NW = 4>
+struct TileBufDma {
+  static constexpr int CH = D / 8;
+  static constexpr int RPB = 64 / CH;
+  static constexpr int RPW = 64 / NW;
+  static constexpr int BLOCKS = RPW / RPB;
+  using Geo = TileGeom<D, kSwz>;
+  uint32_t o[BLOCKS];  // byte offsets from the tile's first row (all 64 rows valid)
+  int row_stride;      // elements
+
+  __device__ __forceinline__ void init(int row_stride_elems) {
+    row_stride = row_stride_elems;
+    const int wave = threadIdx.x >> 6, j = threadIdx.x & 63;
+#pragma unroll
+    for (int b = 0; b < BLOCKS; ++b) {
+      const int row = RPW * wave + RPB * b + j / CH;
+      const int ch = (j % CH) ^ Geo::swz(row);
+      o[b] = (uint32_t)(row * row_stride + 8 * ch) * (uint32_t)sizeof(bf16);
+    }
+  }
+
+  __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const bf16* row0) const {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16*>(row0), (short)0,
+                                             64 * row_stride * (int)sizeof(bf16), kBufRsrcWord3);
+  }
+
+  // Rows row0 .. row0 + 63, all valid.
+  __device__ __forceinline__ void issue(bf16* tile, const bf16* row0) const {
+    const auto r = rsrc(row0);
+    const int wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int b = 0; b < BLOCKS; ++b) {
+      const int rb = RPW * wave + RPB * b;
+      buf_load_lds16(r, tile + rb * D, o[b]);
+    }
+  }
+
+  // Rows past last_row (< 63) are clamped to it.
+  __device__ __forceinline__ void issue_clamped(bf16* tile, const bf16* row0, int last_row) const {
+    const auto r = rsrc(row0);
+    const int wave = threadIdx.x >> 6, j = threadIdx.x & 63;
+#pragma unroll
+    for (int b = 0; b < BLOCKS; ++b) {
+      const int rb = RPW * wave + RPB * b;
+      const int row = rb + j / CH;
+      const int ch = (j % CH) ^ Geo::swz(row);
+      const uint32_t off = (uint32_t)(min(row, last_row) * row_stride + 8 * ch) * (uint32_t)sizeof(bf16);
+      buf_load_lds16(r, tile + rb * D, off);
     }
   }
 };

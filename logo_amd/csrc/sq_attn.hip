@@ -19,18 +19,22 @@
 //   * an optional sliding window (keys [p - w, p]) turns the same kernels into
 //     the local SWA branch (logo/layers/utils.py:144-147).
 //
-// Tiling (32x32x16 bf16 MFMA, wave64, 4 waves per workgroup):
-//   fwd / dq : 128 compacted rows per workgroup (32 per wave, Q and dO held in
-//              registers as B operands), K/V streamed in double-buffered
-//              64-key row-major LDS tiles.  S^T = K Q^T puts one query per lane
-//              pair, so the softmax row statistics need a single cross-lane
-//              exchange (lane ^ 32).  The transposed operands V^T (fwd) and
-//              K^T (dq) come from the same row-major tiles through
-//              ds_read_b64_tr_b16.
-//   dk/dv    : 128 keys per workgroup (32 per wave, K and V in registers),
-//              compacted query rows streamed in double-buffered 64-row LDS
-//              tiles (Q^T and dO^T again by transposing reads), GQA heads
-//              looped inside the workgroup.
+// Tiling (32x32x16 bf16 MFMA, wave64; kBQ = 128 compacted rows per fwd / dq
+// workgroup, kBKV = 128 keys per dk/dv workgroup):
+//   fwd   : 4 waves x 32 rows, two waves per SIMD; Q in registers as the B
+//           operand, K/V streamed through double-buffered 64-key LDS tiles.
+//           Each wave software-pipelines S of the next key tile against the
+//           softmax of the current one.
+//   dq    : 2 waves x 64 rows (two 32-row blocks), one wave per SIMD, so each
+//           K / V operand read from LDS feeds two MFMAs; Q, dO and dQ in
+//           AGPRs; S / dP of the next 32-key half pipelined against dS of the
+//           current one.
+//   dk/dv : 4 waves x 32 keys (K and V in registers), compacted query rows
+//           streamed in double-buffered 64-row LDS tiles, GQA heads looped
+//           inside the workgroup, an explicit MFMA / VALU / LDS slot schedule.
+// S^T = K Q^T puts one query per lane pair, so the softmax row statistics need
+// a single cross-lane exchange (lane ^ 32).  Transposed operands (V^T, K^T,
+// Q^T, dO^T) come from the same row-major tiles through ds_read_b64_tr_b16.
 #include <math.h>
 
 #include <type_traits>
@@ -106,8 +110,8 @@ struct QSide {
 #ifndef LOGO_OCC_FWD
 #define LOGO_OCC_FWD __attribute__((amdgpu_waves_per_eu(2, 2)))
 #endif
-#ifndef LOGO_OCC_DQ
-#define LOGO_OCC_DQ __attribute__((amdgpu_waves_per_eu(2, 2)))
+#ifndef LOGO_OCC_DQ64
+#define LOGO_OCC_DQ64 __attribute__((amdgpu_waves_per_eu(1, 1)))
 #endif
 #ifndef LOGO_OCC_DKV
 #define LOGO_OCC_DKV __attribute__((amdgpu_waves_per_eu(1, 1)))
@@ -128,7 +132,9 @@ struct QTile {
   int64_t t;
   RowView<SPARSE> rv;
 
-  __device__ __forceinline__ bool init(const AttnArgs& a, int wave, int i, bool window) {
+  // rpw: compacted rows per wave (32 or 64); r / t / p / valid describe the
+  // lane's row in the wave's first 32-row block (row_at gives the others).
+  __device__ __forceinline__ bool init(const AttnArgs& a, int wave, int i, bool window, int rpw = 32) {
     int rank;
     xcd_remap(blockIdx.x, a.hq, rank, hq);
     lane_sel = a.lanes > 1 ? hq : 0;
@@ -145,10 +151,10 @@ struct QTile {
     seqlen = a.cu[s + 1] - bos;
     h = hq / a.g;
     rv = row_view<SPARSE>(a, lane_sel, bos);
-    const int rw0 = r0 + 32 * wave;
+    const int rw0 = r0 + rpw * wave;
     wave_active = rw0 < r_end;
     pmin = wave_active ? rv.posn(rw0) : 0;
-    pmax = wave_active ? rv.posn(min(rw0 + 31, r_end - 1)) : -1;
+    pmax = wave_active ? rv.posn(min(rw0 + rpw - 1, r_end - 1)) : -1;
     r = rw0 + i;
     valid = r < r_end;
     t = valid ? rv.token(r) : 0;
@@ -165,12 +171,39 @@ struct QTile {
 template <int B>
 using BufTag = std::integral_constant<int, B>;
 
+// ---------------------------------------------------------------------------
+// Forward, software-pipelined inside each wave
+// ---------------------------------------------------------------------------
+// Iteration t of the workgroup loop (t = -1 .. nt - 1; key tile t starts at
+// kv_lo + 64 t) runs two phases of MFMA slots on every wave:
+//   X: the S^T MFMAs of tile t + 1 (K(t+1) rows from LDS), while the VALU turns
+//      S(t) into P(t) = exp2(S c - base), sums it and packs it to bf16;
+//   Y: the O += V(t)^T P(t) MFMAs, while the VALU masks S(t+1) and takes its
+//      row max.
+// The row statistics of tile t + 1 (new reference max, rescale of O and l)
+// follow Y.  K therefore runs one tile ahead of V: iteration t reads K(t+1)
+// from K slot (t+1)&1 and V(t) from V slot t&1, and loads K(t+2) into K slot
+// t&1 and V(t+1) into V slot (t+1)&1, both last read in iteration t - 1.
+// Each wave only works on the tiles its own rows can see ([tw_lo, tw_hi));
+// outside them it still copies its share of the tiles and meets the barriers.
+// Four waves x 32 rows per workgroup (kBQ = 128), two waves per SIMD.
+//
+// Online softmax with a lazy rescale: the reference max of a row moves only
+// when the row's max grew by more than 2^8 in the exp2 domain (or on its first
+// visible key), so O and l are rarely rescaled and P <= 2^8 stays exact.
+// Masks compare a compile-time offset per accumulator item with one per-lane
+// bound: key j0 + 32 kk + rowmap(g, jj) is visible iff its offset from
+// j0 + 4 g lies in [hi - W, hi], hi = p - j0 - 4 g.
 template <int D, bool SPARSE, bool WINDOW>
-__global__ __launch_bounds__(256) LOGO_OCC_FWD void sq_fwd_kernel(const AttnArgs a) {
+__global__ __launch_bounds__(256) LOGO_OCC_FWD void sq_fwd_pipe_kernel(const AttnArgs a) {
   constexpr int DS = D / 16, DT = D / 32;
+  constexpr int NX = 2 * DS;   // S MFMAs per tile (two 32-key halves x DS k-steps)
+  constexpr int NY = 4 * DT;   // PV MFMAs per tile (DT column blocks x 4 key steps)
+  constexpr int IX = 32 / NX;  // softmax items per X slot
+  constexpr int IY = 32 / NY;  // mask / max items per Y slot
+  constexpr int PF = 4;        // operand prefetch distance, in slots
   using GT = TileGeom<D, kSwz>;
   bf16* const smem = dyn_smem();
-  // [K tile 0][K tile 1][V tile 0][V tile 1], swizzled
   auto tileK = [&](int b) { return smem + b * GT::ELEMS; };
   auto tileV = [&](int b) { return smem + 2 * GT::ELEMS + b * GT::ELEMS; };
 
@@ -190,7 +223,9 @@ __global__ __launch_bounds__(256) LOGO_OCC_FWD void sq_fwd_kernel(const AttnArgs
   f32x16 oacc[DT];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) oacc[dt] = f32x16{};
-  float m_run = -INFINITY, l_run = 0.f;
+  f32x16 sbuf[2][2];  // [t & 1][32-key half]: S of the current and the next tile
+  bf16x8 pb[4];       // P(t) as the B operand of PV, one per 16-key step
+  float m_run = -INFINITY, l_run = 0.f, base = 0.f;
   const float c = a.scale_log2;
 
   TileReader<D, kSwz> rd;  // K read along rows, V transposed
@@ -199,103 +234,140 @@ __global__ __launch_bounds__(256) LOGO_OCC_FWD void sq_fwd_kernel(const AttnArgs
   const bf16* kbase = a.k + ((int64_t)qt.bos * a.h + qt.h) * D;
   const bf16* vbase = a.v + ((int64_t)qt.bos * a.h + qt.h) * D;
   const int seqlen = qt.seqlen;
-  // rows past the sequence end are clamped to its last key: the causal mask
-  // hides every key > p, and p < seqlen
-  const auto dma_off = TileDma<D>::offsets((int)rstride);
-  auto load_tile = [&](int j0, int b) {
-    if (j0 + 64 <= seqlen) {
-      TileDma<D>::issue_fast(tileK(b), kbase + j0 * rstride, dma_off);
-      TileDma<D>::issue_fast(tileV(b), vbase + j0 * rstride, dma_off);
-    } else {
-      TileDma<D>::issue_strided(tileK(b), kbase + j0 * rstride, (int)rstride, seqlen - 1 - j0);
-      TileDma<D>::issue_strided(tileV(b), vbase + j0 * rstride, (int)rstride, seqlen - 1 - j0);
-    }
+  TileBufDma<D> dma;
+  dma.init((int)rstride);
+  // rows past the sequence end are clamped to its last key (masked: p < seqlen)
+  auto load_one = [&](bf16* tile, const bf16* src, int j0) {
+    if (j0 + 64 <= seqlen) dma.issue(tile, src + j0 * rstride);
+    else dma.issue_clamped(tile, src + j0 * rstride, seqlen - 1 - j0);
   };
 
-  // One 64-key tile on LDS buffer B while the next one streams into B ^ 1.
-  auto step = [&](auto buf_tag, int j0) {
-    constexpr int B = decltype(buf_tag)::value;
-    const bool has_next = j0 + 64 < qt.kv_hi;
-    if (has_next) load_tile(j0 + 64, B ^ 1);
-    const bf16* kb = tileK(B);
-    const bf16* vb = tileV(B);
-    // one instantiation per masking mode: fully visible tiles carry no mask work
-    auto compute = [&](auto mask_tag) {
-      constexpr bool MASK = decltype(mask_tag)::value;
-      f32x16 sacc[2];
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
-        sacc[kk] = f32x16{};
-#pragma unroll
-        for (int ds = 0; ds < DS; ++ds) sacc[kk] = mfma32(rd.row(kb, 32 * kk, ds), qreg[ds], sacc[kk]);
-      }
-      if constexpr (MASK) {
-        // key j0 + 32kk + rowmap(g, jj) is visible iff its offset from
-        // j0 + 4g (a compile-time constant per item) lies in [lo, hi]
-        const int hi = p - j0 - 4 * g;
-        const int lo = hi - W;
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-          for (int jj = 0; jj < 16; ++jj) {
-            const int off = 32 * kk + 8 * (jj / 4) + (jj % 4);
-            bool vis = off <= hi;
-            if (WINDOW) vis = vis && off >= lo;
-            if (!vis) sacc[kk][jj] = -INFINITY;
-          }
-      }
-      float mx = -INFINITY;
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-        for (int jj = 0; jj < 16; ++jj) mx = fmaxf(mx, sacc[kk][jj]);
-      mx = pair_max(mx);
-      // Lazy rescale: the reference max only moves when some row's max grew
-      // by more than 2^8 in the exp2 domain (or on the first visible key);
-      // otherwise p <= 2^8, exact in fp32 and bf16, and O, l keep their scale.
-      const bool grow = (mx - m_run) * c > 8.f;
-      const float m_new = __ballot(grow) ? fmaxf(m_run, mx) : m_run;
-      const float base = (m_new == -INFINITY) ? 0.f : m_new * c;
-      const float alpha = fast_exp2(m_run * c - base);
-      float psum = 0.f;
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-        for (int jj = 0; jj < 16; ++jj) {
-          const float pv = fast_exp2(fmaf(sacc[kk][jj], c, -base));
-          sacc[kk][jj] = pv;
-          psum += pv;
+  const int kv_lo = qt.kv_lo;
+  const int nt = (qt.kv_hi - kv_lo + 63) >> 6;
+  int tw_lo = 0, tw_hi = 0;  // tiles this wave's rows can see
+  if (qt.wave_active) {
+    tw_hi = ((qt.pmax - kv_lo) >> 6) + 1;
+    tw_lo = WINDOW ? (max(0, qt.pmin - W - kv_lo) >> 6) : 0;
+  }
+
+  auto step = [&](auto par_tag, int t) {
+    constexpr int PAR = decltype(par_tag)::value;  // t & 1
+    if (t + 2 < nt) load_one(tileK(PAR), kbase, kv_lo + 64 * (t + 2));
+    if (t + 1 < nt) load_one(tileV(PAR ^ 1), vbase, kv_lo + 64 * (t + 1));
+    const bf16* kb = tileK(PAR ^ 1);
+    const bf16* vb = tileV(PAR);
+    const int j0n = kv_lo + 64 * (t + 1);
+
+    auto body = [&](auto dos_tag, auto dopv_tag, auto mask_tag) {
+      constexpr bool DOS = decltype(dos_tag)::value;    // S(t+1) and its statistics
+      constexpr bool DOPV = decltype(dopv_tag)::value;  // P(t) and O += V^T P
+      constexpr bool MASK = decltype(mask_tag)::value;  // S(t+1) crosses a mask edge
+      // slot s < NX: K row operand (half s / DS, k-step s % DS);
+      // slot s >= NX: V^T operand (column block (s - NX) / 4, key step (s - NX) % 4)
+      bf16x8 op[NX + NY];
+      auto load_op = [&](auto s_c) {
+        constexpr int S = decltype(s_c)::value;
+        if constexpr (S < NX) {
+          if constexpr (DOS) op[S] = rd.row(kb, 32 * (S / DS), S % DS);
+        } else {
+          if constexpr (DOPV) op[S] = rd.tr(vb, 16 * ((S - NX) % 4), (S - NX) / 4);
         }
-      l_run = l_run * alpha + psum;
-      m_run = m_new;
-      if (__ballot(alpha != 1.f)) {
+      };
+      static_for<PF>([&](auto s_c) { load_op(s_c); });
+      const int hi = p - j0n - 4 * g;  // mask bound of S(t+1) items
+      float mx = -INFINITY, psum = 0.f;
+      static_for<NX + NY>([&](auto s_c) {
+        constexpr int S = decltype(s_c)::value;
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (S < NX) {
+          if constexpr (DOS) {
+            constexpr int KK = S / DS, DSI = S % DS;
+            bf16x8 o = op[S];
+            pin(o);
+            sbuf[PAR ^ 1][KK] = mfma32(o, qreg[DSI], DSI == 0 ? f32x16{} : sbuf[PAR ^ 1][KK]);
+          }
+          if constexpr (DOPV) {
+            static_for<IX>([&](auto e_c) {
+              constexpr int IT = S * IX + decltype(e_c)::value;
+              constexpr int KK = IT / 16, JJ = IT % 16;
+              float sv = sbuf[PAR][KK][JJ];
+              pin(sv);
+              float pv = fast_exp2(fmaf(sv, c, -base));
+              pin(pv);
+              sbuf[PAR][KK][JJ] = pv;
+              psum += pv;
+              pin(psum);
+              if constexpr (IT % 8 == 7) pb[IT / 8] = acc_to_bf16(sbuf[PAR][IT / 16], (IT / 8) & 1);
+            });
+          }
+        } else {
+          constexpr int Y = S - NX;
+          if constexpr (DOPV) {
+            bf16x8 o = op[S];
+            pin(o);
+            oacc[Y / 4] = mfma32(o, pb[Y % 4], oacc[Y / 4]);
+          }
+          if constexpr (DOS) {
+            float sv[IY];
+            static_for<IY>([&](auto e_c) {
+              constexpr int E = decltype(e_c)::value, IT = Y * IY + E;
+              constexpr int KK = IT / 16, JJ = IT % 16;
+              sv[E] = sbuf[PAR ^ 1][KK][JJ];
+              pin(sv[E]);
+              if constexpr (MASK) {
+                constexpr int off = 32 * KK + 8 * (JJ / 4) + (JJ % 4);
+                bool vis = off <= hi;
+                if (WINDOW) vis = vis && off >= hi - W;
+                if (!vis) sv[E] = -INFINITY;
+                sbuf[PAR ^ 1][KK][JJ] = sv[E];
+              }
+            });
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) oacc[dt] *= alpha;
+            for (int e = 0; e < IY; e += 2) mx = max3_f32(mx, sv[e], sv[e + 1]);
+          }
+        }
+        if constexpr (S + PF < NX + NY) load_op(std::integral_constant<int, S + PF>{});
+      });
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (DOPV) l_run += psum;
+      if constexpr (DOS) {
+        mx = pair_max(mx);
+        const bool grow = (mx - m_run) * c > 8.f;
+        const float m_new = __ballot(grow) ? fmaxf(m_run, mx) : m_run;
+        const float nbase = (m_new == -INFINITY) ? 0.f : m_new * c;
+        const float alpha = fast_exp2(m_run * c - nbase);
+        l_run *= alpha;
+        m_run = m_new;
+        base = nbase;
+        if (__ballot(alpha != 1.f)) {
+#pragma unroll
+          for (int dt = 0; dt < DT; ++dt) oacc[dt] *= alpha;
+        }
       }
-      bf16x8 pb[4];
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) pb[ks] = acc_to_bf16(sacc[ks >> 1], ks & 1);
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) oacc[dt] = mfma32(rd.tr(vb, 16 * ks, dt), pb[ks], oacc[dt]);
     };
-    const bool skip = !qt.wave_active || j0 > qt.pmax || (WINDOW && j0 + 63 < qt.pmin - W);
-    if (!skip) {
-      const bool need_mask = (j0 + 63 > qt.pmin) || (WINDOW && j0 < qt.pmax - W);
-      if (need_mask) compute(std::true_type{});
-      else compute(std::false_type{});
+    using T_ = std::true_type;
+    using F_ = std::false_type;
+    const bool doS = t + 1 >= tw_lo && t + 1 < tw_hi;
+    const bool doPV = t >= tw_lo && t < tw_hi;
+    const bool maskn = (j0n + 63 > qt.pmin) || (WINDOW && j0n < qt.pmax - W);
+    if (doS && doPV) {
+      if (maskn) body(T_{}, T_{}, T_{});
+      else body(T_{}, T_{}, F_{});
+    } else if (doS) {
+      body(T_{}, F_{}, T_{});
+    } else if (doPV) {
+      body(F_{}, T_{}, F_{});
     }
     wait_vmem();
     __syncthreads();
   };
 
-  load_tile(qt.kv_lo, 0);
+  load_one(tileK(0), kbase, kv_lo);
   wait_vmem();
   __syncthreads();
-  for (int j0 = qt.kv_lo; j0 < qt.kv_hi; j0 += 128) {
-    step(BufTag<0>{}, j0);
-    if (j0 + 64 < qt.kv_hi) step(BufTag<1>{}, j0 + 64);
+  for (int t = -1; t < nt; t += 2) {
+    step(BufTag<1>{}, t);
+    if (t + 1 < nt) step(BufTag<0>{}, t + 1);
   }
 
   const float l_tot = pair_sum(l_run);
@@ -349,39 +421,73 @@ __global__ __launch_bounds__(256) void sq_delta_kernel(const AttnArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Backward dq
+// Backward dq, 64 rows per wave
 // ---------------------------------------------------------------------------
+// Two waves x 64 compacted rows (two 32-row blocks) per workgroup (kBQ = 128),
+// one wave per SIMD and two workgroups per CU, so every K / V operand read from
+// LDS feeds the MFMAs of both row blocks (half the LDS traffic per MFMA of 32
+// rows per wave).  Q, dO (MFMA B
+// operands) and the dQ accumulators live in AGPRs; S and dP in VGPRs.
+// Keys are processed in 32-key halves; step (t, h) of key tile t runs
+//   X: the S^T / dP^T MFMAs of the next half ((t, 1) or (t + 1, 0)) while the
+//      VALU forms P = exp2(S c - lse) and dS = P (dP - delta) of half (t, h);
+//   Y: the dQ^T += K^T dS^T MFMAs of half (t, h).
+// K and V tiles (64 keys) sit in two LDS slots each (slot = tile & 1).
+// K(t + 1) is copied during step (t, 0), after K(t - 1)'s last read (step
+// (t - 1, 1)); V(t + 2) during step (t, 1), after V(t)'s last read (step
+// (t, 0)).  Every step ends with the copy wait and a barrier.
 template <int D, bool SPARSE, bool WINDOW>
-__global__ __launch_bounds__(256) LOGO_OCC_DQ void sq_dq_kernel(const AttnArgs a) {
+__global__ __launch_bounds__(128) LOGO_OCC_DQ64 void sq_dq64_kernel(const AttnArgs a) {
   constexpr int DS = D / 16, DT = D / 32;
-  using GT = TileGeom<D, kSwz>;  // K read along rows (S) and transposed (dQ); V along rows
+  constexpr int NX = 2 * DS;    // X slots: K row operand (even), V row operand (odd)
+  constexpr int NY = 2 * DT;    // Y slots: K^T operands (16-key step hh, column block dt)
+  constexpr int IX = 16 / NX;   // VALU items per X slot and row block (16 per half)
+  constexpr int PF = 3;         // operand prefetch distance, in slots
+  using GT = TileGeom<D, kSwz>;
   bf16* const smem = dyn_smem();
   auto tileK = [&](int b) { return smem + b * GT::ELEMS; };
   auto tileV = [&](int b) { return smem + 2 * GT::ELEMS + b * GT::ELEMS; };
 
   const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63, i = l & 31, g = l >> 5;
   QTile<SPARSE> qt;
-  if (!qt.init(a, wave, i, WINDOW)) return;
-  const int hq = qt.hq, p = qt.p, W = a.window;
+  if (!qt.init(a, wave, i, WINDOW, 64)) return;
+  const int hq = qt.hq, W = a.window;
+  int rr[2], pr[2];
+  bool vr[2];
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    rr[b] = qt.r0 + 64 * wave + 32 * b + i;
+    vr[b] = rr[b] < qt.r_end;
+    pr[b] = vr[b] ? qt.rv.posn(rr[b]) : -1;
+  }
 
-  bf16x8 qreg[DS], doreg[DS];
+  bf16x8 qreg[2][DS], doreg[2][DS];
+  float lse_q[2], delta_q[2];
   {
     const QSide<D, SPARSE> qs(a, a.q_sel, a.q, hq), os(a, a.do_sel, a.dout, hq);
-    const bf16* qrow = qs.row(qt.r) + 8 * g;
-    const bf16* orow = os.row(qt.r) + 8 * g;
 #pragma unroll
-    for (int ds = 0; ds < DS; ++ds) {
-      qreg[ds] = qt.valid ? *reinterpret_cast<const bf16x8*>(qrow + 16 * ds) : bf16x8{};
-      doreg[ds] = qt.valid ? *reinterpret_cast<const bf16x8*>(orow + 16 * ds) : bf16x8{};
+    for (int b = 0; b < 2; ++b) {
+      const int rc = vr[b] ? rr[b] : qt.r0;
+      const bf16* qrow = qs.row(rc) + 8 * g;
+      const bf16* orow = os.row(rc) + 8 * g;
+#pragma unroll
+      for (int ds = 0; ds < DS; ++ds) {
+        qreg[b][ds] = vr[b] ? *reinterpret_cast<const bf16x8*>(qrow + 16 * ds) : bf16x8{};
+        doreg[b][ds] = vr[b] ? *reinterpret_cast<const bf16x8*>(orow + 16 * ds) : bf16x8{};
+      }
+      lse_q[b] = vr[b] ? a.lse[(int64_t)hq * a.n + rr[b]] : 0.f;
+      delta_q[b] = vr[b] ? a.delta[(int64_t)hq * a.n + rr[b]] : 0.f;
     }
   }
-  const float lse_q = qt.valid ? a.lse[(int64_t)hq * a.n + qt.r] : 0.f;
-  const float delta_q = qt.valid ? a.delta[(int64_t)hq * a.n + qt.r] : 0.f;
   const float c = a.scale_log2;
 
-  f32x16 dqacc[DT];
+  f32x16 dqacc[2][DT];  // AGPRs
 #pragma unroll
-  for (int dt = 0; dt < DT; ++dt) dqacc[dt] = f32x16{};
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) dqacc[b][dt] = f32x16{};
+  f32x16 sp[2][2][2];  // [half parity][row block][S, dP]
+  bf16x8 dsb[2][2];    // dS of the current half as B operands [row block][16-key step]
 
   TileReader<D, kSwz> rd;
   rd.init();
@@ -389,102 +495,155 @@ __global__ __launch_bounds__(256) LOGO_OCC_DQ void sq_dq_kernel(const AttnArgs a
   const bf16* kbase = a.k + ((int64_t)qt.bos * a.h + qt.h) * D;
   const bf16* vbase = a.v + ((int64_t)qt.bos * a.h + qt.h) * D;
   const int seqlen = qt.seqlen;
-  const auto dma_off = TileDma<D>::offsets((int)rstride);
-  auto load_tile = [&](int j0, int b) {
-    if (j0 + 64 <= seqlen) {
-      TileDma<D>::issue_fast(tileK(b), kbase + j0 * rstride, dma_off);
-      TileDma<D>::issue_fast(tileV(b), vbase + j0 * rstride, dma_off);
-    } else {
-      TileDma<D>::issue_strided(tileK(b), kbase + j0 * rstride, (int)rstride, seqlen - 1 - j0);
-      TileDma<D>::issue_strided(tileV(b), vbase + j0 * rstride, (int)rstride, seqlen - 1 - j0);
-    }
+  TileBufDma<D, 2> dma;
+  dma.init((int)rstride);
+  auto load_one = [&](bf16* tile, const bf16* src, int j0) {
+    if (j0 + 64 <= seqlen) dma.issue(tile, src + j0 * rstride);
+    else dma.issue_clamped(tile, src + j0 * rstride, seqlen - 1 - j0);
   };
 
-  auto step = [&](auto buf_tag, int j0) {
-    constexpr int B = decltype(buf_tag)::value;
-    const bool has_next = j0 + 64 < qt.kv_hi;
-    if (has_next) load_tile(j0 + 64, B ^ 1);
-    const bf16* kb = tileK(B);
-    const bf16* vb = tileV(B);
-    auto compute = [&](auto mask_tag) {
-      constexpr bool MASK = decltype(mask_tag)::value;
-      // Two 32-key halves in turn keep only one S / dP accumulator pair live.
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
-        f32x16 sacc{}, pacc{};
-        // operands fetched one step ahead; the fences keep the compiler from
-        // hoisting every LDS read of the tile (which overflows 256 VGPRs)
-        bf16x8 ka = rd.row(kb, 32 * kk, 0), va = rd.row(vb, 32 * kk, 0);
-#pragma unroll
-        for (int ds = 0; ds < DS; ++ds) {
-          bf16x8 kn = ka, vn = va;
-          if (ds + 1 < DS) {
-            kn = rd.row(kb, 32 * kk, ds + 1);
-            vn = rd.row(vb, 32 * kk, ds + 1);
-          }
-          sacc = mfma32(ka, qreg[ds], sacc);
-          pacc = mfma32(va, doreg[ds], pacc);
-          ka = kn;
-          va = vn;
-          __builtin_amdgcn_sched_barrier(0);
+  const int kv_lo = qt.kv_lo;
+  const int nt = (qt.kv_hi - kv_lo + 63) >> 6;
+  int hw_lo = 0, hw_hi = 0;  // 32-key halves this wave's rows can see
+  if (qt.wave_active) {
+    hw_hi = ((qt.pmax - kv_lo) >> 5) + 1;
+    hw_lo = WINDOW ? (max(0, qt.pmin - W - kv_lo) >> 5) : 0;
+  }
+
+  // step (t, H): PAR = t & 1 (K / V slot of tile t)
+  auto step = [&](auto par_tag, auto h_tag, int t) {
+    constexpr int PAR = decltype(par_tag)::value, H = decltype(h_tag)::value;
+    if (H == 0) {
+      if (t + 1 < nt) load_one(tileK(PAR ^ 1), kbase, kv_lo + 64 * (t + 1));
+    } else {
+      if (t + 2 < nt) load_one(tileV(PAR), vbase, kv_lo + 64 * (t + 2));
+    }
+    // X reads the next half: rows 32 of tile t (H = 0) or rows 0 of tile t + 1
+    const bf16* kx = tileK(H == 0 ? PAR : PAR ^ 1);
+    const bf16* vx = tileV(H == 0 ? PAR : PAR ^ 1);
+    constexpr int XR = H == 0 ? 32 : 0;
+    const bf16* ky = tileK(PAR);  // K^T of the current half, rows 32 H
+    const int hx = 2 * t + H;     // current half
+    const int j0h = kv_lo + 32 * hx;
+
+    auto body = [&](auto dox_tag, auto dov_tag, auto mask_tag) {
+      constexpr bool DOX = decltype(dox_tag)::value;    // S / dP of the next half
+      constexpr bool DOV = decltype(dov_tag)::value;    // dS and dQ of the current half
+      constexpr bool MASK = decltype(mask_tag)::value;  // the current half crosses a mask edge
+      bf16x8 op[NX + NY];
+      auto load_op = [&](auto s_c) {
+        constexpr int S = decltype(s_c)::value;
+        if constexpr (S < NX) {
+          if constexpr (DOX) op[S] = rd.row(S % 2 ? vx : kx, XR, S / 2);
+        } else {
+          constexpr int Y = S - NX;
+          if constexpr (DOV) op[S] = rd.tr(ky, 32 * H + 16 * (Y / DT), Y % DT);
         }
+      };
+      static_for<PF>([&](auto s_c) { load_op(s_c); });
+      int hi[2];
 #pragma unroll
-        for (int jj = 0; jj < 16; ++jj) {
-          float pv = fast_exp2(fmaf(sacc[jj], c, -lse_q));
-          if constexpr (MASK) {
-            // key j0 + 32kk + rowmap(g, jj) against the lane's [p - W, p]
-            const int off = 8 * (jj / 4) + (jj % 4);
-            const int hi = p - j0 - 32 * kk - 4 * g;
-            bool vis = off <= hi;
-            if (WINDOW) vis = vis && off >= hi - W;
-            if (!vis) pv = 0.f;
+      for (int b = 0; b < 2; ++b) hi[b] = pr[b] - j0h - 4 * g;
+      static_for<NX + NY>([&](auto s_c) {
+        constexpr int S = decltype(s_c)::value;
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (S < NX) {
+          // one wave per SIMD issues in order: each MFMA is followed by the
+          // VALU items of its row block, which run under it
+          constexpr int DSI = S / 2, KIND = S % 2;
+          bf16x8 o;
+          if constexpr (DOX) {
+            o = op[S];
+            pin(o);
           }
-          sacc[jj] = pv * (pacc[jj] - delta_q);
-        }
-#pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-          const bf16x8 db = acc_to_bf16(sacc, hh);
-          bf16x8 kt = rd.tr(kb, 16 * (2 * kk + hh), 0);
-#pragma unroll
-          for (int dt = 0; dt < DT; ++dt) {
-            bf16x8 kn = kt;
-            if (dt + 1 < DT) kn = rd.tr(kb, 16 * (2 * kk + hh), dt + 1);
-            dqacc[dt] = mfma32(kt, db, dqacc[dt]);
-            kt = kn;
-            __builtin_amdgcn_sched_barrier(0);
+          static_for<2>([&](auto b_c) {
+            constexpr int B = decltype(b_c)::value;
+            if constexpr (B == 1) __builtin_amdgcn_sched_barrier(0);
+            if constexpr (DOX) {
+              const bf16x8 bop = KIND ? doreg[B][DSI] : qreg[B][DSI];
+              sp[H ^ 1][B][KIND] = mfma32(o, bop, DSI == 0 ? f32x16{} : sp[H ^ 1][B][KIND]);
+            }
+            if constexpr (DOV) {
+              static_for<IX>([&](auto e_c) {
+                constexpr int JJ = S * IX + decltype(e_c)::value;
+                float sv = sp[H][B][0][JJ], dpv = sp[H][B][1][JJ];
+                pin(sv);
+                pin(dpv);
+                float pv = fast_exp2(fmaf(sv, c, -lse_q[B]));
+                if constexpr (MASK) {
+                  constexpr int off = 8 * (JJ / 4) + (JJ % 4);
+                  bool vis = off <= hi[B];
+                  if (WINDOW) vis = vis && off >= hi[B] - W;
+                  if (!vis) pv = 0.f;
+                }
+                float dsv = pv * (dpv - delta_q[B]);
+                pin(dsv);
+                sp[H][B][0][JJ] = pv;
+                sp[H][B][1][JJ] = dsv;
+                if constexpr (JJ % 8 == 7) dsb[B][JJ / 8] = acc_to_bf16(sp[H][B][1], JJ / 8);
+              });
+            }
+          });
+        } else {
+          constexpr int Y = S - NX;
+          if constexpr (DOV) {
+            bf16x8 o = op[S];
+            pin(o);
+            mfma32_agpr(dqacc[0][Y % DT], o, dsb[0][Y / DT]);
+            mfma32_agpr(dqacc[1][Y % DT], o, dsb[1][Y / DT]);
           }
         }
-      }
+        if constexpr (S + PF < NX + NY) load_op(std::integral_constant<int, S + PF>{});
+      });
+      __builtin_amdgcn_sched_barrier(0);
     };
-    const bool skip = !qt.wave_active || j0 > qt.pmax || (WINDOW && j0 + 63 < qt.pmin - W);
-    if (!skip) {
-      const bool need_mask = (j0 + 63 > qt.pmin) || (WINDOW && j0 < qt.pmax - W);
-      if (need_mask) compute(std::true_type{});
-      else compute(std::false_type{});
+    using T_ = std::true_type;
+    using F_ = std::false_type;
+    const bool dox = hx + 1 >= hw_lo && hx + 1 < hw_hi;
+    const bool dov = hx >= hw_lo && hx < hw_hi;
+    const bool mask = (j0h + 31 > qt.pmin) || (WINDOW && j0h < qt.pmax - W);
+    if (dox && dov) {
+      if (mask) body(T_{}, T_{}, T_{});
+      else body(T_{}, T_{}, F_{});
+    } else if (dox) {
+      body(T_{}, F_{}, F_{});
+    } else if (dov) {
+      body(F_{}, T_{}, T_{});
     }
     wait_vmem();
     __syncthreads();
   };
 
-  load_tile(qt.kv_lo, 0);
+  load_one(tileK(0), kbase, kv_lo);
+  load_one(tileV(0), vbase, kv_lo);
   wait_vmem();
   __syncthreads();
-  for (int j0 = qt.kv_lo; j0 < qt.kv_hi; j0 += 128) {
-    step(BufTag<0>{}, j0);
-    if (j0 + 64 < qt.kv_hi) step(BufTag<1>{}, j0 + 64);
+  step(BufTag<1>{}, BufTag<1>{}, -1);  // S / dP of half (0, 0); copies V(1)
+  for (int t = 0; t < nt; t += 2) {
+    step(BufTag<0>{}, BufTag<0>{}, t);
+    step(BufTag<0>{}, BufTag<1>{}, t);
+    if (t + 1 < nt) {
+      step(BufTag<1>{}, BufTag<0>{}, t + 1);
+      step(BufTag<1>{}, BufTag<1>{}, t + 1);
+    }
   }
 
-  if (qt.valid) {
-    bf16* dqrow = a.dq + (qt.t * a.hq + hq) * D;
+  agpr_acc_drain();
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
+  for (int b = 0; b < 2; ++b) {
+    if (vr[b]) {
+      const int64_t tok = qt.rv.token(rr[b]);
+      bf16* dqrow = a.dq + (tok * a.hq + hq) * D;
 #pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) {
-        bf16x4 v;
+      for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = (bf16)(dqacc[dt][4 * q4 + e] * a.scale);
-        *reinterpret_cast<bf16x4*>(dqrow + 32 * dt + 8 * q4 + 4 * g) = v;
-      }
+        for (int q4 = 0; q4 < 4; ++q4) {
+          bf16x4 v;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = (bf16)(dqacc[b][dt][4 * q4 + e] * a.scale);
+          *reinterpret_cast<bf16x4*>(dqrow + 32 * dt + 8 * q4 + 4 * g) = v;
+        }
+    }
   }
 }
 
@@ -812,10 +971,10 @@ static int launch_fwd(const AttnArgs& a, hipStream_t st) {
   const int64_t ntmax = (a.n + kBQ - 1) / kBQ + a.nseq;
   const int64_t nblk = ntmax * a.hq;
   LOGO_REQUIRE(nblk < ((int64_t)1 << 31), "grid too large");
-  auto kern = sq_fwd_kernel<D, SPARSE, WINDOW>;
+  auto kern = sq_fwd_pipe_kernel<D, SPARSE, WINDOW>;
   LOGO_HIP_CHECK(allow_smem(kern, fwd_smem<D>()));
   hipLaunchKernelGGL(kern, dim3((unsigned)nblk), dim3(256), fwd_smem<D>(), st, a);
-  LOGO_LAUNCH_CHECK("sq_fwd_kernel");
+  LOGO_LAUNCH_CHECK("sq_fwd_pipe_kernel");
   return LOGO_OK;
 }
 
@@ -830,10 +989,10 @@ static int launch_bwd_phase(const AttnArgs& a, hipStream_t st, int phase) {
   }
   if (phase < 0 || phase == 1) {
     const int64_t ntmax = (a.n + kBQ - 1) / kBQ + a.nseq;
-    auto kern = sq_dq_kernel<D, SPARSE, WINDOW>;
+    auto kern = sq_dq64_kernel<D, SPARSE, WINDOW>;
     LOGO_HIP_CHECK(allow_smem(kern, dq_smem<D>()));
-    hipLaunchKernelGGL(kern, dim3((unsigned)(ntmax * a.hq)), dim3(256), dq_smem<D>(), st, a);
-    LOGO_LAUNCH_CHECK("sq_dq_kernel");
+    hipLaunchKernelGGL(kern, dim3((unsigned)(ntmax * a.hq)), dim3(128), dq_smem<D>(), st, a);
+    LOGO_LAUNCH_CHECK("sq_dq64_kernel");
   }
   if (phase < 0 || phase == 2) {
     const int64_t ntmax = (a.n + kBKV - 1) / kBKV + a.nseq;
