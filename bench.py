@@ -70,6 +70,7 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seed", type=int, default=2)
     ap.add_argument("--no-extra", action="store_true", help="skip the secondary measurements")
+    ap.add_argument("--no-decode", action="store_true", help="skip the config-5 model decode measurement")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run one 1 GiB device-to-device copy before the workload (the reference kernel "
                          "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters to bytes)")
@@ -263,6 +264,73 @@ def extra_measurements(dev):
     return out
 
 
+def decode_model_measurement(dev, batch=32, prompt=16384, steps=256, seed=4):
+    """the LoGo 1.5B shapes (24 layers, hidden 2048, 16 heads,
+    vocab 32000, tied embeddings), random-init bf16, a batch of random-id
+    prompts, then greedy decode steps through the preallocated cache and the
+    gate-aware decode kernel.  tok/s counts decode steps only (prefill is timed
+    separately); every decode step runs the whole model (projections and MLP
+    through torch / hipBLASLt, attention, cache and epilogue through this
+    package's kernels), launched eagerly from Python."""
+    from logo_amd.layers import LoGoConfig
+    from logo_amd.model import LoGoForCausalLM
+
+    cfg = LoGoConfig(vocab_size=32000, hidden_size=2048, intermediate_size=5632, num_hidden_layers=24,
+                     num_attention_heads=16, window_size=128, global_qk_param="linear_proj",
+                     use_context_norm=True, gate_thres_init=0.5, sparse_full_attn_backend="hip")
+    gen = torch.Generator()
+    gen.manual_seed(seed)
+    model = LoGoForCausalLM(cfg)
+    model.init_weights(gen)
+    model = model.to(device=dev, dtype=torch.bfloat16).eval()
+    params = sum(p.numel() for p in model.parameters())
+    ids = torch.randint(0, cfg.vocab_size, (batch, prompt), generator=gen).to(dev)
+    cache = model.new_cache(batch, prompt + steps + 1, device=dev)
+
+    # realised global ratio: gate decisions of every layer at the first decode step
+    gates = []
+    hooks = [layer.self_attn.gate_proj.register_forward_hook(lambda m_, i_, o_: gates.append(torch.sigmoid(o_)))
+             for layer in model.model.layers]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    tok = model.prefill(ids, cache).argmax(-1)
+    torch.cuda.synchronize()
+    prefill_s = time.perf_counter() - t0
+    gates.clear()
+    tok = model.decode_step(tok, cache).argmax(-1)
+    for hk in hooks:
+        hk.remove()
+    thres = float(cfg.gate_thres_init)
+    active = [float((gt.float() >= thres).float().mean()) for gt in gates[:cfg.num_hidden_layers]]
+    ratio = float(np.mean(active))
+    torch.cuda.synchronize()
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(steps):
+        tok = model.decode_step(tok, cache).argmax(-1)
+    b.record()
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b)
+    H, D, L = cfg.num_attention_heads, cfg.head_dim, cfg.num_hidden_layers
+    ctx = prompt + 1 + steps // 2  # mean cached length over the timed steps
+    per_step_bytes = (L * (batch * H * (cfg.window_size + 1) * D * 2 * 2 + ratio * batch * H * ctx * D * 2 * 2)
+                      + 2 * params)
+    step_ms = ms / steps
+    return {
+        "tok_s": round(batch * steps / (ms * 1e-3), 1),
+        "ms_per_step": round(step_ms, 3),
+        "prefill_s": round(prefill_s, 3),
+        "batch": batch, "prompt": prompt, "steps": steps,
+        "global_ratio": round(ratio, 4),
+        "params": params,
+        "est_hbm_bytes_per_step": int(per_step_bytes),
+        "est_gbs": round(per_step_bytes / (step_ms * 1e-3) / 1e9, 1),
+        "roofline_tok_s": round(batch / (per_step_bytes / (HBM_PEAK_GBS * 1e9)), 1),
+        "data": "synthetic random ids, random-init weights",
+    }
+
+
 def main():
     args = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -346,6 +414,8 @@ def main():
         cpu = cpu_baseline(q, k, v, sel_np, [0, T], do, min(args.cpu_heads, H), f_step / H)
 
     extra = None if args.no_extra else extra_measurements(dev)
+    if not args.no_extra and not args.no_decode:
+        extra["decode_cfg5_model"] = decode_model_measurement(dev)
 
     line = {
         "metric": "sq_full_attn fwd+bwd effective TFLOP/s @T=32K, 25% global; decode tok/s",

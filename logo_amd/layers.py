@@ -110,8 +110,14 @@ def apply_rope(x, cos, sin):
 
 
 def _per_head_linear(x, w):
-    """``x [..., H, D] @ w [H, D, E]`` per head with 2-D GEMMs."""
-    return torch.stack([x[..., h, :] @ w[h] for h in range(w.shape[0])], dim=-2)
+    """``x [..., H, D] @ w [H, D, E]`` per head as one batched GEMM over heads
+    (both operands contiguous: bf16 batched products are only used with
+    contiguous right operands here)."""
+    lead = x.shape[:-2]
+    H, D = x.shape[-2], x.shape[-1]
+    xh = x.reshape(-1, H, D).transpose(0, 1).contiguous()  # [H, N, D]
+    y = torch.bmm(xh, w.to(x.dtype).contiguous())  # [H, N, E]
+    return y.transpose(0, 1).reshape(*lead, H, w.shape[-1])
 
 
 class LoGoAttention(nn.Module):

@@ -1,0 +1,155 @@
+"""Minimal LoGo causal LM around the HIP attention path, for decode with a KV cache.
+
+Counterpart of ``LoGoForCausalLM`` (logo/modeling_logo.py:308-380) with the
+decoder stack of :42-106 and :136-275 (pre-norm RMSNorm layers, SwiGLU MLP
+logo/modules/mlp.py:10-27, final RMSNorm, tied or separate LM head).  Parameter
+names follow the reference so its state dict loads.  It exists to drive the
+prefill + greedy decode workload through ``LoGoAttention``
+and ``LogoKVCache``: the preallocated cache replaces the reference's
+``torch.cat`` growth (logo/cache.py:115-118) and the gate-aware decode kernel
+its dense ``active.any()`` branch (logo/layers/logo.py:228-249).
+
+Out of scope here, as for the rest of this package: training losses, the HF
+``generate`` machinery, sampling strategies other than greedy, and the budget
+controller (logo/update.py).
+"""
+
+import math
+from typing import Optional
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from .layers import LoGoAttention, LoGoConfig, RMSNorm
+from .ops.decode import LogoKVCache
+
+__all__ = ["LoGoMLP", "LoGoDecoderLayer", "LoGoModel", "LoGoForCausalLM"]
+
+
+class LoGoMLP(nn.Module):
+    """SwiGLU feed-forward (logo/modules/mlp.py:10-27, ``hidden_act = silu``)."""
+
+    def __init__(self, config: LoGoConfig):
+        super().__init__()
+        self.gate_proj = nn.Linear(config.hidden_size, config.intermediate_size, bias=False)
+        self.up_proj = nn.Linear(config.hidden_size, config.intermediate_size, bias=False)
+        self.down_proj = nn.Linear(config.intermediate_size, config.hidden_size, bias=False)
+
+    def forward(self, x):
+        return self.down_proj(F.silu(self.gate_proj(x)) * self.up_proj(x))
+
+
+class LoGoDecoderLayer(nn.Module):
+    """Pre-norm attention + MLP block (logo/modeling_logo.py:42-106)."""
+
+    def __init__(self, config: LoGoConfig, layer_idx: int):
+        super().__init__()
+        self.self_attn = LoGoAttention(config, layer_idx)
+        self.mlp = LoGoMLP(config)
+        self.input_layernorm = RMSNorm(config.hidden_size, eps=config.rms_norm_eps)
+        self.post_attention_layernorm = RMSNorm(config.hidden_size, eps=config.rms_norm_eps)
+
+    def forward(self, hidden_states, cu_seqlens=None, past_key_value: Optional[LogoKVCache] = None):
+        residual = hidden_states
+        h = self.input_layernorm(hidden_states)
+        h, _, _ = self.self_attn(h, cu_seqlens=cu_seqlens, past_key_value=past_key_value)
+        hidden_states = residual + h
+        residual = hidden_states
+        h = self.mlp(self.post_attention_layernorm(hidden_states))
+        return residual + h
+
+
+class LoGoModel(nn.Module):
+    """Embedding, decoder layers and the final norm (logo/modeling_logo.py:136-275)."""
+
+    def __init__(self, config: LoGoConfig):
+        super().__init__()
+        self.config = config
+        self.embed_tokens = nn.Embedding(config.vocab_size, config.hidden_size)
+        self.layers = nn.ModuleList([LoGoDecoderLayer(config, i) for i in range(config.num_hidden_layers)])
+        self.norm = RMSNorm(config.hidden_size, eps=config.rms_norm_eps)
+
+    def forward(self, input_ids, cu_seqlens=None, past_key_value: Optional[LogoKVCache] = None):
+        h = self.embed_tokens(input_ids)
+        for layer in self.layers:
+            h = layer(h, cu_seqlens=cu_seqlens, past_key_value=past_key_value)
+        return self.norm(h)
+
+
+class LoGoForCausalLM(nn.Module):
+    """Causal LM head over ``LoGoModel`` (logo/modeling_logo.py:308-380)."""
+
+    def __init__(self, config: LoGoConfig):
+        super().__init__()
+        self.config = config
+        self.model = LoGoModel(config)
+        self.lm_head = nn.Linear(config.hidden_size, config.vocab_size, bias=False)
+        if config.tie_word_embeddings:
+            self.lm_head.weight = self.model.embed_tokens.weight
+
+    @torch.no_grad()
+    def init_weights(self, generator: Optional[torch.Generator] = None):
+        """Random init as ``post_init`` / ``_init_weights`` do
+        (logo/modeling_logo.py:117-133): Linear ~ N(0, initializer_range), with
+        std / sqrt(2 L) for o_proj and down_proj; Embedding ~ N(0, 1 / (2 hidden));
+        norms at one and the global ``linear_proj`` matrices at identity (they
+        are not Linear modules).  A tied LM head keeps the embedding's values."""
+        c = self.config
+        std = c.initializer_range
+        out_std = std / math.sqrt(2 * c.num_hidden_layers)
+        tied = self.lm_head.weight is self.model.embed_tokens.weight
+        for name, mod in self.named_modules():
+            if isinstance(mod, nn.Embedding):
+                mod.weight.normal_(0.0, math.sqrt(1.0 / (2 * c.hidden_size)), generator=generator)
+            elif isinstance(mod, nn.Linear):
+                if tied and mod is self.lm_head:
+                    continue
+                s = out_std if name.endswith(("o_proj", "down_proj")) else std
+                mod.weight.normal_(0.0, s, generator=generator)
+                if mod.bias is not None:
+                    mod.bias.zero_()
+
+    def new_cache(self, batch: int, max_len: int, device=None) -> LogoKVCache:
+        c = self.config
+        return LogoKVCache(c.num_hidden_layers, batch, c.num_key_value_heads, c.head_dim, max_len,
+                           window=c.window_size, device=device)
+
+    def forward(self, input_ids, cu_seqlens=None, past_key_value: Optional[LogoKVCache] = None,
+                last_only: bool = False):
+        """Logits ``[B, T, V]`` (or ``[B, V]`` of the last position with
+        ``last_only``: a 16K-token prompt batch would otherwise materialise
+        tens of GB of logits)."""
+        h = self.model(input_ids, cu_seqlens=cu_seqlens, past_key_value=past_key_value)
+        if last_only:
+            h = h[:, -1]
+        return self.lm_head(h)
+
+    @torch.no_grad()
+    def prefill(self, input_ids, cache: LogoKVCache):
+        """Run the prompt ``[B, T]`` through the model, filling ``cache``; returns
+        the last position's logits ``[B, V]``."""
+        logits = self.forward(input_ids, past_key_value=cache, last_only=True)
+        cache.set_length(input_ids.shape[1])
+        return logits
+
+    @torch.no_grad()
+    def decode_step(self, tokens, cache: LogoKVCache):
+        """One decode step for ``tokens [B]`` at position ``cache.seen``;
+        returns logits ``[B, V]``."""
+        logits = self.forward(tokens[:, None], past_key_value=cache, last_only=True)
+        cache.set_length(cache.seen + 1)
+        return logits
+
+    @torch.no_grad()
+    def greedy_generate(self, input_ids, max_new_tokens: int, cache: Optional[LogoKVCache] = None):
+        """Greedy decoding: returns the generated tokens ``[B, max_new_tokens]``."""
+        B, T = input_ids.shape
+        if cache is None:
+            cache = self.new_cache(B, T + max_new_tokens, device=input_ids.device)
+        tok = self.prefill(input_ids, cache).argmax(-1)
+        out = [tok]
+        for _ in range(max_new_tokens - 1):
+            tok = self.decode_step(tok, cache).argmax(-1)
+            out.append(tok)
+        return torch.stack(out, dim=1)
