@@ -271,7 +271,8 @@ def decode_model_measurement(dev, batch=32, prompt=16384, steps=256, seed=4):
     gate-aware decode kernel.  tok/s counts decode steps only (prefill is timed
     separately); every decode step runs the whole model (projections and MLP
     through torch / hipBLASLt, attention, cache and epilogue through this
-    package's kernels), launched eagerly from Python."""
+    package's kernels).  The timed steps replay one captured decode step (HIP
+    graph); a few eager, Python-launched steps are timed beside them."""
     from logo_amd.layers import LoGoConfig
     from logo_amd.model import LoGoForCausalLM
 
@@ -285,7 +286,7 @@ def decode_model_measurement(dev, batch=32, prompt=16384, steps=256, seed=4):
     model = model.to(device=dev, dtype=torch.bfloat16).eval()
     params = sum(p.numel() for p in model.parameters())
     ids = torch.randint(0, cfg.vocab_size, (batch, prompt), generator=gen).to(dev)
-    cache = model.new_cache(batch, prompt + steps + 1, device=dev)
+    cache = model.new_cache(batch, prompt + steps + 32, device=dev)
 
     # realised global ratio: gate decisions of every layer at the first decode step
     gates = []
@@ -303,23 +304,37 @@ def decode_model_measurement(dev, batch=32, prompt=16384, steps=256, seed=4):
     thres = float(cfg.gate_thres_init)
     active = [float((gt.float() >= thres).float().mean()) for gt in gates[:cfg.num_hidden_layers]]
     ratio = float(np.mean(active))
-    torch.cuda.synchronize()
     a = torch.cuda.Event(enable_timing=True)
     b = torch.cuda.Event(enable_timing=True)
+    # eager steps (Python-launched, for reference)
+    eager_steps = 16
+    torch.cuda.synchronize()
+    a.record()
+    for _ in range(eager_steps):
+        tok = model.decode_step(tok, cache).argmax(-1)
+    b.record()
+    torch.cuda.synchronize()
+    eager_ms = a.elapsed_time(b) / eager_steps
+    # the timed steps: one captured decode step, replayed
+    step = model.capture_greedy_decode(tok, cache)
+    torch.cuda.synchronize()
     a.record()
     for _ in range(steps):
-        tok = model.decode_step(tok, cache).argmax(-1)
+        step()
     b.record()
     torch.cuda.synchronize()
     ms = a.elapsed_time(b)
     H, D, L = cfg.num_attention_heads, cfg.head_dim, cfg.num_hidden_layers
-    ctx = prompt + 1 + steps // 2  # mean cached length over the timed steps
+    ctx = prompt + 18 + steps // 2  # mean cached length over the timed steps
     per_step_bytes = (L * (batch * H * (cfg.window_size + 1) * D * 2 * 2 + ratio * batch * H * ctx * D * 2 * 2)
                       + 2 * params)
     step_ms = ms / steps
     return {
         "tok_s": round(batch * steps / (ms * 1e-3), 1),
         "ms_per_step": round(step_ms, 3),
+        "mode": "one decode step captured in a HIP graph, replayed; greedy argmax between replays",
+        "eager_tok_s": round(batch / (eager_ms * 1e-3), 1),
+        "eager_ms_per_step": round(eager_ms, 3),
         "prefill_s": round(prefill_s, 3),
         "batch": batch, "prompt": prompt, "steps": steps,
         "global_ratio": round(ratio, 4),

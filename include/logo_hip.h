@@ -195,6 +195,26 @@ int logo_cache_append(const void* k_new, const void* v_new, void* k_cache, void*
                       const int32_t* pos, int batch, int h, int d, int64_t t_cap, int ring,
                       int dtype, void* stream);
 
+/*
+ * Rotary embedding, in place, of up to four [N, H_i, D] bf16 tensors (q, k and
+ * the global q, k; a NULL tensor is skipped) with one [N, D] cos / sin pair:
+ * x' = x * cos + rotate_half(x) * sin with the eager bf16 rounding of
+ * logo/modules/rotary.py:81-106 (apply_rotary_pos_emb, rotate_half), called at
+ * logo/layers/logo.py:132-139.
+ */
+int logo_rope_apply(void* x0, int h0, void* x1, int h1, void* x2, int h2, void* x3, int h3,
+                    const void* cos, const void* sin, int64_t n_tokens, int d, int dtype,
+                    void* stream);
+
+/*
+ * RMSNorm of rows [rows, cols] bf16 with weight [cols]: y = w * bf16(x *
+ * rsqrt(mean(x^2) + eps)), mean in fp32 (logo/modules/layernorm.py:17-22; the
+ * decoder's input / post-attention / final norms, logo/modeling_logo.py:58-59,
+ * :152).  cols: a multiple of 8, at most 4096.
+ */
+int logo_rmsnorm(const void* x, const void* w, void* y, int64_t rows, int cols, float eps,
+                 int dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

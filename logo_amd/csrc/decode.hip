@@ -52,11 +52,14 @@ __global__ __launch_bounds__(256) void decode_split_kernel(const DecArgs a) {
   const int split = blockIdx.x;
   const int bq = blockIdx.y;                // b * HQ + hq
   const int b = bq / a.hq, hq = bq % a.hq, h = hq / a.g;
-  if (!dec_active(a, b)) return;
+  const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63;
   const int len = a.lens[b];
   const int k0 = split * kDecKeysPerWG;
-  if (k0 >= len) return;
-  const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63;
+  // a single split writes the output itself (no combine launch)
+  if (!dec_active(a, b) || k0 >= len) {
+    if (a.nsplit == 1 && tid < D) a.out[(int64_t)bq * D + tid] = (bf16)0.f;
+    return;
+  }
   const int c = l % CH, kk = l / CH;
   const int kw = k0 + wave * kDecKeysPerWave;
 
@@ -136,39 +139,72 @@ __global__ __launch_bounds__(256) void decode_split_kernel(const DecArgs a) {
       L += f * sl[w];
       O += f * so[w][tid];
     }
-    float* pp = a.part + ((int64_t)bq * a.nsplit + split) * (D + 2);
-    pp[2 + tid] = O;
-    if (tid == 0) {
-      pp[0] = M;
-      pp[1] = L;
+    if (a.nsplit == 1) {
+      a.out[(int64_t)bq * D + tid] = (bf16)(L > 0.f ? O / L : 0.f);
+    } else {
+      float* pp = a.part + ((int64_t)bq * a.nsplit + split) * (D + 2);
+      pp[2 + tid] = O;
+      if (tid == 0) {
+        pp[0] = M;
+        pp[1] = L;
+      }
     }
   }
 }
 
+// Merge the split partials of one (b, q-head) row: the splits' maxima and
+// sums are reduced across the 256 threads, then thread (group gi, column d)
+// sums the rescaled partial outputs of splits gi, gi + G, ... with
+// independent loads, and the groups are added through LDS.
 template <int D>
-__global__ __launch_bounds__(D) void decode_combine_kernel(const DecArgs a) {
+__global__ __launch_bounds__(256) void decode_combine_kernel(const DecArgs a) {
+  constexpr int G = 256 / D;  // split groups
   const int bq = blockIdx.x;
   const int b = bq / a.hq;
-  const int d = threadIdx.x;
+  const int tid = threadIdx.x, l = tid & 63, wave = tid >> 6;
   bf16* out = a.out + (int64_t)bq * D;
   if (!dec_active(a, b)) {
-    out[d] = (bf16)0.f;
+    if (tid < D) out[tid] = (bf16)0.f;
     return;
   }
   const int len = a.lens[b];
   const int ns = min(a.nsplit, (len + kDecKeysPerWG - 1) / kDecKeysPerWG);
   const float* pp = a.part + (int64_t)bq * a.nsplit * (D + 2);
-  float M = -INFINITY;
-  for (int s = 0; s < ns; ++s) M = fmaxf(M, pp[(int64_t)s * (D + 2)]);
+  __shared__ float red[4];
+  __shared__ float so[G][D];
+  float m = -INFINITY;
+  for (int s = tid; s < ns; s += 256) m = fmaxf(m, pp[(int64_t)s * (D + 2)]);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+  if (l == 0) red[wave] = m;
+  __syncthreads();
+  const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
   const float Mb = M == -INFINITY ? 0.f : M;
-  float L = 0.f, O = 0.f;
-  for (int s = 0; s < ns; ++s) {
+  __syncthreads();
+  float lsum = 0.f;
+  for (int s = tid; s < ns; s += 256) {
     const float* ps = pp + (int64_t)s * (D + 2);
-    const float f = fast_exp2(ps[0] - Mb);
-    L += f * ps[1];
-    O += f * ps[2 + d];
+    lsum += fast_exp2(ps[0] - Mb) * ps[1];
   }
-  out[d] = (bf16)(L > 0.f ? O / L : 0.f);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) lsum += __shfl_xor(lsum, off);
+  if (l == 0) red[wave] = lsum;
+  const int gi = tid / D, d = tid % D;
+  float o = 0.f;
+#pragma unroll 4
+  for (int s = gi; s < ns; s += G) {
+    const float* ps = pp + (int64_t)s * (D + 2);
+    o = fmaf(fast_exp2(ps[0] - Mb), ps[2 + d], o);
+  }
+  so[gi][d] = o;
+  __syncthreads();
+  if (tid < D) {
+    const float L = red[0] + red[1] + red[2] + red[3];
+    float O = 0.f;
+#pragma unroll
+    for (int k = 0; k < G; ++k) O += so[k][tid];
+    out[tid] = (bf16)(L > 0.f ? O / L : 0.f);
+  }
 }
 
 // Write one new key/value row per (b, h) at position pos[b] (mod ring if > 0).
@@ -228,16 +264,18 @@ extern "C" int logo_decode_attn(const void* q, const void* k_cache, const void* 
   a.scale_log2 = scale * 1.4426950408889634f;
   hipStream_t st = as_stream(stream);
   dim3 grid(a.nsplit, batch * hq);
-  if (d == 128) {
+  if (d == 128)
     hipLaunchKernelGGL(decode_split_kernel<128>, grid, dim3(256), 0, st, a);
-    LOGO_LAUNCH_CHECK("decode_split_kernel");
-    hipLaunchKernelGGL(decode_combine_kernel<128>, dim3(batch * hq), dim3(128), 0, st, a);
-  } else {
+  else
     hipLaunchKernelGGL(decode_split_kernel<64>, grid, dim3(256), 0, st, a);
-    LOGO_LAUNCH_CHECK("decode_split_kernel");
-    hipLaunchKernelGGL(decode_combine_kernel<64>, dim3(batch * hq), dim3(64), 0, st, a);
+  LOGO_LAUNCH_CHECK("decode_split_kernel");
+  if (a.nsplit > 1) {  // a single split wrote the output already
+    if (d == 128)
+      hipLaunchKernelGGL(decode_combine_kernel<128>, dim3(batch * hq), dim3(256), 0, st, a);
+    else
+      hipLaunchKernelGGL(decode_combine_kernel<64>, dim3(batch * hq), dim3(256), 0, st, a);
+    LOGO_LAUNCH_CHECK("decode_combine_kernel");
   }
-  LOGO_LAUNCH_CHECK("decode_combine_kernel");
   return LOGO_OK;
 }
 

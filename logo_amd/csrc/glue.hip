@@ -1,0 +1,166 @@
+// Fused glue of the LoGo layer and model for gfx950: rotary embedding and
+// RMSNorm, each in one launch instead of a chain of eager element-wise ops.
+//
+// RoPE (logo/modules/rotary.py:81-106): x' = bf16(bf16(x * cos) +
+// bf16(rotate_half(x) * sin)) with rotate_half(x) = [-x2, x1], the rounding
+// points of the reference's eager bf16 ops kept (products of two bf16 values
+// are exact in fp32, so each rounds exactly as the eager op does).  Up to four
+// [N, H_i, D] tensors (q, k and the global q, k) are rotated in place with one
+// [N, D] cos / sin pair.
+//
+// RMSNorm (logo/modules/layernorm.py:17-22): y = bf16(w * bf16(x *
+// rsqrt(mean(x^2) + eps))), the mean taken in fp32.
+#include <math.h>
+
+#include "capi.hpp"
+#include "common.hpp"
+
+// every product and sum rounds as its own eager bf16 op (no fma contraction)
+#pragma clang fp contract(off)
+
+namespace logo {
+
+struct RopeArgs {
+  bf16* x[4];
+  int heads[4];
+  int nt;  // tensors in use
+  const bf16* cos;
+  const bf16* sin;
+  int64_t n;  // rows (tokens)
+};
+
+__device__ __forceinline__ float bfr_g(float x) { return (float)(bf16)x; }
+
+// One thread per (tensor, token, head, 8-element chunk of the first half):
+// it rotates the pair of chunks (c, c + D/16) together.
+template <int D>
+__global__ __launch_bounds__(256) void rope_kernel(const RopeArgs a, int64_t per_tensor_max) {
+  constexpr int HC = D / 16;  // chunks of 8 in each half
+  const int ti = blockIdx.y;
+  if (ti >= a.nt) return;
+  const int H = a.heads[ti];
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t total = a.n * H * HC;
+  if (idx >= total || idx >= per_tensor_max) return;
+  const int c = (int)(idx % HC);
+  const int64_t row = idx / HC;  // token * H + head
+  const int64_t tok = row / H;
+  bf16* xr = a.x[ti] + row * D;
+  const bf16x8 x1 = *reinterpret_cast<const bf16x8*>(xr + 8 * c);
+  const bf16x8 x2 = *reinterpret_cast<const bf16x8*>(xr + D / 2 + 8 * c);
+  const bf16x8 c1 = *reinterpret_cast<const bf16x8*>(a.cos + tok * D + 8 * c);
+  const bf16x8 c2 = *reinterpret_cast<const bf16x8*>(a.cos + tok * D + D / 2 + 8 * c);
+  const bf16x8 s1 = *reinterpret_cast<const bf16x8*>(a.sin + tok * D + 8 * c);
+  const bf16x8 s2 = *reinterpret_cast<const bf16x8*>(a.sin + tok * D + D / 2 + 8 * c);
+  bf16x8 y1, y2;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    // first half:  x1 * cos1 + (-x2) * sin1;  second half: x2 * cos2 + x1 * sin2
+    const float a1 = bfr_g((float)x1[e] * (float)c1[e]);
+    const float b1 = bfr_g(-(float)x2[e] * (float)s1[e]);
+    const float a2 = bfr_g((float)x2[e] * (float)c2[e]);
+    const float b2 = bfr_g((float)x1[e] * (float)s2[e]);
+    y1[e] = (bf16)(a1 + b1);
+    y2[e] = (bf16)(a2 + b2);
+  }
+  *reinterpret_cast<bf16x8*>(xr + 8 * c) = y1;
+  *reinterpret_cast<bf16x8*>(xr + D / 2 + 8 * c) = y2;
+}
+
+// One wave per row; rows of `cols` bf16 (a multiple of 8, at most 64 * 8 * 8).
+template <int VPL>
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const bf16* x, const bf16* w, bf16* y, int64_t rows,
+                                                      int cols, float eps) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int l = threadIdx.x & 63;
+  if (row >= rows) return;
+  const bf16* xr = x + row * cols;
+  bf16x8 v[VPL];
+  float ss = 0.f;
+#pragma unroll
+  for (int k = 0; k < VPL; ++k) {
+    const int col = 8 * (l + 64 * k);
+    v[k] = col < cols ? *reinterpret_cast<const bf16x8*>(xr + col) : bf16x8{};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss = fmaf((float)v[k][e], (float)v[k][e], ss);
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+  const float r = rsqrtf(ss / (float)cols + eps);
+#pragma unroll
+  for (int k = 0; k < VPL; ++k) {
+    const int col = 8 * (l + 64 * k);
+    if (col < cols) {
+      const bf16x8 wv = *reinterpret_cast<const bf16x8*>(w + col);
+      bf16x8 o;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = (bf16)((float)wv[e] * bfr_g((float)v[k][e] * r));
+      *reinterpret_cast<bf16x8*>(y + row * cols + col) = o;
+    }
+  }
+}
+
+}  // namespace logo
+
+using namespace logo;
+
+extern "C" int logo_rope_apply(void* x0, int h0, void* x1, int h1, void* x2, int h2, void* x3, int h3,
+                               const void* cos, const void* sin, int64_t n_tokens, int d, int dtype,
+                               void* stream) {
+  LOGO_REQUIRE(d == 64 || d == 128, "head dim %d unsupported (64 or 128)", d);
+  LOGO_REQUIRE(dtype == LOGO_DTYPE_BF16, "only bf16 tensors are supported");
+  LOGO_REQUIRE(n_tokens >= 0, "n_tokens must be >= 0");
+  LOGO_REQUIRE(cos && sin, "null cos / sin");
+  RopeArgs a{};
+  void* xs[4] = {x0, x1, x2, x3};
+  const int hs[4] = {h0, h1, h2, h3};
+  int hmax = 0;
+  for (int i = 0; i < 4; ++i) {
+    if (xs[i] == nullptr) continue;
+    LOGO_REQUIRE(hs[i] >= 1, "tensor %d: heads must be >= 1", i);
+    a.x[a.nt] = static_cast<bf16*>(xs[i]);
+    a.heads[a.nt] = hs[i];
+    ++a.nt;
+    hmax = hs[i] > hmax ? hs[i] : hmax;
+  }
+  if (a.nt == 0 || n_tokens == 0) return LOGO_OK;
+  a.cos = static_cast<const bf16*>(cos);
+  a.sin = static_cast<const bf16*>(sin);
+  a.n = n_tokens;
+  const int64_t per = n_tokens * hmax * (d / 16);
+  const int64_t nblk = (per + 255) / 256;
+  LOGO_REQUIRE(nblk < ((int64_t)1 << 31), "too many rows");
+  hipStream_t st = as_stream(stream);
+  if (d == 128)
+    hipLaunchKernelGGL(rope_kernel<128>, dim3((unsigned)nblk, a.nt), dim3(256), 0, st, a, per);
+  else
+    hipLaunchKernelGGL(rope_kernel<64>, dim3((unsigned)nblk, a.nt), dim3(256), 0, st, a, per);
+  LOGO_LAUNCH_CHECK("rope_kernel");
+  return LOGO_OK;
+}
+
+extern "C" int logo_rmsnorm(const void* x, const void* w, void* y, int64_t rows, int cols, float eps, int dtype,
+                            void* stream) {
+  LOGO_REQUIRE(dtype == LOGO_DTYPE_BF16, "only bf16 tensors are supported");
+  LOGO_REQUIRE(rows >= 0, "rows must be >= 0");
+  LOGO_REQUIRE(cols >= 8 && cols % 8 == 0 && cols <= 64 * 8 * 8, "cols must be a multiple of 8 in [8, 4096]");
+  LOGO_REQUIRE(x && w && y, "null pointer argument");
+  if (rows == 0) return LOGO_OK;
+  const int64_t nblk = (rows + 3) / 4;
+  LOGO_REQUIRE(nblk < ((int64_t)1 << 31), "too many rows");
+  hipStream_t st = as_stream(stream);
+  const int vpl = (cols + 511) / 512;
+  const auto xb = static_cast<const bf16*>(x);
+  const auto wb = static_cast<const bf16*>(w);
+  const auto yb = static_cast<bf16*>(y);
+  if (vpl <= 1)
+    hipLaunchKernelGGL(rmsnorm_kernel<1>, dim3((unsigned)nblk), dim3(256), 0, st, xb, wb, yb, rows, cols, eps);
+  else if (vpl <= 2)
+    hipLaunchKernelGGL(rmsnorm_kernel<2>, dim3((unsigned)nblk), dim3(256), 0, st, xb, wb, yb, rows, cols, eps);
+  else if (vpl <= 4)
+    hipLaunchKernelGGL(rmsnorm_kernel<4>, dim3((unsigned)nblk), dim3(256), 0, st, xb, wb, yb, rows, cols, eps);
+  else
+    hipLaunchKernelGGL(rmsnorm_kernel<8>, dim3((unsigned)nblk), dim3(256), 0, st, xb, wb, yb, rows, cols, eps);
+  LOGO_LAUNCH_CHECK("rmsnorm_kernel");
+  return LOGO_OK;
+}

@@ -28,9 +28,10 @@ import torch.nn.functional as F
 
 from .ops.decode import LogoKVCache, decode_attn
 from .ops.epilogue import logo_epilogue
+from .ops.glue import rms_norm, rope_apply_
 from .ops.sq_attn import dense_causal_attn, sq_full_attn, swa_attn
 
-__all__ = ["LoGoConfig", "LoGoAttention", "RMSNorm", "rope_cos_sin", "apply_rope"]
+__all__ = ["LoGoConfig", "LoGoAttention", "RMSNorm", "rope_cos_sin", "apply_rope", "position_ids_for"]
 
 SPARSE_BACKENDS = ("triton", "hip")
 
@@ -85,10 +86,36 @@ class RMSNorm(nn.Module):
         self.variance_epsilon = eps
 
     def forward(self, x):
+        if _fused_ok(x, self.weight):  # one HIP launch (inference on ROCm tensors)
+            return rms_norm(x, self.weight, self.variance_epsilon)
         dt = x.dtype
         xf = x.to(torch.float32)
         xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.variance_epsilon)
         return self.weight * xf.to(dt)
+
+
+def _fused_ok(*tensors) -> bool:
+    """The fused glue kernels (no autograd) serve bf16 ROCm tensors that need
+    no gradient; anything else takes the plain torch ops."""
+    if any(t.requires_grad for t in tensors) and torch.is_grad_enabled():
+        return False
+    return all(t.is_cuda and t.dtype == torch.bfloat16 for t in tensors)
+
+
+def position_ids_for(B: int, T: int, device, cu_seqlens=None, cache: Optional[LogoKVCache] = None):
+    """Positions ``[B, T]`` of the tokens being processed: restarting at every
+    packed segment (logo/modeling_logo.py:207-222), continuing a cache, or from
+    zero.  A one-token decode step reads the cache's device position (no host
+    value, so the step can be captured in a graph)."""
+    if cu_seqlens is not None:
+        idx = torch.arange(B * T, device=device)
+        cu64 = cu_seqlens.to(device=device, dtype=torch.int64)
+        seg = torch.searchsorted(cu64, idx, right=True) - 1
+        return (idx - cu64[seg]).view(B, T)
+    if cache is not None and T == 1:
+        return cache.positions(T)
+    start = cache.get_seq_length() if cache is not None else 0
+    return torch.arange(start, start + T, device=device)[None].expand(B, T)
 
 
 def rope_cos_sin(positions: torch.Tensor, head_dim: int, theta: float, dtype):
@@ -117,7 +144,7 @@ def _per_head_linear(x, w):
     H, D = x.shape[-2], x.shape[-1]
     xh = x.reshape(-1, H, D).transpose(0, 1).contiguous()  # [H, N, D]
     y = torch.bmm(xh, w.to(x.dtype).contiguous())  # [H, N, E]
-    return y.transpose(0, 1).reshape(*lead, H, w.shape[-1])
+    return y.transpose(0, 1).reshape(*lead, H, w.shape[-1]).contiguous()
 
 
 class LoGoAttention(nn.Module):
@@ -191,7 +218,7 @@ class LoGoAttention(nn.Module):
         return ((1 - g) * local.reshape(B, T, -1) + g * glob.reshape(B, T, -1))
 
     def forward(self, hidden_states, position_ids=None, cu_seqlens=None,
-                past_key_value: Optional[LogoKVCache] = None, **kwargs):
+                past_key_value: Optional[LogoKVCache] = None, position_embeddings=None, **kwargs):
         B, T, _ = hidden_states.shape
         H, HK, D = self.num_heads, self.num_key_value_heads, self.head_dim
         q = self.q_proj(hidden_states).view(B, T, H, D)
@@ -200,20 +227,17 @@ class LoGoAttention(nn.Module):
         gq, gk, gv = self._global_qkv(q, k, v)
         gate = torch.sigmoid(self.gate_proj(hidden_states))  # [B, T, 1]
 
-        if position_ids is None:
-            dev = hidden_states.device
-            if cu_seqlens is not None:
-                # positions restart at every packed segment (logo/modeling_logo.py:207-222)
-                idx = torch.arange(B * T, device=dev)
-                cu64 = cu_seqlens.to(device=dev, dtype=torch.int64)
-                seg = torch.searchsorted(cu64, idx, right=True) - 1
-                position_ids = (idx - cu64[seg]).view(B, T)
-            else:
-                start = past_key_value.get_seq_length() if past_key_value is not None else 0
-                position_ids = torch.arange(start, start + T, device=dev)[None].expand(B, T)
-        cos, sin = rope_cos_sin(position_ids, D, self.config.rope_theta, q.dtype)
-        q, k = apply_rope(q, cos, sin), apply_rope(k, cos, sin)
-        gq, gk = apply_rope(gq, cos, sin), apply_rope(gk, cos, sin)
+        if position_embeddings is not None:
+            cos, sin = position_embeddings
+        else:
+            if position_ids is None:
+                position_ids = position_ids_for(B, T, hidden_states.device, cu_seqlens, past_key_value)
+            cos, sin = rope_cos_sin(position_ids, D, self.config.rope_theta, q.dtype)
+        if _fused_ok(q, k, gq, gk, cos, sin) and all(t.is_contiguous() for t in (q, k, gq, gk)):
+            rope_apply_([q, k, gq, gk], cos, sin)  # in place, one launch
+        else:
+            q, k = apply_rope(q, cos, sin), apply_rope(k, cos, sin)
+            gq, gk = apply_rope(gq, cos, sin), apply_rope(gk, cos, sin)
 
         if past_key_value is not None and T == 1:
             out = self._decode(q, k, v, gq, gk, gv, gate, past_key_value)
@@ -250,9 +274,10 @@ class LoGoAttention(nn.Module):
     def _decode(self, q, k, v, gq, gk, gv, gate, cache: LogoKVCache):
         B, _, H, D = q.shape
         cache.append(self.layer_idx, k[:, 0], v[:, 0], gk[:, 0], gv[:, 0])
-        len_g, len_l = cache.lengths()
+        len_g, len_l = cache.step_lengths()
+        bound_g, bound_l = cache.length_bounds()
         local = decode_attn(q[:, 0], cache.local_k[self.layer_idx], cache.local_v[self.layer_idx], len_l,
-                            max_len=min(cache.seen + 1, cache.ring))
+                            max_len=bound_l)
         glob = decode_attn(gq[:, 0], cache.global_k[self.layer_idx], cache.global_v[self.layer_idx], len_g,
-                           gate.view(B), self.gate_thres, max_len=cache.seen + 1)
+                           gate.view(B), self.gate_thres, max_len=bound_g)
         return self._fuse(local.view(B, 1, H, D), glob.view(B, 1, H, D), gate.view(B, 1))

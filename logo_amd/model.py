@@ -21,7 +21,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from .layers import LoGoAttention, LoGoConfig, RMSNorm
+from .layers import LoGoAttention, LoGoConfig, RMSNorm, position_ids_for, rope_cos_sin
 from .ops.decode import LogoKVCache
 
 __all__ = ["LoGoMLP", "LoGoDecoderLayer", "LoGoModel", "LoGoForCausalLM"]
@@ -50,10 +50,12 @@ class LoGoDecoderLayer(nn.Module):
         self.input_layernorm = RMSNorm(config.hidden_size, eps=config.rms_norm_eps)
         self.post_attention_layernorm = RMSNorm(config.hidden_size, eps=config.rms_norm_eps)
 
-    def forward(self, hidden_states, cu_seqlens=None, past_key_value: Optional[LogoKVCache] = None):
+    def forward(self, hidden_states, cu_seqlens=None, past_key_value: Optional[LogoKVCache] = None,
+                position_embeddings=None):
         residual = hidden_states
         h = self.input_layernorm(hidden_states)
-        h, _, _ = self.self_attn(h, cu_seqlens=cu_seqlens, past_key_value=past_key_value)
+        h, _, _ = self.self_attn(h, cu_seqlens=cu_seqlens, past_key_value=past_key_value,
+                                 position_embeddings=position_embeddings)
         hidden_states = residual + h
         residual = hidden_states
         h = self.mlp(self.post_attention_layernorm(hidden_states))
@@ -72,8 +74,12 @@ class LoGoModel(nn.Module):
 
     def forward(self, input_ids, cu_seqlens=None, past_key_value: Optional[LogoKVCache] = None):
         h = self.embed_tokens(input_ids)
+        B, T = input_ids.shape
+        # rotary cos / sin once for all layers (logo/modeling_logo.py:233-234)
+        pos = position_ids_for(B, T, input_ids.device, cu_seqlens, past_key_value)
+        pe = rope_cos_sin(pos, self.config.head_dim, self.config.rope_theta, h.dtype)
         for layer in self.layers:
-            h = layer(h, cu_seqlens=cu_seqlens, past_key_value=past_key_value)
+            h = layer(h, cu_seqlens=cu_seqlens, past_key_value=past_key_value, position_embeddings=pe)
         return self.norm(h)
 
 
@@ -138,8 +144,45 @@ class LoGoForCausalLM(nn.Module):
         """One decode step for ``tokens [B]`` at position ``cache.seen``;
         returns logits ``[B, V]``."""
         logits = self.forward(tokens[:, None], past_key_value=cache, last_only=True)
-        cache.set_length(cache.seen + 1)
+        cache.advance()
         return logits
+
+    @torch.no_grad()
+    def capture_greedy_decode(self, tokens, cache: LogoKVCache):
+        """Capture one decode step into a HIP graph, for greedy decoding.
+
+        ``tokens [B]`` (int64, on the device) seeds a static input buffer.  The
+        returned ``step()`` replays the graph, which runs the whole model on
+        the buffered tokens at the cache's device position, writes the logits
+        to a static buffer, appends the K/V and advances the device position;
+        then, outside the graph (a multi-block reduction may record memset
+        nodes), it writes the argmax tokens back into the input buffer and
+        advances the host ``cache.seen``.  ``step`` returns (logits, next
+        tokens), both static buffers overwritten by the next call.  The cache
+        needs room for every step (``cache.max_len``).  Capturing runs
+        nothing: the cache is unchanged until the first replay.  The eager
+        path should have run once with these shapes (library handles and
+        workspaces initialise on first use)."""
+        tok_buf = tokens.detach().clone()
+        stream = torch.cuda.Stream(device=tokens.device)
+        stream.wait_stream(torch.cuda.current_stream())
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(stream):
+            with torch.cuda.graph(graph, stream=stream):
+                logits = self.forward(tok_buf[:, None], past_key_value=cache, last_only=True)
+                cache.advance_device()
+        torch.cuda.current_stream().wait_stream(stream)
+
+        def step():
+            if cache.seen >= cache.max_len:
+                raise ValueError("cache is full")
+            graph.replay()
+            cache.seen += 1
+            torch.argmax(logits, dim=-1, out=tok_buf)
+            return logits, tok_buf
+
+        step.graph = graph
+        return step
 
     @torch.no_grad()
     def greedy_generate(self, input_ids, max_new_tokens: int, cache: Optional[LogoKVCache] = None):

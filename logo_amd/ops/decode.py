@@ -77,6 +77,8 @@ class LogoKVCache:
         self._pos = torch.zeros(batch, dtype=torch.int32, device=device)
         self._len_g = torch.zeros(batch, dtype=torch.int32, device=device)
         self._len_l = torch.zeros(batch, dtype=torch.int32, device=device)
+        self._step = 0        # host count of position changes
+        self._lens_for = -1   # step whose lengths _len_g / _len_l hold
 
     def get_seq_length(self) -> int:
         return self.seen
@@ -101,9 +103,26 @@ class LogoKVCache:
                 self.local_v[layer][:, :, :n - first].copy_(v_local[:, :, p0 + first:p1])
 
     def set_length(self, seen: int):
-        """Record that ``seen`` tokens are cached (call once per step, after layer 0)."""
+        """Record that ``seen`` tokens are cached (host value; e.g. after a prefill)."""
         self.seen = seen
         self._pos.fill_(seen)
+        self._step += 1
+
+    def advance_device(self):
+        """Move the device-side position one token on (no host value involved,
+        so a captured decode step can replay it); ``seen`` is the caller's
+        to update."""
+        self._pos.add_(1)
+        self._step += 1
+
+    def advance(self):
+        """One decoded token: device position and host ``seen``."""
+        self.advance_device()
+        self.seen += 1
+
+    def positions(self, T: int = 1):
+        """Positions ``[B, T]`` of the next ``T`` tokens, from the device state."""
+        return self._pos[:, None].to(torch.int64) + torch.arange(T, device=self._pos.device)
 
     def append(self, layer: int, k_local, v_local, k_global, v_global):
         """Append the new token (``[B, H, D]`` each) at position ``seen``."""
@@ -113,8 +132,24 @@ class LogoKVCache:
         cache_append(k_local, v_local, self.local_k[layer], self.local_v[layer], self._pos, ring=self.ring)
 
     def lengths(self):
-        """(global length, local length) device tensors for the token at ``seen``."""
-        n = self.seen + 1
-        self._len_g.fill_(n)
-        self._len_l.fill_(min(n, self.ring))
+        """(global length, local length) device tensors for the token at the
+        device position (computed on the device)."""
+        torch.add(self._pos, 1, out=self._len_g)
+        torch.clamp(self._len_g, max=self.ring, out=self._len_l)
+        self._lens_for = self._step
         return self._len_g, self._len_l
+
+    def step_lengths(self):
+        """``lengths()`` computed once per decode step and shared by the layers."""
+        if self._lens_for != self._step:
+            return self.lengths()
+        return self._len_g, self._len_l
+
+    def length_bounds(self):
+        """Host-side bounds on (global, local) lengths for kernel grids: tight
+        in eager mode, the capacity while a decode step is being captured (the
+        device lengths then grow across replays)."""
+        if torch.cuda.is_current_stream_capturing():
+            return self.max_len, self.ring
+        n = self.seen + 1
+        return n, min(n, self.ring)

@@ -1,0 +1,47 @@
+"""GPU checks of the fused RoPE and RMSNorm kernels against the eager torch ops."""
+
+import pytest
+import torch
+
+from logo_amd.layers import apply_rope, rope_cos_sin
+from logo_amd.ops.glue import rms_norm, rope_apply_
+from tests.helpers import gen
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_rope_bitwise_equal_to_eager(gpu, D):
+    g = gen(D)
+    B, T, H, HK = 2, 37, 4, 2
+    pos = torch.randint(0, 20000, (B, T), generator=g).to(gpu)
+    cos, sin = rope_cos_sin(pos, D, 10000.0, torch.bfloat16)
+    xs = [torch.randn(B, T, h, D, generator=g).bfloat16().to(gpu) for h in (H, HK, H, HK)]
+    ref = [apply_rope(x, cos, sin) for x in xs]
+    got = [x.clone() for x in xs]
+    rope_apply_(got, cos, sin)
+    for r, o in zip(ref, got):
+        assert torch.equal(r, o)
+    # fewer tensors, and a one-token decode shape
+    one = [torch.randn(32, 1, 16, D, generator=g).bfloat16().to(gpu)]
+    c1, s1 = rope_cos_sin(torch.full((32, 1), 16400, device=gpu), D, 10000.0, torch.bfloat16)
+    ref1 = apply_rope(one[0], c1, s1)
+    rope_apply_(one, c1, s1)
+    assert torch.equal(ref1, one[0])
+
+
+@pytest.mark.parametrize("rows,cols", [(7, 2048), (64, 128), (3, 4096), (5, 200)])
+def test_rmsnorm_matches_eager(gpu, rows, cols):
+    g = gen(rows * cols)
+    x = (torch.randn(rows, cols, generator=g) * 3).bfloat16().to(gpu)
+    w = (1 + 0.1 * torch.randn(cols, generator=g)).bfloat16().to(gpu)
+    eps = 1e-5
+    xf = x.float()
+    eager = w * (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)).to(torch.bfloat16)
+    got = rms_norm(x, w, eps)
+    same = (got == eager).float().mean().item()
+    diff = (got.float() - eager.float()).abs()
+    assert same >= 0.99, f"only {same:.4f} of outputs bit-identical to the eager sequence"
+    assert (diff <= 2 ** -7 * eager.float().abs().clamp(min=1)).all()
+    ref64 = w.double() * (x.double() / torch.sqrt(x.double().pow(2).mean(-1, keepdim=True) + eps))
+    assert (got.double() - ref64).abs().max().item() <= 2e-2 * ref64.abs().max().item()

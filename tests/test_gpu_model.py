@@ -60,3 +60,33 @@ def test_greedy_generate_shapes(gpu):
     out = m.greedy_generate(ids, 5)
     assert out.shape == (3, 5) and out.dtype == torch.int64
     assert int(out.min()) >= 0 and int(out.max()) < 512
+
+
+def test_graph_decode_matches_eager(gpu):
+    """Replays of the captured decode step, with eager decoding and
+    synchronisations in between, match eager decode steps on a twin cache."""
+    m = _model(gpu, 0.5)
+    B, T, steps = 2, 150, 6
+    g = torch.Generator()
+    g.manual_seed(3)
+    ids = torch.randint(0, 512, (B, T), generator=g).to(gpu)
+    ca = m.new_cache(B, T + steps + 2, device=gpu)
+    cb = m.new_cache(B, T + steps + 2, device=gpu)
+    tok_a = m.prefill(ids, ca).argmax(-1)
+    tok_b = m.prefill(ids, cb).argmax(-1)
+    tok_a = m.decode_step(tok_a, ca).argmax(-1)  # one eager step on each initialises the libraries
+    tok_b = m.decode_step(tok_b, cb).argmax(-1)
+    step = m.capture_greedy_decode(tok_b, cb)
+    assert cb.seen == T + 1
+    for s in range(steps):
+        la = m.decode_step(tok_a, ca)
+        tok_a = la.argmax(-1)
+        torch.cuda.synchronize()
+        lb, tok_b = step()
+        torch.cuda.synchronize()
+        err = (la.float() - lb.float()).abs().max().item()
+        scale = la.float().abs().max().item()
+        assert err <= 1e-2 * scale + 1e-3, f"replay {s}: max |eager - graph| {err:.4f} (scale {scale:.3f})"
+        assert torch.equal(tok_a, tok_b), f"replay {s}: greedy tokens differ"
+    assert cb.seen == ca.seen == T + 1 + steps
+    assert torch.equal(ca._pos, cb._pos)
