@@ -1,6 +1,6 @@
 """Shared test inputs, tolerances and a chunked torch fp32 attention reference.
 
-Inputs follow the BASELINE configs restated in SURVEY 8(d) (seeded
+Inputs follow the benchmark configurations of BASELINE.json (seeded
 ``torch.Generator``).  ``torch_sq_attn`` is a plain-PyTorch fp32 restatement of
 the same semantics as ``oracle.attn`` used where the numpy oracle would be too
 slow (full-size cases on the GPU); it is itself pinned against the oracle on
