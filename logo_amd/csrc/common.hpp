@@ -37,7 +37,11 @@ constexpr int kMetaHdr = 8;
 // kernel built with VGPR-form results keep theirs in VGPRs).  The compiler
 // does not see inside the asm, so it supplies its own wait states: the
 // leading s_nop covers a VALU write of A, B or D just before it, and
-// agpr_acc_drain() must run before any other instruction reads D.
+// agpr_acc_drain() must run before any other instruction reads D.  That
+// includes copies the register allocator itself inserts: a kernel whose
+// loop ends up with v_accvgpr_mov of such an accumulator (seen when a
+// branch around the MFMA phase became scalar) reads it before the MFMA has
+// written it, so the ISA of these kernels is checked for in-loop copies.
 __device__ __forceinline__ void mfma32_agpr(f32x16& d, const bf16x8& a, const bf16x8& b) {
   asm volatile("s_nop 2\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(d) : "v"(a), "v"(b));
 }
@@ -164,83 +168,21 @@ struct Tile64 {
 };
 
 // Global -> LDS copy of a 64-row x D-column bf16 tile into the kSwz layout
-// with global_load_lds_dwordx4 (no register staging, no LDS store
+// with buffer_load_dwordx4 ... lds (no register staging, no LDS store
 // instructions).  Each such load writes 64 lanes x 16 bytes = 1 KB contiguous
 // at a wave-uniform LDS address, i.e. RPB = 64 / CH whole rows; lane j fills
 // physical chunk j % CH of row (block row + j / CH), so it loads that row's
 // logical chunk (j % CH) ^ swz(row).  With NW waves, wave w copies rows
 // (64 / NW) w .. (64 / NW)(w + 1) - 1.  The caller waits for the loads
 // (s_waitcnt vmcnt) before the barrier that publishes the tile.
-template <int D, int NW = 4>
-struct TileDma {
-  static constexpr int CH = D / 8;
-  static constexpr int RPB = 64 / CH;
-  static constexpr int RPW = 64 / NW;  // rows per wave
-  static constexpr int BLOCKS = RPW / RPB;
-  using Geo = TileGeom<D, kSwz>;
-
-  template <typename F>
-  __device__ __forceinline__ static void issue(bf16* tile, F rowptr) {
-    const int wave = threadIdx.x >> 6, j = threadIdx.x & 63;
-#pragma unroll
-    for (int b = 0; b < BLOCKS; ++b) {
-      const int rb = RPW * wave + RPB * b;
-      const int row = rb + j / CH;
-      const int ch = (j % CH) ^ Geo::swz(row);
-      __builtin_amdgcn_global_load_lds(rowptr(row) + 8 * ch,
-                                       (__attribute__((address_space(3))) void*)(tile + rb * D), 16, 0, 0);
-    }
-  }
-
-  // Byte offsets, from a tile's first row, of the 16-byte chunks this lane
-  // copies for a fixed row stride (loop-invariant: computed once).
-  struct Offsets {
-    uint32_t o[BLOCKS];
-  };
-  __device__ __forceinline__ static Offsets offsets(int row_stride) {
-    Offsets r;
-    const int wave = threadIdx.x >> 6, j = threadIdx.x & 63;
-#pragma unroll
-    for (int b = 0; b < BLOCKS; ++b) {
-      const int row = RPW * wave + RPB * b + j / CH;
-      const int ch = (j % CH) ^ Geo::swz(row);
-      r.o[b] = (uint32_t)(row * row_stride + 8 * ch) * (uint32_t)sizeof(bf16);
-    }
-    return r;
-  }
-  // All 64 rows valid: a wave-uniform base plus the precomputed lane offsets
-  // (the scalar-base form of the load; no per-tile address arithmetic).
-  __device__ __forceinline__ static void issue_fast(bf16* tile, const bf16* base, const Offsets& off) {
-    const int wave = threadIdx.x >> 6;
-#pragma unroll
-    for (int b = 0; b < BLOCKS; ++b) {
-      const int rb = RPW * wave + RPB * b;
-      __builtin_amdgcn_global_load_lds(reinterpret_cast<const char*>(base) + off.o[b],
-                                       (__attribute__((address_space(3))) void*)(tile + rb * D), 16, 0, 0);
-    }
-  }
-
-  // Rows evenly strided from a wave-uniform base; tile rows past last_row
-  // are clamped to it.  The address is the uniform base plus a 32-bit lane
-  // offset (the 64 rows of a tile span far less than 2^31 elements).
-  __device__ __forceinline__ static void issue_strided(bf16* tile, const bf16* base, int row_stride, int last_row) {
-    const int wave = threadIdx.x >> 6, j = threadIdx.x & 63;
-#pragma unroll
-    for (int b = 0; b < BLOCKS; ++b) {
-      const int rb = RPW * wave + RPB * b;
-      const int row = rb + j / CH;
-      const int ch = (j % CH) ^ Geo::swz(row);
-      __builtin_amdgcn_global_load_lds(base + (min(row, last_row) * row_stride + 8 * ch),
-                                       (__attribute__((address_space(3))) void*)(tile + rb * D), 16, 0, 0);
-    }
-  }
-};
-
-// The same tile copy through buffer_load_dwordx4 ... lds: a scalar buffer
-// descriptor based at the tile's first row, a scalar byte offset and one
-// 32-bit lane offset per 1 KB block (loop-invariant for full tiles).  The
+//
+// The loads use a scalar buffer descriptor based at the tile's first row and
+// one 32-bit lane offset per 1 KB block (loop-invariant for full tiles).  The
 // descriptor's extent is the 64 rows of the tile, so the hardware returns
 // zeros for any read past them instead of touching memory outside the tile.
+// (The FLAT-encoded global_load_lds form is avoided: while one is in flight
+// the compiler treats the LDS counter as out of order and turns every LDS
+// operand wait into a full lgkmcnt(0) drain.)
 constexpr int kBufRsrcWord3 = 0x00020000;  // raw, untyped 32-bit buffer (gfx9 family)
 
 // One buffer_load_dwordx4 ... lds: 64 lanes x 16 bytes to LDS at `lds`

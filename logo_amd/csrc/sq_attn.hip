@@ -712,8 +712,11 @@ __global__ __launch_bounds__(256) LOGO_OCC_DKV void sq_dkv_kernel(const AttnArgs
 
   TileReader<D, kSwz> rd;
   rd.init();
-  // q / dO rows: stride D (compacted copies) or HQ * D (dense inputs)
-  const auto dma_off = TileDma<D>::offsets(SPARSE ? D : a.hq * D);
+  // q / dO rows: stride D (compacted copies) or HQ * D (dense inputs).  The
+  // copies are buffer loads: a FLAT-encoded copy in flight would make every
+  // LDS operand wait of the compute phases a full lgkmcnt(0) drain.
+  TileBufDma<D> dma;
+  dma.init(SPARSE ? D : a.hq * D);
   float lse_n = 0.f, delta_n = 0.f;
   int pos_n = -1;
   for (int gg = 0; gg < a.g; ++gg) {
@@ -748,11 +751,11 @@ __global__ __launch_bounds__(256) LOGO_OCC_DKV void sq_dkv_kernel(const AttnArgs
 #pragma unroll
       for (int u = 0; u < NSUB; ++u) {
         if (rt + 64 * (u + 1) <= rq_end) {
-          TileDma<D>::issue_fast(sQ(b) + 64 * D * u, qs.row(rt + 64 * u), dma_off);
-          TileDma<D>::issue_fast(sO(b) + 64 * D * u, os.row(rt + 64 * u), dma_off);
+          dma.issue(sQ(b) + 64 * D * u, qs.row(rt + 64 * u));
+          dma.issue(sO(b) + 64 * D * u, os.row(rt + 64 * u));
         } else {
-          TileDma<D>::issue_strided(sQ(b) + 64 * D * u, qs.row(rt + 64 * u), (int)qs.stride, rq_end - 1 - rt - 64 * u);
-          TileDma<D>::issue_strided(sO(b) + 64 * D * u, os.row(rt + 64 * u), (int)os.stride, rq_end - 1 - rt - 64 * u);
+          dma.issue_clamped(sQ(b) + 64 * D * u, qs.row(rt + 64 * u), rq_end - 1 - rt - 64 * u);
+          dma.issue_clamped(sO(b) + 64 * D * u, os.row(rt + 64 * u), rq_end - 1 - rt - 64 * u);
         }
       }
     };
