@@ -264,6 +264,84 @@ def extra_measurements(dev):
     return out
 
 
+def layer_cfg4_measurement(dev, iters=5, seed=3):
+    """one LoGo attention layer fwd+bwd at the 1.5B shapes
+    (hidden 2048, 16 heads, D=128, window 128, linear_proj global
+    re-parameterisation, context norms), B=4, T=8192, bf16.  Linear weights
+    ~ N(0, 0.02); the global projections are identity + N(0, 0.02) so the
+    branches differ; hidden ~ N(0, 1) and gate_proj std 1/sqrt(2048), so the
+    gate logits are ~ N(0, 1) and threshold 0.5 selects about half the tokens.
+    A step is the layer forward plus the backward of a random upstream
+    gradient into the hidden states and every parameter.  The HIP kernels'
+    own durations (HIP events around each C-ABI launch) are listed beside the
+    step time; the remainder is the projections (hipBLASLt through torch)
+    and the torch glue (RoPE and norms under autograd)."""
+    from logo_amd import _lib
+    from logo_amd.layers import LoGoAttention, LoGoConfig
+
+    B, T, hidden, H = 4, 8192, 2048, 16
+    D = hidden // H
+    cfg = LoGoConfig(hidden_size=hidden, num_attention_heads=H, num_hidden_layers=1, window_size=128,
+                     global_qk_param="linear_proj", use_context_norm=True, gate_thres_init=0.5,
+                     sparse_full_attn_backend="hip")
+    gen = torch.Generator()
+    gen.manual_seed(seed)
+    layer = LoGoAttention(cfg)
+    with torch.no_grad():
+        for name, p in layer.named_parameters():
+            if name.endswith("_global_proj"):
+                p.add_(torch.randn(p.shape, generator=gen) * 0.02)
+            elif name == "gate_proj.weight":
+                p.copy_(torch.randn(p.shape, generator=gen) / hidden ** 0.5)
+            elif p.dim() == 2:
+                p.copy_(torch.randn(p.shape, generator=gen) * 0.02)
+    layer = layer.to(device=dev, dtype=torch.bfloat16).train()
+    h = torch.randn(B, T, hidden, generator=gen).bfloat16().to(dev).requires_grad_()
+    dout = torch.randn(B, T, hidden, generator=gen).bfloat16().to(dev)
+    params = [p for p in layer.parameters() if p.requires_grad]
+    with torch.no_grad():
+        sel = (torch.sigmoid(layer.gate_proj(h)) >= layer.gate_thres).reshape(B, T).cpu().numpy()
+    pairs = float(sum((np.flatnonzero(sel[b]) + 1).sum() for b in range(B)))
+
+    def step():
+        out, _, _ = layer(h)
+        torch.autograd.grad(out, [h] + params, dout)
+
+    for _ in range(2):
+        step()
+    torch.cuda.synchronize()
+    timer = EventTimer()
+    _lib.set_launch_hook(timer)
+    timer.enabled = True
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(iters):
+        step()
+    b.record()
+    torch.cuda.synchronize()
+    timer.enabled = False
+    _lib.set_launch_hook(None)
+    ms = a.elapsed_time(b) / iters
+    counts = timer.counts()
+    kern = {k_: round(v_ * counts[k_] / iters, 4) for k_, v_ in sorted(timer.averages_ms().items())}
+    N = B * T
+    proj_flops = 3 * (4 * 2 * N * hidden * hidden + 3 * 2 * N * H * D * D)  # fwd + 2x bwd
+    sq_flops = 3.5 * 4 * D * H * pairs
+    swa_pairs = sum(min(p, 128) + 1 for p in range(T)) * B
+    swa_flops = 3.5 * 4 * D * H * swa_pairs
+    return {
+        "ms": round(ms, 3),
+        "tflops": round((proj_flops + sq_flops + swa_flops) / (ms * 1e-3) / 1e12, 1),
+        "flops_per_step": {"projections": proj_flops, "sq_attn": sq_flops, "swa": swa_flops},
+        "global_ratio": round(float(sel.mean()), 4),
+        "hip_kernel_ms_per_step": kern,
+        "hip_kernel_ms_total": round(sum(kern.values()), 3),
+        "shape": {"B": B, "T": T, "hidden": hidden, "heads": H, "head_dim": D, "window": 128},
+        "data": "synthetic hidden states ~N(0,1), random-init weights",
+    }
+
+
 def decode_model_measurement(dev, batch=32, prompt=16384, steps=256, seed=4):
     """the LoGo 1.5B shapes (24 layers, hidden 2048, 16 heads,
     vocab 32000, tied embeddings), random-init bf16, a batch of random-id
@@ -429,6 +507,8 @@ def main():
         cpu = cpu_baseline(q, k, v, sel_np, [0, T], do, min(args.cpu_heads, H), f_step / H)
 
     extra = None if args.no_extra else extra_measurements(dev)
+    if not args.no_extra:
+        extra["layer_cfg4_fwd_bwd"] = layer_cfg4_measurement(dev)
     if not args.no_extra and not args.no_decode:
         extra["decode_cfg5_model"] = decode_model_measurement(dev)
 
