@@ -207,6 +207,21 @@ int logo_rope_apply(void* x0, int h0, void* x1, int h1, void* x2, int h2, void* 
                     void* stream);
 
 /*
+ * Rotary embedding of up to four [N, H_i, D] bf16 tensors x_i into outputs y_i
+ * (y_i == x_i allowed; a NULL x_i is skipped) with one [N, D] cos / sin pair.
+ * inverse = 0: the forward rotation of logo_rope_apply (same rounding);
+ * inverse = 1: its transpose, the gradient of the rotation: with x = dL/dy,
+ * y1 = bf16(bf16(x1 * cos1) + bf16(x2 * sin2)) and
+ * y2 = bf16(bf16(x2 * cos2) - bf16(x1 * sin1)), the rounding points of eager
+ * autograd through logo/modules/rotary.py:81-106 (mul backward, then the
+ * cat / neg backward of rotate_half), so a training step's RoPE forward and
+ * backward are one launch each (logo/layers/logo.py:132-139).
+ */
+int logo_rope(const void* x0, void* y0, int h0, const void* x1, void* y1, int h1, const void* x2,
+              void* y2, int h2, const void* x3, void* y3, int h3, const void* cos, const void* sin,
+              int64_t n_tokens, int d, int inverse, int dtype, void* stream);
+
+/*
  * RMSNorm of rows [rows, cols] bf16 with weight [cols]: y = w * bf16(x *
  * rsqrt(mean(x^2) + eps)), mean in fp32 (logo/modules/layernorm.py:17-22; the
  * decoder's input / post-attention / final norms, logo/modeling_logo.py:58-59,

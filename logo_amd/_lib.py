@@ -39,6 +39,7 @@ SIGNATURES = {
     "logo_decode_attn": ([_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I64, _I, _F, _I, _P], _I),
     "logo_cache_append": ([_P, _P, _P, _P, _P, _I, _I, _I, _I64, _I, _I, _P], _I),
     "logo_rope_apply": ([_P, _I, _P, _I, _P, _I, _P, _I, _P, _P, _I64, _I, _I, _P], _I),
+    "logo_rope": ([_P, _P, _I, _P, _P, _I, _P, _P, _I, _P, _P, _I, _P, _P, _I64, _I, _I, _I, _P], _I),
     "logo_rmsnorm": ([_P, _P, _P, _I64, _I, _F, _I, _P], _I),
 }
 _BWD = ([_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I, _I, _I, _I, _I, _F, _I, _I, _P], _I)

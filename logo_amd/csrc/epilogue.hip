@@ -183,20 +183,41 @@ __global__ __launch_bounds__(256) void epi_bwd_kernel(const EpiArgs a) {
 }
 
 // dgate per token (sum of its heads' partials, zero where masked) and the
-// weight gradients (fixed-order sum over workgroup partials).
+// weight gradients.  Workgroups past the token blocks each reduce 32 of the
+// 2 * D (branch, column) weight sums: thread (column, group pg) adds the
+// partials b = pg, pg + 8, ... with four independent accumulators, and the 8
+// groups are combined in a fixed order, so the sums are deterministic and no
+// thread walks all the partials in one dependent chain.
+constexpr int kEpiDwCols = 32;
+
 template <int D>
-__global__ __launch_bounds__(256) void epi_bwd_finalize_kernel(const EpiArgs a, int64_t n_tokens, int nparts) {
-  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (blockIdx.x == gridDim.x - 1) {
-    // last workgroup: weight gradients
-    for (int k = threadIdx.x; k < 2 * D; k += 256) {
-      const int br = k / D, d = k % D;
-      float s = 0.f;
-      for (int b = 0; b < nparts; ++b) s += a.dw_part[((int64_t)b * 2 + br) * D + d];
-      (br == 0 ? a.dw_l : a.dw_g)[d] = (bf16)s;
+__global__ __launch_bounds__(256) void epi_bwd_finalize_kernel(const EpiArgs a, int64_t n_tokens, int nparts,
+                                                               int tok_blocks) {
+  if ((int)blockIdx.x >= tok_blocks) {
+    __shared__ float red[8][kEpiDwCols];
+    const int col = threadIdx.x % kEpiDwCols, pg = threadIdx.x / kEpiDwCols;
+    const int k = ((int)blockIdx.x - tok_blocks) * kEpiDwCols + col;  // br * D + d
+    const float* src = a.dw_part + k;
+    float acc0 = 0.f, acc1 = 0.f, acc2 = 0.f, acc3 = 0.f;
+    int b = pg;
+    for (; b + 24 < nparts; b += 32) {
+      acc0 += src[(int64_t)b * 2 * D];
+      acc1 += src[(int64_t)(b + 8) * 2 * D];
+      acc2 += src[(int64_t)(b + 16) * 2 * D];
+      acc3 += src[(int64_t)(b + 24) * 2 * D];
+    }
+    for (; b < nparts; b += 8) acc0 += src[(int64_t)b * 2 * D];
+    red[pg][col] = (acc0 + acc1) + (acc2 + acc3);
+    __syncthreads();
+    if (pg == 0) {
+      float s = red[0][col];
+#pragma unroll
+      for (int j = 1; j < 8; ++j) s += red[j][col];
+      (k < D ? a.dw_l : a.dw_g)[k % D] = (bf16)s;
     }
     return;
   }
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (t >= n_tokens) return;
   const float g = (float)a.gate[t];
   float s = 0.f;
@@ -289,11 +310,14 @@ extern "C" int logo_epilogue_bwd(const void* L, const void* G, const void* gate,
   if (d == 128) hipLaunchKernelGGL(epi_bwd_kernel<128>, dim3((unsigned)grid), dim3(256), 0, st, a);
   else hipLaunchKernelGGL(epi_bwd_kernel<64>, dim3((unsigned)grid), dim3(256), 0, st, a);
   LOGO_LAUNCH_CHECK("epi_bwd_kernel");
-  const int64_t fblk = (n_tokens + 255) / 256 + 1;
+  const int tok_blocks = (int)((n_tokens + 255) / 256);
+  const int fblk = tok_blocks + 2 * d / kEpiDwCols;
   if (d == 128)
-    hipLaunchKernelGGL(epi_bwd_finalize_kernel<128>, dim3((unsigned)fblk), dim3(256), 0, st, a, n_tokens, (int)grid);
+    hipLaunchKernelGGL(epi_bwd_finalize_kernel<128>, dim3((unsigned)fblk), dim3(256), 0, st, a, n_tokens, (int)grid,
+                       tok_blocks);
   else
-    hipLaunchKernelGGL(epi_bwd_finalize_kernel<64>, dim3((unsigned)fblk), dim3(256), 0, st, a, n_tokens, (int)grid);
+    hipLaunchKernelGGL(epi_bwd_finalize_kernel<64>, dim3((unsigned)fblk), dim3(256), 0, st, a, n_tokens, (int)grid,
+                       tok_blocks);
   LOGO_LAUNCH_CHECK("epi_bwd_finalize_kernel");
   return LOGO_OK;
 }

@@ -5,8 +5,14 @@
 // bf16(rotate_half(x) * sin)) with rotate_half(x) = [-x2, x1], the rounding
 // points of the reference's eager bf16 ops kept (products of two bf16 values
 // are exact in fp32, so each rounds exactly as the eager op does).  Up to four
-// [N, H_i, D] tensors (q, k and the global q, k) are rotated in place with one
-// [N, D] cos / sin pair.
+// [N, H_i, D] tensors (q, k and the global q, k) are rotated with one [N, D]
+// cos / sin pair, in place or into separate outputs.  The inverse rotation is
+// the backward: eager autograd of the forward gives
+//   dx1 = bf16(bf16(dy1 * cos1) + bf16(dy2 * sin2))
+//   dx2 = bf16(bf16(dy2 * cos2) + bf16(-(dy1 * sin1)))
+// (mul backward rounds each product; rotate_half's cat / neg backward moves
+// and negates exactly; the two contributions are summed in bf16), and the
+// kernel keeps those rounding points too.
 //
 // RMSNorm (logo/modules/layernorm.py:17-22): y = bf16(w * bf16(x *
 // rsqrt(mean(x^2) + eps))), the mean taken in fp32.
@@ -21,7 +27,8 @@
 namespace logo {
 
 struct RopeArgs {
-  bf16* x[4];
+  const bf16* x[4];
+  bf16* y[4];
   int heads[4];
   int nt;  // tensors in use
   const bf16* cos;
@@ -32,8 +39,9 @@ struct RopeArgs {
 __device__ __forceinline__ float bfr_g(float x) { return (float)(bf16)x; }
 
 // One thread per (tensor, token, head, 8-element chunk of the first half):
-// it rotates the pair of chunks (c, c + D/16) together.
-template <int D>
+// it rotates the pair of chunks (c, c + D/16) together (reading both before
+// writing either, so x == y is allowed).
+template <int D, bool INV>
 __global__ __launch_bounds__(256) void rope_kernel(const RopeArgs a, int64_t per_tensor_max) {
   constexpr int HC = D / 16;  // chunks of 8 in each half
   const int ti = blockIdx.y;
@@ -45,7 +53,8 @@ __global__ __launch_bounds__(256) void rope_kernel(const RopeArgs a, int64_t per
   const int c = (int)(idx % HC);
   const int64_t row = idx / HC;  // token * H + head
   const int64_t tok = row / H;
-  bf16* xr = a.x[ti] + row * D;
+  const bf16* xr = a.x[ti] + row * D;
+  bf16* yr = a.y[ti] + row * D;
   const bf16x8 x1 = *reinterpret_cast<const bf16x8*>(xr + 8 * c);
   const bf16x8 x2 = *reinterpret_cast<const bf16x8*>(xr + D / 2 + 8 * c);
   const bf16x8 c1 = *reinterpret_cast<const bf16x8*>(a.cos + tok * D + 8 * c);
@@ -55,16 +64,26 @@ __global__ __launch_bounds__(256) void rope_kernel(const RopeArgs a, int64_t per
   bf16x8 y1, y2;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    // first half:  x1 * cos1 + (-x2) * sin1;  second half: x2 * cos2 + x1 * sin2
-    const float a1 = bfr_g((float)x1[e] * (float)c1[e]);
-    const float b1 = bfr_g(-(float)x2[e] * (float)s1[e]);
-    const float a2 = bfr_g((float)x2[e] * (float)c2[e]);
-    const float b2 = bfr_g((float)x1[e] * (float)s2[e]);
-    y1[e] = (bf16)(a1 + b1);
-    y2[e] = (bf16)(a2 + b2);
+    if constexpr (!INV) {
+      // first half:  x1 * cos1 + (-x2) * sin1;  second half: x2 * cos2 + x1 * sin2
+      const float a1 = bfr_g((float)x1[e] * (float)c1[e]);
+      const float b1 = bfr_g(-(float)x2[e] * (float)s1[e]);
+      const float a2 = bfr_g((float)x2[e] * (float)c2[e]);
+      const float b2 = bfr_g((float)x1[e] * (float)s2[e]);
+      y1[e] = (bf16)(a1 + b1);
+      y2[e] = (bf16)(a2 + b2);
+    } else {
+      // transpose of the rotation: x1 * cos1 + x2 * sin2;  x2 * cos2 - x1 * sin1
+      const float a1 = bfr_g((float)x1[e] * (float)c1[e]);
+      const float b1 = bfr_g((float)x2[e] * (float)s2[e]);
+      const float a2 = bfr_g((float)x2[e] * (float)c2[e]);
+      const float b2 = -bfr_g((float)x1[e] * (float)s1[e]);
+      y1[e] = (bf16)(a1 + b1);
+      y2[e] = (bf16)(a2 + b2);
+    }
   }
-  *reinterpret_cast<bf16x8*>(xr + 8 * c) = y1;
-  *reinterpret_cast<bf16x8*>(xr + D / 2 + 8 * c) = y2;
+  *reinterpret_cast<bf16x8*>(yr + 8 * c) = y1;
+  *reinterpret_cast<bf16x8*>(yr + D / 2 + 8 * c) = y2;
 }
 
 // One wave per row; rows of `cols` bf16 (a multiple of 8, at most 64 * 8 * 8).
@@ -104,21 +123,20 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const bf16* x, const bf16*
 
 using namespace logo;
 
-extern "C" int logo_rope_apply(void* x0, int h0, void* x1, int h1, void* x2, int h2, void* x3, int h3,
-                               const void* cos, const void* sin, int64_t n_tokens, int d, int dtype,
-                               void* stream) {
+static int rope_launch(const void* const xs[4], void* const ys[4], const int hs[4], const void* cos,
+                       const void* sin, int64_t n_tokens, int d, int inverse, int dtype, void* stream) {
   LOGO_REQUIRE(d == 64 || d == 128, "head dim %d unsupported (64 or 128)", d);
   LOGO_REQUIRE(dtype == LOGO_DTYPE_BF16, "only bf16 tensors are supported");
   LOGO_REQUIRE(n_tokens >= 0, "n_tokens must be >= 0");
   LOGO_REQUIRE(cos && sin, "null cos / sin");
   RopeArgs a{};
-  void* xs[4] = {x0, x1, x2, x3};
-  const int hs[4] = {h0, h1, h2, h3};
   int hmax = 0;
   for (int i = 0; i < 4; ++i) {
     if (xs[i] == nullptr) continue;
+    LOGO_REQUIRE(ys[i] != nullptr, "tensor %d: null output", i);
     LOGO_REQUIRE(hs[i] >= 1, "tensor %d: heads must be >= 1", i);
-    a.x[a.nt] = static_cast<bf16*>(xs[i]);
+    a.x[a.nt] = static_cast<const bf16*>(xs[i]);
+    a.y[a.nt] = static_cast<bf16*>(ys[i]);
     a.heads[a.nt] = hs[i];
     ++a.nt;
     hmax = hs[i] > hmax ? hs[i] : hmax;
@@ -131,12 +149,34 @@ extern "C" int logo_rope_apply(void* x0, int h0, void* x1, int h1, void* x2, int
   const int64_t nblk = (per + 255) / 256;
   LOGO_REQUIRE(nblk < ((int64_t)1 << 31), "too many rows");
   hipStream_t st = as_stream(stream);
-  if (d == 128)
-    hipLaunchKernelGGL(rope_kernel<128>, dim3((unsigned)nblk, a.nt), dim3(256), 0, st, a, per);
-  else
-    hipLaunchKernelGGL(rope_kernel<64>, dim3((unsigned)nblk, a.nt), dim3(256), 0, st, a, per);
+  const dim3 grid((unsigned)nblk, a.nt);
+  if (d == 128) {
+    if (inverse) hipLaunchKernelGGL((rope_kernel<128, true>), grid, dim3(256), 0, st, a, per);
+    else hipLaunchKernelGGL((rope_kernel<128, false>), grid, dim3(256), 0, st, a, per);
+  } else {
+    if (inverse) hipLaunchKernelGGL((rope_kernel<64, true>), grid, dim3(256), 0, st, a, per);
+    else hipLaunchKernelGGL((rope_kernel<64, false>), grid, dim3(256), 0, st, a, per);
+  }
   LOGO_LAUNCH_CHECK("rope_kernel");
   return LOGO_OK;
+}
+
+extern "C" int logo_rope_apply(void* x0, int h0, void* x1, int h1, void* x2, int h2, void* x3, int h3,
+                               const void* cos, const void* sin, int64_t n_tokens, int d, int dtype,
+                               void* stream) {
+  const void* xs[4] = {x0, x1, x2, x3};
+  void* ys[4] = {x0, x1, x2, x3};
+  const int hs[4] = {h0, h1, h2, h3};
+  return rope_launch(xs, ys, hs, cos, sin, n_tokens, d, 0, dtype, stream);
+}
+
+extern "C" int logo_rope(const void* x0, void* y0, int h0, const void* x1, void* y1, int h1, const void* x2,
+                         void* y2, int h2, const void* x3, void* y3, int h3, const void* cos, const void* sin,
+                         int64_t n_tokens, int d, int inverse, int dtype, void* stream) {
+  const void* xs[4] = {x0, x1, x2, x3};
+  void* ys[4] = {y0, y1, y2, y3};
+  const int hs[4] = {h0, h1, h2, h3};
+  return rope_launch(xs, ys, hs, cos, sin, n_tokens, d, inverse, dtype, stream);
 }
 
 extern "C" int logo_rmsnorm(const void* x, const void* w, void* y, int64_t rows, int cols, float eps, int dtype,

@@ -28,7 +28,7 @@ import torch.nn.functional as F
 
 from .ops.decode import LogoKVCache, decode_attn
 from .ops.epilogue import logo_epilogue
-from .ops.glue import rms_norm, rope_apply_
+from .ops.glue import rms_norm, rope, rope_apply_
 from .ops.sq_attn import dense_causal_attn, sq_full_attn, swa_attn
 
 __all__ = ["LoGoConfig", "LoGoAttention", "RMSNorm", "rope_cos_sin", "apply_rope", "position_ids_for"]
@@ -233,8 +233,12 @@ class LoGoAttention(nn.Module):
             if position_ids is None:
                 position_ids = position_ids_for(B, T, hidden_states.device, cu_seqlens, past_key_value)
             cos, sin = rope_cos_sin(position_ids, D, self.config.rope_theta, q.dtype)
-        if _fused_ok(q, k, gq, gk, cos, sin) and all(t.is_contiguous() for t in (q, k, gq, gk)):
+        on_dev = all(t.is_cuda and t.dtype == torch.bfloat16 for t in (q, k, gq, gk, cos, sin)) and all(
+            t.is_contiguous() for t in (q, k, gq, gk))
+        if on_dev and _fused_ok(q, k, gq, gk):
             rope_apply_([q, k, gq, gk], cos, sin)  # in place, one launch
+        elif on_dev:
+            q, k, gq, gk = rope([q, k, gq, gk], cos, sin)  # one launch each way under autograd
         else:
             q, k = apply_rope(q, cos, sin), apply_rope(k, cos, sin)
             gq, gk = apply_rope(gq, cos, sin), apply_rope(gk, cos, sin)

@@ -1,8 +1,10 @@
 """Fused RoPE and RMSNorm launches (``csrc/glue.hip``) for the layer and model glue.
 
-``rope_apply_`` rotates q, k and the global q, k in one launch with the eager
-bf16 rounding of logo/modules/rotary.py:81-106; ``rms_norm`` computes
-logo/modules/layernorm.py:17-22 in one launch.  Both run only on ROCm tensors
+``rope_apply_`` rotates q, k and the global q, k in place in one launch with
+the eager bf16 rounding of logo/modules/rotary.py:81-106; ``rope`` is the
+differentiable form (new outputs, one launch forward and one backward, both
+bit-identical to eager autograd through ``apply_rotary_pos_emb``);
+``rms_norm`` computes logo/modules/layernorm.py:17-22 in one launch.  Both run only on ROCm tensors
 and raise otherwise (the modules that call them keep plain torch math for CPU
 tensors).
 """
@@ -11,7 +13,23 @@ import torch
 
 from .. import _lib
 
-__all__ = ["rope_apply_", "rms_norm"]
+__all__ = ["rope_apply_", "rope", "RopeFunction", "rms_norm"]
+
+
+def _rope_checked(tensors, cos, sin, what):
+    if not 1 <= len(tensors) <= 4:
+        raise ValueError(f"{what} takes one to four tensors")
+    _lib.require_gpu(*tensors, cos, sin)
+    D = tensors[0].shape[-1]
+    n = tensors[0][..., 0, 0].numel()
+    for t in tensors:
+        if t.dtype != torch.bfloat16 or not t.is_contiguous() or t.shape[-1] != D or t[..., 0, 0].numel() != n:
+            raise ValueError(f"{what} needs contiguous bf16 [..., T, H, D] tensors of one shape prefix")
+    cos = cos.to(torch.bfloat16).contiguous()
+    sin = sin.to(torch.bfloat16).contiguous()
+    if cos.numel() != n * D or sin.numel() != n * D:
+        raise ValueError("cos / sin must be [..., T, D] matching the tensors")
+    return cos, sin, n, D
 
 
 def rope_apply_(tensors, cos, sin):
@@ -19,18 +37,7 @@ def rope_apply_(tensors, cos, sin):
     contiguous, all with the same leading ``[..., T]``) in place with
     ``cos/sin [..., T, D]``."""
     tensors = [t for t in tensors if t is not None]
-    if not 1 <= len(tensors) <= 4:
-        raise ValueError("rope_apply_ takes one to four tensors")
-    _lib.require_gpu(*tensors, cos, sin)
-    D = tensors[0].shape[-1]
-    n = tensors[0][..., 0, 0].numel()
-    for t in tensors:
-        if t.dtype != torch.bfloat16 or not t.is_contiguous() or t.shape[-1] != D or t[..., 0, 0].numel() != n:
-            raise ValueError("rope_apply_ needs contiguous bf16 [..., T, H, D] tensors of one shape prefix")
-    cos = cos.to(torch.bfloat16).contiguous()
-    sin = sin.to(torch.bfloat16).contiguous()
-    if cos.numel() != n * D or sin.numel() != n * D:
-        raise ValueError("cos / sin must be [..., T, D] matching the tensors")
+    cos, sin, n, D = _rope_checked(tensors, cos, sin, "rope_apply_")
     args = []
     for i in range(4):
         if i < len(tensors):
@@ -41,6 +48,53 @@ def rope_apply_(tensors, cos, sin):
     _lib.launch("logo_rope_apply", lib.logo_rope_apply, *args, _lib.ptr(cos), _lib.ptr(sin), n, D,
                 _lib.DTYPE_BF16, _lib.stream_of(tensors[0]))
     return tensors
+
+
+def _rope_launch(xs, cos, sin, n, D, inverse):
+    ys = [torch.empty_like(x) for x in xs]
+    args = []
+    for i in range(4):
+        if i < len(xs):
+            args += [_lib.ptr(xs[i]), _lib.ptr(ys[i]), xs[i].shape[-2]]
+        else:
+            args += [None, None, 0]
+    lib = _lib.lib()
+    _lib.launch("logo_rope", lib.logo_rope, *args, _lib.ptr(cos), _lib.ptr(sin), n, D, int(inverse),
+                _lib.DTYPE_BF16, _lib.stream_of(xs[0]))
+    return ys
+
+
+class RopeFunction(torch.autograd.Function):
+    """RoPE of up to four tensors as one autograd node: the forward rotation
+    and, for the backward, the transposed rotation of the incoming gradients,
+    each one HIP launch (eager autograd through logo/modules/rotary.py:81-106
+    takes about six element-wise passes per tensor each way)."""
+
+    @staticmethod
+    def forward(ctx, cos, sin, *xs):
+        cos, sin, n, D = _rope_checked(list(xs), cos, sin, "rope")
+        ctx.set_materialize_grads(False)  # unused outputs: no zero gradients to rotate
+        ctx.save_for_backward(cos, sin)
+        ctx.nd = (n, D)
+        return tuple(_rope_launch(list(xs), cos, sin, n, D, inverse=False))
+
+    @staticmethod
+    def backward(ctx, *gys):
+        cos, sin = ctx.saved_tensors
+        n, D = ctx.nd
+        live = [i for i, g in enumerate(gys) if g is not None]
+        gxs = [None] * len(gys)
+        if live:
+            gin = [gys[i].to(torch.bfloat16).contiguous() for i in live]
+            for i, gx in zip(live, _rope_launch(gin, cos, sin, n, D, inverse=True)):
+                gxs[i] = gx
+        return (None, None, *gxs)
+
+
+def rope(tensors, cos, sin):
+    """Differentiable RoPE of up to four contiguous bf16 ``[..., T, H_i, D]``
+    tensors with ``cos/sin [..., T, D]``; returns new tensors."""
+    return list(RopeFunction.apply(cos, sin, *tensors))
 
 
 def rms_norm(x, weight, eps):

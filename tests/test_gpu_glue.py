@@ -4,7 +4,7 @@ import pytest
 import torch
 
 from logo_amd.layers import apply_rope, rope_cos_sin
-from logo_amd.ops.glue import rms_norm, rope_apply_
+from logo_amd.ops.glue import rms_norm, rope, rope_apply_
 from tests.helpers import gen
 
 pytestmark = pytest.mark.gpu
@@ -28,6 +28,31 @@ def test_rope_bitwise_equal_to_eager(gpu, D):
     ref1 = apply_rope(one[0], c1, s1)
     rope_apply_(one, c1, s1)
     assert torch.equal(ref1, one[0])
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_rope_autograd_bitwise_equal_to_eager_autograd(gpu, D):
+    """The differentiable fused RoPE: outputs and input gradients equal eager
+    autograd through apply_rope bit for bit, with one output unused (no
+    gradient) and a non-contiguous upstream gradient."""
+    g = gen(D + 1)
+    B, T, H, HK = 2, 45, 4, 2
+    pos = torch.randint(0, 30000, (B, T), generator=g).to(gpu)
+    cos, sin = rope_cos_sin(pos, D, 10000.0, torch.bfloat16)
+    xs = [torch.randn(B, T, h, D, generator=g).bfloat16().to(gpu) for h in (H, HK, H, HK)]
+    dys = [torch.randn(B, T, h, D, generator=g).bfloat16().to(gpu) for h in (H, HK, H)]
+    dys[1] = torch.randn(B, T, D, HK, generator=g).bfloat16().to(gpu).transpose(-1, -2)
+    ref_in = [x.clone().requires_grad_() for x in xs]
+    ref_out = [apply_rope(x, cos, sin) for x in ref_in]
+    torch.autograd.backward(ref_out[:3], dys)
+    got_in = [x.clone().requires_grad_() for x in xs]
+    got_out = rope(got_in, cos, sin)
+    torch.autograd.backward(got_out[:3], dys)
+    for r, o in zip(ref_out, got_out):
+        assert torch.equal(r.detach(), o.detach())
+    for r, o in zip(ref_in[:3], got_in[:3]):
+        assert torch.equal(r.grad, o.grad)
+    assert got_in[3].grad is None or not got_in[3].grad.any()
 
 
 @pytest.mark.parametrize("rows,cols", [(7, 2048), (64, 128), (3, 4096), (5, 200)])
