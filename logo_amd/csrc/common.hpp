@@ -46,7 +46,10 @@ __device__ __forceinline__ void mfma32_agpr(f32x16& d, const bf16x8& a, const bf
   asm volatile("s_nop 2\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(d) : "v"(a), "v"(b));
 }
 // Wait states between the last mfma32_agpr and a VALU read of its result
-// (an 8-pass MFMA needs fewer than 32).
+// (an 8-pass MFMA needs fewer than 32).  The compiler may place its own
+// copies out of the AGPRs ahead of this operand-less asm, so kernels also run
+// it at the end of every iteration of their MFMA loop: the epilogue's reads,
+// which cannot move into the loop, then always follow wait states.
 __device__ __forceinline__ void agpr_acc_drain() { asm volatile("s_nop 15\n\ts_nop 15"); }
 
 // Reductions over the lane pair (l, l ^ 32): v_permlane32_swap hands every

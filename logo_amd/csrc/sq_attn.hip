@@ -626,6 +626,7 @@ __global__ __launch_bounds__(128) LOGO_OCC_DQ64 void sq_dq64_kernel(const AttnAr
       step(BufTag<1>{}, BufTag<0>{}, t + 1);
       step(BufTag<1>{}, BufTag<1>{}, t + 1);
     }
+    if (t + 2 >= nt) agpr_acc_drain();  // the epilogue reads dQ next
   }
 
   agpr_acc_drain();
@@ -908,6 +909,7 @@ __global__ __launch_bounds__(256) LOGO_OCC_DKV void sq_dkv_kernel(const AttnArgs
         else compute(std::false_type{});
       }
       if (has_next) store_stats(B ^ 1);
+      else agpr_acc_drain();  // the head's last step: dK / dV may be read next
       wait_vmem();
       __syncthreads();
     };
