@@ -11,7 +11,10 @@ import re
 
 import torch
 
-LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "liblogo_hip.so")
+# LOGO_HIP_LIB overrides the in-tree library (e.g. to time a variant build
+# against the default one in the same run).
+LIB_PATH = os.environ.get("LOGO_HIP_LIB") or os.path.join(os.path.dirname(os.path.abspath(__file__)),
+                                                          "liblogo_hip.so")
 HEADER_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include",
                            "logo_hip.h")
 

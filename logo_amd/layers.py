@@ -31,7 +31,7 @@ from .ops.epilogue import logo_epilogue
 from .ops.glue import rms_norm, rope, rope_apply_
 from .ops.sq_attn import dense_causal_attn, sq_full_attn, swa_attn
 
-__all__ = ["LoGoConfig", "LoGoAttention", "RMSNorm", "rope_cos_sin", "apply_rope", "position_ids_for"]
+__all__ = ["LoGoConfig", "LoGoAttention", "Attention", "RMSNorm", "rope_cos_sin", "apply_rope", "position_ids_for"]
 
 SPARSE_BACKENDS = ("triton", "hip")
 
@@ -136,6 +136,37 @@ def apply_rope(x, cos, sin):
     return x * cos + rot * sin
 
 
+def _rope_all(tensors, cos, sin):
+    """RoPE of ``[B, T, H_i, D]`` tensors with one cos / sin: one in-place HIP
+    launch when no gradient is needed, one launch each way under autograd,
+    the eager ops for tensors that are not contiguous bf16 ROCm tensors."""
+    tensors = list(tensors)
+    on_dev = all(t.is_cuda and t.dtype == torch.bfloat16 for t in (*tensors, cos, sin)) and all(
+        t.is_contiguous() for t in tensors)
+    if on_dev and _fused_ok(*tensors):
+        return rope_apply_(tensors, cos, sin)
+    if on_dev:
+        return rope(tensors, cos, sin)
+    return [apply_rope(t, cos, sin) for t in tensors]
+
+
+def _cos_sin(layer, B, T, device, dtype, position_ids, cu_seqlens, cache, position_embeddings):
+    if position_embeddings is not None:
+        return position_embeddings
+    if position_ids is None:
+        position_ids = position_ids_for(B, T, device, cu_seqlens, cache)
+    return rope_cos_sin(position_ids, layer.head_dim, layer.config.rope_theta, dtype)
+
+
+def _pack_cu(B, T, cu_seqlens, device):
+    """Packed ``[1, B*T]`` segments: the given ``cu_seqlens`` (for ``B == 1``)
+    or one segment per batch row (logo/layers/logo.py:199-209)."""
+    if cu_seqlens is None:
+        return torch.arange(0, (B + 1) * T, T, dtype=torch.int32, device=device)
+    assert B == 1, "cu_seqlens requires packed [1, N] input"
+    return cu_seqlens.to(torch.int32)
+
+
 def _per_head_linear(x, w):
     """``x [..., H, D] @ w [H, D, E]`` per head as one batched GEMM over heads
     (both operands contiguous: bf16 batched products are only used with
@@ -227,21 +258,9 @@ class LoGoAttention(nn.Module):
         gq, gk, gv = self._global_qkv(q, k, v)
         gate = torch.sigmoid(self.gate_proj(hidden_states))  # [B, T, 1]
 
-        if position_embeddings is not None:
-            cos, sin = position_embeddings
-        else:
-            if position_ids is None:
-                position_ids = position_ids_for(B, T, hidden_states.device, cu_seqlens, past_key_value)
-            cos, sin = rope_cos_sin(position_ids, D, self.config.rope_theta, q.dtype)
-        on_dev = all(t.is_cuda and t.dtype == torch.bfloat16 for t in (q, k, gq, gk, cos, sin)) and all(
-            t.is_contiguous() for t in (q, k, gq, gk))
-        if on_dev and _fused_ok(q, k, gq, gk):
-            rope_apply_([q, k, gq, gk], cos, sin)  # in place, one launch
-        elif on_dev:
-            q, k, gq, gk = rope([q, k, gq, gk], cos, sin)  # one launch each way under autograd
-        else:
-            q, k = apply_rope(q, cos, sin), apply_rope(k, cos, sin)
-            gq, gk = apply_rope(gq, cos, sin), apply_rope(gk, cos, sin)
+        cos, sin = _cos_sin(self, B, T, hidden_states.device, q.dtype, position_ids, cu_seqlens, past_key_value,
+                            position_embeddings)
+        q, k, gq, gk = _rope_all((q, k, gq, gk), cos, sin)
 
         if past_key_value is not None and T == 1:
             out = self._decode(q, k, v, gq, gk, gv, gate, past_key_value)
@@ -261,11 +280,7 @@ class LoGoAttention(nn.Module):
     def _prefill(self, q, k, v, gq, gk, gv, gate, cu_seqlens):
         B, T, H, D = q.shape
         N = B * T
-        if cu_seqlens is None:
-            cu = torch.arange(0, (B + 1) * T, T, dtype=torch.int32, device=q.device)
-        else:
-            assert B == 1, "cu_seqlens requires packed [1, N] input"
-            cu = cu_seqlens.to(torch.int32)
+        cu = _pack_cu(B, T, cu_seqlens, q.device)
         pk = lambda x: x.reshape(1, N, x.shape[2], x.shape[3])
         local = swa_attn(pk(q), pk(k), pk(v), cu, window=self.local_window_size)
         if self.sparse_full_attn_backend in SPARSE_BACKENDS:
@@ -285,3 +300,59 @@ class LoGoAttention(nn.Module):
         glob = decode_attn(gq[:, 0], cache.global_k[self.layer_idx], cache.global_v[self.layer_idx], len_g,
                            gate.view(B), self.gate_thres, max_len=bound_g)
         return self._fuse(local.view(B, 1, H, D), glob.view(B, 1, H, D), gate.view(B, 1))
+
+
+class Attention(nn.Module):
+    """Plain causal attention layer, used where ``attn_type_list[i] != 0``
+    (logo/layers/attn.py:22-127, selected at logo/modeling_logo.py:47-51):
+    q / k / v projections, RoPE, dense causal attention over each packed
+    segment, o_proj.  The reference runs flash-attn; here the attention is this
+    package's HIP kernel in dense mode (every row, no compaction), prefill and
+    training alike, and a decode step reads the layer's full K/V from the
+    preallocated cache with the decode kernel (every row active).  Same
+    parameter names as the reference, so its state dict loads."""
+
+    def __init__(self, config: LoGoConfig, layer_idx: int = 0):
+        super().__init__()
+        self.config = config
+        self.layer_idx = layer_idx
+        self.hidden_size = config.hidden_size
+        self.num_heads = config.num_attention_heads
+        self.num_key_value_heads = config.num_key_value_heads
+        self.head_dim = config.head_dim
+        if self.head_dim * self.num_heads != self.hidden_size:
+            raise ValueError(f"hidden_size must be divisible by num_heads (got `hidden_size`: {self.hidden_size}"
+                             f" and `num_heads`: {self.num_heads}).")
+        H, HK, D = self.num_heads, self.num_key_value_heads, self.head_dim
+        self.q_proj = nn.Linear(self.hidden_size, H * D, bias=config.attention_bias)
+        self.k_proj = nn.Linear(self.hidden_size, HK * D, bias=config.attention_bias)
+        self.v_proj = nn.Linear(self.hidden_size, HK * D, bias=config.attention_bias)
+        self.o_proj = nn.Linear(self.hidden_size, self.hidden_size, bias=config.attention_out_bias)
+
+    def forward(self, hidden_states, position_ids=None, cu_seqlens=None,
+                past_key_value: Optional[LogoKVCache] = None, position_embeddings=None, **kwargs):
+        B, T, _ = hidden_states.shape
+        H, HK, D = self.num_heads, self.num_key_value_heads, self.head_dim
+        q = self.q_proj(hidden_states).view(B, T, H, D)
+        k = self.k_proj(hidden_states).view(B, T, HK, D)
+        v = self.v_proj(hidden_states).view(B, T, HK, D)
+        cos, sin = _cos_sin(self, B, T, hidden_states.device, q.dtype, position_ids, cu_seqlens, past_key_value,
+                            position_embeddings)
+        q, k = _rope_all((q, k), cos, sin)
+        if past_key_value is not None and T == 1:
+            cache = past_key_value
+            # the local ring of a plain layer is never read; it takes the same rows
+            cache.append(self.layer_idx, k[:, 0], v[:, 0], k[:, 0], v[:, 0])
+            len_g, _ = cache.step_lengths()
+            bound_g, _ = cache.length_bounds()
+            out = decode_attn(q[:, 0], cache.global_k[self.layer_idx], cache.global_v[self.layer_idx], len_g,
+                              max_len=bound_g).view(B, 1, H * D)
+        else:
+            if past_key_value is not None:
+                kt, vt = k.transpose(1, 2), v.transpose(1, 2)
+                past_key_value.prefill(self.layer_idx, kt, vt, kt, vt)
+            N = B * T
+            cu = _pack_cu(B, T, cu_seqlens, q.device)
+            pk = lambda x: x.reshape(1, N, x.shape[2], x.shape[3])
+            out = dense_causal_attn(pk(q), pk(k), pk(v), cu).view(B, T, H * D)
+        return self.o_proj(out), None, past_key_value

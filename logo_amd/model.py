@@ -21,7 +21,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from .layers import LoGoAttention, LoGoConfig, RMSNorm, position_ids_for, rope_cos_sin
+from .layers import Attention, LoGoAttention, LoGoConfig, RMSNorm, position_ids_for, rope_cos_sin
 from .ops.decode import LogoKVCache
 
 __all__ = ["LoGoMLP", "LoGoDecoderLayer", "LoGoModel", "LoGoForCausalLM"]
@@ -41,11 +41,17 @@ class LoGoMLP(nn.Module):
 
 
 class LoGoDecoderLayer(nn.Module):
-    """Pre-norm attention + MLP block (logo/modeling_logo.py:42-106)."""
+    """Pre-norm attention + MLP block (logo/modeling_logo.py:42-106); the
+    attention is LoGo's or plain per ``config.attn_type_list``."""
 
     def __init__(self, config: LoGoConfig, layer_idx: int):
         super().__init__()
-        self.self_attn = LoGoAttention(config, layer_idx)
+        # attn_type_list[i] == 0: LoGo attention, else plain causal attention
+        # (logo/modeling_logo.py:47-51)
+        if config.attn_type_list[layer_idx] == 0:
+            self.self_attn = LoGoAttention(config, layer_idx)
+        else:
+            self.self_attn = Attention(config, layer_idx)
         self.mlp = LoGoMLP(config)
         self.input_layernorm = RMSNorm(config.hidden_size, eps=config.rms_norm_eps)
         self.post_attention_layernorm = RMSNorm(config.hidden_size, eps=config.rms_norm_eps)

@@ -89,3 +89,29 @@ def logo_layer_ref(h, p, cfg, sel_bt, cu=None, backend="hip"):
     g = gate.masked_fill(~sel_bt.reshape(B, T, 1), 0.0)
     out = (1 - g) * local + g * glob
     return out @ p["o_proj.weight"].T
+
+
+def plain_attn_layer_ref(h, p, cfg, cu=None):
+    """Float64 restatement of the plain attention layer
+    (logo/layers/attn.py:62-127): projections, RoPE, dense causal attention per
+    packed segment, o_proj."""
+    B, T, C = h.shape
+    H, HK, D = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+    q = (h @ p["q_proj.weight"].T).view(B, T, H, D)
+    k = (h @ p["k_proj.weight"].T).view(B, T, HK, D)
+    v = (h @ p["v_proj.weight"].T).view(B, T, HK, D)
+    N = B * T
+    if cu is None:
+        seg = torch.arange(N) // T
+        pos = torch.arange(N) % T
+    else:
+        cul = cu.tolist()
+        seg = torch.zeros(N, dtype=torch.long)
+        pos = torch.zeros(N, dtype=torch.long)
+        for s in range(len(cul) - 1):
+            seg[cul[s]:cul[s + 1]] = s
+            pos[cul[s]:cul[s + 1]] = torch.arange(cul[s + 1] - cul[s])
+    posbt = pos.view(B, T)
+    q, k = _rope(q, posbt, cfg.rope_theta), _rope(k, posbt, cfg.rope_theta)
+    o = _attn(q.reshape(N, H, D), k.reshape(N, HK, D), v.reshape(N, HK, D), seg, pos, None, None)
+    return o.reshape(B, T, C) @ p["o_proj.weight"].T

@@ -92,3 +92,35 @@ def test_layer_cfg4_shapes_forward(gpu):
         ratio = (torch.sigmoid(layer.gate_proj(h)) >= 0.5).float().mean().item()
     assert 0.4 < ratio < 0.6
     assert torch.isfinite(out).all() and torch.isfinite(h.grad).all()
+
+
+@pytest.mark.parametrize("cu,hk", [(None, 4), ([0, 70, 70, 200], 2)])
+def test_plain_attention_layer_fwd_bwd(gpu, cu, hk):
+    """The plain attention layer (attn_type_list != 0) on the dense HIP path
+    against its float64 restatement: outputs, input and weight gradients."""
+    from logo_amd.layers import Attention
+    from tests.layer_ref import plain_attn_layer_ref
+
+    cfg = LoGoConfig(hidden_size=256, num_attention_heads=4, num_key_value_heads=hk, num_hidden_layers=1)
+    torch.manual_seed(5)
+    layer = Attention(cfg, 0)
+    with torch.no_grad():
+        for prm in layer.parameters():
+            prm.normal_(0, 0.05)
+    layer = layer.to(gpu).to(torch.bfloat16)
+    B, T = (2, 150) if cu is None else (1, 200)
+    g = gen(6)
+    h = torch.randn(B, T, 256, generator=g).bfloat16()
+    dout = torch.randn(B, T, 256, generator=g).bfloat16()
+    cu_t = None if cu is None else torch.tensor(cu, dtype=torch.int32)
+    hg = h.to(gpu).requires_grad_()
+    out, _, _ = layer(hg, cu_seqlens=None if cu_t is None else cu_t.to(gpu))
+    out.backward(dout.to(gpu))
+    params = {n: prm.detach().double().cpu().requires_grad_() for n, prm in layer.named_parameters()}
+    h64 = h.double().requires_grad_()
+    ref = plain_attn_layer_ref(h64, params, cfg, cu_t)
+    ref.backward(dout.double())
+    _scaled("out", out, ref)
+    _scaled("dh", hg.grad, h64.grad)
+    for n, prm in layer.named_parameters():
+        assert_close(n, params[n].grad, prm.grad.double().cpu(), 1e-2)

@@ -18,24 +18,29 @@ from logo_amd.model import LoGoForCausalLM
 pytestmark = pytest.mark.gpu
 
 
-def _model(gpu, thres, seed=0):
-    cfg = LoGoConfig(vocab_size=512, hidden_size=256, intermediate_size=512, num_hidden_layers=2,
-                     num_attention_heads=4, window_size=128, gate_thres_init=thres)
+def _model(gpu, thres, seed=0, attn_types=None):
+    cfg = LoGoConfig(vocab_size=512, hidden_size=256, intermediate_size=512,
+                     num_hidden_layers=2 if attn_types is None else len(attn_types),
+                     num_attention_heads=4, window_size=128, gate_thres_init=thres, attn_type_list=attn_types)
     m = LoGoForCausalLM(cfg)
     g = torch.Generator()
     g.manual_seed(seed)
     m.init_weights(g)
     with torch.no_grad():
         for layer in m.model.layers:  # global branch differs from the local one
+            if not hasattr(layer.self_attn, "q_global_proj"):
+                continue
             for p in (layer.self_attn.q_global_proj, layer.self_attn.k_global_proj,
                       layer.self_attn.v_global_proj):
                 p.add_(torch.randn(p.shape, generator=g) * 0.05)
     return m.to(device=gpu, dtype=torch.bfloat16).eval()
 
 
-@pytest.mark.parametrize("thres", [-1.0, 2.0])
-def test_decode_matches_prefill(gpu, thres):
-    m = _model(gpu, thres)
+@pytest.mark.parametrize("thres,attn_types", [(-1.0, None), (2.0, None), (0.5, [1, 1]), (-1.0, [0, 1, 0])])
+def test_decode_matches_prefill(gpu, thres, attn_types):
+    """Also with plain attention layers (attn_type_list != 0), alone and mixed
+    with LoGo layers."""
+    m = _model(gpu, thres, attn_types=attn_types)
     B, T, steps = 2, 190, 12
     g = torch.Generator()
     g.manual_seed(1)
