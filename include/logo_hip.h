@@ -222,6 +222,18 @@ int logo_rope(const void* x0, void* y0, int h0, const void* x1, void* y1, int h1
               int64_t n_tokens, int d, int inverse, int dtype, void* stream);
 
 /*
+ * Per-head projection of a few tokens, for up to three tensors in one launch
+ * (a NULL x_i is skipped): y_i[t, h, :] = x_i[t, h, :] W_i[h] with x_i
+ * [n_tokens, h_i, d], W_i [h_i, d, e], y_i [n_tokens, h_i, e], bf16, fp32
+ * accumulation.  The LoGo layer's linear_proj global re-parameterisation
+ * (logo/layers/logo.py:86-94, the einsum over heads of q, k and v) at decode
+ * sizes (n_tokens <= 4096; d <= 256, e <= 128).
+ */
+int logo_head_proj(const void* x0, const void* w0, void* y0, int h0, const void* x1, const void* w1, void* y1,
+                   int h1, const void* x2, const void* w2, void* y2, int h2, int n_tokens, int d, int e, int dtype,
+                   void* stream);
+
+/*
  * RMSNorm of rows [rows, cols] bf16 with weight [cols]: y = w * bf16(x *
  * rsqrt(mean(x^2) + eps)), mean in fp32 (logo/modules/layernorm.py:17-22; the
  * decoder's input / post-attention / final norms, logo/modeling_logo.py:58-59,

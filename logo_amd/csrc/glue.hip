@@ -16,6 +16,11 @@
 //
 // RMSNorm (logo/modules/layernorm.py:17-22): y = bf16(w * bf16(x *
 // rsqrt(mean(x^2) + eps))), the mean taken in fp32.
+//
+// Per-head projection for a few tokens (the LoGo global re-parameterisation
+// at decode, logo/layers/logo.py:86-94: gq = q W_q[h], gk = k W_k[h],
+// gv = v W_v[h] per head): one launch for the three tensors instead of three
+// batched GEMMs and six layout copies; fp32 accumulation, one bf16 rounding.
 #include <math.h>
 
 #include "capi.hpp"
@@ -119,6 +124,51 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const bf16* x, const bf16*
   }
 }
 
+struct HeadProjArgs {
+  const bf16* x[3];  // [T, H_i, D]
+  const bf16* w[3];  // [H_i, D, E]
+  bf16* y[3];        // [T, H_i, E]
+  int heads[3];
+  int head0[4];      // prefix of heads over the tensors
+  int nt, t, d, e;
+};
+
+constexpr int kHpTok = 8;  // tokens per workgroup
+
+// Workgroup (global head gh, token block): thread n computes output column n
+// of kHpTok tokens; W's row k is read once per block (coalesced over n) and
+// the tokens' x rows sit in LDS.
+__global__ __launch_bounds__(128) void head_proj_kernel(const HeadProjArgs a) {
+  const int gh = blockIdx.x;
+  int ti = 0;
+  while (ti + 1 < a.nt && gh >= a.head0[ti + 1]) ++ti;
+  const int h = gh - a.head0[ti], H = a.heads[ti];
+  const int t0 = blockIdx.y * kHpTok;
+  const int n = threadIdx.x;
+  __shared__ float xs[kHpTok][256];
+  for (int idx = threadIdx.x; idx < kHpTok * a.d; idx += 128) {
+    const int tt = idx / a.d, k = idx % a.d;
+    const int t = t0 + tt;
+    xs[tt][k] = t < a.t ? (float)a.x[ti][((int64_t)t * H + h) * a.d + k] : 0.f;
+  }
+  __syncthreads();
+  if (n >= a.e) return;
+  const bf16* w = a.w[ti] + (int64_t)h * a.d * a.e + n;
+  float acc[kHpTok];
+#pragma unroll
+  for (int tt = 0; tt < kHpTok; ++tt) acc[tt] = 0.f;
+  for (int k = 0; k < a.d; ++k) {
+    const float wk = (float)w[(int64_t)k * a.e];
+#pragma unroll
+    for (int tt = 0; tt < kHpTok; ++tt) acc[tt] = fmaf(xs[tt][k], wk, acc[tt]);
+  }
+#pragma unroll
+  for (int tt = 0; tt < kHpTok; ++tt) {
+    const int t = t0 + tt;
+    if (t < a.t) a.y[ti][((int64_t)t * H + h) * a.e + n] = (bf16)acc[tt];
+  }
+}
+
 }  // namespace logo
 
 using namespace logo;
@@ -202,5 +252,40 @@ extern "C" int logo_rmsnorm(const void* x, const void* w, void* y, int64_t rows,
   else
     hipLaunchKernelGGL(rmsnorm_kernel<8>, dim3((unsigned)nblk), dim3(256), 0, st, xb, wb, yb, rows, cols, eps);
   LOGO_LAUNCH_CHECK("rmsnorm_kernel");
+  return LOGO_OK;
+}
+
+extern "C" int logo_head_proj(const void* x0, const void* w0, void* y0, int h0, const void* x1, const void* w1,
+                              void* y1, int h1, const void* x2, const void* w2, void* y2, int h2, int n_tokens,
+                              int d, int e, int dtype, void* stream) {
+  LOGO_REQUIRE(dtype == LOGO_DTYPE_BF16, "only bf16 tensors are supported");
+  LOGO_REQUIRE(n_tokens >= 0 && n_tokens <= 4096, "n_tokens (%d) must be in [0, 4096]", n_tokens);
+  LOGO_REQUIRE(d >= 1 && d <= 256 && e >= 1 && e <= 128, "d must be in [1, 256] and e in [1, 128] (d %d, e %d)", d,
+               e);
+  HeadProjArgs a{};
+  const void* xs[3] = {x0, x1, x2};
+  const void* ws[3] = {w0, w1, w2};
+  void* ys[3] = {y0, y1, y2};
+  const int hs[3] = {h0, h1, h2};
+  int total = 0;
+  for (int i = 0; i < 3; ++i) {
+    if (xs[i] == nullptr) continue;
+    LOGO_REQUIRE(ws[i] && ys[i] && hs[i] >= 1, "tensor %d: null weight / output or no heads", i);
+    a.x[a.nt] = static_cast<const bf16*>(xs[i]);
+    a.w[a.nt] = static_cast<const bf16*>(ws[i]);
+    a.y[a.nt] = static_cast<bf16*>(ys[i]);
+    a.heads[a.nt] = hs[i];
+    a.head0[a.nt] = total;
+    total += hs[i];
+    ++a.nt;
+  }
+  a.head0[a.nt] = total;
+  if (a.nt == 0 || n_tokens == 0) return LOGO_OK;
+  a.t = n_tokens;
+  a.d = d;
+  a.e = e;
+  const dim3 grid((unsigned)total, (unsigned)((n_tokens + kHpTok - 1) / kHpTok));
+  hipLaunchKernelGGL(head_proj_kernel, grid, dim3(128), 0, as_stream(stream), a);
+  LOGO_LAUNCH_CHECK("head_proj_kernel");
   return LOGO_OK;
 }

@@ -28,7 +28,7 @@ import torch.nn.functional as F
 
 from .ops.decode import LogoKVCache, decode_attn
 from .ops.epilogue import logo_epilogue
-from .ops.glue import rms_norm, rope, rope_apply_
+from .ops.glue import head_proj, rms_norm, rope, rope_apply_
 from .ops.sq_attn import dense_causal_attn, sq_full_attn, swa_attn
 
 __all__ = ["LoGoConfig", "LoGoAttention", "Attention", "RMSNorm", "rope_cos_sin", "apply_rope", "position_ids_for"]
@@ -236,6 +236,11 @@ class LoGoAttention(nn.Module):
             return (sh(q, self.q_global_scale, self.q_global_offset),
                     sh(k, self.k_global_scale, self.k_global_offset),
                     sh(v, self.v_global_scale, self.v_global_offset))
+        ws = (self.q_global_proj, self.k_global_proj, self.v_global_proj)
+        n_tok = q.shape[0] * q.shape[1]
+        if n_tok <= 64 and _fused_ok(q, k, v, *ws) and q.shape[-1] <= 128:
+            # decode sizes: one launch for the three projections
+            return tuple(head_proj((q, k, v), ws))
         return (_per_head_linear(q, self.q_global_proj), _per_head_linear(k, self.k_global_proj),
                 _per_head_linear(v, self.v_global_proj))
 

@@ -13,7 +13,7 @@ import torch
 
 from .. import _lib
 
-__all__ = ["rope_apply_", "rope", "RopeFunction", "rms_norm"]
+__all__ = ["rope_apply_", "rope", "RopeFunction", "rms_norm", "head_proj"]
 
 
 def _rope_checked(tensors, cos, sin, what):
@@ -109,3 +109,31 @@ def rms_norm(x, weight, eps):
     _lib.launch("logo_rmsnorm", lib.logo_rmsnorm, _lib.ptr(xc), _lib.ptr(weight.contiguous()), _lib.ptr(y),
                 xc.numel() // cols, cols, float(eps), _lib.DTYPE_BF16, _lib.stream_of(xc))
     return y
+
+
+def head_proj(xs, ws):
+    """Per-head projections ``x_i [..., H_i, D] @ w_i [H_i, D, E]`` of up to
+    three bf16 tensors sharing their leading ``[...]`` (at most 4096 tokens),
+    one HIP launch; returns ``[..., H_i, E]`` tensors."""
+    if not 1 <= len(xs) == len(ws) <= 3:
+        raise ValueError("head_proj takes one to three (x, w) pairs")
+    _lib.require_gpu(*xs, *ws)
+    D, E = xs[0].shape[-1], ws[0].shape[-1]
+    n = xs[0][..., 0, 0].numel()
+    xs = [x.contiguous() for x in xs]
+    ws = [w.to(torch.bfloat16).contiguous() for w in ws]
+    for x, w in zip(xs, ws):
+        if x.dtype != torch.bfloat16 or x.shape[-1] != D or x[..., 0, 0].numel() != n:
+            raise ValueError("head_proj needs bf16 [..., H, D] inputs of one shape prefix")
+        if w.shape != (x.shape[-2], D, E):
+            raise ValueError("each weight must be [H, D, E] for its input's H")
+    ys = [torch.empty(*x.shape[:-1], E, dtype=torch.bfloat16, device=x.device) for x in xs]
+    args = []
+    for i in range(3):
+        if i < len(xs):
+            args += [_lib.ptr(xs[i]), _lib.ptr(ws[i]), _lib.ptr(ys[i]), xs[i].shape[-2]]
+        else:
+            args += [None, None, None, 0]
+    lib = _lib.lib()
+    _lib.launch("logo_head_proj", lib.logo_head_proj, *args, n, D, E, _lib.DTYPE_BF16, _lib.stream_of(xs[0]))
+    return ys

@@ -70,3 +70,19 @@ def test_rmsnorm_matches_eager(gpu, rows, cols):
     assert (diff <= 2 ** -7 * eager.float().abs().clamp(min=1)).all()
     ref64 = w.double() * (x.double() / torch.sqrt(x.double().pow(2).mean(-1, keepdim=True) + eps))
     assert (got.double() - ref64).abs().max().item() <= 2e-2 * ref64.abs().max().item()
+
+
+@pytest.mark.parametrize("T,H,HK,D", [(32, 16, 16, 128), (13, 8, 2, 128), (5, 4, 4, 64)])
+def test_head_proj_matches_fp64(gpu, T, H, HK, D):
+    """Per-head projection kernel (decode path of the global re-parameterisation)
+    against a float64 einsum of the same bf16 inputs, within bf16 rounding."""
+    from logo_amd.ops.glue import head_proj
+
+    g = gen(T * H + D)
+    xs = [torch.randn(T, h, D, generator=g).bfloat16().to(gpu) for h in (H, HK, HK)]
+    ws = [(torch.eye(D) + 0.05 * torch.randn(h, D, D, generator=g)).bfloat16().to(gpu) for h in (H, HK, HK)]
+    ys = head_proj(xs, ws)
+    for x, w, y in zip(xs, ws, ys):
+        ref = torch.einsum("thd,hde->the", x.double(), w.double())
+        assert y.shape == ref.shape
+        assert ((y.double() - ref).abs() <= 2 ** -8 * ref.abs() + 1e-3).all()
