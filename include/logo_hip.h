@@ -46,6 +46,7 @@ extern "C" {
 #define LOGO_META_STRIDE(nseq) (LOGO_META_HDR + 3 * ((nseq) + 1))
 
 #define LOGO_DTYPE_BF16 0
+#define LOGO_DTYPE_F32 1
 
 /* Message of the calling thread's last error ("" if none). */
 const char* logo_last_error(void);
@@ -149,10 +150,11 @@ int logo_sq_bwd_dkv(const void* q, const void* k, const void* v, const void* o,
  * (one [D] weight each, shared by all heads) and the gated fusion, with the
  * reference's eager bf16 rounding points (logo/modules/layernorm.py:17-22;
  * logo/layers/logo.py:180-181, :225-226, :256-258).  L, G: [N, H, D];
- * gate: [N] (post-sigmoid); thres: one float on the device; w_l, w_g: [D];
- * out: [N, H*D].
+ * gate: [N] (post-sigmoid); thres: one value on the device, of thres_dtype
+ * (LOGO_DTYPE_BF16 or LOGO_DTYPE_F32: the threshold buffer as the model holds
+ * it, read in place); w_l, w_g: [D]; out: [N, H*D].
  */
-int logo_epilogue_fwd(const void* L, const void* G, const void* gate, const float* thres,
+int logo_epilogue_fwd(const void* L, const void* G, const void* gate, const void* thres, int thres_dtype,
                       const void* w_l, const void* w_g, void* out, int64_t n_tokens,
                       int heads, int d, float eps, int dtype, void* stream);
 
@@ -164,7 +166,7 @@ size_t logo_epilogue_bwd_workspace_bytes(int64_t n_tokens, int heads, int d);
  * dgate [N] (zero where gate < thres: the masked_fill at logo/layers/logo.py:256
  * blocks it), dw_l, dw_g [D]; reductions are deterministic.
  */
-int logo_epilogue_bwd(const void* L, const void* G, const void* gate, const float* thres,
+int logo_epilogue_bwd(const void* L, const void* G, const void* gate, const void* thres, int thres_dtype,
                       const void* w_l, const void* w_g, const void* dout, void* dL, void* dG,
                       void* dgate, void* dw_l, void* dw_g, int64_t n_tokens, int heads, int d,
                       float eps, void* workspace, int dtype, void* stream);
@@ -174,7 +176,8 @@ size_t logo_decode_workspace_bytes(int batch, int hq, int d, int max_len);
 
 /*
  * Gate-aware decode attention, one query token per sequence: for row b with
- * gate[b] >= *thres (or every row when gate is NULL), out[b, hq] =
+ * gate[b] >= *thres (thres of thres_dtype, as for logo_epilogue_fwd; or every
+ * row when gate is NULL), out[b, hq] =
  * softmax(scale * q[b, hq] K[b, h, 0:lens[b]]^T) V[b, h, 0:lens[b]]; rows
  * whose gate fails get zeros and read no cache (the reference runs dense
  * attention for all rows and masks, logo/layers/logo.py:228-249, :256-258).
@@ -182,7 +185,7 @@ size_t logo_decode_workspace_bytes(int batch, int hq, int d, int max_len);
  * layout, preallocated); max_len >= every lens[b] (sizes the grid).
  */
 int logo_decode_attn(const void* q, const void* k_cache, const void* v_cache, const int32_t* lens,
-                     const void* gate, const float* thres, void* out, void* workspace, int batch,
+                     const void* gate, const void* thres, int thres_dtype, void* out, void* workspace, int batch,
                      int hq, int h, int d, int64_t t_cap, int max_len, float scale, int dtype,
                      void* stream);
 

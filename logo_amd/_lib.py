@@ -34,12 +34,12 @@ SIGNATURES = {
     "logo_chunk_indices": ([_P, _I, _I, _P, _I64, _P, _P, _P], _I),
     "logo_q_start_blk": ([_P, _P, _P, _P, _I64, _I, _P, _P], _I),
     "logo_sq_fwd": ([_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I, _I, _I, _I, _I, _F, _I, _I, _P], _I),
-    "logo_epilogue_fwd": ([_P, _P, _P, _P, _P, _P, _P, _I64, _I, _I, _F, _I, _P], _I),
+    "logo_epilogue_fwd": ([_P, _P, _P, _P, _I, _P, _P, _P, _I64, _I, _I, _F, _I, _P], _I),
     "logo_epilogue_bwd_workspace_bytes": ([_I64, _I, _I], _SZ),
-    "logo_epilogue_bwd": ([_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I, _I, _F, _P, _I, _P],
+    "logo_epilogue_bwd": ([_P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I, _I, _F, _P, _I, _P],
                           _I),
     "logo_decode_workspace_bytes": ([_I, _I, _I, _I], _SZ),
-    "logo_decode_attn": ([_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I64, _I, _F, _I, _P], _I),
+    "logo_decode_attn": ([_P, _P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I64, _I, _F, _I, _P], _I),
     "logo_cache_append": ([_P, _P, _P, _P, _P, _I, _I, _I, _I64, _I, _I, _P], _I),
     "logo_rope_apply": ([_P, _I, _P, _I, _P, _I, _P, _I, _P, _P, _I64, _I, _I, _P], _I),
     "logo_rope": ([_P, _P, _I, _P, _P, _I, _P, _P, _I, _P, _P, _I, _P, _P, _I64, _I, _I, _I, _P], _I),
@@ -55,6 +55,17 @@ BQ = 128
 BKV = 128
 META_HDR = 8
 DTYPE_BF16 = 0
+DTYPE_F32 = 1
+
+
+def thres_arg(thres: torch.Tensor):
+    """(pointer, dtype code) of a one-element threshold tensor, read in place
+    when it is bf16 or fp32 (no conversion launch)."""
+    t = thres.detach().reshape(1)
+    if t.dtype not in (torch.bfloat16, torch.float32):
+        t = t.to(torch.float32)
+    t = t.contiguous()
+    return t, (DTYPE_BF16 if t.dtype == torch.bfloat16 else DTYPE_F32)
 
 
 def meta_stride(nseq: int) -> int:

@@ -322,6 +322,12 @@ struct TileReader {
   }
 };
 
+// A threshold held on the device as bf16 or fp32 (the model's buffer, read in
+// place).
+__device__ __forceinline__ float load_thres(const void* p, bool bf16_value) {
+  return bf16_value ? (float)*static_cast<const bf16*>(p) : *static_cast<const float*>(p);
+}
+
 // Largest s in [0, n) with arr[s] <= x (arr ascending, arr[0] <= x).
 __device__ __forceinline__ int seg_of(const int32_t* arr, int n, int64_t x) {
   int lo = 0, hi = n;  // invariant: arr[lo] <= x, answer < hi

@@ -32,7 +32,8 @@ struct DecArgs {
   const bf16* v;
   const int32_t* lens;  // [B] keys per row
   const bf16* gate;     // [B] or null (all active)
-  const float* thres;
+  const void* thres;
+  bool thres_bf16;
   bf16* out;            // [B, HQ, D]
   float* part;          // [B*HQ, nsplit, D + 2]
   int batch, hq, h, g, nsplit;
@@ -41,7 +42,7 @@ struct DecArgs {
 };
 
 __device__ __forceinline__ bool dec_active(const DecArgs& a, int b) {
-  return a.gate == nullptr || !((float)a.gate[b] < *a.thres);
+  return a.gate == nullptr || !((float)a.gate[b] < load_thres(a.thres, a.thres_bf16));
 }
 
 template <int D>
@@ -237,7 +238,7 @@ extern "C" size_t logo_decode_workspace_bytes(int batch, int hq, int d, int max_
 }
 
 extern "C" int logo_decode_attn(const void* q, const void* k_cache, const void* v_cache, const int32_t* lens,
-                                const void* gate, const float* thres, void* out, void* workspace, int batch,
+                                const void* gate, const void* thres, int thres_dtype, void* out, void* workspace, int batch,
                                 int hq, int h, int d, int64_t t_cap, int max_len, float scale, int dtype,
                                 void* stream) {
   LOGO_REQUIRE(batch >= 1 && h >= 1 && hq % h == 0, "bad batch / head counts");
@@ -246,6 +247,7 @@ extern "C" int logo_decode_attn(const void* q, const void* k_cache, const void* 
   LOGO_REQUIRE(max_len >= 1 && max_len <= t_cap, "max_len must be in [1, t_cap]");
   LOGO_REQUIRE(q && k_cache && v_cache && lens && out && workspace, "null pointer argument");
   LOGO_REQUIRE(gate == nullptr || thres != nullptr, "gate needs thres");
+  LOGO_REQUIRE(thres_dtype == LOGO_DTYPE_BF16 || thres_dtype == LOGO_DTYPE_F32, "thres_dtype must be bf16 or f32");
   DecArgs a{};
   a.q = static_cast<const bf16*>(q);
   a.k = static_cast<const bf16*>(k_cache);
@@ -253,6 +255,7 @@ extern "C" int logo_decode_attn(const void* q, const void* k_cache, const void* 
   a.lens = lens;
   a.gate = static_cast<const bf16*>(gate);
   a.thres = thres;
+  a.thres_bf16 = thres_dtype == LOGO_DTYPE_BF16;
   a.out = static_cast<bf16*>(out);
   a.part = static_cast<float*>(workspace);
   a.batch = batch;

@@ -26,7 +26,8 @@ struct EpiArgs {
   const bf16* L;
   const bf16* G;
   const bf16* gate;
-  const float* thres;
+  const void* thres;
+  bool thres_bf16;
   const bf16* w_l;
   const bf16* w_g;
   bf16* out;
@@ -80,7 +81,7 @@ __global__ __launch_bounds__(256) void epi_fwd_kernel(const EpiArgs a) {
   const float rl = rsqrtf(ssl / (float)D + a.eps);
   const float rg = rsqrtf(ssg / (float)D + a.eps);
   const float g = (float)a.gate[r / a.heads];
-  const float gp = g < *a.thres ? 0.f : g;
+  const float gp = g < load_thres(a.thres, a.thres_bf16) ? 0.f : g;
   const float om = bfr(1.f - gp);
   const bf16x8 wl = *reinterpret_cast<const bf16x8*>(a.w_l + 8 * c);
   const bf16x8 wg = *reinterpret_cast<const bf16x8*>(a.w_g + 8 * c);
@@ -110,7 +111,7 @@ __global__ __launch_bounds__(256) void epi_bwd_kernel(const EpiArgs a) {
     dwl[e] = 0.f;
     dwg[e] = 0.f;
   }
-  const float thres = *a.thres;
+  const float thres = load_thres(a.thres, a.thres_bf16);
   const int64_t nrb = (a.rows + RPB - 1) / RPB;
   for (int64_t rb = blockIdx.x; rb < nrb; rb += gridDim.x) {
     const int64_t r = rb * RPB + rg_;
@@ -221,13 +222,14 @@ __global__ __launch_bounds__(256) void epi_bwd_finalize_kernel(const EpiArgs a, 
   if (t >= n_tokens) return;
   const float g = (float)a.gate[t];
   float s = 0.f;
-  if (!(g < *a.thres)) {
+  if (!(g < load_thres(a.thres, a.thres_bf16))) {
     for (int h = 0; h < a.heads; ++h) s += a.dgate_part[t * a.heads + h];
   }
   a.dgate[t] = (bf16)s;
 }
 
-static int epi_check(int64_t n, int heads, int d, int dtype) {
+static int epi_check(int64_t n, int heads, int d, int dtype, int thres_dtype) {
+  LOGO_REQUIRE(thres_dtype == LOGO_DTYPE_BF16 || thres_dtype == LOGO_DTYPE_F32, "thres_dtype must be bf16 or f32");
   LOGO_REQUIRE(n >= 0 && heads >= 1, "bad token / head counts");
   LOGO_REQUIRE(d == 64 || d == 128, "head dim %d unsupported (64 or 128)", d);
   LOGO_REQUIRE(dtype == LOGO_DTYPE_BF16, "only bf16 tensors are supported");
@@ -244,10 +246,10 @@ static int64_t epi_bwd_grid(int64_t rows, int d) {
 
 using namespace logo;
 
-extern "C" int logo_epilogue_fwd(const void* L, const void* G, const void* gate, const float* thres,
-                                 const void* w_l, const void* w_g, void* out, int64_t n_tokens,
+extern "C" int logo_epilogue_fwd(const void* L, const void* G, const void* gate, const void* thres,
+                                 int thres_dtype, const void* w_l, const void* w_g, void* out, int64_t n_tokens,
                                  int heads, int d, float eps, int dtype, void* stream) {
-  int rc = epi_check(n_tokens, heads, d, dtype);
+  int rc = epi_check(n_tokens, heads, d, dtype, thres_dtype);
   if (rc != LOGO_OK) return rc;
   if (n_tokens == 0) return LOGO_OK;
   LOGO_REQUIRE(L && G && gate && thres && w_l && w_g && out, "null pointer argument");
@@ -256,6 +258,7 @@ extern "C" int logo_epilogue_fwd(const void* L, const void* G, const void* gate,
   a.G = static_cast<const bf16*>(G);
   a.gate = static_cast<const bf16*>(gate);
   a.thres = thres;
+  a.thres_bf16 = thres_dtype == LOGO_DTYPE_BF16;
   a.w_l = static_cast<const bf16*>(w_l);
   a.w_g = static_cast<const bf16*>(w_g);
   a.out = static_cast<bf16*>(out);
@@ -277,12 +280,12 @@ extern "C" size_t logo_epilogue_bwd_workspace_bytes(int64_t n_tokens, int heads,
          (size_t)epi_bwd_grid(rows, d) * 2 * (size_t)d * sizeof(float);
 }
 
-extern "C" int logo_epilogue_bwd(const void* L, const void* G, const void* gate, const float* thres,
-                                 const void* w_l, const void* w_g, const void* dout, void* dL,
+extern "C" int logo_epilogue_bwd(const void* L, const void* G, const void* gate, const void* thres,
+                                 int thres_dtype, const void* w_l, const void* w_g, const void* dout, void* dL,
                                  void* dG, void* dgate, void* dw_l, void* dw_g, int64_t n_tokens,
                                  int heads, int d, float eps, void* workspace, int dtype,
                                  void* stream) {
-  int rc = epi_check(n_tokens, heads, d, dtype);
+  int rc = epi_check(n_tokens, heads, d, dtype, thres_dtype);
   if (rc != LOGO_OK) return rc;
   LOGO_REQUIRE(L && G && gate && thres && w_l && w_g && dout && dL && dG && dgate && dw_l && dw_g &&
                    workspace,
@@ -292,6 +295,7 @@ extern "C" int logo_epilogue_bwd(const void* L, const void* G, const void* gate,
   a.G = static_cast<const bf16*>(G);
   a.gate = static_cast<const bf16*>(gate);
   a.thres = thres;
+  a.thres_bf16 = thres_dtype == LOGO_DTYPE_BF16;
   a.w_l = static_cast<const bf16*>(w_l);
   a.w_g = static_cast<const bf16*>(w_g);
   a.dout = static_cast<const bf16*>(dout);

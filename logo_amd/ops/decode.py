@@ -38,12 +38,12 @@ def decode_attn(q, k_cache, v_cache, lens, gate=None, thres=None, max_len: Optio
     lib = _lib.lib()
     ws = torch.empty((lib.logo_decode_workspace_bytes(B, HQ, D, max_len) + 3) // 4, dtype=torch.float32,
                      device=q.device)
-    th = None
+    th, th_dt = None, _lib.DTYPE_F32
     if gate is not None:
         gate = gate.contiguous().view(B)
-        th = thres.detach().reshape(1).to(torch.float32).contiguous()
+        th, th_dt = _lib.thres_arg(thres)
     _lib.launch("logo_decode_attn", lib.logo_decode_attn, _lib.ptr(qc), _lib.ptr(k_cache), _lib.ptr(v_cache),
-                _lib.ptr(lens), _lib.ptr(gate), _lib.ptr(th), _lib.ptr(out), _lib.ptr(ws), B, HQ, H, D, t_cap,
+                _lib.ptr(lens), _lib.ptr(gate), _lib.ptr(th), th_dt, _lib.ptr(out), _lib.ptr(ws), B, HQ, H, D, t_cap,
                 int(max_len), float(scale), _lib.DTYPE_BF16, _lib.stream_of(q))
     return out
 

@@ -23,13 +23,15 @@ class LogoEpilogueFunction(torch.autograd.Function):
         Lc = L.contiguous().view(n, H, D)
         Gc = G.contiguous().view(n, H, D)
         gc = gate.contiguous().view(n)
-        th = thres.detach().reshape(1).to(torch.float32).contiguous()
+        th, th_dt = _lib.thres_arg(thres)
         out = torch.empty(n, H * D, dtype=L.dtype, device=L.device)
         lib = _lib.lib()
         _lib.launch("logo_epilogue_fwd", lib.logo_epilogue_fwd, _lib.ptr(Lc), _lib.ptr(Gc), _lib.ptr(gc),
-                    _lib.ptr(th), _lib.ptr(w_l), _lib.ptr(w_g), _lib.ptr(out), n, H, D, float(eps),
+                    _lib.ptr(th), th_dt, _lib.ptr(w_l), _lib.ptr(w_g), _lib.ptr(out), n, H, D, float(eps),
                     _lib.DTYPE_BF16, _lib.stream_of(L))
-        ctx.save_for_backward(Lc, Gc, gc, th, w_l, w_g)
+        # the threshold is read in place; the backward keeps its own copy (the
+        # buffer may be stepped by the budget controller in between)
+        ctx.save_for_backward(Lc, Gc, gc, th.clone() if any(ctx.needs_input_grad) else th, w_l, w_g)
         ctx.eps = eps
         ctx.shapes = (shape, gate.shape)
         return out.view(*shape[:-2], H * D)
@@ -49,7 +51,8 @@ class LogoEpilogueFunction(torch.autograd.Function):
         ws_bytes = lib.logo_epilogue_bwd_workspace_bytes(n, H, D)
         ws = torch.empty((ws_bytes + 3) // 4, dtype=torch.float32, device=Lc.device)
         _lib.launch("logo_epilogue_bwd", lib.logo_epilogue_bwd, _lib.ptr(Lc), _lib.ptr(Gc), _lib.ptr(gc),
-                    _lib.ptr(th), _lib.ptr(w_l), _lib.ptr(w_g), _lib.ptr(do), _lib.ptr(dL), _lib.ptr(dG),
+                    _lib.ptr(th), _lib.thres_arg(th)[1], _lib.ptr(w_l), _lib.ptr(w_g), _lib.ptr(do), _lib.ptr(dL),
+                    _lib.ptr(dG),
                     _lib.ptr(dgate), _lib.ptr(dwl), _lib.ptr(dwg), n, H, D, float(ctx.eps), _lib.ptr(ws),
                     _lib.DTYPE_BF16, _lib.stream_of(Lc))
         return dL.view(shape), dG.view(shape), dgate.view(gshape), None, dwl, dwg, None
