@@ -71,6 +71,9 @@ def parse():
     ap.add_argument("--seed", type=int, default=2)
     ap.add_argument("--no-extra", action="store_true", help="skip the secondary measurements")
     ap.add_argument("--no-decode", action="store_true", help="skip the config-5 model decode measurement")
+    ap.add_argument("--decode-layer", action="store_true",
+                    help="run only the config-5 global decode branch of one layer (the kernel the "
+                         "decode HBM-traffic profile measures) and print its time and bandwidth")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run one 1 GiB device-to-device copy before the workload (the reference kernel "
                          "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters to bytes)")
@@ -342,6 +345,28 @@ def layer_cfg4_measurement(dev, iters=5, seed=3):
     }
 
 
+def decode_layer_only(dev, calls=10):
+    """Config 5's global decode branch for one layer (batch 32, 16 heads,
+    D=128, 16385 cached tokens, gates alternating 0.75 / 0.25 so 16 rows are
+    active), called ``calls`` times; prints one JSON line."""
+    from logo_amd.ops.decode import decode_attn
+
+    gen = torch.Generator()
+    gen.manual_seed(7)
+    B, H, D, ctx = 32, 16, 128, 16385
+    kc = (torch.randn(B, H, ctx, D, generator=gen) * 0.5).bfloat16().to(dev)
+    vc = torch.randn(B, H, ctx, D, generator=gen).bfloat16().to(dev)
+    q = torch.randn(B, H, D, generator=gen).bfloat16().to(dev)
+    gate = torch.tensor([0.75, 0.25] * (B // 2), dtype=torch.bfloat16, device=dev)
+    thres = torch.tensor([0.5], dtype=torch.bfloat16, device=dev)
+    lens = torch.full((B,), ctx, dtype=torch.int32, device=dev)
+    ms = _time_ms(lambda: decode_attn(q, kc, vc, lens, gate, thres, max_len=ctx), calls)
+    nbytes = (B // 2) * H * ctx * D * 2 * 2
+    print(json.dumps({"workload": "cfg5 global decode branch, one layer, 16 of 32 rows active",
+                      "ms": round(ms, 4), "algorithmic_bytes": nbytes, "gbs": round(nbytes / ms / 1e6, 1),
+                      "hbm_peak_gbs": HBM_PEAK_GBS}), flush=True)
+
+
 def decode_model_measurement(dev, batch=32, prompt=16384, steps=256, seed=4):
     """the LoGo 1.5B shapes (24 layers, hidden 2048, 16 heads,
     vocab 32000, tied embeddings), random-init bf16, a batch of random-id
@@ -436,6 +461,16 @@ def main():
     from logo_amd.ops import sq_full_attn
 
     dev = torch.device("cuda", 0)
+    if args.decode_layer:
+        if args.copy_calibration:
+            src = torch.ones(1 << 29, dtype=torch.bfloat16, device=dev)
+            dst = torch.empty_like(src)
+            torch.cuda.synchronize()
+            dst.copy_(src)
+            torch.cuda.synchronize()
+            del src, dst
+        decode_layer_only(dev)
+        return
     T, H, D = args.seq_len, args.heads, args.head_dim
     gen = torch.Generator()
     gen.manual_seed(args.seed)
