@@ -313,7 +313,10 @@ __global__ __launch_bounds__(256) LOGO_OCC_FWD void sq_fwd_pipe_kernel(const Att
               constexpr int E = decltype(e_c)::value, IT = Y * IY + E;
               constexpr int KK = IT / 16, JJ = IT % 16;
               sv[E] = sbuf[PAR ^ 1][KK][JJ];
-              pin(sv[E]);
+              // the masked path rewrites S, so it anchors its value here; the
+              // unmasked path only reads it (the max3 asm keeps the order),
+              // and an anchor would force a copy of every score
+              if constexpr (MASK) pin(sv[E]);
               if constexpr (MASK) {
                 constexpr int off = 32 * KK + 8 * (JJ / 4) + (JJ % 4);
                 bool vis = off <= hi;
