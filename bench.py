@@ -393,8 +393,11 @@ def decode_model_measurement(dev, batch=32, prompt=16384, steps=256, seed=4):
 
     # realised global ratio: gate decisions of every layer at the first decode step
     gates = []
-    hooks = [layer.self_attn.gate_proj.register_forward_hook(lambda m_, i_, o_: gates.append(torch.sigmoid(o_)))
-             for layer in model.model.layers]
+    # the gate of each layer from its input (the fused decode path computes the
+    # gate logits inside its stacked projection, not through gate_proj)
+    hooks = [layer.self_attn.register_forward_pre_hook(
+        lambda m_, args: gates.append(torch.sigmoid(m_.gate_proj(args[0]))))
+        for layer in model.model.layers]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     tok = model.prefill(ids, cache).argmax(-1)

@@ -237,6 +237,24 @@ int logo_head_proj(const void* x0, const void* w0, void* y0, int h0, const void*
                    void* stream);
 
 /*
+ * One decode step's q / k / v transform for a LoGo layer (linear_proj): from
+ * each token's stacked projection row qkv[b, :] = [q | k | v] (row stride ldq
+ * elements; H, HK, HK heads of d), the per-head global projections with wq
+ * [H, d, d], wk / wv [HK, d, d] (as logo_head_proj), RoPE with cos / sin
+ * [batch, d] of q, k and the global q, k (as logo_rope_apply), and the cache
+ * appends of logo_cache_append: rotated k and v into the local ring
+ * [batch, HK, ring, d] at pos[b] % ring, rotated global k and global v into the
+ * global cache [batch, HK, t_cap, d] at pos[b].  Writes the rotated q and
+ * global q to q_out / gq_out [batch, H, d].  Replaces the layer's global
+ * projection, RoPE and cache update of a decode step (logo/layers/logo.py:
+ * 86-94, :132-150; logo/cache.py:97-118) with one launch.
+ */
+int logo_decode_qkv(const void* qkv, int64_t ldq, const void* wq, const void* wk, const void* wv, const void* cos,
+                    const void* sin, const int32_t* pos, void* q_out, void* gq_out, void* local_k, void* local_v,
+                    void* global_k, void* global_v, int batch, int h, int hk, int d, int ring, int64_t t_cap,
+                    int dtype, void* stream);
+
+/*
  * RMSNorm of rows [rows, cols] bf16 with weight [cols]: y = w * bf16(x *
  * rsqrt(mean(x^2) + eps)), mean in fp32 (logo/modules/layernorm.py:17-22; the
  * decoder's input / post-attention / final norms, logo/modeling_logo.py:58-59,

@@ -45,6 +45,8 @@ SIGNATURES = {
     "logo_rope": ([_P, _P, _I, _P, _P, _I, _P, _P, _I, _P, _P, _I, _P, _P, _I64, _I, _I, _I, _P], _I),
     "logo_rmsnorm": ([_P, _P, _P, _I64, _I, _F, _I, _P], _I),
     "logo_head_proj": ([_P, _P, _P, _I, _P, _P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I, _P], _I),
+    "logo_decode_qkv": ([_P, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I64, _I, _P],
+                        _I),
 }
 _BWD = ([_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I, _I, _I, _I, _I, _F, _I, _I, _P], _I)
 for _name in ("logo_sq_bwd", "logo_sq_bwd_delta", "logo_sq_bwd_dq", "logo_sq_bwd_dkv"):

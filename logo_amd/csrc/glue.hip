@@ -169,6 +169,87 @@ __global__ __launch_bounds__(128) void head_proj_kernel(const HeadProjArgs a) {
   }
 }
 
+// One decode step's q / k / v transform for a LoGo layer: from the stacked
+// projection output row of each token ([q | k | v], row stride ldq), the
+// global projections (as head_proj), RoPE of q, k, gq, gk (the rounding of
+// rope_kernel) and both cache appends (k, v into the local ring at pos % ring,
+// gk, gv into the global cache at pos), replacing head_proj, rope and two
+// cache_append launches.  Outputs q (local, rotated) and gq (rotated).
+struct DecQkvArgs {
+  const bf16* qkv;
+  int64_t ldq;
+  const bf16* w[3];  // [H, D, D], [HK, D, D], [HK, D, D]
+  const bf16* cos;   // [B, D]
+  const bf16* sin;
+  const int32_t* pos;
+  bf16* q_out;       // [B, H, D]
+  bf16* gq_out;
+  bf16* lk;          // [B, HK, ring, D]
+  bf16* lv;
+  bf16* gk;          // [B, HK, t_cap, D]
+  bf16* gv;
+  int b, h, hk, ring;
+  int64_t t_cap;
+};
+
+template <int D>
+__global__ __launch_bounds__(D) void decode_qkv_kernel(const DecQkvArgs a) {
+  // blockIdx.x: heads of q (0 .. H-1), then k (H .. H+HK-1), then v
+  const int gh = blockIdx.x;
+  const int ti = gh < a.h ? 0 : (gh < a.h + a.hk ? 1 : 2);
+  const int hh = ti == 0 ? gh : (ti == 1 ? gh - a.h : gh - a.h - a.hk);
+  const int col0 = ti == 0 ? hh * D : (ti == 1 ? (a.h + hh) * D : (a.h + a.hk + hh) * D);
+  const int t0 = blockIdx.y * kHpTok;
+  const int n = threadIdx.x;
+  __shared__ float xs[kHpTok][D];
+  __shared__ float ys[kHpTok][D];
+  for (int idx = threadIdx.x; idx < kHpTok * D; idx += D) {
+    const int tt = idx / D, k = idx % D;
+    const int t = t0 + tt;
+    xs[tt][k] = t < a.b ? (float)a.qkv[(int64_t)t * a.ldq + col0 + k] : 0.f;
+  }
+  __syncthreads();
+  const bf16* w = a.w[ti] + (int64_t)hh * D * D + n;
+  float acc[kHpTok];
+#pragma unroll
+  for (int tt = 0; tt < kHpTok; ++tt) acc[tt] = 0.f;
+  for (int k = 0; k < D; ++k) {
+    const float wk = (float)w[(int64_t)k * D];
+#pragma unroll
+    for (int tt = 0; tt < kHpTok; ++tt) acc[tt] = fmaf(xs[tt][k], wk, acc[tt]);
+  }
+#pragma unroll
+  for (int tt = 0; tt < kHpTok; ++tt) ys[tt][n] = (float)(bf16)acc[tt];
+  __syncthreads();
+  const int pn = n < D / 2 ? n + D / 2 : n - D / 2;
+  for (int tt = 0; tt < kHpTok; ++tt) {
+    const int t = t0 + tt;
+    if (t >= a.b) break;
+    const float x = xs[tt][n], xp = xs[tt][pn];
+    const float y = ys[tt][n], yp = ys[tt][pn];
+    float xo = x, yo = y;
+    if (ti < 2) {
+      const float c = (float)a.cos[(int64_t)t * D + n], s = (float)a.sin[(int64_t)t * D + n];
+      // first half: v * cos + (-v[n + D/2]) * sin; second half: v * cos + v[n - D/2] * sin
+      const float sg = n < D / 2 ? -1.f : 1.f;
+      xo = bfr_g(bfr_g(x * c) + bfr_g(sg * xp * s));
+      yo = bfr_g(bfr_g(y * c) + bfr_g(sg * yp * s));
+    }
+    if (ti == 0) {
+      const int64_t o = ((int64_t)t * a.h + hh) * D + n;
+      a.q_out[o] = (bf16)xo;
+      a.gq_out[o] = (bf16)yo;
+    } else {
+      const int p = a.pos[t];
+      const int64_t row = (int64_t)t * a.hk + hh;
+      bf16* lc = ti == 1 ? a.lk : a.lv;
+      bf16* gc = ti == 1 ? a.gk : a.gv;
+      lc[(row * a.ring + p % a.ring) * D + n] = (bf16)xo;
+      gc[(row * a.t_cap + p) * D + n] = (bf16)yo;
+    }
+  }
+}
+
 }  // namespace logo
 
 using namespace logo;
@@ -287,5 +368,47 @@ extern "C" int logo_head_proj(const void* x0, const void* w0, void* y0, int h0, 
   const dim3 grid((unsigned)total, (unsigned)((n_tokens + kHpTok - 1) / kHpTok));
   hipLaunchKernelGGL(head_proj_kernel, grid, dim3(128), 0, as_stream(stream), a);
   LOGO_LAUNCH_CHECK("head_proj_kernel");
+  return LOGO_OK;
+}
+
+extern "C" int logo_decode_qkv(const void* qkv, int64_t ldq, const void* wq, const void* wk, const void* wv,
+                               const void* cos, const void* sin, const int32_t* pos, void* q_out, void* gq_out,
+                               void* local_k, void* local_v, void* global_k, void* global_v, int batch, int h,
+                               int hk, int d, int ring, int64_t t_cap, int dtype, void* stream) {
+  LOGO_REQUIRE(dtype == LOGO_DTYPE_BF16, "only bf16 tensors are supported");
+  LOGO_REQUIRE(d == 64 || d == 128, "head dim %d unsupported (64 or 128)", d);
+  LOGO_REQUIRE(batch >= 0 && batch <= 4096 && h >= 1 && hk >= 1 && h % hk == 0, "bad batch / head counts");
+  LOGO_REQUIRE(ldq >= (int64_t)(h + 2 * hk) * d, "ldq (%lld) shorter than the stacked q | k | v row",
+               (long long)ldq);
+  LOGO_REQUIRE(ring >= 1 && t_cap >= 1, "ring and t_cap must be positive");
+  LOGO_REQUIRE(qkv && wq && wk && wv && cos && sin && pos && q_out && gq_out && local_k && local_v && global_k &&
+                   global_v,
+               "null pointer argument");
+  if (batch == 0) return LOGO_OK;
+  DecQkvArgs a{};
+  a.qkv = static_cast<const bf16*>(qkv);
+  a.ldq = ldq;
+  a.w[0] = static_cast<const bf16*>(wq);
+  a.w[1] = static_cast<const bf16*>(wk);
+  a.w[2] = static_cast<const bf16*>(wv);
+  a.cos = static_cast<const bf16*>(cos);
+  a.sin = static_cast<const bf16*>(sin);
+  a.pos = pos;
+  a.q_out = static_cast<bf16*>(q_out);
+  a.gq_out = static_cast<bf16*>(gq_out);
+  a.lk = static_cast<bf16*>(local_k);
+  a.lv = static_cast<bf16*>(local_v);
+  a.gk = static_cast<bf16*>(global_k);
+  a.gv = static_cast<bf16*>(global_v);
+  a.b = batch;
+  a.h = h;
+  a.hk = hk;
+  a.ring = ring;
+  a.t_cap = t_cap;
+  const dim3 grid((unsigned)(h + 2 * hk), (unsigned)((batch + kHpTok - 1) / kHpTok));
+  hipStream_t st = as_stream(stream);
+  if (d == 128) hipLaunchKernelGGL(decode_qkv_kernel<128>, grid, dim3(128), 0, st, a);
+  else hipLaunchKernelGGL(decode_qkv_kernel<64>, grid, dim3(64), 0, st, a);
+  LOGO_LAUNCH_CHECK("decode_qkv_kernel");
   return LOGO_OK;
 }

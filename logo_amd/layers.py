@@ -26,7 +26,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from .ops.decode import LogoKVCache, decode_attn
+from .ops.decode import LogoKVCache, decode_attn, decode_qkv
 from .ops.epilogue import logo_epilogue
 from .ops.glue import head_proj, rms_norm, rope, rope_apply_
 from .ops.sq_attn import dense_causal_attn, sq_full_attn, swa_attn
@@ -253,10 +253,62 @@ class LoGoAttention(nn.Module):
         B, T = local.shape[:2]
         return ((1 - g) * local.reshape(B, T, -1) + g * glob.reshape(B, T, -1))
 
+    def _decode_weight(self):
+        """The q, k, v and gate projection weights stacked for one decode GEMM
+        (gate row then zero rows up to a multiple of 8, so every stacked row
+        starts 16-byte aligned), rebuilt when a weight changes."""
+        ws = (self.q_proj.weight, self.k_proj.weight, self.v_proj.weight, self.gate_proj.weight)
+        key = tuple((w.data_ptr(), w._version, w.dtype) for w in ws)
+        cached = getattr(self, "_decode_w", None)
+        if cached is None or cached[0] != key:
+            pad = (-sum(w.shape[0] for w in ws)) % 8
+            stacked = torch.cat([w.detach() for w in ws]
+                                + [ws[0].new_zeros(pad, ws[0].shape[1])]).contiguous()
+            self._decode_w = (key, stacked)
+        return self._decode_w[1]
+
+    def _fused_decode_ok(self, hidden_states, past_key_value):
+        if past_key_value is None or hidden_states.shape[1] != 1 or self.global_qk_param != "linear_proj":
+            return False
+        if self.q_proj.bias is not None or self.k_proj.bias is not None or self.v_proj.bias is not None:
+            return False
+        ws = (self.q_proj.weight, self.k_proj.weight, self.v_proj.weight, self.gate_proj.weight,
+              self.q_global_proj, self.k_global_proj, self.v_global_proj)
+        return self.head_dim in (64, 128) and _fused_ok(hidden_states, *ws)
+
+    def _decode_fused(self, hidden_states, cache: LogoKVCache, position_embeddings, position_ids):
+        """Decode step with the stacked q / k / v / gate GEMM and one launch for
+        the global projections, RoPE and cache appends (same arithmetic as the
+        step-by-step path: the same roundings, in the same order)."""
+        B = hidden_states.shape[0]
+        H, HK, D = self.num_heads, self.num_key_value_heads, self.head_dim
+        qkv = F.linear(hidden_states, self._decode_weight()).view(B, -1)
+        n_qkv = (H + 2 * HK) * D
+        gate = torch.sigmoid(qkv[:, n_qkv:n_qkv + 1]).view(B, 1, 1)
+        cos, sin = _cos_sin(self, B, 1, hidden_states.device, qkv.dtype, position_ids, None, cache,
+                            position_embeddings)
+        q, gq = decode_qkv(qkv, self.q_global_proj, self.k_global_proj, self.v_global_proj, cos, sin, cache,
+                           self.layer_idx, H, HK)
+        len_g, len_l = cache.step_lengths()
+        bound_g, bound_l = cache.length_bounds()
+        local = decode_attn(q, cache.local_k[self.layer_idx], cache.local_v[self.layer_idx], len_l,
+                            max_len=bound_l)
+        glob = decode_attn(gq, cache.global_k[self.layer_idx], cache.global_v[self.layer_idx], len_g,
+                           gate.view(B), self.gate_thres, max_len=bound_g)
+        return self._fuse(local.view(B, 1, H, D), glob.view(B, 1, H, D), gate.view(B, 1)), gate
+
     def forward(self, hidden_states, position_ids=None, cu_seqlens=None,
                 past_key_value: Optional[LogoKVCache] = None, position_embeddings=None, **kwargs):
         B, T, _ = hidden_states.shape
         H, HK, D = self.num_heads, self.num_key_value_heads, self.head_dim
+        if self._fused_decode_ok(hidden_states, past_key_value):
+            out, gate = self._decode_fused(hidden_states, past_key_value, position_embeddings, position_ids)
+            if self.training:
+                with torch.no_grad():
+                    self.gate_avg.add_(gate.sum().float())
+                    self.global_token_count.add_((gate >= self.gate_thres).sum().float())
+                    self.total_token_count.add_(gate.numel())
+            return self.o_proj(out), None, past_key_value
         q = self.q_proj(hidden_states).view(B, T, H, D)
         k = self.k_proj(hidden_states).view(B, T, HK, D)
         v = self.v_proj(hidden_states).view(B, T, HK, D)

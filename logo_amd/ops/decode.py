@@ -17,7 +17,7 @@ import torch
 
 from .. import _lib
 
-__all__ = ["decode_attn", "cache_append", "LogoKVCache"]
+__all__ = ["decode_attn", "cache_append", "decode_qkv", "LogoKVCache"]
 
 
 def decode_attn(q, k_cache, v_cache, lens, gate=None, thres=None, max_len: Optional[int] = None,
@@ -55,6 +55,34 @@ def cache_append(k_new, v_new, k_cache, v_cache, pos, ring: int = 0):
     _lib.launch("logo_cache_append", lib.logo_cache_append, _lib.ptr(k_new.contiguous()),
                 _lib.ptr(v_new.contiguous()), _lib.ptr(k_cache), _lib.ptr(v_cache), _lib.ptr(pos), B, H, D,
                 k_cache.shape[2], int(ring), _lib.DTYPE_BF16, _lib.stream_of(k_new))
+
+
+def decode_qkv(qkv, wq, wk, wv, cos, sin, cache: "LogoKVCache", layer: int, heads: int, kv_heads: int):
+    """One decode step's q / k / v transform for a LoGo layer in one launch.
+
+    ``qkv [B, ldq]``: each token's stacked projection row ``[q | k | v | ...]``;
+    ``wq/wk/wv``: the global ``linear_proj`` matrices; ``cos/sin [B, D]``.
+    Appends the rotated k, v (local ring) and global k, v (global cache) at the
+    cache's device position and returns the rotated q and global q
+    ``[B, H, D]``."""
+    _lib.require_gpu(qkv, wq, wk, wv, cos, sin)
+    B = qkv.shape[0]
+    D = wq.shape[-1]
+    if qkv.stride(-1) != 1 or qkv.stride(0) % 8 != 0:
+        raise ValueError("decode_qkv needs rows with unit column stride and 16-byte aligned row starts")
+    if cache.seen >= cache.max_len:
+        raise ValueError("cache is full")
+    q = torch.empty(B, heads, D, dtype=torch.bfloat16, device=qkv.device)
+    gq = torch.empty_like(q)
+    cos = cos.reshape(B, D).contiguous()
+    sin = sin.reshape(B, D).contiguous()
+    lib = _lib.lib()
+    _lib.launch("logo_decode_qkv", lib.logo_decode_qkv, _lib.ptr(qkv), qkv.stride(0), _lib.ptr(wq.contiguous()),
+                _lib.ptr(wk.contiguous()), _lib.ptr(wv.contiguous()), _lib.ptr(cos), _lib.ptr(sin),
+                _lib.ptr(cache._pos), _lib.ptr(q), _lib.ptr(gq), _lib.ptr(cache.local_k[layer]),
+                _lib.ptr(cache.local_v[layer]), _lib.ptr(cache.global_k[layer]), _lib.ptr(cache.global_v[layer]),
+                B, heads, kv_heads, D, cache.ring, cache.max_len, _lib.DTYPE_BF16, _lib.stream_of(qkv))
+    return q, gq
 
 
 class LogoKVCache:

@@ -55,3 +55,39 @@ def test_cache_ring_and_local_decode(gpu):
     assert_within("local", out_l, ref_l)
     assert_within("global", out_g, ref_g)
     assert torch.equal(cache.global_k[0][:, :, :T + 1].cpu(), kg)
+
+
+@pytest.mark.parametrize("B,H,HK,D", [(32, 16, 16, 128), (5, 4, 2, 64)])
+def test_decode_qkv_equals_step_by_step(gpu, B, H, HK, D):
+    """The fused decode q / k / v transform is bit-identical to the separate
+    launches it replaces (global projection, RoPE of q, k, gq, gk, cache
+    appends into the local ring and the global cache) on the same stacked
+    projection rows."""
+    from logo_amd.layers import rope_cos_sin
+    from logo_amd.ops.decode import decode_qkv
+    from logo_amd.ops.glue import head_proj, rope_apply_
+
+    g = gen(B + H + D)
+    ldq = (H + 2 * HK) * D + 8
+    qkv = torch.randn(B, ldq, generator=g).bfloat16().to(gpu)
+    ws = [(torch.eye(D) + 0.05 * torch.randn(h, D, D, generator=g)).bfloat16().to(gpu) for h in (H, HK, HK)]
+    T = 300
+    cache_a = LogoKVCache(1, B, HK, D, max_len=T + 4, window=128, device=gpu)
+    cache_b = LogoKVCache(1, B, HK, D, max_len=T + 4, window=128, device=gpu)
+    for c in (cache_a, cache_b):
+        for t in (c.global_k[0], c.global_v[0], c.local_k[0], c.local_v[0]):
+            t.zero_()
+        c.set_length(T)
+    cos, sin = rope_cos_sin(torch.full((B, 1), T, device=gpu), D, 10000.0, torch.bfloat16)
+    q, gq = decode_qkv(qkv, *ws, cos, sin, cache_a, 0, H, HK)
+    # step by step
+    qv = qkv[:, :H * D].reshape(B, 1, H, D).contiguous()
+    kv = qkv[:, H * D:(H + HK) * D].reshape(B, 1, HK, D).contiguous()
+    vv = qkv[:, (H + HK) * D:(H + 2 * HK) * D].reshape(B, 1, HK, D).contiguous()
+    gqr, gkr, gvr = head_proj((qv, kv, vv), ws)
+    rope_apply_([qv, kv, gqr, gkr], cos, sin)
+    cache_b.append(0, kv[:, 0], vv[:, 0], gkr[:, 0], gvr[:, 0])
+    torch.cuda.synchronize()
+    assert torch.equal(q, qv[:, 0]) and torch.equal(gq, gqr[:, 0])
+    for name in ("global_k", "global_v", "local_k", "local_v"):
+        assert torch.equal(getattr(cache_a, name)[0], getattr(cache_b, name)[0]), name

@@ -95,3 +95,29 @@ def test_graph_decode_matches_eager(gpu):
         assert torch.equal(tok_a, tok_b), f"replay {s}: greedy tokens differ"
     assert cb.seen == ca.seen == T + 1 + steps
     assert torch.equal(ca._pos, cb._pos)
+
+
+def test_fused_decode_step_matches_unfused(gpu):
+    """The decode step with the stacked q/k/v/gate GEMM and the fused
+    transform launch gives the step-by-step path's logits (up to the
+    stacked GEMM's own rounding) and the same greedy tokens."""
+    from logo_amd.layers import LoGoAttention
+
+    m = _model(gpu, 0.5)
+    g = torch.Generator()
+    g.manual_seed(3)
+    ids = torch.randint(0, 512, (4, 150), generator=g).to(gpu)
+    ca, cb = m.new_cache(4, 170, device=gpu), m.new_cache(4, 170, device=gpu)
+    tok = m.prefill(ids, ca).argmax(-1)
+    m.prefill(ids, cb)
+    for _ in range(6):
+        la = m.decode_step(tok, ca)
+        orig = LoGoAttention._fused_decode_ok
+        LoGoAttention._fused_decode_ok = lambda self, h, c: False
+        try:
+            lb = m.decode_step(tok, cb)
+        finally:
+            LoGoAttention._fused_decode_ok = orig
+        err = (la.float() - lb.float()).abs().max().item()
+        assert err <= 0.02 * lb.float().abs().max().item() + 1e-3
+        tok = lb.argmax(-1)
