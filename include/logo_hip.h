@@ -255,6 +255,23 @@ int logo_decode_qkv(const void* qkv, int64_t ldq, const void* wq, const void* wk
                     int dtype, void* stream);
 
 /*
+ * Residual add + RMSNorm of the decoder: s_out = r + x (bf16, as the eager
+ * add rounds) and y = RMSNorm(s_out) with weight w (as logo_rmsnorm), rows of
+ * cols bf16 (a multiple of 8, at most 4096): the residual adds and the
+ * post-attention / next input norms of logo/modeling_logo.py:58-66.
+ */
+int logo_add_rmsnorm(const void* r, const void* x, const void* w, void* s_out, void* y, int64_t rows, int cols,
+                     float eps, int dtype, void* stream);
+
+/*
+ * SwiGLU activation y[row] = silu(g) * u with g = gu[row, 0:cols] and
+ * u = gu[row, cols:2 cols] (row stride ld >= 2 cols, the stacked gate / up
+ * projection), each op rounded to bf16 as the eager F.silu and mul
+ * (logo/modules/mlp.py:24-27).
+ */
+int logo_silu_mul(const void* gu, int64_t ld, void* y, int64_t rows, int cols, int dtype, void* stream);
+
+/*
  * RMSNorm of rows [rows, cols] bf16 with weight [cols]: y = w * bf16(x *
  * rsqrt(mean(x^2) + eps)), mean in fp32 (logo/modules/layernorm.py:17-22; the
  * decoder's input / post-attention / final norms, logo/modeling_logo.py:58-59,

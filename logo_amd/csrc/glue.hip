@@ -169,6 +169,69 @@ __global__ __launch_bounds__(128) void head_proj_kernel(const HeadProjArgs a) {
   }
 }
 
+// Residual add + RMSNorm of the decoder (logo/modeling_logo.py:60-66 with
+// logo/modules/layernorm.py:17-22): s = bf16(r + x) (the eager bf16 add) and
+// y = bf16(w * bf16(s * rsqrt(mean(s^2) + eps))), one wave per row.
+template <int VPL>
+__global__ __launch_bounds__(256) void add_rmsnorm_kernel(const bf16* r, const bf16* x, const bf16* w, bf16* s_out,
+                                                          bf16* y, int64_t rows, int cols, float eps) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int l = threadIdx.x & 63;
+  if (row >= rows) return;
+  bf16x8 v[VPL];
+  float ss = 0.f;
+#pragma unroll
+  for (int k = 0; k < VPL; ++k) {
+    const int col = 8 * (l + 64 * k);
+    if (col < cols) {
+      const bf16x8 rv = *reinterpret_cast<const bf16x8*>(r + row * cols + col);
+      const bf16x8 xv = *reinterpret_cast<const bf16x8*>(x + row * cols + col);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[k][e] = (bf16)((float)rv[e] + (float)xv[e]);
+      *reinterpret_cast<bf16x8*>(s_out + row * cols + col) = v[k];
+    } else {
+      v[k] = bf16x8{};
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss = fmaf((float)v[k][e], (float)v[k][e], ss);
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+  const float rs = rsqrtf(ss / (float)cols + eps);
+#pragma unroll
+  for (int k = 0; k < VPL; ++k) {
+    const int col = 8 * (l + 64 * k);
+    if (col < cols) {
+      const bf16x8 wv = *reinterpret_cast<const bf16x8*>(w + col);
+      bf16x8 o;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = (bf16)((float)wv[e] * bfr_g((float)v[k][e] * rs));
+      *reinterpret_cast<bf16x8*>(y + row * cols + col) = o;
+    }
+  }
+}
+
+// SwiGLU activation of logo/modules/mlp.py:24-27: y = bf16(bf16(silu(g)) * u)
+// with silu(g) = g / (1 + exp(-g)) in fp32 (the rounding of the eager bf16
+// F.silu and mul); g and u are the two halves of a stacked projection row.
+__global__ __launch_bounds__(256) void silu_mul_kernel(const bf16* gu, int64_t ld, bf16* y, int64_t rows,
+                                                       int cols) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t row = idx / (cols / 8);
+  const int c8 = (int)(idx % (cols / 8)) * 8;
+  if (row >= rows) return;
+  const bf16x8 g = *reinterpret_cast<const bf16x8*>(gu + row * ld + c8);
+  const bf16x8 u = *reinterpret_cast<const bf16x8*>(gu + row * ld + cols + c8);
+  bf16x8 o;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float gf = (float)g[e];
+    const float sg = bfr_g(gf / (1.f + expf(-gf)));
+    o[e] = (bf16)(sg * (float)u[e]);
+  }
+  *reinterpret_cast<bf16x8*>(y + row * cols + c8) = o;
+}
+
 // One decode step's q / k / v transform for a LoGo layer: from the stacked
 // projection output row of each token ([q | k | v], row stride ldq), the
 // global projections (as head_proj), RoPE of q, k, gq, gk (the rounding of
@@ -410,5 +473,48 @@ extern "C" int logo_decode_qkv(const void* qkv, int64_t ldq, const void* wq, con
   if (d == 128) hipLaunchKernelGGL(decode_qkv_kernel<128>, grid, dim3(128), 0, st, a);
   else hipLaunchKernelGGL(decode_qkv_kernel<64>, grid, dim3(64), 0, st, a);
   LOGO_LAUNCH_CHECK("decode_qkv_kernel");
+  return LOGO_OK;
+}
+
+extern "C" int logo_add_rmsnorm(const void* r, const void* x, const void* w, void* s_out, void* y, int64_t rows,
+                                int cols, float eps, int dtype, void* stream) {
+  LOGO_REQUIRE(dtype == LOGO_DTYPE_BF16, "only bf16 tensors are supported");
+  LOGO_REQUIRE(rows >= 0, "rows must be >= 0");
+  LOGO_REQUIRE(cols >= 8 && cols % 8 == 0 && cols <= 64 * 8 * 8, "cols must be a multiple of 8 in [8, 4096]");
+  LOGO_REQUIRE(r && x && w && s_out && y, "null pointer argument");
+  if (rows == 0) return LOGO_OK;
+  const int64_t nblk = (rows + 3) / 4;
+  LOGO_REQUIRE(nblk < ((int64_t)1 << 31), "too many rows");
+  hipStream_t st = as_stream(stream);
+  const int vpl = (cols + 511) / 512;
+  const auto rb = static_cast<const bf16*>(r);
+  const auto xb = static_cast<const bf16*>(x);
+  const auto wb = static_cast<const bf16*>(w);
+  const auto sb = static_cast<bf16*>(s_out);
+  const auto yb = static_cast<bf16*>(y);
+  if (vpl <= 1)
+    hipLaunchKernelGGL(add_rmsnorm_kernel<1>, dim3((unsigned)nblk), dim3(256), 0, st, rb, xb, wb, sb, yb, rows, cols, eps);
+  else if (vpl <= 2)
+    hipLaunchKernelGGL(add_rmsnorm_kernel<2>, dim3((unsigned)nblk), dim3(256), 0, st, rb, xb, wb, sb, yb, rows, cols, eps);
+  else if (vpl <= 4)
+    hipLaunchKernelGGL(add_rmsnorm_kernel<4>, dim3((unsigned)nblk), dim3(256), 0, st, rb, xb, wb, sb, yb, rows, cols, eps);
+  else
+    hipLaunchKernelGGL(add_rmsnorm_kernel<8>, dim3((unsigned)nblk), dim3(256), 0, st, rb, xb, wb, sb, yb, rows, cols, eps);
+  LOGO_LAUNCH_CHECK("add_rmsnorm_kernel");
+  return LOGO_OK;
+}
+
+extern "C" int logo_silu_mul(const void* gu, int64_t ld, void* y, int64_t rows, int cols, int dtype, void* stream) {
+  LOGO_REQUIRE(dtype == LOGO_DTYPE_BF16, "only bf16 tensors are supported");
+  LOGO_REQUIRE(rows >= 0 && cols >= 8 && cols % 8 == 0, "cols must be a positive multiple of 8");
+  LOGO_REQUIRE(ld >= 2 * (int64_t)cols && ld % 8 == 0, "ld must hold both halves and be a multiple of 8");
+  LOGO_REQUIRE(gu && y, "null pointer argument");
+  if (rows == 0) return LOGO_OK;
+  const int64_t total = rows * (cols / 8);
+  const int64_t nblk = (total + 255) / 256;
+  LOGO_REQUIRE(nblk < ((int64_t)1 << 31), "too many rows");
+  hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned)nblk), dim3(256), 0, as_stream(stream),
+                     static_cast<const bf16*>(gu), ld, static_cast<bf16*>(y), rows, cols);
+  LOGO_LAUNCH_CHECK("silu_mul_kernel");
   return LOGO_OK;
 }

@@ -21,8 +21,9 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from .layers import Attention, LoGoAttention, LoGoConfig, RMSNorm, position_ids_for, rope_cos_sin
+from .layers import Attention, LoGoAttention, LoGoConfig, RMSNorm, _fused_ok, position_ids_for, rope_cos_sin
 from .ops.decode import LogoKVCache
+from .ops.glue import add_rms_norm, silu_mul
 
 __all__ = ["LoGoMLP", "LoGoDecoderLayer", "LoGoModel", "LoGoForCausalLM"]
 
@@ -36,7 +37,20 @@ class LoGoMLP(nn.Module):
         self.up_proj = nn.Linear(config.hidden_size, config.intermediate_size, bias=False)
         self.down_proj = nn.Linear(config.intermediate_size, config.hidden_size, bias=False)
 
+    def _gate_up_weight(self):
+        """gate_proj and up_proj weights stacked for one GEMM, rebuilt when
+        either changes."""
+        ws = (self.gate_proj.weight, self.up_proj.weight)
+        key = tuple((w.data_ptr(), w._version, w.dtype) for w in ws)
+        cached = getattr(self, "_gu_w", None)
+        if cached is None or cached[0] != key:
+            self._gu_w = (key, torch.cat([w.detach() for w in ws]).contiguous())
+        return self._gu_w[1]
+
     def forward(self, x):
+        if _fused_ok(x, self.gate_proj.weight, self.up_proj.weight) and self.gate_proj.weight.shape[0] % 8 == 0:
+            # inference: one GEMM for gate and up, one launch for silu * mul
+            return self.down_proj(silu_mul(F.linear(x, self._gate_up_weight())))
         return self.down_proj(F.silu(self.gate_proj(x)) * self.up_proj(x))
 
 
@@ -84,6 +98,19 @@ class LoGoModel(nn.Module):
         # rotary cos / sin once for all layers (logo/modeling_logo.py:233-234)
         pos = position_ids_for(B, T, input_ids.device, cu_seqlens, past_key_value)
         pe = rope_cos_sin(pos, self.config.head_dim, self.config.rope_theta, h.dtype)
+        if _fused_ok(h) and h.shape[-1] <= 4096:
+            # inference: each residual add fused with the norm that follows it
+            # (post-attention norm, the next layer's input norm, the final norm)
+            resid, normed = h, self.layers[0].input_layernorm(h)
+            for i, layer in enumerate(self.layers):
+                a, _, _ = layer.self_attn(normed, cu_seqlens=cu_seqlens, past_key_value=past_key_value,
+                                          position_embeddings=pe)
+                pn = layer.post_attention_layernorm
+                resid, normed = add_rms_norm(resid, a, pn.weight, pn.variance_epsilon)
+                m = layer.mlp(normed)
+                nn_ = self.layers[i + 1].input_layernorm if i + 1 < len(self.layers) else self.norm
+                resid, normed = add_rms_norm(resid, m, nn_.weight, nn_.variance_epsilon)
+            return normed
         for layer in self.layers:
             h = layer(h, cu_seqlens=cu_seqlens, past_key_value=past_key_value, position_embeddings=pe)
         return self.norm(h)

@@ -13,7 +13,7 @@ import torch
 
 from .. import _lib
 
-__all__ = ["rope_apply_", "rope", "RopeFunction", "rms_norm", "head_proj"]
+__all__ = ["rope_apply_", "rope", "RopeFunction", "rms_norm", "head_proj", "add_rms_norm", "silu_mul"]
 
 
 def _rope_checked(tensors, cos, sin, what):
@@ -137,3 +137,42 @@ def head_proj(xs, ws):
     lib = _lib.lib()
     _lib.launch("logo_head_proj", lib.logo_head_proj, *args, n, D, E, _lib.DTYPE_BF16, _lib.stream_of(xs[0]))
     return ys
+
+
+def add_rms_norm(residual, x, weight, eps):
+    """``s = residual + x`` and ``RMSNorm(s)`` (bf16, last dimension) in one
+    launch; returns ``(s, normed)``."""
+    _lib.require_gpu(residual, x, weight)
+    for t in (residual, x, weight):
+        if t.dtype != torch.bfloat16:
+            raise ValueError("add_rms_norm takes bf16 tensors")
+    r = residual.contiguous()
+    xc = x.contiguous()
+    if r.shape != xc.shape:
+        raise ValueError("residual and x must have one shape")
+    cols = r.shape[-1]
+    s = torch.empty_like(r)
+    y = torch.empty_like(r)
+    lib = _lib.lib()
+    _lib.launch("logo_add_rmsnorm", lib.logo_add_rmsnorm, _lib.ptr(r), _lib.ptr(xc), _lib.ptr(weight.contiguous()),
+                _lib.ptr(s), _lib.ptr(y), r.numel() // cols, cols, float(eps), _lib.DTYPE_BF16, _lib.stream_of(r))
+    return s, y
+
+
+def silu_mul(gu):
+    """``silu(g) * u`` for ``gu [..., 2 * I]`` holding ``[g | u]`` (a stacked
+    gate / up projection), bf16; returns ``[..., I]``."""
+    _lib.require_gpu(gu)
+    if gu.dtype != torch.bfloat16:
+        raise ValueError("silu_mul takes bf16 tensors")
+    lead = gu.shape[:-1]
+    I2 = gu.shape[-1]
+    g2 = gu.reshape(-1, I2)
+    if g2.stride(-1) != 1 or g2.stride(0) % 8 != 0:
+        g2 = g2.contiguous()
+    cols = I2 // 2
+    y = torch.empty(g2.shape[0], cols, dtype=torch.bfloat16, device=gu.device)
+    lib = _lib.lib()
+    _lib.launch("logo_silu_mul", lib.logo_silu_mul, _lib.ptr(g2), g2.stride(0), _lib.ptr(y), g2.shape[0], cols,
+                _lib.DTYPE_BF16, _lib.stream_of(g2))
+    return y.view(*lead, cols)
