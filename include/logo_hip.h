@@ -189,6 +189,26 @@ int logo_decode_attn(const void* q, const void* k_cache, const void* v_cache, co
                      int hq, int h, int d, int64_t t_cap, int max_len, float scale, int dtype,
                      void* stream);
 
+/* Bytes of workspace logo_decode_attn_fused needs (global rows of <= max_len_global keys). */
+size_t logo_decode_fused_workspace_bytes(int batch, int hq, int d, int max_len_global);
+
+/*
+ * One decode step's attention for both LoGo branches and the fused epilogue
+ * in two launches: the local branch (q_local over its window cache, every row
+ * active, max_len_local <= 256), the gate-aware global branch (as
+ * logo_decode_attn with gate / thres), then the context norms, gate mask and
+ * fusion of logo_epilogue_fwd (weights w_local, w_global [D], eps) into
+ * out [B, HQ, D].  Bit-identical to logo_decode_attn twice followed by
+ * logo_epilogue_fwd; replaces logo/layers/logo.py:228-258 at decode.
+ */
+int logo_decode_attn_fused(const void* q_local, const void* k_local, const void* v_local,
+                           const int32_t* lens_local, int64_t t_cap_local, int max_len_local,
+                           const void* q_global, const void* k_global, const void* v_global,
+                           const int32_t* lens_global, int64_t t_cap_global, int max_len_global,
+                           const void* gate, const void* thres, int thres_dtype, const void* w_local,
+                           const void* w_global, float eps, void* out, void* workspace, int batch, int hq,
+                           int h, int d, float scale, int dtype, void* stream);
+
 /*
  * Append one key/value row per (b, h) at position pos[b] of a preallocated
  * cache [B, H, t_cap, D] (ring > 0: at pos[b] % ring, the local window),

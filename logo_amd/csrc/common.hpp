@@ -328,6 +328,56 @@ __device__ __forceinline__ float load_thres(const void* p, bool bf16_value) {
   return bf16_value ? (float)*static_cast<const bf16*>(p) : *static_cast<const float*>(p);
 }
 
+// Sum over the LPR lanes of a row group (butterfly, fixed order).
+template <int LPR>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int off = LPR / 2; off > 0; off >>= 1) v += __shfl_xor(v, off);
+  return v;
+}
+
+__device__ __forceinline__ float bfr(float x) { return (float)(bf16)x; }
+
+// Fused attention epilogue of one (token, head) row of D elements, held by D/8
+// consecutive lanes (lane c owns elements 8c..8c+7), with the eager bf16
+// rounding points of the reference (logo/modules/layernorm.py:17-22,
+// logo/layers/logo.py:180-181, :225-226, :256-258):
+//   Ln  = bf16(w_l * bf16(L * rsqrt(mean(L^2) + eps)))      (same for G)
+//   g'  = gate < thres ? 0 : gate
+//   out = bf16(bf16(bf16(1 - g') * Ln) + bf16(g' * Gn))
+// Every lane of the group must call it (the sums are lane shuffles); the
+// result is this lane's 8 elements.
+template <int D>
+__device__ __forceinline__ bf16x8 epi_fwd_chunk(const bf16x8 lv, const bf16x8 gv, float gate, float thres,
+                                                const bf16* w_l, const bf16* w_g, float eps, int c) {
+  // Every eager bf16 op of the reference rounds its result; without this the
+  // compiler contracts bf16(om * ln) + b into one fma and skips a rounding.
+#pragma clang fp contract(off)
+  constexpr int LPR = D / 8;
+  float ssl = 0.f, ssg = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    ssl = fmaf((float)lv[e], (float)lv[e], ssl);
+    ssg = fmaf((float)gv[e], (float)gv[e], ssg);
+  }
+  ssl = group_sum<LPR>(ssl);
+  ssg = group_sum<LPR>(ssg);
+  const float rl = rsqrtf(ssl / (float)D + eps);
+  const float rg = rsqrtf(ssg / (float)D + eps);
+  const float gp = gate < thres ? 0.f : gate;
+  const float om = bfr(1.f - gp);
+  const bf16x8 wl = *reinterpret_cast<const bf16x8*>(w_l + 8 * c);
+  const bf16x8 wg = *reinterpret_cast<const bf16x8*>(w_g + 8 * c);
+  bf16x8 o;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float ln = bfr((float)wl[e] * bfr((float)lv[e] * rl));
+    const float gn = bfr((float)wg[e] * bfr((float)gv[e] * rg));
+    o[e] = (bf16)(bfr(om * ln) + bfr(gp * gn));
+  }
+  return o;
+}
+
 // Largest s in [0, n) with arr[s] <= x (arr ascending, arr[0] <= x).
 __device__ __forceinline__ int seg_of(const int32_t* arr, int n, int64_t x) {
   int lo = 0, hi = n;  // invariant: arr[lo] <= x, answer < hi

@@ -45,13 +45,12 @@ __device__ __forceinline__ bool dec_active(const DecArgs& a, int b) {
   return a.gate == nullptr || !((float)a.gate[b] < load_thres(a.thres, a.thres_bf16));
 }
 
+// One workgroup's split: keys [256 split, 256 split + 256) of row bq = b * HQ + hq.
 template <int D>
-__global__ __launch_bounds__(256) void decode_split_kernel(const DecArgs a) {
+__device__ __forceinline__ void dec_split(const DecArgs& a, const int split, const int bq) {
   constexpr int CH = D / 8;                 // 16-byte chunks per row
   constexpr int KPS = 64 / CH;              // keys per load step (4 for D=128)
   constexpr int STEPS = kDecKeysPerWave / KPS;
-  const int split = blockIdx.x;
-  const int bq = blockIdx.y;                // b * HQ + hq
   const int b = bq / a.hq, hq = bq % a.hq, h = hq / a.g;
   const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63;
   const int len = a.lens[b];
@@ -153,19 +152,32 @@ __global__ __launch_bounds__(256) void decode_split_kernel(const DecArgs a) {
   }
 }
 
+template <int D>
+__global__ __launch_bounds__(256) void decode_split_kernel(const DecArgs a) {
+  dec_split<D>(a, blockIdx.x, blockIdx.y);
+}
+
+// Both branches of a decode step in one launch: x < glo.nsplit are the global
+// branch's splits, x == glo.nsplit the local window's single split (at most
+// 256 keys), which writes its output row itself.
+template <int D>
+__global__ __launch_bounds__(256) void decode_dual_split_kernel(const DecArgs loc, const DecArgs glo) {
+  if ((int)blockIdx.x == glo.nsplit) dec_split<D>(loc, 0, blockIdx.y);
+  else dec_split<D>(glo, blockIdx.x, blockIdx.y);
+}
+
 // Merge the split partials of one (b, q-head) row: the splits' maxima and
 // sums are reduced across the 256 threads, then thread (group gi, column d)
 // sums the rescaled partial outputs of splits gi, gi + G, ... with
-// independent loads, and the groups are added through LDS.
+// independent loads, and the groups are added through LDS.  The bf16 output
+// row goes to out (global memory) or, with out == nullptr, to sout (LDS).
 template <int D>
-__global__ __launch_bounds__(256) void decode_combine_kernel(const DecArgs a) {
+__device__ __forceinline__ void dec_combine(const DecArgs& a, const int bq, bf16* out, bf16* sout) {
   constexpr int G = 256 / D;  // split groups
-  const int bq = blockIdx.x;
   const int b = bq / a.hq;
   const int tid = threadIdx.x, l = tid & 63, wave = tid >> 6;
-  bf16* out = a.out + (int64_t)bq * D;
   if (!dec_active(a, b)) {
-    if (tid < D) out[tid] = (bf16)0.f;
+    if (tid < D) (out ? out : sout)[tid] = (bf16)0.f;
     return;
   }
   const int len = a.lens[b];
@@ -204,7 +216,44 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(const DecArgs a) {
     float O = 0.f;
 #pragma unroll
     for (int k = 0; k < G; ++k) O += so[k][tid];
-    out[tid] = (bf16)(L > 0.f ? O / L : 0.f);
+    (out ? out : sout)[tid] = (bf16)(L > 0.f ? O / L : 0.f);
+  }
+}
+
+template <int D>
+__global__ __launch_bounds__(256) void decode_combine_kernel(const DecArgs a) {
+  dec_combine<D>(a, blockIdx.x, a.out + (int64_t)blockIdx.x * D, nullptr);
+}
+
+// The global branch's combine and the fused epilogue (context norms, gate
+// mask, fusion; the same arithmetic as the epilogue kernel) of one (b, q-head)
+// row: the global row stays in LDS, the local row comes from the dual split.
+struct DecEpiArgs {
+  const bf16* local;  // [B * HQ, D], the local branch's output
+  const bf16* w_l;
+  const bf16* w_g;
+  bf16* out;          // [B * HQ, D]
+  float eps;
+};
+
+template <int D>
+__global__ __launch_bounds__(256) void decode_combine_epi_kernel(const DecArgs glo, const DecEpiArgs e) {
+  const int bq = blockIdx.x, b = bq / glo.hq;
+  __shared__ bf16x8 sg[D / 8];
+  bf16* sgb = reinterpret_cast<bf16*>(sg);
+  if (glo.nsplit > 1) {
+    dec_combine<D>(glo, bq, nullptr, sgb);
+  } else if (threadIdx.x < D) {  // the single split wrote the row already
+    sgb[threadIdx.x] = glo.out[(int64_t)bq * D + threadIdx.x];
+  }
+  __syncthreads();
+  constexpr int LPR = D / 8;
+  if (threadIdx.x < LPR) {
+    const int c = threadIdx.x;
+    const bf16x8 lv = *reinterpret_cast<const bf16x8*>(e.local + (int64_t)bq * D + 8 * c);
+    const bf16x8 o = epi_fwd_chunk<D>(lv, sg[c], (float)glo.gate[b], load_thres(glo.thres, glo.thres_bf16), e.w_l,
+                                      e.w_g, e.eps, c);
+    *reinterpret_cast<bf16x8*>(e.out + (int64_t)bq * D + 8 * c) = o;
   }
 }
 
@@ -237,17 +286,9 @@ extern "C" size_t logo_decode_workspace_bytes(int batch, int hq, int d, int max_
   return (size_t)batch * hq * ns * (d + 2) * sizeof(float);
 }
 
-extern "C" int logo_decode_attn(const void* q, const void* k_cache, const void* v_cache, const int32_t* lens,
-                                const void* gate, const void* thres, int thres_dtype, void* out, void* workspace, int batch,
-                                int hq, int h, int d, int64_t t_cap, int max_len, float scale, int dtype,
-                                void* stream) {
-  LOGO_REQUIRE(batch >= 1 && h >= 1 && hq % h == 0, "bad batch / head counts");
-  LOGO_REQUIRE(d == 64 || d == 128, "head dim %d unsupported (64 or 128)", d);
-  LOGO_REQUIRE(dtype == LOGO_DTYPE_BF16, "only bf16 tensors are supported");
-  LOGO_REQUIRE(max_len >= 1 && max_len <= t_cap, "max_len must be in [1, t_cap]");
-  LOGO_REQUIRE(q && k_cache && v_cache && lens && out && workspace, "null pointer argument");
-  LOGO_REQUIRE(gate == nullptr || thres != nullptr, "gate needs thres");
-  LOGO_REQUIRE(thres_dtype == LOGO_DTYPE_BF16 || thres_dtype == LOGO_DTYPE_F32, "thres_dtype must be bf16 or f32");
+static DecArgs dec_args(const void* q, const void* k_cache, const void* v_cache, const int32_t* lens,
+                        const void* gate, const void* thres, int thres_dtype, void* out, void* part, int batch,
+                        int hq, int h, int64_t t_cap, int max_len, float scale) {
   DecArgs a{};
   a.q = static_cast<const bf16*>(q);
   a.k = static_cast<const bf16*>(k_cache);
@@ -257,7 +298,7 @@ extern "C" int logo_decode_attn(const void* q, const void* k_cache, const void* 
   a.thres = thres;
   a.thres_bf16 = thres_dtype == LOGO_DTYPE_BF16;
   a.out = static_cast<bf16*>(out);
-  a.part = static_cast<float*>(workspace);
+  a.part = static_cast<float*>(part);
   a.batch = batch;
   a.hq = hq;
   a.h = h;
@@ -265,6 +306,28 @@ extern "C" int logo_decode_attn(const void* q, const void* k_cache, const void* 
   a.nsplit = dec_nsplit(max_len);
   a.t_cap = t_cap;
   a.scale_log2 = scale * 1.4426950408889634f;
+  return a;
+}
+
+static int dec_check(int batch, int hq, int h, int d, int dtype, int thres_dtype) {
+  LOGO_REQUIRE(batch >= 1 && h >= 1 && hq % h == 0, "bad batch / head counts");
+  LOGO_REQUIRE(d == 64 || d == 128, "head dim %d unsupported (64 or 128)", d);
+  LOGO_REQUIRE(dtype == LOGO_DTYPE_BF16, "only bf16 tensors are supported");
+  LOGO_REQUIRE(thres_dtype == LOGO_DTYPE_BF16 || thres_dtype == LOGO_DTYPE_F32, "thres_dtype must be bf16 or f32");
+  return LOGO_OK;
+}
+
+extern "C" int logo_decode_attn(const void* q, const void* k_cache, const void* v_cache, const int32_t* lens,
+                                const void* gate, const void* thres, int thres_dtype, void* out, void* workspace, int batch,
+                                int hq, int h, int d, int64_t t_cap, int max_len, float scale, int dtype,
+                                void* stream) {
+  const int rc = dec_check(batch, hq, h, d, dtype, thres_dtype);
+  if (rc != LOGO_OK) return rc;
+  LOGO_REQUIRE(max_len >= 1 && max_len <= t_cap, "max_len must be in [1, t_cap]");
+  LOGO_REQUIRE(q && k_cache && v_cache && lens && out && workspace, "null pointer argument");
+  LOGO_REQUIRE(gate == nullptr || thres != nullptr, "gate needs thres");
+  const DecArgs a = dec_args(q, k_cache, v_cache, lens, gate, thres, thres_dtype, out, workspace, batch, hq, h, t_cap,
+                             max_len, scale);
   hipStream_t st = as_stream(stream);
   dim3 grid(a.nsplit, batch * hq);
   if (d == 128)
@@ -279,6 +342,60 @@ extern "C" int logo_decode_attn(const void* q, const void* k_cache, const void* 
       hipLaunchKernelGGL(decode_combine_kernel<64>, dim3(batch * hq), dim3(256), 0, st, a);
     LOGO_LAUNCH_CHECK("decode_combine_kernel");
   }
+  return LOGO_OK;
+}
+
+// Workspace of logo_decode_attn_fused: the global branch's split partials,
+// then the local and the global bf16 rows, each region 256-byte aligned.
+static size_t dec_align(size_t x) { return (x + 255) & ~(size_t)255; }
+
+extern "C" size_t logo_decode_fused_workspace_bytes(int batch, int hq, int d, int max_len_global) {
+  const size_t rows = (size_t)batch * hq * d * sizeof(bf16);
+  return dec_align(logo_decode_workspace_bytes(batch, hq, d, max_len_global)) + 2 * dec_align(rows);
+}
+
+extern "C" int logo_decode_attn_fused(const void* q_local, const void* k_local, const void* v_local,
+                                      const int32_t* lens_local, int64_t t_cap_local, int max_len_local,
+                                      const void* q_global, const void* k_global, const void* v_global,
+                                      const int32_t* lens_global, int64_t t_cap_global, int max_len_global,
+                                      const void* gate, const void* thres, int thres_dtype, const void* w_local,
+                                      const void* w_global, float eps, void* out, void* workspace, int batch, int hq,
+                                      int h, int d, float scale, int dtype, void* stream) {
+  const int rc = dec_check(batch, hq, h, d, dtype, thres_dtype);
+  if (rc != LOGO_OK) return rc;
+  LOGO_REQUIRE(max_len_local >= 1 && max_len_local <= t_cap_local && max_len_local <= kDecKeysPerWG,
+               "max_len_local must be in [1, min(t_cap_local, %d)]", kDecKeysPerWG);
+  LOGO_REQUIRE(max_len_global >= 1 && max_len_global <= t_cap_global, "max_len_global must be in [1, t_cap_global]");
+  LOGO_REQUIRE(q_local && k_local && v_local && lens_local && q_global && k_global && v_global && lens_global && gate &&
+                   thres && w_local && w_global && out && workspace,
+               "null pointer argument");
+  char* ws = static_cast<char*>(workspace);
+  const size_t part_bytes = dec_align(logo_decode_workspace_bytes(batch, hq, d, max_len_global));
+  const size_t row_bytes = dec_align((size_t)batch * hq * d * sizeof(bf16));
+  void* lrow = ws + part_bytes;
+  void* grow = ws + part_bytes + row_bytes;
+  const DecArgs loc = dec_args(q_local, k_local, v_local, lens_local, nullptr, nullptr, thres_dtype, lrow, nullptr,
+                               batch, hq, h, t_cap_local, max_len_local, scale);
+  const DecArgs glo = dec_args(q_global, k_global, v_global, lens_global, gate, thres, thres_dtype, grow, ws, batch, hq,
+                               h, t_cap_global, max_len_global, scale);
+  DecEpiArgs e{};
+  e.local = static_cast<const bf16*>(lrow);
+  e.w_l = static_cast<const bf16*>(w_local);
+  e.w_g = static_cast<const bf16*>(w_global);
+  e.out = static_cast<bf16*>(out);
+  e.eps = eps;
+  hipStream_t st = as_stream(stream);
+  const dim3 grid(glo.nsplit + 1, batch * hq);
+  if (d == 128) {
+    hipLaunchKernelGGL(decode_dual_split_kernel<128>, grid, dim3(256), 0, st, loc, glo);
+    LOGO_LAUNCH_CHECK("decode_dual_split_kernel");
+    hipLaunchKernelGGL(decode_combine_epi_kernel<128>, dim3(batch * hq), dim3(256), 0, st, glo, e);
+  } else {
+    hipLaunchKernelGGL(decode_dual_split_kernel<64>, grid, dim3(256), 0, st, loc, glo);
+    LOGO_LAUNCH_CHECK("decode_dual_split_kernel");
+    hipLaunchKernelGGL(decode_combine_epi_kernel<64>, dim3(batch * hq), dim3(256), 0, st, glo, e);
+  }
+  LOGO_LAUNCH_CHECK("decode_combine_epi_kernel");
   return LOGO_OK;
 }
 

@@ -46,53 +46,20 @@ struct EpiArgs {
 
 constexpr int kEpiMaxGrid = 1024;
 
-template <int LPR>
-__device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-  for (int off = LPR / 2; off > 0; off >>= 1) v += __shfl_xor(v, off);
-  return v;
-}
-
-__device__ __forceinline__ float bfr(float x) { return (float)(bf16)x; }
-
 template <int D>
 __global__ __launch_bounds__(256) void epi_fwd_kernel(const EpiArgs a) {
-  // Every eager bf16 op of the reference rounds its result; without this the
-  // compiler contracts bf16(om * ln) + b into one fma and skips a rounding.
-#pragma clang fp contract(off)
   constexpr int LPR = D / 8, RPB = 256 / LPR;
-  const int64_t r = (int64_t)blockIdx.x * RPB + threadIdx.x / LPR;
+  const int64_t r0 = (int64_t)blockIdx.x * RPB + threadIdx.x / LPR;
   const int c = threadIdx.x % LPR;
-  const bool ok = r < a.rows;
-  bf16x8 lv{}, gv{};
-  if (ok) {
-    lv = *reinterpret_cast<const bf16x8*>(a.L + r * D + 8 * c);
-    gv = *reinterpret_cast<const bf16x8*>(a.G + r * D + 8 * c);
-  }
-  float ssl = 0.f, ssg = 0.f;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    ssl = fmaf((float)lv[e], (float)lv[e], ssl);
-    ssg = fmaf((float)gv[e], (float)gv[e], ssg);
-  }
-  ssl = group_sum<LPR>(ssl);
-  ssg = group_sum<LPR>(ssg);
-  if (!ok) return;
-  const float rl = rsqrtf(ssl / (float)D + a.eps);
-  const float rg = rsqrtf(ssg / (float)D + a.eps);
-  const float g = (float)a.gate[r / a.heads];
-  const float gp = g < load_thres(a.thres, a.thres_bf16) ? 0.f : g;
-  const float om = bfr(1.f - gp);
-  const bf16x8 wl = *reinterpret_cast<const bf16x8*>(a.w_l + 8 * c);
-  const bf16x8 wg = *reinterpret_cast<const bf16x8*>(a.w_g + 8 * c);
-  bf16x8 o;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const float ln = bfr((float)wl[e] * bfr((float)lv[e] * rl));
-    const float gn = bfr((float)wg[e] * bfr((float)gv[e] * rg));
-    o[e] = (bf16)(bfr(om * ln) + bfr(gp * gn));
-  }
-  *reinterpret_cast<bf16x8*>(a.out + r * D + 8 * c) = o;
+  const bool ok = r0 < a.rows;
+  // rows past the end compute on row 0 (every lane of a group joins the
+  // shuffles) and store nothing
+  const int64_t r = ok ? r0 : 0;
+  const bf16x8 lv = *reinterpret_cast<const bf16x8*>(a.L + r * D + 8 * c);
+  const bf16x8 gv = *reinterpret_cast<const bf16x8*>(a.G + r * D + 8 * c);
+  const bf16x8 o = epi_fwd_chunk<D>(lv, gv, (float)a.gate[r / a.heads], load_thres(a.thres, a.thres_bf16),
+                                    a.w_l, a.w_g, a.eps, c);
+  if (ok) *reinterpret_cast<bf16x8*>(a.out + r * D + 8 * c) = o;
 }
 
 template <int D>

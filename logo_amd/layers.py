@@ -26,7 +26,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from .ops.decode import LogoKVCache, decode_attn, decode_qkv
+from .ops.decode import LogoKVCache, decode_attn, decode_attn_fused, decode_qkv
 from .ops.epilogue import logo_epilogue
 from .ops.glue import head_proj, rms_norm, rope, rope_apply_
 from .ops.sq_attn import dense_causal_attn, sq_full_attn, swa_attn
@@ -291,10 +291,18 @@ class LoGoAttention(nn.Module):
                            self.layer_idx, H, HK)
         len_g, len_l = cache.step_lengths()
         bound_g, bound_l = cache.length_bounds()
-        local = decode_attn(q, cache.local_k[self.layer_idx], cache.local_v[self.layer_idx], len_l,
-                            max_len=bound_l)
-        glob = decode_attn(gq, cache.global_k[self.layer_idx], cache.global_v[self.layer_idx], len_g,
-                           gate.view(B), self.gate_thres, max_len=bound_g)
+        li = self.layer_idx
+        if self.use_context_norm and bound_l <= 256 and _fused_ok(self.context_norm_local.weight,
+                                                                 self.context_norm_global.weight):
+            # both branches and the epilogue in two launches
+            out = decode_attn_fused(q, cache.local_k[li], cache.local_v[li], len_l, bound_l, gq, cache.global_k[li],
+                                    cache.global_v[li], len_g, bound_g, gate.view(B), self.gate_thres,
+                                    self.context_norm_local.weight, self.context_norm_global.weight,
+                                    self.context_norm_local.variance_epsilon)
+            return out.view(B, 1, H * D), gate
+        local = decode_attn(q, cache.local_k[li], cache.local_v[li], len_l, max_len=bound_l)
+        glob = decode_attn(gq, cache.global_k[li], cache.global_v[li], len_g, gate.view(B), self.gate_thres,
+                           max_len=bound_g)
         return self._fuse(local.view(B, 1, H, D), glob.view(B, 1, H, D), gate.view(B, 1)), gate
 
     def forward(self, hidden_states, position_ids=None, cu_seqlens=None,

@@ -17,7 +17,7 @@ import torch
 
 from .. import _lib
 
-__all__ = ["decode_attn", "cache_append", "decode_qkv", "LogoKVCache"]
+__all__ = ["decode_attn", "decode_attn_fused", "cache_append", "decode_qkv", "LogoKVCache"]
 
 
 def decode_attn(q, k_cache, v_cache, lens, gate=None, thres=None, max_len: Optional[int] = None,
@@ -45,6 +45,44 @@ def decode_attn(q, k_cache, v_cache, lens, gate=None, thres=None, max_len: Optio
     _lib.launch("logo_decode_attn", lib.logo_decode_attn, _lib.ptr(qc), _lib.ptr(k_cache), _lib.ptr(v_cache),
                 _lib.ptr(lens), _lib.ptr(gate), _lib.ptr(th), th_dt, _lib.ptr(out), _lib.ptr(ws), B, HQ, H, D, t_cap,
                 int(max_len), float(scale), _lib.DTYPE_BF16, _lib.stream_of(q))
+    return out
+
+
+def decode_attn_fused(q_local, k_local, v_local, lens_local, max_len_local: int, q_global, k_global, v_global,
+                      lens_global, max_len_global: int, gate, thres, w_local, w_global, eps: float,
+                      scale: Optional[float] = None):
+    """Both decode branches and the fused epilogue in two launches:
+    ``decode_attn`` of the local window (every row) and of the global cache
+    (gate-aware), then the context norms, gate mask and fusion of
+    ``logo_epilogue`` (logo/layers/logo.py:228-258), bit-identical to those
+    three calls.  ``q_* [B, HQ, D]``; caches ``[B, H, T_cap, D]``; ``lens_*``
+    int32 ``[B]``; ``max_len_local <= 256``; ``gate [B]`` post-sigmoid;
+    ``w_* [D]`` the context-norm weights.  Returns ``[B, HQ, D]``."""
+    _lib.require_gpu(q_local, k_local, v_local, lens_local, q_global, k_global, v_global, lens_global, gate)
+    B, HQ, D = q_global.shape
+    H = k_global.shape[1]
+    if q_local.shape != q_global.shape or k_local.shape[:2] != (B, H) or k_global.shape[0] != B:
+        raise ValueError("decode_attn_fused: q / cache shapes disagree")
+    if w_local.numel() != D or w_global.numel() != D or w_local.dtype != torch.bfloat16 \
+            or w_global.dtype != torch.bfloat16:
+        raise ValueError("decode_attn_fused: context-norm weights must be bf16 [D]")
+    if scale is None:
+        scale = D ** -0.5
+    ql, qg = q_local.contiguous(), q_global.contiguous()
+    wl, wg = w_local.detach().contiguous(), w_global.detach().contiguous()
+    out = torch.empty_like(qg)
+    lib = _lib.lib()
+    ws = torch.empty(lib.logo_decode_fused_workspace_bytes(B, HQ, D, int(max_len_global)), dtype=torch.uint8,
+                     device=qg.device)
+    gate = gate.contiguous().view(B)
+    th, th_dt = _lib.thres_arg(thres)
+    _lib.launch("logo_decode_attn_fused", lib.logo_decode_attn_fused,
+                _lib.ptr(ql), _lib.ptr(k_local), _lib.ptr(v_local), _lib.ptr(lens_local), k_local.shape[2],
+                int(max_len_local),
+                _lib.ptr(qg), _lib.ptr(k_global), _lib.ptr(v_global), _lib.ptr(lens_global), k_global.shape[2],
+                int(max_len_global),
+                _lib.ptr(gate), _lib.ptr(th), th_dt, _lib.ptr(wl), _lib.ptr(wg), float(eps), _lib.ptr(out),
+                _lib.ptr(ws), B, HQ, H, D, float(scale), _lib.DTYPE_BF16, _lib.stream_of(qg))
     return out
 
 

@@ -91,3 +91,44 @@ def test_decode_qkv_equals_step_by_step(gpu, B, H, HK, D):
     assert torch.equal(q, qv[:, 0]) and torch.equal(gq, gqr[:, 0])
     for name in ("global_k", "global_v", "local_k", "local_v"):
         assert torch.equal(getattr(cache_a, name)[0], getattr(cache_b, name)[0]), name
+
+
+@pytest.mark.parametrize("B,HQ,H,D,lens_g,lens_l,thres_dtype", [
+    (4, 16, 16, 128, [1, 257, 4096, 3000], [1, 129, 129, 129], torch.bfloat16),
+    (3, 8, 2, 64, [200, 128, 37], [129, 128, 37], torch.float32),
+])
+def test_decode_attn_fused_equals_separate_calls(gpu, B, HQ, H, D, lens_g, lens_l, thres_dtype):
+    """Both branches and the epilogue in two launches give, bit for bit, what
+    decode_attn (local), decode_attn (global, gate-aware) and logo_epilogue
+    give; inactive rows, a single-split global branch (every length <= 256)
+    and grouped heads included."""
+    from logo_amd.ops.decode import decode_attn_fused
+    from logo_amd.ops.epilogue import logo_epilogue
+
+    g = gen(B * D + 7)
+    W1 = 129
+    tg = max(lens_g) + 32
+    dev = lambda t: t.to(gpu)
+    q_l = dev(torch.randn(B, HQ, D, generator=g).bfloat16())
+    q_g = dev(torch.randn(B, HQ, D, generator=g).bfloat16())
+    k_l = dev((torch.randn(B, H, W1, D, generator=g) * 0.5).bfloat16())
+    v_l = dev(torch.randn(B, H, W1, D, generator=g).bfloat16())
+    k_g = dev((torch.randn(B, H, tg, D, generator=g) * 0.5).bfloat16())
+    v_g = dev(torch.randn(B, H, tg, D, generator=g).bfloat16())
+    gate = dev(torch.tensor([0.7, 0.2, 0.5, 0.9][:B]).bfloat16())
+    thres = torch.tensor([0.5], device=gpu).to(thres_dtype)
+    w_l = dev((1 + 0.1 * torch.randn(D, generator=g)).bfloat16())
+    w_g = dev((1 + 0.1 * torch.randn(D, generator=g)).bfloat16())
+    len_l = torch.tensor(lens_l, dtype=torch.int32, device=gpu)
+    len_g = torch.tensor(lens_g, dtype=torch.int32, device=gpu)
+    eps = 1e-5
+    for _ in range(2):  # the second call reuses nothing from the first
+        out = decode_attn_fused(q_l, k_l, v_l, len_l, max(lens_l), q_g, k_g, v_g, len_g, max(lens_g), gate, thres,
+                                w_l, w_g, eps)
+        local = decode_attn(q_l, k_l, v_l, len_l, max_len=max(lens_l))
+        glob = decode_attn(q_g, k_g, v_g, len_g, gate, thres, max_len=max(lens_g))
+        ref = logo_epilogue(local.view(B, 1, HQ, D), glob.view(B, 1, HQ, D), gate.view(B, 1), thres, w_l, w_g, eps)
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(B, 1, HQ * D), ref)
+    inactive = (gate.float() < 0.5).nonzero().flatten()
+    assert inactive.numel() > 0
