@@ -265,14 +265,17 @@ int logo_head_proj(const void* x0, const void* w0, void* y0, int h0, const void*
  * appends of logo_cache_append: rotated k and v into the local ring
  * [batch, HK, ring, d] at pos[b] % ring, rotated global k and global v into the
  * global cache [batch, HK, t_cap, d] at pos[b].  Writes the rotated q and
- * global q to q_out / gq_out [batch, H, d].  Replaces the layer's global
- * projection, RoPE and cache update of a decode step (logo/layers/logo.py:
- * 86-94, :132-150; logo/cache.py:97-118) with one launch.
+ * global q to q_out / gq_out [batch, H, d].  With gate_out non-NULL it also
+ * writes the gate sigmoid(qkv[b, gate_col]) of each token to gate_out [batch]
+ * (logo/layers/logo.py:130, the gate projection stacked into the same row).
+ * Replaces the layer's global projection, gate sigmoid, RoPE and cache update
+ * of a decode step (logo/layers/logo.py:86-94, :130-150; logo/cache.py:97-118)
+ * with one launch.
  */
 int logo_decode_qkv(const void* qkv, int64_t ldq, const void* wq, const void* wk, const void* wv, const void* cos,
                     const void* sin, const int32_t* pos, void* q_out, void* gq_out, void* local_k, void* local_v,
-                    void* global_k, void* global_v, int batch, int h, int hk, int d, int ring, int64_t t_cap,
-                    int dtype, void* stream);
+                    void* global_k, void* global_v, int64_t gate_col, void* gate_out, int batch, int h, int hk,
+                    int d, int ring, int64_t t_cap, int dtype, void* stream);
 
 /*
  * Residual add + RMSNorm of the decoder: s_out = r + x (bf16, as the eager

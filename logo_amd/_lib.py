@@ -50,7 +50,8 @@ SIGNATURES = {
     "logo_add_rmsnorm": ([_P, _P, _P, _P, _P, _I64, _I, _F, _I, _P], _I),
     "logo_silu_mul": ([_P, _I64, _P, _I64, _I, _I, _P], _I),
     "logo_head_proj": ([_P, _P, _P, _I, _P, _P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I, _P], _I),
-    "logo_decode_qkv": ([_P, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I64, _I, _P],
+    "logo_decode_qkv": ([_P, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _P, _I, _I, _I, _I, _I, _I64,
+                         _I, _P],
                         _I),
 }
 _BWD = ([_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I, _I, _I, _I, _I, _F, _I, _I, _P], _I)

@@ -237,7 +237,11 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const bf16* gu, int64_t l
 // global projections (as head_proj), RoPE of q, k, gq, gk (the rounding of
 // rope_kernel) and both cache appends (k, v into the local ring at pos % ring,
 // gk, gv into the global cache at pos), replacing head_proj, rope and two
-// cache_append launches.  Outputs q (local, rotated) and gq (rotated).
+// cache_append launches.  Outputs q (local, rotated) and gq (rotated), and,
+// when gate_out is set, the gate sigmoid(qkv[b, gate_col]) of each token.
+// Each workgroup stages its head's [D, D] projection in LDS with 16-byte
+// loads (all in flight at once), then every thread runs the same sequential
+// fp32 k-loop as head_proj_kernel for its output column.
 struct DecQkvArgs {
   const bf16* qkv;
   int64_t ldq;
@@ -251,6 +255,8 @@ struct DecQkvArgs {
   bf16* lv;
   bf16* gk;          // [B, HK, t_cap, D]
   bf16* gv;
+  bf16* gate_out;    // [B] or null
+  int64_t gate_col;
   int b, h, hk, ring;
   int64_t t_cap;
 };
@@ -264,20 +270,33 @@ __global__ __launch_bounds__(D) void decode_qkv_kernel(const DecQkvArgs a) {
   const int col0 = ti == 0 ? hh * D : (ti == 1 ? (a.h + hh) * D : (a.h + a.hk + hh) * D);
   const int t0 = blockIdx.y * kHpTok;
   const int n = threadIdx.x;
+  __shared__ bf16x8 wsm[D * D / 8];  // this head's projection, [k][n]
   __shared__ float xs[kHpTok][D];
   __shared__ float ys[kHpTok][D];
+  {
+    const bf16x8* wsrc = reinterpret_cast<const bf16x8*>(a.w[ti] + (int64_t)hh * D * D);
+    bf16x8 wv[D / 8];
+#pragma unroll
+    for (int i = 0; i < D / 8; ++i) wv[i] = wsrc[i * D + n];
+#pragma unroll
+    for (int i = 0; i < D / 8; ++i) wsm[i * D + n] = wv[i];
+  }
   for (int idx = threadIdx.x; idx < kHpTok * D; idx += D) {
     const int tt = idx / D, k = idx % D;
     const int t = t0 + tt;
     xs[tt][k] = t < a.b ? (float)a.qkv[(int64_t)t * a.ldq + col0 + k] : 0.f;
   }
+  if (a.gate_out != nullptr && gh == 0 && n < kHpTok && t0 + n < a.b) {
+    const float z = (float)a.qkv[(int64_t)(t0 + n) * a.ldq + a.gate_col];
+    a.gate_out[t0 + n] = (bf16)(1.f / (1.f + expf(-z)));
+  }
   __syncthreads();
-  const bf16* w = a.w[ti] + (int64_t)hh * D * D + n;
+  const bf16* w = reinterpret_cast<const bf16*>(wsm) + n;
   float acc[kHpTok];
 #pragma unroll
   for (int tt = 0; tt < kHpTok; ++tt) acc[tt] = 0.f;
   for (int k = 0; k < D; ++k) {
-    const float wk = (float)w[(int64_t)k * D];
+    const float wk = (float)w[k * D];
 #pragma unroll
     for (int tt = 0; tt < kHpTok; ++tt) acc[tt] = fmaf(xs[tt][k], wk, acc[tt]);
   }
@@ -436,14 +455,16 @@ extern "C" int logo_head_proj(const void* x0, const void* w0, void* y0, int h0, 
 
 extern "C" int logo_decode_qkv(const void* qkv, int64_t ldq, const void* wq, const void* wk, const void* wv,
                                const void* cos, const void* sin, const int32_t* pos, void* q_out, void* gq_out,
-                               void* local_k, void* local_v, void* global_k, void* global_v, int batch, int h,
-                               int hk, int d, int ring, int64_t t_cap, int dtype, void* stream) {
+                               void* local_k, void* local_v, void* global_k, void* global_v, int64_t gate_col,
+                               void* gate_out, int batch, int h, int hk, int d, int ring, int64_t t_cap, int dtype,
+                               void* stream) {
   LOGO_REQUIRE(dtype == LOGO_DTYPE_BF16, "only bf16 tensors are supported");
   LOGO_REQUIRE(d == 64 || d == 128, "head dim %d unsupported (64 or 128)", d);
   LOGO_REQUIRE(batch >= 0 && batch <= 4096 && h >= 1 && hk >= 1 && h % hk == 0, "bad batch / head counts");
   LOGO_REQUIRE(ldq >= (int64_t)(h + 2 * hk) * d, "ldq (%lld) shorter than the stacked q | k | v row",
                (long long)ldq);
   LOGO_REQUIRE(ring >= 1 && t_cap >= 1, "ring and t_cap must be positive");
+  LOGO_REQUIRE(gate_out == nullptr || (gate_col >= 0 && gate_col < ldq), "gate_col outside the row");
   LOGO_REQUIRE(qkv && wq && wk && wv && cos && sin && pos && q_out && gq_out && local_k && local_v && global_k &&
                    global_v,
                "null pointer argument");
@@ -463,6 +484,8 @@ extern "C" int logo_decode_qkv(const void* qkv, int64_t ldq, const void* wq, con
   a.lv = static_cast<bf16*>(local_v);
   a.gk = static_cast<bf16*>(global_k);
   a.gv = static_cast<bf16*>(global_v);
+  a.gate_out = static_cast<bf16*>(gate_out);
+  a.gate_col = gate_col;
   a.b = batch;
   a.h = h;
   a.hk = hk;

@@ -284,11 +284,11 @@ class LoGoAttention(nn.Module):
         H, HK, D = self.num_heads, self.num_key_value_heads, self.head_dim
         qkv = F.linear(hidden_states, self._decode_weight()).view(B, -1)
         n_qkv = (H + 2 * HK) * D
-        gate = torch.sigmoid(qkv[:, n_qkv:n_qkv + 1]).view(B, 1, 1)
         cos, sin = _cos_sin(self, B, 1, hidden_states.device, qkv.dtype, position_ids, None, cache,
                             position_embeddings)
-        q, gq = decode_qkv(qkv, self.q_global_proj, self.k_global_proj, self.v_global_proj, cos, sin, cache,
-                           self.layer_idx, H, HK)
+        q, gq, gate = decode_qkv(qkv, self.q_global_proj, self.k_global_proj, self.v_global_proj, cos, sin, cache,
+                                 self.layer_idx, H, HK, gate_col=n_qkv)
+        gate = gate.view(B, 1, 1)
         len_g, len_l = cache.step_lengths()
         bound_g, bound_l = cache.length_bounds()
         li = self.layer_idx

@@ -95,14 +95,16 @@ def cache_append(k_new, v_new, k_cache, v_cache, pos, ring: int = 0):
                 k_cache.shape[2], int(ring), _lib.DTYPE_BF16, _lib.stream_of(k_new))
 
 
-def decode_qkv(qkv, wq, wk, wv, cos, sin, cache: "LogoKVCache", layer: int, heads: int, kv_heads: int):
+def decode_qkv(qkv, wq, wk, wv, cos, sin, cache: "LogoKVCache", layer: int, heads: int, kv_heads: int,
+               gate_col: Optional[int] = None):
     """One decode step's q / k / v transform for a LoGo layer in one launch.
 
     ``qkv [B, ldq]``: each token's stacked projection row ``[q | k | v | ...]``;
     ``wq/wk/wv``: the global ``linear_proj`` matrices; ``cos/sin [B, D]``.
     Appends the rotated k, v (local ring) and global k, v (global cache) at the
     cache's device position and returns the rotated q and global q
-    ``[B, H, D]``."""
+    ``[B, H, D]``; with ``gate_col`` (the gate logit's column in the row) also
+    the gate ``sigmoid(qkv[:, gate_col])`` ``[B]`` as a third result."""
     _lib.require_gpu(qkv, wq, wk, wv, cos, sin)
     B = qkv.shape[0]
     D = wq.shape[-1]
@@ -112,6 +114,7 @@ def decode_qkv(qkv, wq, wk, wv, cos, sin, cache: "LogoKVCache", layer: int, head
         raise ValueError("cache is full")
     q = torch.empty(B, heads, D, dtype=torch.bfloat16, device=qkv.device)
     gq = torch.empty_like(q)
+    gate = torch.empty(B, dtype=torch.bfloat16, device=qkv.device) if gate_col is not None else None
     cos = cos.reshape(B, D).contiguous()
     sin = sin.reshape(B, D).contiguous()
     lib = _lib.lib()
@@ -119,8 +122,9 @@ def decode_qkv(qkv, wq, wk, wv, cos, sin, cache: "LogoKVCache", layer: int, head
                 _lib.ptr(wk.contiguous()), _lib.ptr(wv.contiguous()), _lib.ptr(cos), _lib.ptr(sin),
                 _lib.ptr(cache._pos), _lib.ptr(q), _lib.ptr(gq), _lib.ptr(cache.local_k[layer]),
                 _lib.ptr(cache.local_v[layer]), _lib.ptr(cache.global_k[layer]), _lib.ptr(cache.global_v[layer]),
-                B, heads, kv_heads, D, cache.ring, cache.max_len, _lib.DTYPE_BF16, _lib.stream_of(qkv))
-    return q, gq
+                int(gate_col) if gate_col is not None else 0, _lib.ptr(gate), B, heads, kv_heads, D, cache.ring,
+                cache.max_len, _lib.DTYPE_BF16, _lib.stream_of(qkv))
+    return (q, gq) if gate is None else (q, gq, gate)
 
 
 class LogoKVCache:

@@ -79,7 +79,15 @@ def test_decode_qkv_equals_step_by_step(gpu, B, H, HK, D):
             t.zero_()
         c.set_length(T)
     cos, sin = rope_cos_sin(torch.full((B, 1), T, device=gpu), D, 10000.0, torch.bfloat16)
-    q, gq = decode_qkv(qkv, *ws, cos, sin, cache_a, 0, H, HK)
+    gate_col = (H + 2 * HK) * D  # first column past the stacked q | k | v
+    qkv[:B, gate_col] = torch.linspace(-12, 12, B, device=gpu).bfloat16()
+    q, gq, gate = decode_qkv(qkv, *ws, cos, sin, cache_a, 0, H, HK, gate_col=gate_col)
+    # the gate against torch's sigmoid of the same bf16 logits: equal up to the
+    # last bf16 bit (both round an fp32 1 / (1 + exp(-z)))
+    ref_gate = torch.sigmoid(qkv[:, gate_col])
+    diff = (gate.float() - ref_gate.float()).abs()
+    assert (diff <= ref_gate.float().abs() * 2.0 ** -8).all()
+    assert (gate == ref_gate).float().mean().item() >= 0.99
     # step by step
     qv = qkv[:, :H * D].reshape(B, 1, H, D).contiguous()
     kv = qkv[:, H * D:(H + HK) * D].reshape(B, 1, HK, D).contiguous()
