@@ -278,6 +278,27 @@ int logo_decode_qkv(const void* qkv, int64_t ldq, const void* wq, const void* wk
                     int d, int ring, int64_t t_cap, int dtype, void* stream);
 
 /*
+ * Per-head linear map on the [N, H, d] layout in place: y[n, h, :] =
+ * x[n, h, :] W_h (transpose_w = 0) or x[n, h, :] W_h^T (transpose_w = 1), W
+ * [H, d, d]; x row n at x + n * ldx, y row n at y + n * ldy (elements).  The
+ * linear_proj global re-parameterisation at training sizes
+ * (logo/layers/logo.py:86-94) and its input gradient, without the head-major
+ * copies of a batched GEMM.
+ */
+int logo_head_linear(const void* x, int64_t ldx, const void* w, void* y, int64_t ldy, int64_t n_tokens, int heads,
+                     int d, int transpose_w, int dtype, void* stream);
+
+/* Bytes of fp32 workspace logo_head_linear_dw needs. */
+size_t logo_head_linear_dw_workspace_bytes(int64_t n_tokens, int heads, int d);
+
+/*
+ * Weight gradient of logo_head_linear: dw[h] = sum_n x[n, h, :]^T dy[n, h, :]
+ * ([H, d, d], d = 128), reduced over token chunks in a fixed order.
+ */
+int logo_head_linear_dw(const void* x, int64_t ldx, const void* dy, int64_t ldy, void* dw, void* workspace,
+                        int64_t n_tokens, int heads, int d, int dtype, void* stream);
+
+/*
  * Residual add + RMSNorm of the decoder: s_out = r + x (bf16, as the eager
  * add rounds) and y = RMSNorm(s_out) with weight w (as logo_rmsnorm), rows of
  * cols bf16 (a multiple of 8, at most 4096): the residual adds and the

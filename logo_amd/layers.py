@@ -4,8 +4,9 @@ Counterpart of ``LoGoAttention`` (logo/layers/logo.py:34-262), with the same
 parameter names and config knobs, so a reference state dict loads unchanged.
 The hot path (local SWA, query-sparse or dense global attention, the fused
 gate / context-norm / fusion epilogue, gate-aware decode) runs on this
-package's HIP kernels; the projections, the global re-parameterisation and
-RoPE stay plain PyTorch glue.
+package's HIP kernels, and so do RoPE, the per-head global re-parameterisation
+and, at decode, the transform, gate and cache appends; the dense projections
+are hipBLASLt GEMMs through torch.
 
 Differences in structure (not in results): tensors stay in ``[B, T, H, D]``
 (no ``transpose(1, 2).contiguous()`` round trips, :121-158); equal-length
@@ -28,7 +29,7 @@ import torch.nn.functional as F
 
 from .ops.decode import LogoKVCache, decode_attn, decode_attn_fused, decode_qkv
 from .ops.epilogue import logo_epilogue
-from .ops.glue import head_proj, rms_norm, rope, rope_apply_
+from .ops.glue import head_linear, head_proj, rms_norm, rope, rope_apply_
 from .ops.sq_attn import dense_causal_attn, sq_full_attn, swa_attn
 
 __all__ = ["LoGoConfig", "LoGoAttention", "Attention", "RMSNorm", "rope_cos_sin", "apply_rope", "position_ids_for"]
@@ -168,11 +169,17 @@ def _pack_cu(B, T, cu_seqlens, device):
 
 
 def _per_head_linear(x, w):
-    """``x [..., H, D] @ w [H, D, E]`` per head as one batched GEMM over heads
-    (both operands contiguous: bf16 batched products are only used with
-    contiguous right operands here)."""
+    """``x [..., H, D] @ w [H, D, E]`` per head.  bf16 ROCm tensors with square
+    per-head maps take the HIP kernels, which read and write the ``[..., H,
+    D]`` layout in place (forward, input and weight gradients); anything else
+    one batched GEMM over heads (both operands contiguous: bf16 batched
+    products are only used with contiguous right operands here)."""
     lead = x.shape[:-2]
     H, D = x.shape[-2], x.shape[-1]
+    wgrad = w.requires_grad and torch.is_grad_enabled()
+    if (x.is_cuda and x.dtype == torch.bfloat16 and w.dtype == torch.bfloat16 and tuple(w.shape) == (H, D, D)
+            and (D == 128 or (D == 64 and not wgrad))):
+        return head_linear(x, w)
     xh = x.reshape(-1, H, D).transpose(0, 1).contiguous()  # [H, N, D]
     y = torch.bmm(xh, w.to(x.dtype).contiguous())  # [H, N, E]
     return y.transpose(0, 1).reshape(*lead, H, w.shape[-1]).contiguous()

@@ -13,7 +13,8 @@ import torch
 
 from .. import _lib
 
-__all__ = ["rope_apply_", "rope", "RopeFunction", "rms_norm", "head_proj", "add_rms_norm", "silu_mul"]
+__all__ = ["rope_apply_", "rope", "RopeFunction", "rms_norm", "head_proj", "add_rms_norm", "silu_mul",
+           "head_linear", "HeadLinearFunction"]
 
 
 def _rope_checked(tensors, cos, sin, what):
@@ -176,3 +177,67 @@ def silu_mul(gu):
     _lib.launch("logo_silu_mul", lib.logo_silu_mul, _lib.ptr(g2), g2.stride(0), _lib.ptr(y), g2.shape[0], cols,
                 _lib.DTYPE_BF16, _lib.stream_of(g2))
     return y.view(*lead, cols)
+
+
+def _rows(x):
+    """``x [..., H, D]`` as (tensor, token count, row stride) with the head and
+    dim axes dense; other layouts are copied."""
+    H, D = x.shape[-2], x.shape[-1]
+    if not (x.stride(-1) == 1 and x.stride(-2) == D):
+        x = x.contiguous()
+    x2 = x.reshape(-1, H, D) if x.dim() != 3 else x
+    if x2.dim() != 3 or x2.stride(-1) != 1 or x2.stride(-2) != D or x2.stride(0) % 8 != 0 or x2.data_ptr() % 16:
+        x2 = x2.contiguous()
+    return x2, x2.shape[0], x2.stride(0)
+
+
+def _head_linear_launch(x, w, transpose_w: bool):
+    x2, n, ldx = _rows(x)
+    H, D = x2.shape[1], x2.shape[2]
+    y = torch.empty(n, H, D, dtype=torch.bfloat16, device=x.device)
+    lib = _lib.lib()
+    _lib.launch("logo_head_linear", lib.logo_head_linear, _lib.ptr(x2), ldx, _lib.ptr(w), _lib.ptr(y), H * D, n, H, D,
+                int(transpose_w), _lib.DTYPE_BF16, _lib.stream_of(x2))
+    return y.view(x.shape)
+
+
+class HeadLinearFunction(torch.autograd.Function):
+    """``y[..., h, :] = x[..., h, :] @ w[h]`` with its gradients, every pass on
+    the ``[..., H, D]`` layout in place (no head-major copies)."""
+
+    @staticmethod
+    def forward(ctx, x, w):
+        wc = w.contiguous()
+        ctx.save_for_backward(x, wc)
+        return _head_linear_launch(x, wc, False)
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, w = ctx.saved_tensors
+        dx = dw = None
+        if ctx.needs_input_grad[0]:
+            dx = _head_linear_launch(dy, w, True)
+        if ctx.needs_input_grad[1]:
+            x2, n, ldx = _rows(x)
+            d2, _, ldy = _rows(dy)
+            H, D = x2.shape[1], x2.shape[2]
+            lib = _lib.lib()
+            ws = torch.empty((lib.logo_head_linear_dw_workspace_bytes(n, H, D) + 3) // 4, dtype=torch.float32,
+                             device=x.device)
+            dw = torch.empty(H, D, D, dtype=torch.bfloat16, device=x.device)
+            _lib.launch("logo_head_linear_dw", lib.logo_head_linear_dw, _lib.ptr(x2), ldx, _lib.ptr(d2), ldy,
+                        _lib.ptr(dw), _lib.ptr(ws), n, H, D, _lib.DTYPE_BF16, _lib.stream_of(x2))
+            dw = dw.to(w.dtype)
+        return dx, dw
+
+
+def head_linear(x, w):
+    """``x [..., H, D] @ w [H, D, D]`` per head (bf16 ROCm tensors, D = 128 for
+    the weight gradient), differentiable."""
+    _lib.require_gpu(x, w)
+    if x.dtype != torch.bfloat16 or w.dtype != torch.bfloat16:
+        raise ValueError("head_linear takes bf16 tensors")
+    H, D = x.shape[-2], x.shape[-1]
+    if tuple(w.shape) != (H, D, D):
+        raise ValueError(f"head_linear: weight {tuple(w.shape)} does not match heads {H}, dim {D}")
+    return HeadLinearFunction.apply(x, w)

@@ -116,3 +116,38 @@ def test_silu_mul_matches_eager(gpu, rows, cols):
     ref = torch.nn.functional.silu(gu[:, :cols]) * gu[:, cols:]
     assert (got == ref).float().mean().item() >= 0.999
     assert ((got.float() - ref.float()).abs() <= 2 ** -7 * ref.float().abs() + 1e-6).all()
+
+
+@pytest.mark.parametrize("N,H,D,pad", [(300, 4, 128, 0), (2500, 2, 128, 24), (77, 3, 64, 0)])
+def test_head_linear_fwd_bwd_matches_fp32(gpu, N, H, D, pad):
+    """The per-head linear map on the [N, H, D] layout (strided rows
+    included) against fp32 autograd through einsum: forward and input gradient
+    within bf16 rounding, weight gradient (D = 128) within an fp32 sum's; two
+    runs bit-identical."""
+    from logo_amd.ops.glue import head_linear
+
+    g = gen(N + H + D + pad)
+    base = torch.randn(N, H * D + pad, generator=g).bfloat16().to(gpu)
+    x = base[:, pad:].view(N, H, D) if pad == 0 else base[:, pad:].unflatten(1, (H, D))
+    w = (torch.eye(D) + 0.05 * torch.randn(H, D, D, generator=g)).bfloat16().to(gpu)
+    dy = torch.randn(N, H, D, generator=g).bfloat16().to(gpu)
+    wgrad = D == 128
+    xa = x.detach().clone().requires_grad_(True)
+    wa = w.detach().clone().requires_grad_(wgrad)
+    y = head_linear(xa, wa)
+    y.backward(dy)
+    xr = x.detach().float().requires_grad_(True)
+    wr = w.detach().float().requires_grad_(wgrad)
+    yr = torch.einsum("nhd,hde->nhe", xr, wr)
+    yr.backward(dy.float())
+
+    def close(a, b, rel):
+        b = b.float()
+        return ((a.float() - b).abs() <= rel * b.abs() + 2e-3 * b.abs().max()).all()
+
+    assert close(y, yr.detach(), 2.0 ** -7)
+    assert close(xa.grad, xr.grad, 2.0 ** -7)
+    if wgrad:
+        assert close(wa.grad, wr.grad, 2.0 ** -7)
+    y2 = head_linear(x, w)
+    assert torch.equal(y2, y.detach())
