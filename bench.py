@@ -74,6 +74,12 @@ def parse():
     ap.add_argument("--decode-layer", action="store_true",
                     help="run only the config-5 global decode branch of one layer (the kernel the "
                          "decode HBM-traffic profile measures) and print its time and bandwidth")
+    ap.add_argument("--decode-model", action="store_true",
+                    help="run only the config-5 model decode measurement (prefill, then captured decode "
+                         "steps) and print its result")
+    ap.add_argument("--layer", action="store_true",
+                    help="run only the config-4 LoGoAttention layer forward + backward measurement and "
+                         "print its result")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run one 1 GiB device-to-device copy before the workload (the reference kernel "
                          "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters to bytes)")
@@ -473,6 +479,12 @@ def main():
             torch.cuda.synchronize()
             del src, dst
         decode_layer_only(dev)
+        return
+    if args.decode_model:
+        print(json.dumps(decode_model_measurement(dev)), flush=True)
+        return
+    if args.layer:
+        print(json.dumps(layer_cfg4_measurement(dev)), flush=True)
         return
     T, H, D = args.seq_len, args.heads, args.head_dim
     gen = torch.Generator()
