@@ -134,19 +134,28 @@ struct QTile {
 
   // rpw: compacted rows per wave (32 or 64); r / t / p / valid describe the
   // lane's row in the wave's first 32-row block (row_at gives the others).
-  __device__ __forceinline__ bool init(const AttnArgs& a, int wave, int i, bool window, int rpw = 32) {
+  // paired: the workgroup takes two consecutive kBQ-row tiles (a single
+  // segment only, nseq == 1, so both tiles share one key range).
+  __device__ __forceinline__ bool init(const AttnArgs& a, int wave, int i, bool window, int rpw = 32,
+                                       bool paired = false) {
     int rank;
     xcd_remap(blockIdx.x, a.hq, rank, hq);
     lane_sel = a.lanes > 1 ? hq : 0;
     const int32_t* meta = a.meta + (int64_t)lane_sel * a.meta_stride;
-    const int nt = meta[1];
+    const int nt = paired ? (meta[1] + 1) >> 1 : meta[1];
     if (rank >= nt) return false;
     const int tile = nt - 1 - rank;  // heaviest (latest) blocks first
     const int32_t* cu_q = meta + kMetaHdr;
     const int32_t* cu_tq = cu_q + (a.nseq + 1);
-    s = seg_of(cu_tq, a.nseq, tile);
-    r0 = cu_q[s] + (tile - cu_tq[s]) * kBQ;
-    r_end = min(r0 + kBQ, cu_q[s + 1]);
+    if (paired) {
+      s = 0;
+      r0 = cu_q[0] + tile * 2 * kBQ;
+      r_end = min(r0 + 2 * kBQ, cu_q[1]);
+    } else {
+      s = seg_of(cu_tq, a.nseq, tile);
+      r0 = cu_q[s] + (tile - cu_tq[s]) * kBQ;
+      r_end = min(r0 + kBQ, cu_q[s + 1]);
+    }
     bos = a.cu[s];
     seqlen = a.cu[s + 1] - bos;
     h = hq / a.g;
@@ -186,7 +195,8 @@ using BufTag = std::integral_constant<int, B>;
 // t&1 and V(t+1) into V slot (t+1)&1, both last read in iteration t - 1.
 // Each wave only works on the tiles its own rows can see ([tw_lo, tw_hi));
 // outside them it still copies its share of the tiles and meets the barriers.
-// Four waves x 32 rows per workgroup (kBQ = 128), two waves per SIMD.
+// NW waves x 32 rows per workgroup (kBQ = 128 rows, or two tiles with 8
+// waves), two waves per SIMD.
 //
 // Online softmax with a lazy rescale: the reference max of a row moves only
 // when the row's max grew by more than 2^8 in the exp2 domain (or on its first
@@ -194,8 +204,8 @@ using BufTag = std::integral_constant<int, B>;
 // Masks compare a compile-time offset per accumulator item with one per-lane
 // bound: key j0 + 32 kk + rowmap(g, jj) is visible iff its offset from
 // j0 + 4 g lies in [hi - W, hi], hi = p - j0 - 4 g.
-template <int D, bool SPARSE, bool WINDOW>
-__global__ __launch_bounds__(256) LOGO_OCC_FWD void sq_fwd_pipe_kernel(const AttnArgs a) {
+template <int D, bool SPARSE, bool WINDOW, int NW>
+__global__ __launch_bounds__(64 * NW) LOGO_OCC_FWD void sq_fwd_pipe_kernel(const AttnArgs a) {
   constexpr int DS = D / 16, DT = D / 32;
   constexpr int NX = 2 * DS;   // S MFMAs per tile (two 32-key halves x DS k-steps)
   constexpr int NY = 4 * DT;   // PV MFMAs per tile (DT column blocks x 4 key steps)
@@ -209,7 +219,7 @@ __global__ __launch_bounds__(256) LOGO_OCC_FWD void sq_fwd_pipe_kernel(const Att
 
   const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63, i = l & 31, g = l >> 5;
   QTile<SPARSE> qt;
-  if (!qt.init(a, wave, i, WINDOW)) return;
+  if (!qt.init(a, wave, i, WINDOW, 32, NW == 8)) return;
   const int hq = qt.hq, p = qt.p, W = a.window;
 
   bf16x8 qreg[DS];
@@ -234,7 +244,7 @@ __global__ __launch_bounds__(256) LOGO_OCC_FWD void sq_fwd_pipe_kernel(const Att
   const bf16* kbase = a.k + ((int64_t)qt.bos * a.h + qt.h) * D;
   const bf16* vbase = a.v + ((int64_t)qt.bos * a.h + qt.h) * D;
   const int seqlen = qt.seqlen;
-  TileBufDma<D> dma;
+  TileBufDma<D, NW> dma;
   dma.init((int)rstride);
   // rows past the sequence end are clamped to its last key (masked: p < seqlen)
   auto load_one = [&](bf16* tile, const bf16* src, int j0) {
@@ -974,14 +984,28 @@ static int check_common(int64_t n, int nseq, int hq, int h, int d, int lanes, in
   return LOGO_OK;
 }
 
+// Single long sequences take 8-wave workgroups of two query tiles, which
+// share each K / V tile copy between 256 rows (half the copy traffic and
+// issue per row); packed or short inputs keep 4-wave single-tile workgroups,
+// which give more workgroups where rows are few.
+constexpr int64_t kFwdPairMinTokens = 16384;
+
 template <int D, bool SPARSE, bool WINDOW>
 static int launch_fwd(const AttnArgs& a, hipStream_t st) {
-  const int64_t ntmax = (a.n + kBQ - 1) / kBQ + a.nseq;
+  const bool paired = a.nseq == 1 && a.n >= kFwdPairMinTokens;
+  const int64_t rows = paired ? 2 * kBQ : kBQ;
+  const int64_t ntmax = (a.n + rows - 1) / rows + a.nseq;
   const int64_t nblk = ntmax * a.hq;
   LOGO_REQUIRE(nblk < ((int64_t)1 << 31), "grid too large");
-  auto kern = sq_fwd_pipe_kernel<D, SPARSE, WINDOW>;
-  LOGO_HIP_CHECK(allow_smem(kern, fwd_smem<D>()));
-  hipLaunchKernelGGL(kern, dim3((unsigned)nblk), dim3(256), fwd_smem<D>(), st, a);
+  if (paired) {
+    auto kern = sq_fwd_pipe_kernel<D, SPARSE, WINDOW, 8>;
+    LOGO_HIP_CHECK(allow_smem(kern, fwd_smem<D>()));
+    hipLaunchKernelGGL(kern, dim3((unsigned)nblk), dim3(512), fwd_smem<D>(), st, a);
+  } else {
+    auto kern = sq_fwd_pipe_kernel<D, SPARSE, WINDOW, 4>;
+    LOGO_HIP_CHECK(allow_smem(kern, fwd_smem<D>()));
+    hipLaunchKernelGGL(kern, dim3((unsigned)nblk), dim3(256), fwd_smem<D>(), st, a);
+  }
   LOGO_LAUNCH_CHECK("sq_fwd_pipe_kernel");
   return LOGO_OK;
 }

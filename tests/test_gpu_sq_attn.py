@@ -165,3 +165,32 @@ def test_deterministic(gpu):
     assert torch.equal(a[0], b[0])
     for x, y in zip(a[1], b[1]):
         assert torch.equal(x, y)
+
+
+@pytest.mark.parametrize("per_head,hq,h", [(False, 4, 2), (True, 4, 4)])
+def test_long_single_sequence_paired_forward(gpu, per_head, hq, h):
+    """A single sequence of >= 16K tokens takes the 8-wave two-tile forward
+    workgroups; the same tokens as a pack with an extra empty segment take the
+    4-wave one-tile workgroups.  Every row visits the same 64-key tiles in the
+    same order either way, so outputs and gradients are bit-identical; the
+    first case is also checked against the torch fp32 reference (ragged last
+    tile, GQA)."""
+    g = gen(16 + hq + int(per_head))
+    n, d = 16384 + 77, 128
+    sel = torch.rand((n, hq) if per_head else (n,), generator=g) < 0.3
+    if per_head:
+        sel[0, :] = True
+    q, k, v = (randn((n, hq if i == 0 else h, d), g, 0.5) for i in range(3))
+    do = randn((n, hq, d), g)
+    one = torch.tensor([0, n], dtype=torch.int32)
+    two = torch.tensor([0, n, n], dtype=torch.int32)
+    o1, gr1 = _run(q, k, v, sel, one, gpu, do)
+    o2, gr2 = _run(q, k, v, sel, two, gpu, do)
+    assert torch.equal(o1, o2)
+    for a, b in zip(gr1, gr2):
+        assert torch.equal(a, b)
+    if not per_head:
+        ro, rgr = torch_sq_attn(q.to(gpu), k.to(gpu), v.to(gpu), sel.to(gpu), one, do=do.to(gpu))
+        assert_within("o", o1, ro)
+        for name, a, b in zip(("dq", "dk", "dv"), gr1, rgr):
+            assert_within(name, a, b)
