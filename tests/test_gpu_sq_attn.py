@@ -194,3 +194,21 @@ def test_long_single_sequence_paired_forward(gpu, per_head, hq, h):
         assert_within("o", o1, ro)
         for name, a, b in zip(("dq", "dk", "dv"), gr1, rgr):
             assert_within(name, a, b)
+
+
+def test_long_single_sequence_paired_swa_forward(gpu):
+    """Sliding-window attention over a single sequence of >= 16K tokens (the
+    8-wave two-tile forward in dense mode with a window) equals, bit for bit,
+    the same tokens packed with an extra empty segment (4-wave forward)."""
+    n, hq, h, d = 16384 + 200, 4, 2, 128
+    g = gen(31)
+    q, k, v = randn((n, hq, d), g), randn((n, h, d), g), randn((n, h, d), g)
+    do = randn((n, hq, d), g)
+    outs = []
+    for cu in (torch.tensor([0, n], dtype=torch.int32), torch.tensor([0, n, n], dtype=torch.int32)):
+        qg, kg, vg = (x.to(gpu).requires_grad_() for x in (q, k, v))
+        o = swa_attn(qg[None], kg[None], vg[None], cu.to(gpu), window=128)[0]
+        o.backward(do.to(gpu))
+        outs.append((o.detach(), qg.grad, kg.grad, vg.grad))
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
