@@ -664,9 +664,12 @@ __global__ __launch_bounds__(128) LOGO_OCC_DQ64 void sq_dq64_kernel(const AttnAr
 // ---------------------------------------------------------------------------
 // Backward dk / dv
 // ---------------------------------------------------------------------------
-// Query rows staged per LDS buffer (64-row sub-tiles; 128 would halve the
-// barriers but needs a second set of LDS address registers past 64 KB).
-constexpr int kDkvRows = 64;
+// Query rows staged per LDS buffer: two 64-row sub-tiles per step, half the
+// barriers, copy issues and step bookkeeping per row of 64-row steps.  Two
+// stages take 131 KB (one workgroup per CU, as its registers already allow);
+// the second stage's LDS addresses lie past the 64 KB reach of the
+// instruction offset, so the compiler keeps them in spare AGPRs.
+constexpr int kDkvRows = 128;
 constexpr int kDkvStages = 2;
 template <int D>
 constexpr int dkv_stage_bytes() { return 2 * kDkvRows * D * 2 + 3 * kDkvRows * 4; }
@@ -795,40 +798,41 @@ __global__ __launch_bounds__(256) LOGO_OCC_DKV void sq_dkv_kernel(const AttnArgs
       const int last = min(rt + RS - 1, rq_end - 1);
       const int p_first = pob[0];
       const int p_last = pob[last - rt];
-      // Each 64-row sub-tile as two 32-row halves h0, h1 in four phases of NS
-      // MFMA slots (one wave per SIMD):
-      //   P0: S/dP MFMAs of h0
-      //   P1: S/dP MFMAs of h1  | P = exp2(S*c - lse), dS = P * (dP - delta) of h0
-      //   P2: dV/dK MFMAs of h0 | the same arithmetic for h1
-      //   P3: dV/dK MFMAs of h1
-      // A slot is one MFMA, one row's share of the arithmetic and the LDS reads
-      // of the operand used PF slots later (across sub-tiles too).  Scheduling
-      // fences between slots keep this order, so the VALU work issues under
-      // the MFMAs.
+      // Each 64-row sub-tile as two 32-row halves h0, h1, its MFMAs in eight
+      // blocks of DS slots (one wave per SIMD):
+      //   S(h0) | dP(h0) | S(h1) | dP(h1) | dV(h0) | dK(h0) | dV(h1) | dK(h1)
+      // The softmax arithmetic of a half is split into P = exp2(S*c - lse)
+      // (needs S) and dS = P * (dP - delta) (needs dP and P), placed under
+      // blocks 1-2 (P of h0), 3 (dS of h0), 4-5 (P of h1) and 6 (dS of h1),
+      // so six of the eight blocks carry VALU work.  A slot is one MFMA, its
+      // share of the arithmetic and the LDS read of the operand used PF slots
+      // later (across sub-tiles too).  Scheduling fences between slots keep
+      // this order, so the VALU work issues under the MFMAs.
       auto compute = [&](auto mask_tag) {
         constexpr bool MASK = decltype(mask_tag)::value;
-        constexpr int NS = 2 * DS;  // MFMAs per phase: S and dP over D / 16 k-steps
+        constexpr int NS = 2 * DS;  // MFMAs per half and pass: S and dP over D / 16 k-steps
         constexpr int SPT = 4 * NS; // slots per sub-tile
         constexpr int PF = 6;       // operand prefetch distance, in slots
-        constexpr int IPS = 16 / NS;  // row items per slot
-        static_assert(IPS * NS == 16, "a half has 16 row items per lane");
+        constexpr int IPP = 16 / (2 * DS);  // P items per slot (over two blocks)
+        constexpr int IPD = 16 / DS;        // dS items per slot (over one block)
+        static_assert(IPP * 2 * DS == 16 && IPD * DS == 16, "a half has 16 row items per lane");
         f32x16 sacc[2], pacc[2];
         bf16x8 pbf[2][2], dbf[2][2];  // [half][hh]
-        bf16x8 opA[NSUB * 2 * NS];    // S/dP operands: Q row (even) / dO row (odd)
-        bf16x8 opC[NSUB * 2 * NS];    // dV/dK operands: dO^T (even) / Q^T (odd)
+        bf16x8 opA[NSUB * 2 * NS];    // S/dP operands: Q rows / dO rows
+        bf16x8 opC[NSUB * 2 * NS];    // dV/dK operands: dO^T / Q^T
         f32x4 l4[NSUB][2][4], d4[NSUB][2][4];
         int4 p4[NSUB][2][4];
-        // A operand a of sub-tile u: half a / NS, k-step (a % NS) / 2
+        // A operand a of sub-tile u: half a / NS; S (first DS) or dP (next DS), k-step a % DS
         auto load_a = [&](auto u_c, auto a_c) {
           constexpr int U = decltype(u_c)::value, A = decltype(a_c)::value;
-          constexpr int QQ = A / NS, K = A % NS;
-          opA[U * 2 * NS + A] = rd.row(K % 2 ? ob : qb, 64 * U + 32 * QQ, K / 2);
+          constexpr int QQ = A / NS, KK = A % NS;
+          opA[U * 2 * NS + A] = rd.row(KK >= DS ? ob : qb, 64 * U + 32 * QQ, KK % DS);
         };
-        // C operand c of sub-tile u: half c / NS, hh, dt
+        // C operand c of sub-tile u: half c / NS; dV (first DS) or dK (next DS); hh, dt
         auto load_c = [&](auto u_c, auto c_c) {
           constexpr int U = decltype(u_c)::value, C = decltype(c_c)::value;
-          constexpr int QQ = C / NS, K = C % NS, HH = K / (2 * DT), DTI = (K / 2) % DT;
-          opC[U * 2 * NS + C] = rd.tr(K % 2 ? qb : ob, 64 * U + 16 * (2 * QQ + HH), DTI);
+          constexpr int QQ = C / NS, KK = C % NS, HH = (KK % DS) / DT, DTI = KK % DT;
+          opC[U * 2 * NS + C] = rd.tr(KK >= DS ? qb : ob, 64 * U + 16 * (2 * QQ + HH), DTI);
         };
         // the operand first used at slot T
         auto load_for_slot = [&](auto t_c) {
@@ -836,39 +840,43 @@ __global__ __launch_bounds__(256) LOGO_OCC_DKV void sq_dkv_kernel(const AttnArgs
           if constexpr (L < 2 * NS) load_a(std::integral_constant<int, U>{}, std::integral_constant<int, L>{});
           else load_c(std::integral_constant<int, U>{}, std::integral_constant<int, L - 2 * NS>{});
         };
-        // lse / delta / positions of query rows 64u + 32qq + 8m + 4g + (0..3)
-        auto load_stats = [&](int u, int qq, int m) {
+        // lse / positions (P) and delta (dS) of query rows 64u + 32qq + 8m + 4g + (0..3)
+        auto load_pstats = [&](int u, int qq, int m) {
           const int qr = 64 * u + 32 * qq + 8 * m + 4 * g;
           l4[u][qq][m] = lds_load(reinterpret_cast<const f32x4*>(lb + qr));
-          d4[u][qq][m] = lds_load(reinterpret_cast<const f32x4*>(dlb + qr));
           if constexpr (MASK) p4[u][qq][m] = lds_load(reinterpret_cast<const int4*>(pob + qr));
+        };
+        auto load_dstats = [&](int u, int qq, int m) {
+          const int qr = 64 * u + 32 * qq + 8 * m + 4 * g;
+          d4[u][qq][m] = lds_load(reinterpret_cast<const f32x4*>(dlb + qr));
         };
         auto mfma_a = [&](auto u_c, auto a_c) {
           constexpr int U = decltype(u_c)::value, A = decltype(a_c)::value;
-          constexpr int QQ = A / NS, K = A % NS;
+          constexpr int QQ = A / NS, KK = A % NS;
           bf16x8 op = opA[U * 2 * NS + A];
           pin(op);
-          if constexpr (K % 2 == 0) {
-            sacc[QQ] = mfma32(op, kreg[K / 2], K == 0 ? f32x16{} : sacc[QQ]);
+          if constexpr (KK < DS) {
+            sacc[QQ] = mfma32(op, kreg[KK], KK == 0 ? f32x16{} : sacc[QQ]);
           } else {
-            pacc[QQ] = mfma32(op, vreg[K / 2], K == 1 ? f32x16{} : pacc[QQ]);
+            pacc[QQ] = mfma32(op, vreg[KK - DS], KK == DS ? f32x16{} : pacc[QQ]);
           }
         };
         auto mfma_c = [&](auto u_c, auto c_c) {
           constexpr int U = decltype(u_c)::value, C = decltype(c_c)::value;
-          constexpr int QQ = C / NS, K = C % NS, HH = K / (2 * DT), DTI = (K / 2) % DT;
+          constexpr int QQ = C / NS, KK = C % NS, HH = (KK % DS) / DT, DTI = KK % DT;
           bf16x8 op = opC[U * 2 * NS + C];
           pin(op);
-          if constexpr (K % 2 == 0) mfma32_agpr(dvacc[DTI], op, pbf[QQ][HH]);
+          if constexpr (KK < DS) mfma32_agpr(dvacc[DTI], op, pbf[QQ][HH]);
           else mfma32_agpr(dkacc[DTI], op, dbf[QQ][HH]);
         };
-        // row item jj of half qq: items 4m..4m+3 are query rows 32qq + 8m + 4g + e
-        auto softmax_item = [&](auto u_c, int qq, auto jj_c) {
+        // row item jj of half qq: items 4m..4m+3 are query rows 32qq + 8m + 4g + e.
+        // P items leave P in sacc (fp32) and pack pairs into pbf; dS items leave
+        // dS in pacc and pack pairs into dbf.
+        auto p_item = [&](auto u_c, int qq, auto jj_c) {
           constexpr int U = decltype(u_c)::value, JJ = decltype(jj_c)::value;
           constexpr int M = JJ / 4, E = JJ % 4;
-          float sv = sacc[qq][JJ], dpv = pacc[qq][JJ];
+          float sv = sacc[qq][JJ];
           pin(sv);
-          pin(dpv);
           float pv = fast_exp2(fmaf(sv, c, -l4[U][qq][M][E]));
           if constexpr (MASK) {
             const int pq = p4[U][qq][M][E];
@@ -876,29 +884,40 @@ __global__ __launch_bounds__(256) LOGO_OCC_DKV void sq_dkv_kernel(const AttnArgs
             if (WINDOW) vis = vis && key >= pq - W;
             if (!vis) pv = 0.f;
           }
-          float dsv = pv * (dpv - d4[U][qq][M][E]);
           pin(pv);
-          pin(dsv);
+          sacc[qq][JJ] = pv;
           if constexpr (JJ % 2 == 1) {
             pbf[qq][JJ / 8][JJ % 8 - 1] = (bf16)sacc[qq][JJ - 1];
             pbf[qq][JJ / 8][JJ % 8] = (bf16)pv;
-            dbf[qq][JJ / 8][JJ % 8 - 1] = (bf16)pacc[qq][JJ - 1];
-            dbf[qq][JJ / 8][JJ % 8] = (bf16)dsv;
-          } else {
-            sacc[qq][JJ] = pv;
-            pacc[qq][JJ] = dsv;
           }
         };
-        // stats of (sub-tile u, half qq, group m) are read NS/2 slots before
-        // row item 4m
-        auto stats_slot = [](int u, int qq, int m) { return SPT * u + NS * (1 + qq) + 4 * m / IPS - NS / 2; };
+        auto ds_item = [&](auto u_c, int qq, auto jj_c) {
+          constexpr int U = decltype(u_c)::value, JJ = decltype(jj_c)::value;
+          constexpr int M = JJ / 4, E = JJ % 4;
+          float pv = sacc[qq][JJ], dpv = pacc[qq][JJ];
+          pin(pv);
+          pin(dpv);
+          float dsv = pv * (dpv - d4[U][qq][M][E]);
+          pin(dsv);
+          pacc[qq][JJ] = dsv;
+          if constexpr (JJ % 2 == 1) {
+            dbf[qq][JJ / 8][JJ % 8 - 1] = (bf16)pacc[qq][JJ - 1];
+            dbf[qq][JJ / 8][JJ % 8] = (bf16)dsv;
+          }
+        };
+        // stats of (sub-tile u, half qq, group m) are read DS/2 slots before
+        // the first item of group m needs them; the P items of half qq start at
+        // block 1 + 3qq, its dS items at block 3 + 3qq
+        auto pstats_slot = [](int u, int qq, int m) { return SPT * u + DS * (1 + 3 * qq) + 4 * m / IPP - DS / 2; };
+        auto dstats_slot = [](int u, int qq, int m) { return SPT * u + DS * (3 + 3 * qq) + 4 * m / IPD - DS / 2; };
 
         static_for<PF>([&](auto t_c) { load_for_slot(t_c); });
         static_for<NSUB * SPT>([&](auto s_c) {
-          constexpr int S = decltype(s_c)::value, U = S / SPT, L = S % SPT, PH = L / NS, K = L % NS;
+          constexpr int S = decltype(s_c)::value, U = S / SPT, L = S % SPT;
+          constexpr int BLK = L / DS, K = L % DS;
           using UC = std::integral_constant<int, U>;
           __builtin_amdgcn_sched_barrier(0);
-          if constexpr (PH <= 1) mfma_a(UC{}, std::integral_constant<int, L>{});
+          if constexpr (L < 2 * NS) mfma_a(UC{}, std::integral_constant<int, L>{});
           else mfma_c(UC{}, std::integral_constant<int, L - 2 * NS>{});
           if constexpr (S + PF < NSUB * SPT) load_for_slot(std::integral_constant<int, S + PF>{});
 #pragma unroll
@@ -906,12 +925,22 @@ __global__ __launch_bounds__(256) LOGO_OCC_DKV void sq_dkv_kernel(const AttnArgs
 #pragma unroll
             for (int qq = 0; qq < 2; ++qq)
 #pragma unroll
-              for (int m = 0; m < 4; ++m)
-                if (stats_slot(u, qq, m) == S) load_stats(u, qq, m);
-          if constexpr (PH == 1 || PH == 2)
-            static_for<IPS>([&](auto i_c) {
-              softmax_item(UC{}, PH - 1, std::integral_constant<int, K * IPS + decltype(i_c)::value>{});
+              for (int m = 0; m < 4; ++m) {
+                if (pstats_slot(u, qq, m) == S) load_pstats(u, qq, m);
+                if (dstats_slot(u, qq, m) == S) load_dstats(u, qq, m);
+              }
+          if constexpr (BLK == 1 || BLK == 2 || BLK == 4 || BLK == 5) {
+            constexpr int QQ = BLK >= 4, J0 = ((BLK - 1) % 3) * DS + K;
+            static_for<IPP>([&](auto i_c) {
+              p_item(UC{}, QQ, std::integral_constant<int, J0 * IPP + decltype(i_c)::value>{});
             });
+          }
+          if constexpr (BLK == 3 || BLK == 6) {
+            constexpr int QQ = BLK == 6;
+            static_for<IPD>([&](auto i_c) {
+              ds_item(UC{}, QQ, std::integral_constant<int, K * IPD + decltype(i_c)::value>{});
+            });
+          }
         });
         __builtin_amdgcn_sched_barrier(0);
       };
