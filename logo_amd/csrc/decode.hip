@@ -167,13 +167,16 @@ __global__ __launch_bounds__(256) void decode_dual_split_kernel(const DecArgs lo
 }
 
 // Merge the split partials of one (b, q-head) row: the splits' maxima and
-// sums are reduced across the 256 threads, then thread (group gi, column d)
+// sums are reduced across the workgroup, then thread (group gi, column d)
 // sums the rescaled partial outputs of splits gi, gi + G, ... with
 // independent loads, and the groups are added through LDS.  The bf16 output
 // row goes to out (global memory) or, with out == nullptr, to sout (LDS).
+constexpr int kCombThreads = 1024;  // combine workgroup: enough column groups that each
+                                    // thread's split loads go out together
 template <int D>
 __device__ __forceinline__ void dec_combine(const DecArgs& a, const int bq, bf16* out, bf16* sout) {
-  constexpr int G = 256 / D;  // split groups
+  constexpr int G = kCombThreads / D;  // split groups
+  constexpr int NWV = kCombThreads / 64;
   const int b = bq / a.hq;
   const int tid = threadIdx.x, l = tid & 63, wave = tid >> 6;
   if (!dec_active(a, b)) {
@@ -183,19 +186,21 @@ __device__ __forceinline__ void dec_combine(const DecArgs& a, const int bq, bf16
   const int len = a.lens[b];
   const int ns = min(a.nsplit, (len + kDecKeysPerWG - 1) / kDecKeysPerWG);
   const float* pp = a.part + (int64_t)bq * a.nsplit * (D + 2);
-  __shared__ float red[4];
+  __shared__ float red[NWV];
   __shared__ float so[G][D];
   float m = -INFINITY;
-  for (int s = tid; s < ns; s += 256) m = fmaxf(m, pp[(int64_t)s * (D + 2)]);
+  for (int s = tid; s < ns; s += kCombThreads) m = fmaxf(m, pp[(int64_t)s * (D + 2)]);
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
   if (l == 0) red[wave] = m;
   __syncthreads();
-  const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  float M = red[0];
+#pragma unroll
+  for (int w = 1; w < NWV; ++w) M = fmaxf(M, red[w]);
   const float Mb = M == -INFINITY ? 0.f : M;
   __syncthreads();
   float lsum = 0.f;
-  for (int s = tid; s < ns; s += 256) {
+  for (int s = tid; s < ns; s += kCombThreads) {
     const float* ps = pp + (int64_t)s * (D + 2);
     lsum += fast_exp2(ps[0] - Mb) * ps[1];
   }
@@ -204,7 +209,7 @@ __device__ __forceinline__ void dec_combine(const DecArgs& a, const int bq, bf16
   if (l == 0) red[wave] = lsum;
   const int gi = tid / D, d = tid % D;
   float o = 0.f;
-#pragma unroll 4
+#pragma unroll 8
   for (int s = gi; s < ns; s += G) {
     const float* ps = pp + (int64_t)s * (D + 2);
     o = fmaf(fast_exp2(ps[0] - Mb), ps[2 + d], o);
@@ -212,7 +217,9 @@ __device__ __forceinline__ void dec_combine(const DecArgs& a, const int bq, bf16
   so[gi][d] = o;
   __syncthreads();
   if (tid < D) {
-    const float L = red[0] + red[1] + red[2] + red[3];
+    float L = 0.f;
+#pragma unroll
+    for (int w = 0; w < NWV; ++w) L += red[w];
     float O = 0.f;
 #pragma unroll
     for (int k = 0; k < G; ++k) O += so[k][tid];
@@ -221,7 +228,7 @@ __device__ __forceinline__ void dec_combine(const DecArgs& a, const int bq, bf16
 }
 
 template <int D>
-__global__ __launch_bounds__(256) void decode_combine_kernel(const DecArgs a) {
+__global__ __launch_bounds__(kCombThreads) void decode_combine_kernel(const DecArgs a) {
   dec_combine<D>(a, blockIdx.x, a.out + (int64_t)blockIdx.x * D, nullptr);
 }
 
@@ -237,7 +244,7 @@ struct DecEpiArgs {
 };
 
 template <int D>
-__global__ __launch_bounds__(256) void decode_combine_epi_kernel(const DecArgs glo, const DecEpiArgs e) {
+__global__ __launch_bounds__(kCombThreads) void decode_combine_epi_kernel(const DecArgs glo, const DecEpiArgs e) {
   const int bq = blockIdx.x, b = bq / glo.hq;
   __shared__ bf16x8 sg[D / 8];
   bf16* sgb = reinterpret_cast<bf16*>(sg);
@@ -337,9 +344,9 @@ extern "C" int logo_decode_attn(const void* q, const void* k_cache, const void* 
   LOGO_LAUNCH_CHECK("decode_split_kernel");
   if (a.nsplit > 1) {  // a single split wrote the output already
     if (d == 128)
-      hipLaunchKernelGGL(decode_combine_kernel<128>, dim3(batch * hq), dim3(256), 0, st, a);
+      hipLaunchKernelGGL(decode_combine_kernel<128>, dim3(batch * hq), dim3(kCombThreads), 0, st, a);
     else
-      hipLaunchKernelGGL(decode_combine_kernel<64>, dim3(batch * hq), dim3(256), 0, st, a);
+      hipLaunchKernelGGL(decode_combine_kernel<64>, dim3(batch * hq), dim3(kCombThreads), 0, st, a);
     LOGO_LAUNCH_CHECK("decode_combine_kernel");
   }
   return LOGO_OK;
@@ -389,11 +396,11 @@ extern "C" int logo_decode_attn_fused(const void* q_local, const void* k_local, 
   if (d == 128) {
     hipLaunchKernelGGL(decode_dual_split_kernel<128>, grid, dim3(256), 0, st, loc, glo);
     LOGO_LAUNCH_CHECK("decode_dual_split_kernel");
-    hipLaunchKernelGGL(decode_combine_epi_kernel<128>, dim3(batch * hq), dim3(256), 0, st, glo, e);
+    hipLaunchKernelGGL(decode_combine_epi_kernel<128>, dim3(batch * hq), dim3(kCombThreads), 0, st, glo, e);
   } else {
     hipLaunchKernelGGL(decode_dual_split_kernel<64>, grid, dim3(256), 0, st, loc, glo);
     LOGO_LAUNCH_CHECK("decode_dual_split_kernel");
-    hipLaunchKernelGGL(decode_combine_epi_kernel<64>, dim3(batch * hq), dim3(256), 0, st, glo, e);
+    hipLaunchKernelGGL(decode_combine_epi_kernel<64>, dim3(batch * hq), dim3(kCombThreads), 0, st, glo, e);
   }
   LOGO_LAUNCH_CHECK("decode_combine_epi_kernel");
   return LOGO_OK;
