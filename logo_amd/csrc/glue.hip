@@ -261,6 +261,8 @@ struct DecQkvArgs {
   int64_t t_cap;
 };
 
+constexpr int kDqTok = 2;  // tokens per decode_qkv workgroup (more workgroups, short k-chains)
+
 template <int D>
 __global__ __launch_bounds__(D) void decode_qkv_kernel(const DecQkvArgs a) {
   // blockIdx.x: heads of q (0 .. H-1), then k (H .. H+HK-1), then v
@@ -268,11 +270,11 @@ __global__ __launch_bounds__(D) void decode_qkv_kernel(const DecQkvArgs a) {
   const int ti = gh < a.h ? 0 : (gh < a.h + a.hk ? 1 : 2);
   const int hh = ti == 0 ? gh : (ti == 1 ? gh - a.h : gh - a.h - a.hk);
   const int col0 = ti == 0 ? hh * D : (ti == 1 ? (a.h + hh) * D : (a.h + a.hk + hh) * D);
-  const int t0 = blockIdx.y * kHpTok;
+  const int t0 = blockIdx.y * kDqTok;
   const int n = threadIdx.x;
   __shared__ bf16x8 wsm[D * D / 8];  // this head's projection, [k][n]
-  __shared__ float xs[kHpTok][D];
-  __shared__ float ys[kHpTok][D];
+  __shared__ float xs[kDqTok][D];
+  __shared__ float ys[kDqTok][D];
   {
     const bf16x8* wsrc = reinterpret_cast<const bf16x8*>(a.w[ti] + (int64_t)hh * D * D);
     bf16x8 wv[D / 8];
@@ -281,30 +283,30 @@ __global__ __launch_bounds__(D) void decode_qkv_kernel(const DecQkvArgs a) {
 #pragma unroll
     for (int i = 0; i < D / 8; ++i) wsm[i * D + n] = wv[i];
   }
-  for (int idx = threadIdx.x; idx < kHpTok * D; idx += D) {
+  for (int idx = threadIdx.x; idx < kDqTok * D; idx += D) {
     const int tt = idx / D, k = idx % D;
     const int t = t0 + tt;
     xs[tt][k] = t < a.b ? (float)a.qkv[(int64_t)t * a.ldq + col0 + k] : 0.f;
   }
-  if (a.gate_out != nullptr && gh == 0 && n < kHpTok && t0 + n < a.b) {
+  if (a.gate_out != nullptr && gh == 0 && n < kDqTok && t0 + n < a.b) {
     const float z = (float)a.qkv[(int64_t)(t0 + n) * a.ldq + a.gate_col];
     a.gate_out[t0 + n] = (bf16)(1.f / (1.f + expf(-z)));
   }
   __syncthreads();
   const bf16* w = reinterpret_cast<const bf16*>(wsm) + n;
-  float acc[kHpTok];
+  float acc[kDqTok];
 #pragma unroll
-  for (int tt = 0; tt < kHpTok; ++tt) acc[tt] = 0.f;
+  for (int tt = 0; tt < kDqTok; ++tt) acc[tt] = 0.f;
   for (int k = 0; k < D; ++k) {
     const float wk = (float)w[k * D];
 #pragma unroll
-    for (int tt = 0; tt < kHpTok; ++tt) acc[tt] = fmaf(xs[tt][k], wk, acc[tt]);
+    for (int tt = 0; tt < kDqTok; ++tt) acc[tt] = fmaf(xs[tt][k], wk, acc[tt]);
   }
 #pragma unroll
-  for (int tt = 0; tt < kHpTok; ++tt) ys[tt][n] = (float)(bf16)acc[tt];
+  for (int tt = 0; tt < kDqTok; ++tt) ys[tt][n] = (float)(bf16)acc[tt];
   __syncthreads();
   const int pn = n < D / 2 ? n + D / 2 : n - D / 2;
-  for (int tt = 0; tt < kHpTok; ++tt) {
+  for (int tt = 0; tt < kDqTok; ++tt) {
     const int t = t0 + tt;
     if (t >= a.b) break;
     const float x = xs[tt][n], xp = xs[tt][pn];
@@ -491,7 +493,7 @@ extern "C" int logo_decode_qkv(const void* qkv, int64_t ldq, const void* wq, con
   a.hk = hk;
   a.ring = ring;
   a.t_cap = t_cap;
-  const dim3 grid((unsigned)(h + 2 * hk), (unsigned)((batch + kHpTok - 1) / kHpTok));
+  const dim3 grid((unsigned)(h + 2 * hk), (unsigned)((batch + kDqTok - 1) / kDqTok));
   hipStream_t st = as_stream(stream);
   if (d == 128) hipLaunchKernelGGL(decode_qkv_kernel<128>, grid, dim3(128), 0, st, a);
   else hipLaunchKernelGGL(decode_qkv_kernel<64>, grid, dim3(64), 0, st, a);
