@@ -9,8 +9,9 @@
 //     gradient), reading x rows with their head offset and writing y rows the
 //     same way.  A workgroup stages W_h in LDS once (rows padded, conflict-free
 //     16-byte reads) and runs kHlPasses passes of 128 tokens (32 per wave, one
-//     32x32x16 MFMA chain per 32 output columns); each wave's output tile goes
-//     through LDS so the stores are 16-byte row chunks.
+//     32x32x16 MFMA chain per 32 output columns), each wave loading its next
+//     pass's rows while it computes the current one; each wave's output tile
+//     goes through LDS so the stores are 16-byte row chunks.
 //   * head_linear_dw_kernel: the weight gradient dW_h = X_h^T dY_h over a chunk
 //     of tokens per workgroup (64-token tiles of X_h and dY_h copied global ->
 //     LDS, both operands read transposed), fp32 partials per chunk, then
@@ -57,14 +58,22 @@ __global__ __launch_bounds__(256) void head_linear_kernel(const HlArgs a) {
   __syncthreads();
   const int wave = threadIdx.x >> 6, l = threadIdx.x & 63, i = l & 31, g = l >> 5;
   bf16* yw = ys[wave];
-  for (int pass = 0; pass < kHlPasses; ++pass) {
-    const int64_t r0 = ((int64_t)blockIdx.x * kHlPasses + pass) * kHlRows + 32 * wave;
-    if (r0 >= a.n) break;  // wave-uniform; no barrier follows
-    // rows past n read the last row; they are not stored
+  // rows past n read the last row; they are not stored
+  auto row_of = [&](int pass) { return ((int64_t)blockIdx.x * kHlPasses + pass) * kHlRows + 32 * wave; };
+  auto load_x = [&](int64_t r0, bf16x8* dst) {
     const bf16* xr = a.x + (r0 + i < a.n ? r0 + i : a.n - 1) * a.ldx + (int64_t)h * D + 8 * g;
+#pragma unroll
+    for (int s = 0; s < DS; ++s) dst[s] = *reinterpret_cast<const bf16x8*>(xr + 16 * s);
+  };
+  bf16x8 nx[DS];  // the next pass's rows, loaded while this pass computes
+  if (row_of(0) < a.n) load_x(row_of(0), nx);
+  for (int pass = 0; pass < kHlPasses; ++pass) {
+    const int64_t r0 = row_of(pass);
+    if (r0 >= a.n) break;  // wave-uniform; no barrier follows
     bf16x8 av[DS];
 #pragma unroll
-    for (int s = 0; s < DS; ++s) av[s] = *reinterpret_cast<const bf16x8*>(xr + 16 * s);
+    for (int s = 0; s < DS; ++s) av[s] = nx[s];
+    if (pass + 1 < kHlPasses && row_of(pass + 1) < a.n) load_x(row_of(pass + 1), nx);
     f32x16 acc[CT];
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) {
