@@ -102,11 +102,15 @@ int logo_q_start_blk(const int32_t* pos, const int32_t* cu_q, const int32_t* chu
  * compacted row.  q_idx/pos == NULL selects dense mode (every row, meta from
  * logo_dense_meta).  window < 0: full causal; window >= 0: keys
  * [p - window, p] (logo/layers/utils.py:144-147).
+ * d is the head dim of q and k (64 or 128); v_dim is that of v and o, which
+ * the reference keeps separate (V, :341) and which must equal d here: every
+ * kernel strides all of them by d.  The Python op zero-pads other K, V <= 128
+ * to 64 or 128 before it calls this.
  */
 int logo_sq_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
                 const int64_t* q_idx, const int32_t* pos, const int32_t* meta,
                 const int32_t* cu, int64_t n_tokens, int nseq, int hq, int h, int d,
-                int lanes, float scale, int window, int dtype, void* stream);
+                int v_dim, int lanes, float scale, int window, int dtype, void* stream);
 
 /*
  * Backward (logo/ops/selected_full_attn.py:124-138 delta, :141-228 dq,
@@ -121,7 +125,7 @@ int logo_sq_bwd(const void* q, const void* k, const void* v, const void* o,
     const void* dout, const float* lse, float* delta, void* q_sel, void* do_sel,
     void* dq, void* dk, void* dv, const int64_t* q_idx, const int32_t* pos,
     const int32_t* meta, const int32_t* cu, int64_t n_tokens, int nseq, int hq,
-    int h, int d, int lanes, float scale, int window, int dtype, void* stream);
+    int h, int d, int v_dim, int lanes, float scale, int window, int dtype, void* stream);
 
 /*
  * The three backward phases of logo_sq_bwd as separate launches, same
@@ -133,17 +137,17 @@ int logo_sq_bwd_delta(const void* q, const void* k, const void* v, const void* o
     const void* dout, const float* lse, float* delta, void* q_sel, void* do_sel,
     void* dq, void* dk, void* dv, const int64_t* q_idx, const int32_t* pos,
     const int32_t* meta, const int32_t* cu, int64_t n_tokens, int nseq, int hq,
-    int h, int d, int lanes, float scale, int window, int dtype, void* stream);
+    int h, int d, int v_dim, int lanes, float scale, int window, int dtype, void* stream);
 int logo_sq_bwd_dq(const void* q, const void* k, const void* v, const void* o,
     const void* dout, const float* lse, float* delta, void* q_sel, void* do_sel,
     void* dq, void* dk, void* dv, const int64_t* q_idx, const int32_t* pos,
     const int32_t* meta, const int32_t* cu, int64_t n_tokens, int nseq, int hq,
-    int h, int d, int lanes, float scale, int window, int dtype, void* stream);
+    int h, int d, int v_dim, int lanes, float scale, int window, int dtype, void* stream);
 int logo_sq_bwd_dkv(const void* q, const void* k, const void* v, const void* o,
     const void* dout, const float* lse, float* delta, void* q_sel, void* do_sel,
     void* dq, void* dk, void* dv, const int64_t* q_idx, const int32_t* pos,
     const int32_t* meta, const int32_t* cu, int64_t n_tokens, int nseq, int hq,
-    int h, int d, int lanes, float scale, int window, int dtype, void* stream);
+    int h, int d, int v_dim, int lanes, float scale, int window, int dtype, void* stream);
 
 /*
  * Fused epilogue forward: gate threshold, the two branch context RMSNorms

@@ -1003,11 +1003,13 @@ static hipError_t allow_smem(K kernel, size_t bytes) {
                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
 }
 
-static int check_common(int64_t n, int nseq, int hq, int h, int d, int lanes, int dtype) {
+static int check_common(int64_t n, int nseq, int hq, int h, int d, int v_dim, int lanes, int dtype) {
   LOGO_REQUIRE(n > 0 && n < ((int64_t)1 << 31), "n_tokens out of range: %lld", (long long)n);
   LOGO_REQUIRE(nseq >= 1, "nseq must be >= 1");
   LOGO_REQUIRE(h >= 1 && hq >= h && hq % h == 0, "HQ (%d) must be a multiple of H (%d)", hq, h);
   LOGO_REQUIRE(d == 64 || d == 128, "head dim %d unsupported (64 or 128)", d);
+  // every kernel strides q, k, v, o and the gradients by the one head dim d
+  LOGO_REQUIRE(v_dim == d, "value head dim %d must equal the key head dim %d", v_dim, d);
   LOGO_REQUIRE(lanes == 1 || lanes == hq, "lanes must be 1 or HQ");
   LOGO_REQUIRE(dtype == LOGO_DTYPE_BF16, "only bf16 tensors are supported");
   return LOGO_OK;
@@ -1111,8 +1113,8 @@ using namespace logo;
 extern "C" int logo_sq_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
                            const int64_t* q_idx, const int32_t* pos, const int32_t* meta,
                            const int32_t* cu, int64_t n_tokens, int nseq, int hq, int h, int d,
-                           int lanes, float scale, int window, int dtype, void* stream) {
-  int rc = check_common(n_tokens, nseq, hq, h, d, lanes, dtype);
+                           int v_dim, int lanes, float scale, int window, int dtype, void* stream) {
+  int rc = check_common(n_tokens, nseq, hq, h, d, v_dim, lanes, dtype);
   if (rc != LOGO_OK) return rc;
   LOGO_REQUIRE(q && k && v && o && lse && meta && cu, "null pointer argument");
   LOGO_REQUIRE((q_idx == nullptr) == (pos == nullptr), "q_idx and pos must both be set or both be null");
@@ -1128,14 +1130,14 @@ extern "C" int logo_sq_fwd(const void* q, const void* k, const void* v, void* o,
   const void *q, const void *k, const void *v, const void *o, const void *dout, const float *lse, \
       float *delta, void *q_sel, void *do_sel, void *dq, void *dk, void *dv, const int64_t *q_idx, \
       const int32_t *pos, const int32_t *meta, const int32_t *cu, int64_t n_tokens, int nseq,      \
-      int hq, int h, int d, int lanes, float scale, int window, int dtype, void *stream
+      int hq, int h, int d, int v_dim, int lanes, float scale, int window, int dtype, void *stream
 
 #define LOGO_BWD_ARGS                                                                             \
   q, k, v, o, dout, lse, delta, q_sel, do_sel, dq, dk, dv, q_idx, pos, meta, cu, n_tokens, nseq, hq, \
-      h, d, lanes, scale, window, dtype, stream
+      h, d, v_dim, lanes, scale, window, dtype, stream
 
 static int bwd_entry(LOGO_BWD_PARAMS, int phase) {
-  int rc = check_common(n_tokens, nseq, hq, h, d, lanes, dtype);
+  int rc = check_common(n_tokens, nseq, hq, h, d, v_dim, lanes, dtype);
   if (rc != LOGO_OK) return rc;
   LOGO_REQUIRE(q && k && v && o && dout && lse && delta && meta && cu, "null pointer argument");
   LOGO_REQUIRE(phase == 0 || (dq && dk && dv), "null gradient pointer");

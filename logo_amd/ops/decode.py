@@ -154,7 +154,14 @@ class LogoKVCache:
         return self.seen
 
     def prefill(self, layer: int, k_local, v_local, k_global, v_global):
-        """Store a prompt's K/V (``[B, H, T, D]``) for one layer."""
+        """Store a prompt's K/V (``[B, H, T, D]``) for one layer, at positions
+        [0, T).  Only an empty cache takes a prompt: the prefill attends to the
+        prompt alone, so a second chunk on top of cached tokens would lose them
+        (``reset()`` empties the cache for a new prompt)."""
+        if self.seen > 0:
+            raise ValueError(
+                f"prefill into a cache that already holds {self.seen} tokens: a multi-token forward "
+                "attends to its own tokens only; call reset() or use a new cache for a new prompt")
         T = k_global.shape[2]
         if T > self.max_len:
             raise ValueError(f"prompt of {T} tokens exceeds the cache's {self.max_len}")
@@ -171,6 +178,10 @@ class LogoKVCache:
             if first < n:
                 self.local_k[layer][:, :, :n - first].copy_(k_local[:, :, p0 + first:p1])
                 self.local_v[layer][:, :, :n - first].copy_(v_local[:, :, p0 + first:p1])
+
+    def reset(self):
+        """Empty the cache (host and device positions back to 0)."""
+        self.set_length(0)
 
     def set_length(self, seen: int):
         """Record that ``seen`` tokens are cached (host value; e.g. after a prefill)."""

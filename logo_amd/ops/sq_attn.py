@@ -12,6 +12,7 @@ import functools
 from typing import Optional
 
 import torch
+import torch.nn.functional as F
 
 from .. import _lib
 from .common import DeviceSelection, compact_selection, dense_selection
@@ -22,10 +23,32 @@ _custom_fwd = functools.partial(torch.amp.custom_fwd, device_type="cuda")
 _custom_bwd = functools.partial(torch.amp.custom_bwd, device_type="cuda")
 
 
-def _to_kernel_dtype(t: torch.Tensor) -> torch.Tensor:
-    # The kernels compute in bf16 with fp32 accumulation; fp16/fp32 inputs are
-    # rounded to bf16 (the reference's Triton path likewise runs its dots at
-    # reduced precision).
+# Head dims the gfx950 kernels are compiled for.  A call with other K, V <= 128
+# (V != K included, as the reference allows: its V is a separate constexpr,
+# logo/ops/selected_full_attn.py:341-351) runs on the next compiled dim with
+# q, k and v zero-padded: zero columns add nothing to q.k, and they give zero
+# output and gradient columns, which are sliced off.
+KERNEL_HEAD_DIMS = (64, 128)
+
+
+def kernel_head_dim(K: int, V: int) -> int:
+    """The compiled head dim a call with key dim K and value dim V runs on."""
+    assert K <= 256, "K must fit in a single block (<=256)"
+    assert 0 < K <= 128 and 0 < V <= 128, "the gfx950 kernels take head dims K, V in [1, 128]"
+    return 64 if max(K, V) <= 64 else 128
+
+
+def _to_kernel(t: torch.Tensor, d: int) -> torch.Tensor:
+    """[B, T, H, X] -> contiguous bf16 [B*T, H, d], zero-padded along X.
+
+    The kernels compute in bf16 with fp32 accumulation, so fp16 and fp32
+    inputs are rounded to bf16 here (the outputs are cast back to the input
+    dtype).  The reference's Triton dots run in the input dtype
+    (logo/ops/selected_full_attn.py:95-99)."""
+    B, T, H, X = t.shape
+    t = t.reshape(B * T, H, X)
+    if X != d:
+        t = F.pad(t, (0, d - X))
     return t.contiguous() if t.dtype == torch.bfloat16 else t.to(torch.bfloat16).contiguous()
 
 
@@ -38,7 +61,7 @@ def _fwd(q, k, v, dsel: DeviceSelection, scale: float, window: int):
     _lib.launch("logo_sq_fwd", lib.logo_sq_fwd,
                 _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(o), _lib.ptr(lse),
                 _lib.ptr(dsel.q_idx), _lib.ptr(dsel.pos), _lib.ptr(dsel.meta), _lib.ptr(dsel.cu),
-                n, dsel.nseq, hq, h, d, dsel.lanes, float(scale), int(window), _lib.DTYPE_BF16,
+                n, dsel.nseq, hq, h, d, v.shape[2], dsel.lanes, float(scale), int(window), _lib.DTYPE_BF16,
                 _lib.stream_of(q))
     return o, lse
 
@@ -60,7 +83,7 @@ def _bwd(q, k, v, o, lse, do, dsel: DeviceSelection, scale: float, window: int):
     args = (_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(o), _lib.ptr(do), _lib.ptr(lse),
             _lib.ptr(delta), _lib.ptr(q_sel), _lib.ptr(do_sel), _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(dv),
             _lib.ptr(dsel.q_idx), _lib.ptr(dsel.pos), _lib.ptr(dsel.meta), _lib.ptr(dsel.cu),
-            n, dsel.nseq, hq, h, d, dsel.lanes, float(scale), int(window), _lib.DTYPE_BF16,
+            n, dsel.nseq, hq, h, d, v.shape[2], dsel.lanes, float(scale), int(window), _lib.DTYPE_BF16,
             _lib.stream_of(q))
     _lib.launch("logo_sq_bwd_delta", lib.logo_sq_bwd_delta, *args)
     _lib.launch("logo_sq_bwd_dq", lib.logo_sq_bwd_dq, *args)
@@ -77,10 +100,9 @@ class SQFullAttentionFunction(torch.autograd.Function):
         B, T, HQ, K = q.shape
         H = k.shape[2]
         V = v.shape[3]
+        d = kernel_head_dim(K, V)
         in_dtypes = (q.dtype, k.dtype, v.dtype)
-        qf = _to_kernel_dtype(q).view(B * T, HQ, K)
-        kf = _to_kernel_dtype(k).view(B * T, H, K)
-        vf = _to_kernel_dtype(v).view(B * T, H, V)
+        qf, kf, vf = _to_kernel(q, d), _to_kernel(k, d), _to_kernel(v, d)
         o, lse = _fwd(qf, kf, vf, dsel, scale, window)
         ctx.save_for_backward(qf, kf, vf, o, lse)
         ctx.dsel = dsel
@@ -88,7 +110,9 @@ class SQFullAttentionFunction(torch.autograd.Function):
         ctx.window = window
         ctx.shapes = (B, T, HQ, H, K, V)
         ctx.in_dtypes = in_dtypes
-        out = o.view(B, T, HQ, V)
+        out = o.view(B, T, HQ, d)
+        if V != d:
+            out = out[..., :V].contiguous()
         return out if q.dtype == torch.bfloat16 else out.to(q.dtype)
 
     @staticmethod
@@ -96,21 +120,32 @@ class SQFullAttentionFunction(torch.autograd.Function):
     def backward(ctx, do):
         qf, kf, vf, o, lse = ctx.saved_tensors
         B, T, HQ, H, K, V = ctx.shapes
-        dof = _to_kernel_dtype(do).view(B * T, HQ, V)
+        d = qf.shape[2]
+        dof = _to_kernel(do, d)
         dq, dk, dv = _bwd(qf, kf, vf, o, lse, dof, ctx.dsel, ctx.scale, ctx.window)
         tq, tk, tv = ctx.in_dtypes
-        dq = dq.view(B, T, HQ, K).to(tq)
-        dk = dk.view(B, T, H, K).to(tk)
-        dv = dv.view(B, T, H, V).to(tv)
+        dq = dq.view(B, T, HQ, d)[..., :K].to(tq)
+        dk = dk.view(B, T, H, d)[..., :K].to(tk)
+        dv = dv.view(B, T, H, d)[..., :V].to(tv)
         return dq, dk, dv, None, None, None
 
 
-def _check_qkv(q, k, v):
+def _check_shapes(q, k, v):
+    """The reference's rank and GQA checks (logo/ops/selected_full_attn.py:518-519)
+    plus the shape agreement its kernels assume; all before any launch."""
     assert q.dim() == 4 and k.dim() == 4 and v.dim() == 4, "q/k/v must be [B, T, H, D]"
     B, T, HQ, K = q.shape
     H = k.shape[2]
     assert HQ % H == 0, "HQ must be a multiple of H (GQA)"
-    assert K <= 256, "K must fit in a single block (<=256)"
+    assert tuple(k.shape[:2]) == (B, T) and tuple(v.shape[:2]) == (B, T), "q/k/v must share [B, T]"
+    assert v.shape[2] == H, "k and v must have the same number of heads"
+    assert k.shape[3] == K, "q and k must have the same head dim K"
+    kernel_head_dim(K, v.shape[3])
+    return B, T, HQ, H, K
+
+
+def _check_qkv(q, k, v):
+    B, T, HQ, H, K = _check_shapes(q, k, v)
     _lib.require_gpu(q, k, v)
     return B, T, HQ, H, K
 
@@ -137,9 +172,9 @@ def sq_full_attn(
     Returns:
         o: `[1, total_tokens, HQ, V]`; rows for unselected query tokens are 0.
     """
+    assert q.dim() == 4 and k.dim() == 4 and v.dim() == 4, "q/k/v must be [B, T, H, D]"
     B, T, HQ, K = q.shape
     H = k.shape[2]
-    assert q.dim() == 4 and k.dim() == 4 and v.dim() == 4, "q/k/v must be [B, T, H, D]"
     assert HQ % H == 0, "HQ must be a multiple of H (GQA)"
     per_head = selection.dim() == 3
     assert selection.dtype == torch.bool and (
@@ -147,7 +182,7 @@ def sq_full_attn(
     ), "selection must be a bool mask [B, T]"
     assert B == 1, "sq_full_attn only supports B=1 packed-varlen input"
     assert cu_seqlens is not None, "sq_full_attn requires explicit cu_seqlens"
-    assert K <= 256, "K must fit in a single block (<=256)"
+    _check_shapes(q, k, v)
     if scale is None:
         scale = K ** -0.5
     _lib.require_gpu(q, k, v, selection)

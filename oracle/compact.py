@@ -114,13 +114,3 @@ def compute_q_start_blk(pos_ids, cu_seqlens_q, cu_seqlens_k, block: int, T: int)
     local = np.maximum(first - cu_q[i_n], 0)
     return (local // block).astype(np.int32)
 
-
-def first_query_at_or_after(pos_ids, cu_seqlens_q, seq: int, key: int) -> int:
-    """Index (global compacted) of the first query of ``seq`` with pos >= key.
-
-    The un-blocked form of ``compute_q_start_blk`` used by this build's dK/dV
-    kernel, which starts its query loop at the exact row instead of a
-    block-aligned one.
-    """
-    lo, hi = int(cu_seqlens_q[seq]), int(cu_seqlens_q[seq + 1])
-    return lo + int(np.searchsorted(np.asarray(pos_ids)[lo:hi], key, side="left"))

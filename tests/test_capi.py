@@ -22,23 +22,30 @@ def test_header_symbols_are_exported():
 
 def test_abi_version_and_workspace():
     lib = _lib.lib()
-    assert lib.logo_abi_version() == 1
+    assert lib.logo_abi_version() == 2
     assert lib.logo_compact_workspace_bytes(4096, 1) == 4
     assert lib.logo_compact_workspace_bytes(4097, 16) == 2 * 16 * 4
 
 
-@pytest.mark.parametrize("d,hq,h,lanes,msg", [
-    (96, 4, 4, 1, "head dim"),
-    (128, 6, 4, 1, "multiple"),
-    (128, 4, 4, 2, "lanes"),
+@pytest.mark.parametrize("d,v_dim,hq,h,lanes,msg", [
+    (96, 96, 4, 4, 1, "head dim"),
+    (128, 128, 6, 4, 1, "multiple"),
+    (128, 128, 4, 4, 2, "lanes"),
+    (128, 64, 4, 4, 1, "value head dim"),
+    (64, 128, 4, 4, 1, "value head dim"),
 ])
-def test_fwd_rejects_bad_shapes_without_touching_gpu(d, hq, h, lanes, msg):
+def test_fwd_bwd_reject_bad_shapes_without_touching_gpu(d, v_dim, hq, h, lanes, msg):
     lib = _lib.lib()
     p = ctypes.c_void_p(1)
-    rc = lib.logo_sq_fwd(p, p, p, p, p, None, None, p, p, 128, 1, hq, h, d, lanes, 0.1, -1,
+    rc = lib.logo_sq_fwd(p, p, p, p, p, None, None, p, p, 128, 1, hq, h, d, v_dim, lanes, 0.1, -1,
                          _lib.DTYPE_BF16, None)
     assert rc == 1
     assert msg in lib.logo_last_error().decode()
+    for fn in (lib.logo_sq_bwd, lib.logo_sq_bwd_delta, lib.logo_sq_bwd_dq, lib.logo_sq_bwd_dkv):
+        rc = fn(p, p, p, p, p, p, p, p, p, p, p, p, None, None, p, p, 128, 1, hq, h, d, v_dim, lanes, 0.1, -1,
+                _lib.DTYPE_BF16, None)
+        assert rc == 1
+        assert msg in lib.logo_last_error().decode()
 
 
 def test_compact_rejects_bad_arguments():
@@ -78,3 +85,59 @@ def test_reference_assertions_are_kept():
     with pytest.raises(AssertionError, match="GQA"):
         sq_full_attn(torch.zeros(1, 8, 3, 64), k, k, torch.ones(1, 8, dtype=torch.bool),
                      cu_seqlens=torch.tensor([0, 8]))
+
+
+class _LaunchCounter:
+    def __init__(self):
+        self.n = 0
+
+    def __call__(self, name, when):
+        self.n += 1
+
+
+@pytest.mark.parametrize("qshape,kshape,vshape,msg", [
+    ((1, 8, 2, 128), (1, 8, 2, 128), (1, 8, 2, 192), "head dims K, V"),
+    ((1, 8, 2, 192), (1, 8, 2, 192), (1, 8, 2, 64), "head dims K, V"),
+    ((1, 8, 2, 320), (1, 8, 2, 320), (1, 8, 2, 64), "single block"),
+    ((1, 8, 2, 128), (1, 8, 2, 64), (1, 8, 2, 128), "same head dim K"),
+    ((1, 8, 4, 128), (1, 8, 2, 128), (1, 8, 1, 128), "same number of heads"),
+    ((1, 8, 2, 128), (1, 9, 2, 128), (1, 9, 2, 128), "share"),
+])
+def test_unsupported_shapes_are_rejected_before_any_launch(qshape, kshape, vshape, msg):
+    """AssertionError (the reference's error convention) before any launch and
+    before the GPU check, for every op that runs the attention kernels."""
+    import torch
+
+    from logo_amd.ops import dense_causal_attn, sq_full_attn, swa_attn
+
+    q, k, v = torch.zeros(qshape), torch.zeros(kshape), torch.zeros(vshape)
+    cu = torch.tensor([0, qshape[1]], dtype=torch.int32)
+    counter = _LaunchCounter()
+    _lib.set_launch_hook(counter)
+    try:
+        with pytest.raises(AssertionError, match=msg):
+            sq_full_attn(q, k, v, torch.ones(1, qshape[1], dtype=torch.bool), cu_seqlens=cu)
+        with pytest.raises(AssertionError, match=msg):
+            swa_attn(q, k, v, cu)
+        with pytest.raises(AssertionError, match=msg):
+            dense_causal_attn(q, k, v, cu)
+    finally:
+        _lib.set_launch_hook(None)
+    assert counter.n == 0
+
+
+@pytest.mark.parametrize("K,V,d", [(128, 128, 128), (64, 64, 64), (96, 96, 128), (128, 64, 128),
+                                   (64, 128, 128), (48, 32, 64), (1, 1, 64)])
+def test_supported_head_dims_map_to_a_compiled_dim(K, V, d):
+    """K, V <= 128 (V != K included) run on the compiled dim 64 or 128; the
+    GPU parity of the padded calls is in tests/test_gpu_sq_attn.py."""
+    import torch
+
+    from logo_amd.ops import sq_full_attn
+    from logo_amd.ops.sq_attn import kernel_head_dim
+
+    assert kernel_head_dim(K, V) == d
+    q, k, v = torch.zeros(1, 8, 2, K), torch.zeros(1, 8, 2, K), torch.zeros(1, 8, 2, V)
+    # shapes pass the checks; the CPU tensors then stop at the no-fallback guard
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        sq_full_attn(q, k, v, torch.ones(1, 8, dtype=torch.bool), cu_seqlens=torch.tensor([0, 8]))

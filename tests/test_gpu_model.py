@@ -121,3 +121,19 @@ def test_fused_decode_step_matches_unfused(gpu):
         err = (la.float() - lb.float()).abs().max().item()
         assert err <= 0.02 * lb.float().abs().max().item() + 1e-3
         tok = lb.argmax(-1)
+
+
+def test_second_prefill_rejected_and_reset_repeats_first(gpu):
+    """A prompt on top of cached tokens is refused (it would attend to its own
+    chunk only); after reset() the same prompt gives the same logits."""
+    m = _model(gpu, 0.5)
+    g = torch.Generator()
+    g.manual_seed(2)
+    ids = torch.randint(0, 512, (2, 150), generator=g).to(gpu)
+    cache = m.new_cache(2, 300, device=gpu)
+    first = m.prefill(ids, cache)
+    with pytest.raises(ValueError, match="already holds"):
+        m.prefill(ids, cache)
+    cache.reset()
+    again = m.prefill(ids, cache)
+    assert torch.equal(first, again)

@@ -139,18 +139,50 @@ def test_swa_fwd_bwd_matches_oracle(gpu, window):
 
 
 def test_noncontiguous_and_fp32_inputs(gpu):
-    n, hq, d = 256, 2, 64
+    """fp32 inputs (cfg1's dtype) compute in bf16 with fp32 accumulation; the
+    result is compared with the oracle fed the *unrounded* fp32 inputs, at
+    the north-star tolerance (max-abs 2e-2, mean-abs 2e-3), for the output
+    and all three gradients."""
+    n, hq, d = 512, 4, 64
     g = gen(9)
-    base = randn((n, d, hq), g).float()
+    base = torch.randn(n, d, hq, generator=g)
     q = base.transpose(1, 2)  # non-contiguous view [n, hq, d]
-    k = randn((n, hq, d), g).float()
-    v = randn((n, hq, d), g).float()
+    k = torch.randn(n, hq, d, generator=g)
+    v = torch.randn(n, hq, d, generator=g)
+    do = torch.randn(n, hq, d, generator=g)
     sel = torch.rand(n, generator=g) < 0.5
     cu = torch.tensor([0, n], dtype=torch.int32)
-    o = sq_full_attn(q[None].to(gpu), k[None].to(gpu), v[None].to(gpu), sel[None].to(gpu), cu_seqlens=cu.to(gpu))
-    assert o.dtype == torch.float32
-    ro, _ = _oracle(q.bfloat16(), k.bfloat16(), v.bfloat16(), sel, cu)
-    assert_within("o", o[0], ro)
+    o, (dq, dk, dv) = _run(q, k, v, sel, cu, gpu, do)
+    assert o.dtype == dq.dtype == dk.dtype == dv.dtype == torch.float32
+    ro, (rdq, rdk, rdv) = _oracle(q, k, v, sel, cu, do)
+    assert_within("o", o, ro)
+    assert_within("dq", dq, rdq)
+    assert_within("dk", dk, rdk)
+    assert_within("dv", dv, rdv)
+
+
+@pytest.mark.parametrize("K,V,hq,h", [(128, 64, 4, 2), (64, 128, 2, 2), (96, 96, 4, 4), (48, 32, 2, 1),
+                                      (80, 112, 2, 2)])
+def test_head_dims_off_the_compiled_set(gpu, K, V, hq, h):
+    """K, V <= 128 other than K = V in {64, 128} (V != K included) run on the
+    next compiled head dim with zero-padded q, k, v; outputs [.., V] and
+    gradients match the oracle (default scale K**-0.5) at the north-star
+    tolerance, and the unselected rows stay zero."""
+    n = 600
+    g = gen(70 + K + V)
+    q, k, v = randn((n, hq, K), g), randn((n, h, K), g), randn((n, h, V), g)
+    do = randn((n, hq, V), g)
+    sel = torch.rand(n, generator=g) < 0.4
+    cu = torch.tensor([0, 1, 250, 600], dtype=torch.int32)
+    print(f"head dims K={K} V={V} hq={hq} h={h}", flush=True)
+    o, (dq, dk, dv) = _run(q, k, v, sel, cu, gpu, do)
+    assert o.shape == (n, hq, V) and dq.shape == q.shape and dk.shape == k.shape and dv.shape == v.shape
+    ro, (rdq, rdk, rdv) = _oracle(q, k, v, sel, cu, do)
+    assert_within("o", o, ro)
+    assert_within("dq", dq, rdq)
+    assert_within("dk", dk, rdk)
+    assert_within("dv", dv, rdv)
+    assert torch.all(o[~sel.to(gpu)] == 0)
 
 
 def test_deterministic(gpu):

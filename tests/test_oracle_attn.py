@@ -173,3 +173,24 @@ def test_flops_formula_closed_form():
     T, H, D = 100, 3, 8
     f = attn.sq_flops_fwd(np.ones(T, bool), [0, T], H, D)
     assert f == 4 * D * H * T * (T + 1) // 2
+
+
+@pytest.mark.parametrize("K,V", [(8, 5), (6, 12)])
+def test_value_dim_differs_from_key_dim(K, V):
+    """V != K (the reference's V is its own constexpr, selected_full_attn.py:341):
+    forward and backward against the autograd reference, default scale K**-0.5."""
+    cu = [0, 11, 27]
+    rng = np.random.default_rng(40 + K)
+    q = rng.standard_normal((27, 4, K))
+    k = rng.standard_normal((27, 2, K))
+    v = rng.standard_normal((27, 2, V))
+    do = rng.standard_normal((27, 4, V))
+    sel = rng.random(27) < 0.6
+    o, _ = attn.sq_attn_fwd(q, k, v, sel, cu)
+    assert o.shape == (27, 4, V)
+    dq, dk, dv = attn.sq_attn_bwd(q, k, v, o, do, sel, cu)
+    ro, rdq, rdk, rdv = _autograd_ref(q, k, v, sel, cu, do, K ** -0.5)
+    np.testing.assert_allclose(o, ro, rtol=1e-10, atol=1e-12)
+    np.testing.assert_allclose(dq, rdq, rtol=1e-9, atol=1e-11)
+    np.testing.assert_allclose(dk, rdk, rtol=1e-9, atol=1e-11)
+    np.testing.assert_allclose(dv, rdv, rtol=1e-9, atol=1e-11)
