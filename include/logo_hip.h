@@ -68,6 +68,22 @@ int logo_compact(const uint8_t* selection, int64_t n_tokens, int lanes,
                  int32_t* meta, void* workspace, void* stream);
 
 /*
+ * logo_compact without the workspace argument: no counterpart in the
+ * reference.  For callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops).  The per-chunk counts go to a
+ * fixed device array of LOGO_COMPACT_SCRATCH_INTS int32 (256 KB, held by each
+ * GPU the library runs on until the process ends), so lanes *
+ * ceil(n_tokens / 4096) must not exceed it (LOGO_EINVAL otherwise, e.g. up to
+ * 16.7M tokens with 16 lanes).  Every call on one GPU shares that array:
+ * calls that overlap on one GPU (different streams, or threads) race.
+ * Outputs and their meaning are those of logo_compact.
+ */
+#define LOGO_COMPACT_SCRATCH_INTS 65536
+int logo_compact_noalloc(const uint8_t* selection, int64_t n_tokens, int lanes,
+                         const int32_t* cu, int nseq, int64_t* q_idx, int32_t* pos,
+                         int32_t* meta, void* stream);
+
+/*
  * Metadata for dense attention over every row (cu_q = cu, Sq = N), used by
  * the sliding-window branch and the all-ones ("flash") global branch
  * (logo/layers/utils.py:107-234, logo/ops/dense_full_attn.py:12-22).

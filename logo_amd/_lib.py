@@ -30,6 +30,7 @@ SIGNATURES = {
     "logo_abi_version": ([], _I),
     "logo_compact_workspace_bytes": ([_I64, _I], _SZ),
     "logo_compact": ([_P, _I64, _I, _P, _I, _P, _P, _P, _P, _P], _I),
+    "logo_compact_noalloc": ([_P, _I64, _I, _P, _I, _P, _P, _P, _P], _I),
     "logo_dense_meta": ([_P, _I, _I64, _P, _P], _I),
     "logo_chunk_indices": ([_P, _I, _I, _P, _I64, _P, _P, _P], _I),
     "logo_q_start_blk": ([_P, _P, _P, _P, _I64, _I, _P, _P], _I),

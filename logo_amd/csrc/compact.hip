@@ -10,6 +10,8 @@
 //   count    : per 4096-token chunk and lane, popcount of wave ballots
 //   scatter  : chunk prefix + wave prefix (LDS) + mbcnt rank -> q_idx, pos
 //   finalize : Sq, cu_q by binary search over q_idx, tile prefixes by block scan
+#include <mutex>
+
 #include "capi.hpp"
 #include "common.hpp"
 
@@ -238,17 +240,10 @@ extern "C" size_t logo_compact_workspace_bytes(int64_t n_tokens, int lanes) {
   return (size_t)(nchunk > 0 ? nchunk : 1) * (size_t)(lanes > 0 ? lanes : 1) * sizeof(int32_t);
 }
 
-extern "C" int logo_compact(const uint8_t* selection, int64_t n_tokens, int lanes, const int32_t* cu,
-                            int nseq, int64_t* q_idx, int32_t* pos, int32_t* meta, void* workspace,
-                            void* stream) {
-  LOGO_REQUIRE(n_tokens >= 0 && n_tokens < (int64_t)1 << 31, "n_tokens out of range: %lld",
-               (long long)n_tokens);
-  LOGO_REQUIRE(lanes >= 1 && nseq >= 1, "lanes (%d) and nseq (%d) must be >= 1", lanes, nseq);
-  LOGO_REQUIRE(cu && meta && workspace, "null pointer argument");
-  LOGO_REQUIRE(n_tokens == 0 || (selection && q_idx && pos), "null selection/q_idx/pos");
-  hipStream_t st = as_stream(stream);
+static int compact_launch(const uint8_t* selection, int64_t n_tokens, int lanes, const int32_t* cu,
+                          int nseq, int64_t* q_idx, int32_t* pos, int32_t* meta, int32_t* counts,
+                          hipStream_t st) {
   const int nchunk = (int)((n_tokens + kChunk - 1) / kChunk);
-  int32_t* counts = static_cast<int32_t*>(workspace);
   if (nchunk > 0) {
     dim3 grid(nchunk, lanes);
     hipLaunchKernelGGL(compact_count, grid, dim3(256), 0, st, selection, n_tokens, lanes, counts, nchunk);
@@ -261,6 +256,68 @@ extern "C" int logo_compact(const uint8_t* selection, int64_t n_tokens, int lane
                      nchunk, q_idx, meta, 0);
   LOGO_LAUNCH_CHECK("compact_finalize");
   return LOGO_OK;
+}
+
+#define LOGO_COMPACT_CHECK_ARGS()                                                               \
+  LOGO_REQUIRE(n_tokens >= 0 && n_tokens < (int64_t)1 << 31, "n_tokens out of range: %lld",      \
+               (long long)n_tokens);                                                            \
+  LOGO_REQUIRE(lanes >= 1 && nseq >= 1, "lanes (%d) and nseq (%d) must be >= 1", lanes, nseq);  \
+  LOGO_REQUIRE(cu && meta, "null pointer argument");                                            \
+  LOGO_REQUIRE(n_tokens == 0 || (selection && q_idx && pos), "null selection/q_idx/pos")
+
+extern "C" int logo_compact(const uint8_t* selection, int64_t n_tokens, int lanes, const int32_t* cu,
+                            int nseq, int64_t* q_idx, int32_t* pos, int32_t* meta, void* workspace,
+                            void* stream) {
+  LOGO_COMPACT_CHECK_ARGS();
+  LOGO_REQUIRE(workspace, "null workspace");
+  return compact_launch(selection, n_tokens, lanes, cu, nseq, q_idx, pos, meta,
+                        static_cast<int32_t*>(workspace), as_stream(stream));
+}
+
+// ---------------------------------------------------------------------------
+// logo_compact without a workspace argument, for callers that cannot
+// allocate.  The per-chunk counts live in a file-scope device array; each
+// device holds its own copy at its own address, found once per device with
+// hipGetSymbolAddress (the array's name in host code is only a stand-in for
+// the symbol).  The counts are written in full by compact_count before any
+// kernel reads them, so nothing needs clearing between calls.
+// ---------------------------------------------------------------------------
+namespace logo {
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) int32_t scratch[LOGO_COMPACT_SCRATCH_INTS];
+static std::mutex g_scratch_mu;
+static int32_t* g_scratch_ptr[kMaxDevices];  // per device, set on the first call there
+
+// The scratch address on the current device (found on first use there).
+static int scratch_on_current_device(int32_t** out) {
+  int dev = -1;
+  LOGO_HIP_CHECK(hipGetDevice(&dev));
+  LOGO_REQUIRE(dev >= 0 && dev < kMaxDevices, "device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    LOGO_HIP_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    LOGO_REQUIRE(p != nullptr, "no device address for the compaction scratch");
+    g_scratch_ptr[dev] = static_cast<int32_t*>(p);
+  }
+  *out = g_scratch_ptr[dev];
+  return LOGO_OK;
+}
+}  // namespace logo
+
+extern "C" int logo_compact_noalloc(const uint8_t* selection, int64_t n_tokens, int lanes,
+                                    const int32_t* cu, int nseq, int64_t* q_idx, int32_t* pos,
+                                    int32_t* meta, void* stream) {
+  LOGO_COMPACT_CHECK_ARGS();
+  const int64_t need = (int64_t)lanes * ((n_tokens + kChunk - 1) / kChunk);
+  LOGO_REQUIRE(need <= LOGO_COMPACT_SCRATCH_INTS,
+               "logo_compact_noalloc: %lld tokens x %d lanes need %lld scratch counts, above its fixed %d "
+               "(use logo_compact with a workspace)",
+               (long long)n_tokens, lanes, (long long)need, LOGO_COMPACT_SCRATCH_INTS);
+  int32_t* counts = nullptr;
+  const int rc = scratch_on_current_device(&counts);
+  if (rc != LOGO_OK) return rc;
+  return compact_launch(selection, n_tokens, lanes, cu, nseq, q_idx, pos, meta, counts, as_stream(stream));
 }
 
 extern "C" int logo_dense_meta(const int32_t* cu, int nseq, int64_t n_tokens, int32_t* meta,
