@@ -73,6 +73,28 @@ __device__ __forceinline__ float max3_f32(float a, float b, float c) {
   return r;
 }
 
+// min(a, b, c) as one v_min3_f32 (see max3_f32).
+__device__ __forceinline__ float min3_f32(float a, float b, float c) {
+  float r;
+  asm volatile("v_min3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+
+__device__ __forceinline__ float pair_min(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fminf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+// Eight bf16 values times s, each rounded back to bf16 (the pre-scaled query
+// rows of the sparse path: the forward's registers and the backward's
+// compacted copies are made by this same rounding).
+__device__ __forceinline__ bf16x8 scale_bf16x8(const bf16x8 v, float s) {
+  bf16x8 r;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) r[e] = (bf16)((float)v[e] * s);
+  return r;
+}
+
 // Anchors a value at this point of the instruction stream (an empty asm
 // statement that reads and rewrites it): arithmetic on it cannot be hoisted
 // above, nor its producer sunk below, this point.  Used with scheduling

@@ -1,0 +1,171 @@
+// Shared declarations of the query-sparse attention kernels (gfx950): the
+// argument block, the compacted-row views, the per-workgroup query tile and
+// the per-phase launch entry points (one translation unit per kernel).
+#pragma once
+
+#include <math.h>
+
+#include <type_traits>
+
+#include "capi.hpp"
+#include "common.hpp"
+
+namespace logo {
+
+struct AttnArgs {
+  const bf16* q;
+  const bf16* k;
+  const bf16* v;
+  bf16* o;
+  float* lse;
+  const bf16* dout;
+  float* delta;
+  bf16* dq;
+  bf16* dk;
+  bf16* dv;
+  bf16* q_sel;   // [HQ, N, D] compacted q rows (sparse backward)
+  bf16* do_sel;  // [HQ, N, D] compacted dO rows (sparse backward)
+  const int64_t* q_idx;
+  const int32_t* pos;
+  const int32_t* meta;
+  const int32_t* cu;
+  int64_t n;
+  int nseq;
+  int hq;
+  int h;
+  int g;
+  int lanes;
+  int meta_stride;
+  float scale;
+  float scale_log2;
+  int window;
+};
+
+// Per-lane view of the compaction metadata.
+template <bool SPARSE>
+struct RowView {
+  const int64_t* qi;
+  const int32_t* ps;
+  int bos;
+  __device__ __forceinline__ int64_t token(int r) const { return SPARSE ? qi[r] : (int64_t)r; }
+  __device__ __forceinline__ int posn(int r) const { return SPARSE ? ps[r] : r - bos; }
+};
+
+template <bool SPARSE>
+__device__ __forceinline__ RowView<SPARSE> row_view(const AttnArgs& a, int lane_sel, int bos) {
+  RowView<SPARSE> v;
+  v.qi = SPARSE ? a.q_idx + (int64_t)lane_sel * a.n : nullptr;
+  v.ps = SPARSE ? a.pos + (int64_t)lane_sel * a.n : nullptr;
+  v.bos = bos;
+  return v;
+}
+
+// Query-side rows (q or dO) of head hq as the backward reads them: compacted
+// head-major copies [HQ, N, D] in sparse mode, the [N, HQ, D] inputs in dense
+// mode (where the compacted row index is the token).
+template <int D, bool SPARSE>
+struct QSide {
+  const bf16* base;
+  int64_t stride;
+  __device__ __forceinline__ QSide(const AttnArgs& a, const bf16* sel_buf, const bf16* full, int hq) {
+    base = SPARSE ? sel_buf + (int64_t)hq * a.n * D : full + (int64_t)hq * D;
+    stride = SPARSE ? (int64_t)D : (int64_t)a.hq * D;
+  }
+  __device__ __forceinline__ const bf16* row(int r) const { return base + (int64_t)r * stride; }
+};
+
+// Waves per SIMD each kernel is compiled for (caps VGPRs at 512 / waves).
+#ifndef LOGO_OCC_FWD
+#define LOGO_OCC_FWD __attribute__((amdgpu_waves_per_eu(2, 2)))
+#endif
+#ifndef LOGO_OCC_DQ64
+#define LOGO_OCC_DQ64 __attribute__((amdgpu_waves_per_eu(1, 1)))
+#endif
+#ifndef LOGO_OCC_DKV
+#define LOGO_OCC_DKV __attribute__((amdgpu_waves_per_eu(1, 1)))
+#endif
+
+extern __shared__ __attribute__((aligned(16))) char logo_smem[];
+__device__ __forceinline__ bf16* dyn_smem() { return reinterpret_cast<bf16*>(logo_smem); }
+
+
+// Shared front matter of the fwd and dq kernels: which compacted rows this
+// workgroup and this lane own.  Returns false for a workgroup past the last
+// tile (the grid is sized for the worst case).
+template <bool SPARSE>
+struct QTile {
+  int hq, h, lane_sel, s, r0, r_end, bos, seqlen;
+  int pmin, pmax, r, p, kv_lo, kv_hi;
+  bool wave_active, valid;
+  int64_t t;
+  RowView<SPARSE> rv;
+
+  // rpw: compacted rows per wave (32 or 64); r / t / p / valid describe the
+  // lane's row in the wave's first 32-row block (row_at gives the others).
+  // paired: the workgroup takes two consecutive kBQ-row tiles (a single
+  // segment only, nseq == 1, so both tiles share one key range).
+  __device__ __forceinline__ bool init(const AttnArgs& a, int wave, int i, bool window, int rpw = 32,
+                                       bool paired = false) {
+    int rank;
+    xcd_remap(blockIdx.x, a.hq, rank, hq);
+    lane_sel = a.lanes > 1 ? hq : 0;
+    const int32_t* meta = a.meta + (int64_t)lane_sel * a.meta_stride;
+    const int nt = paired ? (meta[1] + 1) >> 1 : meta[1];
+    if (rank >= nt) return false;
+    const int tile = nt - 1 - rank;  // heaviest (latest) blocks first
+    const int32_t* cu_q = meta + kMetaHdr;
+    const int32_t* cu_tq = cu_q + (a.nseq + 1);
+    if (paired) {
+      s = 0;
+      r0 = cu_q[0] + tile * 2 * kBQ;
+      r_end = min(r0 + 2 * kBQ, cu_q[1]);
+    } else {
+      s = seg_of(cu_tq, a.nseq, tile);
+      r0 = cu_q[s] + (tile - cu_tq[s]) * kBQ;
+      r_end = min(r0 + kBQ, cu_q[s + 1]);
+    }
+    bos = a.cu[s];
+    seqlen = a.cu[s + 1] - bos;
+    h = hq / a.g;
+    rv = row_view<SPARSE>(a, lane_sel, bos);
+    const int rw0 = r0 + rpw * wave;
+    wave_active = rw0 < r_end;
+    pmin = wave_active ? rv.posn(rw0) : 0;
+    pmax = wave_active ? rv.posn(min(rw0 + rpw - 1, r_end - 1)) : -1;
+    r = rw0 + i;
+    valid = r < r_end;
+    t = valid ? rv.token(r) : 0;
+    p = valid ? rv.posn(r) : -1;
+    kv_lo = window ? (max(0, rv.posn(r0) - a.window) & ~63) : 0;
+    kv_hi = rv.posn(r_end - 1) + 1;
+    return true;
+  }
+};
+
+// ---------------------------------------------------------------------------
+// Forward
+// ---------------------------------------------------------------------------
+template <int B>
+using BufTag = std::integral_constant<int, B>;
+
+template <typename K>
+static inline hipError_t allow_smem(K kernel, size_t bytes) {
+  return hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+}
+
+// Per-phase launchers (d = 64 or 128; sparse: compacted rows; window: a
+// sliding window is set).  Each returns LOGO_OK or an error code.
+int sq_launch_fwd(const AttnArgs& a, hipStream_t st, int d, bool sparse, bool window);
+int sq_launch_delta(const AttnArgs& a, hipStream_t st, int d, bool sparse);
+int sq_launch_dq(const AttnArgs& a, hipStream_t st, int d, bool sparse, bool window);
+int sq_launch_dkv(const AttnArgs& a, hipStream_t st, int d, bool sparse, bool window);
+
+// Calls FN<D, SPARSE, WINDOW>(a, st) for the runtime (d, sparse, window).
+#define LOGO_DISPATCH(FN, a, st, d, sparse, window)                                                  \
+  ((d) == 128 ? ((sparse) ? ((window) ? FN<128, true, true>(a, st) : FN<128, true, false>(a, st))   \
+                          : ((window) ? FN<128, false, true>(a, st) : FN<128, false, false>(a, st))) \
+              : ((sparse) ? ((window) ? FN<64, true, true>(a, st) : FN<64, true, false>(a, st))     \
+                          : ((window) ? FN<64, false, true>(a, st) : FN<64, false, false>(a, st))))
+
+}  // namespace logo

@@ -1,0 +1,270 @@
+// Query-sparse causal attention forward for gfx950 (logo/ops/selected_full_attn.py:33-121,
+// :340-362): compacted query rows gathered in the kernel, K / V streamed
+// through LDS, online softmax in the exp2 domain, o rows scattered in place.
+#include "sq_attn.hpp"
+
+namespace logo {
+
+// ---------------------------------------------------------------------------
+// Forward, software-pipelined inside each wave
+// ---------------------------------------------------------------------------
+// Iteration t of the workgroup loop (t = -1 .. nt - 1; key tile t starts at
+// kv_lo + 64 t) runs two phases of MFMA slots on every wave:
+//   X: the S^T MFMAs of tile t + 1 (K(t+1) rows from LDS), while the VALU turns
+//      S(t) into P(t) = exp2(S c - base), sums it and packs it to bf16;
+//   Y: the O += V(t)^T P(t) MFMAs, while the VALU masks S(t+1) and takes its
+//      row max.
+// The row statistics of tile t + 1 (new reference max, rescale of O and l)
+// follow Y.  K therefore runs one tile ahead of V: iteration t reads K(t+1)
+// from K slot (t+1)&1 and V(t) from V slot t&1, and loads K(t+2) into K slot
+// t&1 and V(t+1) into V slot (t+1)&1, both last read in iteration t - 1.
+// Each wave only works on the tiles its own rows can see ([tw_lo, tw_hi));
+// outside them it still copies its share of the tiles and meets the barriers.
+// NW waves x 32 rows per workgroup (kBQ = 128 rows, or two tiles with 8
+// waves), two waves per SIMD.
+//
+// Online softmax with a lazy rescale: the reference max of a row moves only
+// when the row's max grew by more than 2^8 in the exp2 domain (or on its first
+// visible key), so O and l are rarely rescaled and P <= 2^8 stays exact.
+// Masks compare a compile-time offset per accumulator item with one per-lane
+// bound: key j0 + 32 kk + rowmap(g, jj) is visible iff its offset from
+// j0 + 4 g lies in [hi - W, hi], hi = p - j0 - 4 g.
+template <int D, bool SPARSE, bool WINDOW, int NW>
+__global__ __launch_bounds__(64 * NW) LOGO_OCC_FWD void sq_fwd_pipe_kernel(const AttnArgs a) {
+  constexpr int DS = D / 16, DT = D / 32;
+  constexpr int NX = 2 * DS;   // S MFMAs per tile (two 32-key halves x DS k-steps)
+  constexpr int NY = 4 * DT;   // PV MFMAs per tile (DT column blocks x 4 key steps)
+  constexpr int IX = 32 / NX;  // softmax items per X slot
+  constexpr int IY = 32 / NY;  // mask / max items per Y slot
+  constexpr int PF = 4;        // operand prefetch distance, in slots
+  using GT = TileGeom<D, kSwz>;
+  bf16* const smem = dyn_smem();
+  auto tileK = [&](int b) { return smem + b * GT::ELEMS; };
+  auto tileV = [&](int b) { return smem + 2 * GT::ELEMS + b * GT::ELEMS; };
+
+  const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63, i = l & 31, g = l >> 5;
+  QTile<SPARSE> qt;
+  if (!qt.init(a, wave, i, WINDOW, 32, NW == 8)) return;
+  const int hq = qt.hq, p = qt.p, W = a.window;
+
+  // Sparse mode holds q pre-scaled and negated, bf16(-c q) with
+  // c = scale * log2(e), the same rounding as the backward's compacted copies:
+  // S' = -c q.k, so the forward's LSE and the backward's recomputed P come
+  // from identical products.  Scores are then in the exp2 domain already,
+  // masked scores are +inf and the row statistic is a minimum.
+  constexpr bool NEG = SPARSE;
+  bf16x8 qreg[DS];
+  {
+    const bf16* qrow = a.q + (qt.t * a.hq + hq) * D + 8 * g;
+#pragma unroll
+    for (int ds = 0; ds < DS; ++ds) {
+      const bf16x8 qv = qt.valid ? *reinterpret_cast<const bf16x8*>(qrow + 16 * ds) : bf16x8{};
+      qreg[ds] = NEG ? scale_bf16x8(qv, -a.scale_log2) : qv;
+    }
+  }
+
+  f32x16 oacc[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) oacc[dt] = f32x16{};
+  f32x16 sbuf[2][2];  // [t & 1][32-key half]: S of the current and the next tile
+  bf16x8 pb[4];       // P(t) as the B operand of PV, one per 16-key step
+  float m_run = -INFINITY, l_run = 0.f, base = 0.f;  // m_run: running row max of c s
+  const float c = a.scale_log2;
+
+  TileReader<D, kSwz> rd;  // K read along rows, V transposed
+  rd.init();
+  const int64_t rstride = (int64_t)a.h * D;
+  const bf16* kbase = a.k + ((int64_t)qt.bos * a.h + qt.h) * D;
+  const bf16* vbase = a.v + ((int64_t)qt.bos * a.h + qt.h) * D;
+  const int seqlen = qt.seqlen;
+  TileBufDma<D, NW> dma;
+  dma.init((int)rstride);
+  // rows past the sequence end are clamped to its last key (masked: p < seqlen)
+  auto load_one = [&](bf16* tile, const bf16* src, int j0) {
+    if (j0 + 64 <= seqlen) dma.issue(tile, src + j0 * rstride);
+    else dma.issue_clamped(tile, src + j0 * rstride, seqlen - 1 - j0);
+  };
+
+  const int kv_lo = qt.kv_lo;
+  const int nt = (qt.kv_hi - kv_lo + 63) >> 6;
+  int tw_lo = 0, tw_hi = 0;  // tiles this wave's rows can see
+  if (qt.wave_active) {
+    tw_hi = ((qt.pmax - kv_lo) >> 6) + 1;
+    tw_lo = WINDOW ? (max(0, qt.pmin - W - kv_lo) >> 6) : 0;
+  }
+
+  auto step = [&](auto par_tag, int t) {
+    constexpr int PAR = decltype(par_tag)::value;  // t & 1
+    if (t + 2 < nt) load_one(tileK(PAR), kbase, kv_lo + 64 * (t + 2));
+    if (t + 1 < nt) load_one(tileV(PAR ^ 1), vbase, kv_lo + 64 * (t + 1));
+    const bf16* kb = tileK(PAR ^ 1);
+    const bf16* vb = tileV(PAR);
+    const int j0n = kv_lo + 64 * (t + 1);
+
+    auto body = [&](auto dos_tag, auto dopv_tag, auto mask_tag) {
+      constexpr bool DOS = decltype(dos_tag)::value;    // S(t+1) and its statistics
+      constexpr bool DOPV = decltype(dopv_tag)::value;  // P(t) and O += V^T P
+      constexpr bool MASK = decltype(mask_tag)::value;  // S(t+1) crosses a mask edge
+      // slot s < NX: K row operand (half s / DS, k-step s % DS);
+      // slot s >= NX: V^T operand (column block (s - NX) / 4, key step (s - NX) % 4)
+      bf16x8 op[NX + NY];
+      auto load_op = [&](auto s_c) {
+        constexpr int S = decltype(s_c)::value;
+        if constexpr (S < NX) {
+          if constexpr (DOS) op[S] = rd.row(kb, 32 * (S / DS), S % DS);
+        } else {
+          if constexpr (DOPV) op[S] = rd.tr(vb, 16 * ((S - NX) % 4), (S - NX) / 4);
+        }
+      };
+      static_for<PF>([&](auto s_c) { load_op(s_c); });
+      const int hi = p - j0n - 4 * g;  // mask bound of S(t+1) items
+      float mx = NEG ? INFINITY : -INFINITY, psum = 0.f;
+      static_for<NX + NY>([&](auto s_c) {
+        constexpr int S = decltype(s_c)::value;
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (S < NX) {
+          if constexpr (DOS) {
+            constexpr int KK = S / DS, DSI = S % DS;
+            bf16x8 o = op[S];
+            pin(o);
+            sbuf[PAR ^ 1][KK] = mfma32(o, qreg[DSI], DSI == 0 ? f32x16{} : sbuf[PAR ^ 1][KK]);
+          }
+          if constexpr (DOPV) {
+            static_for<IX>([&](auto e_c) {
+              constexpr int IT = S * IX + decltype(e_c)::value;
+              constexpr int KK = IT / 16, JJ = IT % 16;
+              float sv = sbuf[PAR][KK][JJ];
+              pin(sv);
+              float pv = NEG ? fast_exp2(-(sv + base)) : fast_exp2(fmaf(sv, c, -base));
+              pin(pv);
+              sbuf[PAR][KK][JJ] = pv;
+              psum += pv;
+              pin(psum);
+              if constexpr (IT % 8 == 7) pb[IT / 8] = acc_to_bf16(sbuf[PAR][IT / 16], (IT / 8) & 1);
+            });
+          }
+        } else {
+          constexpr int Y = S - NX;
+          if constexpr (DOPV) {
+            bf16x8 o = op[S];
+            pin(o);
+            oacc[Y / 4] = mfma32(o, pb[Y % 4], oacc[Y / 4]);
+          }
+          if constexpr (DOS) {
+            float sv[IY];
+            static_for<IY>([&](auto e_c) {
+              constexpr int E = decltype(e_c)::value, IT = Y * IY + E;
+              constexpr int KK = IT / 16, JJ = IT % 16;
+              sv[E] = sbuf[PAR ^ 1][KK][JJ];
+              // the masked path rewrites S, so it anchors its value here; the
+              // unmasked path only reads it (the max3 asm keeps the order),
+              // and an anchor would force a copy of every score
+              if constexpr (MASK) pin(sv[E]);
+              if constexpr (MASK) {
+                constexpr int off = 32 * KK + 8 * (JJ / 4) + (JJ % 4);
+                bool vis = off <= hi;
+                if (WINDOW) vis = vis && off >= hi - W;
+                if (!vis) sv[E] = NEG ? INFINITY : -INFINITY;
+                sbuf[PAR ^ 1][KK][JJ] = sv[E];
+              }
+            });
+#pragma unroll
+            for (int e = 0; e < IY; e += 2)
+              mx = NEG ? min3_f32(mx, sv[e], sv[e + 1]) : max3_f32(mx, sv[e], sv[e + 1]);
+          }
+        }
+        if constexpr (S + PF < NX + NY) load_op(std::integral_constant<int, S + PF>{});
+      });
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (DOPV) l_run += psum;
+      if constexpr (DOS) {
+        const float mxs = NEG ? -pair_min(mx) : pair_max(mx) * c;  // tile max of c s
+        const bool grow = mxs - m_run > 8.f;
+        const float m_new = __ballot(grow) ? fmaxf(m_run, mxs) : m_run;
+        const float nbase = (m_new == -INFINITY) ? 0.f : m_new;
+        const float alpha = fast_exp2(m_run - nbase);
+        l_run *= alpha;
+        m_run = m_new;
+        base = nbase;
+        if (__ballot(alpha != 1.f)) {
+#pragma unroll
+          for (int dt = 0; dt < DT; ++dt) oacc[dt] *= alpha;
+        }
+      }
+    };
+    using T_ = std::true_type;
+    using F_ = std::false_type;
+    const bool doS = t + 1 >= tw_lo && t + 1 < tw_hi;
+    const bool doPV = t >= tw_lo && t < tw_hi;
+    const bool maskn = (j0n + 63 > qt.pmin) || (WINDOW && j0n < qt.pmax - W);
+    if (doS && doPV) {
+      if (maskn) body(T_{}, T_{}, T_{});
+      else body(T_{}, T_{}, F_{});
+    } else if (doS) {
+      body(T_{}, F_{}, T_{});
+    } else if (doPV) {
+      body(F_{}, T_{}, F_{});
+    }
+    wait_vmem();
+    __syncthreads();
+  };
+
+  load_one(tileK(0), kbase, kv_lo);
+  wait_vmem();
+  __syncthreads();
+  for (int t = -1; t < nt; t += 2) {
+    step(BufTag<1>{}, t);
+    if (t + 1 < nt) step(BufTag<0>{}, t + 1);
+  }
+
+  const float l_tot = pair_sum(l_run);
+  if (qt.valid) {
+    const float inv = 1.f / l_tot;
+    bf16* orow = a.o + (qt.t * a.hq + hq) * D;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        bf16x4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = (bf16)(oacc[dt][4 * q4 + e] * inv);
+        *reinterpret_cast<bf16x4*>(orow + 32 * dt + 8 * q4 + 4 * g) = v;
+      }
+    if (g == 0) a.lse[(int64_t)hq * a.n + qt.r] = m_run + log2f(l_tot);
+  }
+}
+
+template <int D>
+constexpr size_t fwd_smem() { return (size_t)4 * TileGeom<D, kSwz>::ELEMS * sizeof(bf16); }
+
+// Single long sequences take 8-wave workgroups of two query tiles, which
+// share each K / V tile copy between 256 rows (half the copy traffic and
+// issue per row); packed or short inputs keep 4-wave single-tile workgroups,
+// which give more workgroups where rows are few.
+constexpr int64_t kFwdPairMinTokens = 16384;
+
+template <int D, bool SPARSE, bool WINDOW>
+static int launch_fwd(const AttnArgs& a, hipStream_t st) {
+  const bool paired = a.nseq == 1 && a.n >= kFwdPairMinTokens;
+  const int64_t rows = paired ? 2 * kBQ : kBQ;
+  const int64_t ntmax = (a.n + rows - 1) / rows + a.nseq;
+  const int64_t nblk = ntmax * a.hq;
+  LOGO_REQUIRE(nblk < ((int64_t)1 << 31), "grid too large");
+  if (paired) {
+    auto kern = sq_fwd_pipe_kernel<D, SPARSE, WINDOW, 8>;
+    LOGO_HIP_CHECK(allow_smem(kern, fwd_smem<D>()));
+    hipLaunchKernelGGL(kern, dim3((unsigned)nblk), dim3(512), fwd_smem<D>(), st, a);
+  } else {
+    auto kern = sq_fwd_pipe_kernel<D, SPARSE, WINDOW, 4>;
+    LOGO_HIP_CHECK(allow_smem(kern, fwd_smem<D>()));
+    hipLaunchKernelGGL(kern, dim3((unsigned)nblk), dim3(256), fwd_smem<D>(), st, a);
+  }
+  LOGO_LAUNCH_CHECK("sq_fwd_pipe_kernel");
+  return LOGO_OK;
+}
+
+int sq_launch_fwd(const AttnArgs& a, hipStream_t st, int d, bool sparse, bool window) {
+  return LOGO_DISPATCH(launch_fwd, a, st, d, sparse, window);
+}
+
+}  // namespace logo
