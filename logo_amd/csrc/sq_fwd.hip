@@ -11,9 +11,11 @@ namespace logo {
 // Iteration t of the workgroup loop (t = -1 .. nt - 1; key tile t starts at
 // kv_lo + 64 t) runs two phases of MFMA slots on every wave:
 //   X: the S^T MFMAs of tile t + 1 (K(t+1) rows from LDS), while the VALU turns
-//      S(t) into P(t) = exp2(S c - base), sums it and packs it to bf16;
-//   Y: the O += V(t)^T P(t) MFMAs, while the VALU masks S(t+1) and takes its
-//      row max.
+//      the first part of S(t) into P(t) = exp2(S c - base), sums it and packs
+//      it to bf16;
+//   Y: the O += V(t)^T P(t) MFMAs, key step by key step, while the VALU
+//      finishes P(t) ahead of the key steps that read it, masks S(t+1) and
+//      takes its row max.
 // The row statistics of tile t + 1 (new reference max, rescale of O and l)
 // follow Y.  K therefore runs one tile ahead of V: iteration t reads K(t+1)
 // from K slot (t+1)&1 and V(t) from V slot t&1, and loads K(t+2) into K slot
@@ -34,8 +36,15 @@ __global__ __launch_bounds__(64 * NW) LOGO_OCC_FWD void sq_fwd_pipe_kernel(const
   constexpr int DS = D / 16, DT = D / 32;
   constexpr int NX = 2 * DS;   // S MFMAs per tile (two 32-key halves x DS k-steps)
   constexpr int NY = 4 * DT;   // PV MFMAs per tile (DT column blocks x 4 key steps)
-  constexpr int IX = 32 / NX;  // softmax items per X slot
   constexpr int IY = 32 / NY;  // mask / max items per Y slot
+  // The 32 P items of a tile (per lane) are spread evenly over the X slots and
+  // the first three quarters of Y: PV runs key-step major (Y slot y: key step
+  // y / DT, column block y % DT), so pb[k] is first read at Y slot DT k, and
+  // the softmax work is split between both phases instead of crowding X.
+  constexpr int NPS = NX + 3 * DT;  // slots that carry P items
+  constexpr auto pslot = [](int it) constexpr { return it * NPS / 32; };
+  static_assert(pslot(7) < NX && pslot(15) < NX + DT && pslot(23) < NX + 2 * DT && pslot(31) < NX + 3 * DT,
+                "each group of eight P items is packed before its PV MFMAs");
   constexpr int PF = 4;        // operand prefetch distance, in slots
   using GT = TileGeom<D, kSwz>;
   bf16* const smem = dyn_smem();
@@ -106,14 +115,14 @@ __global__ __launch_bounds__(64 * NW) LOGO_OCC_FWD void sq_fwd_pipe_kernel(const
       constexpr bool DOPV = decltype(dopv_tag)::value;  // P(t) and O += V^T P
       constexpr bool MASK = decltype(mask_tag)::value;  // S(t+1) crosses a mask edge
       // slot s < NX: K row operand (half s / DS, k-step s % DS);
-      // slot s >= NX: V^T operand (column block (s - NX) / 4, key step (s - NX) % 4)
+      // slot s >= NX: V^T operand (key step (s - NX) / DT, column block (s - NX) % DT)
       bf16x8 op[NX + NY];
       auto load_op = [&](auto s_c) {
         constexpr int S = decltype(s_c)::value;
         if constexpr (S < NX) {
           if constexpr (DOS) op[S] = rd.row(kb, 32 * (S / DS), S % DS);
         } else {
-          if constexpr (DOPV) op[S] = rd.tr(vb, 16 * ((S - NX) % 4), (S - NX) / 4);
+          if constexpr (DOPV) op[S] = rd.tr(vb, 16 * ((S - NX) / DT), (S - NX) % DT);
         }
       };
       static_for<PF>([&](auto s_c) { load_op(s_c); });
@@ -129,26 +138,12 @@ __global__ __launch_bounds__(64 * NW) LOGO_OCC_FWD void sq_fwd_pipe_kernel(const
             pin(o);
             sbuf[PAR ^ 1][KK] = mfma32(o, qreg[DSI], DSI == 0 ? f32x16{} : sbuf[PAR ^ 1][KK]);
           }
-          if constexpr (DOPV) {
-            static_for<IX>([&](auto e_c) {
-              constexpr int IT = S * IX + decltype(e_c)::value;
-              constexpr int KK = IT / 16, JJ = IT % 16;
-              float sv = sbuf[PAR][KK][JJ];
-              pin(sv);
-              float pv = NEG ? fast_exp2(-(sv + base)) : fast_exp2(fmaf(sv, c, -base));
-              pin(pv);
-              sbuf[PAR][KK][JJ] = pv;
-              psum += pv;
-              pin(psum);
-              if constexpr (IT % 8 == 7) pb[IT / 8] = acc_to_bf16(sbuf[PAR][IT / 16], (IT / 8) & 1);
-            });
-          }
         } else {
           constexpr int Y = S - NX;
           if constexpr (DOPV) {
             bf16x8 o = op[S];
             pin(o);
-            oacc[Y / 4] = mfma32(o, pb[Y % 4], oacc[Y / 4]);
+            oacc[Y % DT] = mfma32(o, pb[Y / DT], oacc[Y % DT]);
           }
           if constexpr (DOS) {
             float sv[IY];
@@ -172,6 +167,23 @@ __global__ __launch_bounds__(64 * NW) LOGO_OCC_FWD void sq_fwd_pipe_kernel(const
             for (int e = 0; e < IY; e += 2)
               mx = NEG ? min3_f32(mx, sv[e], sv[e + 1]) : max3_f32(mx, sv[e], sv[e + 1]);
           }
+        }
+        // P(t) items assigned to this slot (X or Y)
+        if constexpr (DOPV) {
+          static_for<32>([&](auto it_c) {
+            constexpr int IT = decltype(it_c)::value;
+            if constexpr (pslot(IT) == S) {
+              constexpr int KK = IT / 16, JJ = IT % 16;
+              float sv = sbuf[PAR][KK][JJ];
+              pin(sv);
+              float pv = NEG ? fast_exp2(-(sv + base)) : fast_exp2(fmaf(sv, c, -base));
+              pin(pv);
+              sbuf[PAR][KK][JJ] = pv;
+              psum += pv;
+              pin(psum);
+              if constexpr (IT % 8 == 7) pb[IT / 8] = acc_to_bf16(sbuf[PAR][IT / 16], (IT / 8) & 1);
+            }
+          });
         }
         if constexpr (S + PF < NX + NY) load_op(std::integral_constant<int, S + PF>{});
       });
