@@ -244,10 +244,14 @@ struct TileBufDma {
                                              64 * row_stride * (int)sizeof(bf16), kBufRsrcWord3);
   }
 
+  // The wave index as a scalar: the LDS destination of each copy (M0) is then
+  // scalar arithmetic instead of a per-copy readfirstlane of a vector value.
+  __device__ __forceinline__ static int wave_s() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
+
   // Rows row0 .. row0 + 63, all valid.
   __device__ __forceinline__ void issue(bf16* tile, const bf16* row0) const {
     const auto r = rsrc(row0);
-    const int wave = threadIdx.x >> 6;
+    const int wave = wave_s();
 #pragma unroll
     for (int b = 0; b < BLOCKS; ++b) {
       const int rb = RPW * wave + RPB * b;
@@ -258,7 +262,7 @@ struct TileBufDma {
   // Rows past last_row (< 63) are clamped to it.
   __device__ __forceinline__ void issue_clamped(bf16* tile, const bf16* row0, int last_row) const {
     const auto r = rsrc(row0);
-    const int wave = threadIdx.x >> 6, j = threadIdx.x & 63;
+    const int wave = wave_s(), j = threadIdx.x & 63;
 #pragma unroll
     for (int b = 0; b < BLOCKS; ++b) {
       const int rb = RPW * wave + RPB * b;
