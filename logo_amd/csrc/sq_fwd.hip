@@ -78,6 +78,10 @@ __global__ __launch_bounds__(64 * NW) LOGO_OCC_FWD void sq_fwd_pipe_kernel(const
   f32x16 sbuf[2][2];  // [t & 1][32-key half]: S of the current and the next tile
   bf16x8 pb[4];       // P(t) as the B operand of PV, one per 16-key step
   float m_run = -INFINITY, l_run = 0.f, base = 0.f;  // m_run: running row max of c s
+  // NEG: the S' accumulators start from the row's current base (a splat C
+  // operand), so they hold S' + base and P = exp2(-acc) needs no add; when a
+  // tile moves the base, its accumulators are shifted once by the difference.
+  f32x16 cbase = f32x16{};
   const float c = a.scale_log2;
 
   TileReader<D, kSwz> rd;  // K read along rows, V transposed
@@ -136,7 +140,7 @@ __global__ __launch_bounds__(64 * NW) LOGO_OCC_FWD void sq_fwd_pipe_kernel(const
             constexpr int KK = S / DS, DSI = S % DS;
             bf16x8 o = op[S];
             pin(o);
-            sbuf[PAR ^ 1][KK] = mfma32(o, qreg[DSI], DSI == 0 ? f32x16{} : sbuf[PAR ^ 1][KK]);
+            sbuf[PAR ^ 1][KK] = mfma32(o, qreg[DSI], DSI == 0 ? (NEG ? cbase : f32x16{}) : sbuf[PAR ^ 1][KK]);
           }
         } else {
           constexpr int Y = S - NX;
@@ -176,7 +180,7 @@ __global__ __launch_bounds__(64 * NW) LOGO_OCC_FWD void sq_fwd_pipe_kernel(const
               constexpr int KK = IT / 16, JJ = IT % 16;
               float sv = sbuf[PAR][KK][JJ];
               pin(sv);
-              float pv = NEG ? fast_exp2(-(sv + base)) : fast_exp2(fmaf(sv, c, -base));
+              float pv = NEG ? fast_exp2(-sv) : fast_exp2(fmaf(sv, c, -base));
               pin(pv);
               sbuf[PAR][KK][JJ] = pv;
               psum += pv;
@@ -190,13 +194,23 @@ __global__ __launch_bounds__(64 * NW) LOGO_OCC_FWD void sq_fwd_pipe_kernel(const
       __builtin_amdgcn_sched_barrier(0);
       if constexpr (DOPV) l_run += psum;
       if constexpr (DOS) {
-        const float mxs = NEG ? -pair_min(mx) : pair_max(mx) * c;  // tile max of c s
+        // tile max of c s (NEG: the accumulators hold base - c s)
+        const float mxs = NEG ? base - pair_min(mx) : pair_max(mx) * c;
         const bool grow = mxs - m_run > 8.f;
-        const float m_new = __ballot(grow) ? fmaxf(m_run, mxs) : m_run;
+        const bool any_grow = __ballot(grow);
+        const float m_new = any_grow ? fmaxf(m_run, mxs) : m_run;
         const float nbase = (m_new == -INFINITY) ? 0.f : m_new;
         const float alpha = fast_exp2(m_run - nbase);
         l_run *= alpha;
         m_run = m_new;
+        if (NEG && any_grow) {
+          // rebase the next tile's scores (S' + base -> S' + nbase) and the splat
+          const float shift = nbase - base;
+#pragma unroll
+          for (int kk = 0; kk < 2; ++kk) sbuf[PAR ^ 1][kk] += shift;
+#pragma unroll
+          for (int j = 0; j < 16; ++j) cbase[j] = nbase;
+        }
         base = nbase;
         if (__ballot(alpha != 1.f)) {
 #pragma unroll
