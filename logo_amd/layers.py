@@ -168,6 +168,66 @@ def _pack_cu(B, T, cu_seqlens, device):
     return cu_seqlens.to(torch.int32)
 
 
+class VarlenPlan:
+    """How the flash-attention branches see a ``[B, T]`` batch
+    (logo/layers/utils.py:136-226): packed segments ``cu`` over the kept
+    tokens, and ``keep`` -- the flat indices of the kept tokens when a padding
+    mask drops some (None: every token, in order)."""
+
+    def __init__(self, cu: torch.Tensor, keep: Optional[torch.Tensor] = None):
+        self.cu, self.keep = cu, keep
+
+    def pack(self, x):
+        """``[B, T, H, D]`` -> ``[1, N_kept, H, D]``."""
+        flat = x.reshape(-1, x.shape[-2], x.shape[-1])
+        return (flat if self.keep is None else flat.index_select(0, self.keep))[None]
+
+    def unpack(self, y, B: int, T: int):
+        """``[1, N_kept, H, D]`` -> ``[B, T, H, D]``, dropped tokens zero (pad_input)."""
+        y = y[0]
+        if self.keep is None:
+            return y.view(B, T, y.shape[-2], y.shape[-1])
+        out = y.new_zeros(B * T, y.shape[-2], y.shape[-1])
+        return out.index_copy(0, self.keep, y).view(B, T, y.shape[-2], y.shape[-1])
+
+
+def padding_mask(attention_mask: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
+    """A 2-D padding mask only when it masks something (logo/layers/utils.py:144,
+    logo/modeling_logo.py:293-305), as bool."""
+    if attention_mask is None:
+        return None
+    mask = attention_mask.bool()
+    return mask if not bool(mask.all()) else None
+
+
+def varlen_plan(B: int, T: int, device, cu_seqlens=None, attention_mask=None, position_ids=None) -> VarlenPlan:
+    """The segments the local (and "flash" global) branch attends within, in
+    the reference's order of precedence (logo/layers/utils.py:155-226):
+    explicit ``cu_seqlens``; else a 2-D padding mask (its kept tokens, one
+    segment per batch row, :180-201); else ``position_ids`` that restart
+    (a new segment at every position 0, :84-104, :203-224); else one segment per
+    batch row.  Host syncs on the mask / position values, as the reference's."""
+    if cu_seqlens is not None:
+        assert B == 1, "cu_seqlens requires packed [1, N] input"
+        return VarlenPlan(cu_seqlens.to(device=device, dtype=torch.int32))
+    mask = padding_mask(attention_mask)
+    if mask is not None:
+        mask = mask.to(device).reshape(B, -1)[:, -T:]
+        keep = torch.nonzero(mask.flatten()).flatten()
+        cu = F.pad(torch.cumsum(mask.sum(-1, dtype=torch.int32), 0, dtype=torch.int32), (1, 0))
+        return VarlenPlan(cu, keep)
+    if position_ids is not None and T != 1:
+        pid = position_ids.to(device).reshape(-1, T).expand(B, T)
+        if not bool((torch.diff(pid, dim=-1) >= 0).all()):
+            flat = pid.flatten()
+            starts = torch.nonzero(flat == 0).flatten().to(torch.int32)
+            n = torch.tensor([B * T], dtype=torch.int32, device=device)
+            if starts.numel() == 0 or int(starts[0]) != 0:
+                starts = torch.cat([torch.zeros(1, dtype=torch.int32, device=device), starts])
+            return VarlenPlan(torch.cat([starts, n]))
+    return VarlenPlan(_pack_cu(B, T, None, device))
+
+
 def _per_head_linear(x, w):
     """``x [..., H, D] @ w [H, D, E]`` per head.  bf16 ROCm tensors with square
     per-head maps take the HIP kernels, which read and write the ``[..., H,
@@ -312,8 +372,12 @@ class LoGoAttention(nn.Module):
                            max_len=bound_g)
         return self._fuse(local.view(B, 1, H, D), glob.view(B, 1, H, D), gate.view(B, 1)), gate
 
-    def forward(self, hidden_states, position_ids=None, cu_seqlens=None,
-                past_key_value: Optional[LogoKVCache] = None, position_embeddings=None, **kwargs):
+    def forward(self, hidden_states, attention_mask=None, position_ids=None, cu_seqlens=None,
+                past_key_value: Optional[LogoKVCache] = None, output_attentions: bool = False,
+                use_cache: bool = False, cache_position=None, position_embeddings=None, max_seqlen=None, **kwargs):
+        """Same arguments as logo/layers/logo.py:96-110.  ``attention_mask`` is a
+        2-D padding mask ``[B, T]``; a decode step ignores it (the cache holds
+        each row's kept tokens only, see ``LogoKVCache.prefill``)."""
         B, T, _ = hidden_states.shape
         H, HK, D = self.num_heads, self.num_key_value_heads, self.head_dim
         if self._fused_decode_ok(hidden_states, past_key_value):
@@ -337,10 +401,13 @@ class LoGoAttention(nn.Module):
         if past_key_value is not None and T == 1:
             out = self._decode(q, k, v, gq, gk, gv, gate, past_key_value)
         else:
+            plan = varlen_plan(B, T, q.device, cu_seqlens, attention_mask, position_ids)
             if past_key_value is not None:
+                keep = padding_mask(attention_mask)
                 past_key_value.prefill(self.layer_idx, k.transpose(1, 2), v.transpose(1, 2),
-                                       gk.transpose(1, 2), gv.transpose(1, 2))
-            out = self._prefill(q, k, v, gq, gk, gv, gate, cu_seqlens)
+                                       gk.transpose(1, 2), gv.transpose(1, 2),
+                                       keep=None if keep is None else keep.reshape(B, -1)[:, -T:])
+            out = self._prefill(q, k, v, gq, gk, gv, gate, cu_seqlens, plan)
 
         if self.training:
             with torch.no_grad():
@@ -349,18 +416,24 @@ class LoGoAttention(nn.Module):
                 self.total_token_count.add_(gate.numel())
         return self.o_proj(out), None, past_key_value
 
-    def _prefill(self, q, k, v, gq, gk, gv, gate, cu_seqlens):
+    def _prefill(self, q, k, v, gq, gk, gv, gate, cu_seqlens, plan: VarlenPlan):
+        """Local SWA within ``plan``'s segments (logo/layers/logo.py:162-182).
+        The sparse global branch packs each batch row as one sequence unless
+        ``cu_seqlens`` is given, ignoring a padding mask and position resets
+        exactly as the reference's does (:188-209); the "flash" global branch
+        attends within ``plan``'s segments like the local one (:210-224)."""
         B, T, H, D = q.shape
         N = B * T
-        cu = _pack_cu(B, T, cu_seqlens, q.device)
-        pk = lambda x: x.reshape(1, N, x.shape[2], x.shape[3])
-        local = swa_attn(pk(q), pk(k), pk(v), cu, window=self.local_window_size)
+        local = plan.unpack(swa_attn(plan.pack(q), plan.pack(k), plan.pack(v), plan.cu,
+                                     window=self.local_window_size), B, T)
         if self.sparse_full_attn_backend in SPARSE_BACKENDS:
+            cu = _pack_cu(B, T, cu_seqlens, q.device)
+            pk = lambda x: x.reshape(1, N, x.shape[2], x.shape[3])  # noqa: E731
             selection = (gate.reshape(1, N) >= self.gate_thres)
-            glob = sq_full_attn(pk(gq), pk(gk), pk(gv), selection, cu_seqlens=cu)
+            glob = sq_full_attn(pk(gq), pk(gk), pk(gv), selection, cu_seqlens=cu).view(B, T, H, D)
         else:
-            glob = dense_causal_attn(pk(gq), pk(gk), pk(gv), cu)
-        return self._fuse(local.view(B, T, H, D), glob.view(B, T, H, D), gate.view(B, T))
+            glob = plan.unpack(dense_causal_attn(plan.pack(gq), plan.pack(gk), plan.pack(gv), plan.cu), B, T)
+        return self._fuse(local, glob, gate.view(B, T))
 
     def _decode(self, q, k, v, gq, gk, gv, gate, cache: LogoKVCache):
         B, _, H, D = q.shape
@@ -401,8 +474,12 @@ class Attention(nn.Module):
         self.v_proj = nn.Linear(self.hidden_size, HK * D, bias=config.attention_bias)
         self.o_proj = nn.Linear(self.hidden_size, self.hidden_size, bias=config.attention_out_bias)
 
-    def forward(self, hidden_states, position_ids=None, cu_seqlens=None,
-                past_key_value: Optional[LogoKVCache] = None, position_embeddings=None, **kwargs):
+    def forward(self, hidden_states, attention_mask=None, position_ids=None, cu_seqlens=None,
+                past_key_value: Optional[LogoKVCache] = None, output_attentions: bool = False,
+                use_cache: bool = False, cache_position=None, position_embeddings=None, max_seqlen=None, **kwargs):
+        """Same arguments as logo/layers/attn.py:62-76; a padding mask or
+        restarting ``position_ids`` select the segments as in the LoGo layer's
+        local branch (``varlen_plan``)."""
         B, T, _ = hidden_states.shape
         H, HK, D = self.num_heads, self.num_key_value_heads, self.head_dim
         q = self.q_proj(hidden_states).view(B, T, H, D)
@@ -420,11 +497,12 @@ class Attention(nn.Module):
             out = decode_attn(q[:, 0], cache.global_k[self.layer_idx], cache.global_v[self.layer_idx], len_g,
                               max_len=bound_g).view(B, 1, H * D)
         else:
+            plan = varlen_plan(B, T, q.device, cu_seqlens, attention_mask, position_ids)
             if past_key_value is not None:
                 kt, vt = k.transpose(1, 2), v.transpose(1, 2)
-                past_key_value.prefill(self.layer_idx, kt, vt, kt, vt)
-            N = B * T
-            cu = _pack_cu(B, T, cu_seqlens, q.device)
-            pk = lambda x: x.reshape(1, N, x.shape[2], x.shape[3])
-            out = dense_causal_attn(pk(q), pk(k), pk(v), cu).view(B, T, H * D)
+                keep = padding_mask(attention_mask)
+                past_key_value.prefill(self.layer_idx, kt, vt, kt, vt,
+                                       keep=None if keep is None else keep.reshape(B, -1)[:, -T:])
+            out = plan.unpack(dense_causal_attn(plan.pack(q), plan.pack(k), plan.pack(v), plan.cu), B, T)
+            out = out.reshape(B, T, H * D)
         return self.o_proj(out), None, past_key_value

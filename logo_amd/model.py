@@ -21,7 +21,8 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from .layers import Attention, LoGoAttention, LoGoConfig, RMSNorm, _fused_ok, position_ids_for, rope_cos_sin
+from .layers import (Attention, LoGoAttention, LoGoConfig, RMSNorm, _fused_ok, padding_mask, position_ids_for,
+                     rope_cos_sin)
 from .ops.decode import LogoKVCache
 from .ops.glue import add_rms_norm, silu_mul
 
@@ -70,12 +71,12 @@ class LoGoDecoderLayer(nn.Module):
         self.input_layernorm = RMSNorm(config.hidden_size, eps=config.rms_norm_eps)
         self.post_attention_layernorm = RMSNorm(config.hidden_size, eps=config.rms_norm_eps)
 
-    def forward(self, hidden_states, cu_seqlens=None, past_key_value: Optional[LogoKVCache] = None,
-                position_embeddings=None):
+    def forward(self, hidden_states, attention_mask=None, position_ids=None, cu_seqlens=None,
+                past_key_value: Optional[LogoKVCache] = None, position_embeddings=None):
         residual = hidden_states
         h = self.input_layernorm(hidden_states)
-        h, _, _ = self.self_attn(h, cu_seqlens=cu_seqlens, past_key_value=past_key_value,
-                                 position_embeddings=position_embeddings)
+        h, _, _ = self.self_attn(h, attention_mask=attention_mask, position_ids=position_ids, cu_seqlens=cu_seqlens,
+                                 past_key_value=past_key_value, position_embeddings=position_embeddings)
         hidden_states = residual + h
         residual = hidden_states
         h = self.mlp(self.post_attention_layernorm(hidden_states))
@@ -92,18 +93,32 @@ class LoGoModel(nn.Module):
         self.layers = nn.ModuleList([LoGoDecoderLayer(config, i) for i in range(config.num_hidden_layers)])
         self.norm = RMSNorm(config.hidden_size, eps=config.rms_norm_eps)
 
-    def forward(self, input_ids, cu_seqlens=None, past_key_value: Optional[LogoKVCache] = None):
+    def forward(self, input_ids, attention_mask=None, position_ids=None, cu_seqlens=None,
+                past_key_value: Optional[LogoKVCache] = None):
+        """``attention_mask``: a 2-D padding mask ``[B, T]`` (passed on only when
+        it masks something, logo/modeling_logo.py:293-305); without explicit
+        ``position_ids`` a padded batch takes generate's positions, the count
+        of kept tokens before each one (pads at 1,
+        logo/modeling_logo.py:421-432).  A decode step reads its positions
+        from the cache."""
         h = self.embed_tokens(input_ids)
         B, T = input_ids.shape
+        mask = padding_mask(attention_mask) if T > 1 else None
+        if position_ids is None and mask is not None:
+            position_ids = mask.long().cumsum(-1) - 1
+            position_ids.masked_fill_(~mask, 1)
+            position_ids = position_ids[:, -T:]
+        pos = position_ids if position_ids is not None else position_ids_for(B, T, input_ids.device, cu_seqlens,
+                                                                             past_key_value)
         # rotary cos / sin once for all layers (logo/modeling_logo.py:233-234)
-        pos = position_ids_for(B, T, input_ids.device, cu_seqlens, past_key_value)
-        pe = rope_cos_sin(pos, self.config.head_dim, self.config.rope_theta, h.dtype)
+        pe = rope_cos_sin(pos.expand(B, T), self.config.head_dim, self.config.rope_theta, h.dtype)
         if _fused_ok(h) and h.shape[-1] <= 4096:
             # inference: each residual add fused with the norm that follows it
             # (post-attention norm, the next layer's input norm, the final norm)
             resid, normed = h, self.layers[0].input_layernorm(h)
             for i, layer in enumerate(self.layers):
-                a, _, _ = layer.self_attn(normed, cu_seqlens=cu_seqlens, past_key_value=past_key_value,
+                a, _, _ = layer.self_attn(normed, attention_mask=mask, position_ids=position_ids,
+                                          cu_seqlens=cu_seqlens, past_key_value=past_key_value,
                                           position_embeddings=pe)
                 pn = layer.post_attention_layernorm
                 resid, normed = add_rms_norm(resid, a, pn.weight, pn.variance_epsilon)
@@ -112,7 +127,8 @@ class LoGoModel(nn.Module):
                 resid, normed = add_rms_norm(resid, m, nn_.weight, nn_.variance_epsilon)
             return normed
         for layer in self.layers:
-            h = layer(h, cu_seqlens=cu_seqlens, past_key_value=past_key_value, position_embeddings=pe)
+            h = layer(h, attention_mask=mask, position_ids=position_ids, cu_seqlens=cu_seqlens,
+                      past_key_value=past_key_value, position_embeddings=pe)
         return self.norm(h)
 
 
@@ -154,22 +170,32 @@ class LoGoForCausalLM(nn.Module):
         return LogoKVCache(c.num_hidden_layers, batch, c.num_key_value_heads, c.head_dim, max_len,
                            window=c.window_size, device=device)
 
-    def forward(self, input_ids, cu_seqlens=None, past_key_value: Optional[LogoKVCache] = None,
-                last_only: bool = False):
+    def forward(self, input_ids, attention_mask=None, position_ids=None, cu_seqlens=None,
+                past_key_value: Optional[LogoKVCache] = None, last_only: bool = False):
         """Logits ``[B, T, V]`` (or ``[B, V]`` of the last position with
         ``last_only``: a 16K-token prompt batch would otherwise materialise
         tens of GB of logits)."""
-        h = self.model(input_ids, cu_seqlens=cu_seqlens, past_key_value=past_key_value)
+        h = self.model(input_ids, attention_mask=attention_mask, position_ids=position_ids, cu_seqlens=cu_seqlens,
+                       past_key_value=past_key_value)
         if last_only:
             h = h[:, -1]
         return self.lm_head(h)
 
     @torch.no_grad()
-    def prefill(self, input_ids, cache: LogoKVCache):
+    def prefill(self, input_ids, cache: LogoKVCache, attention_mask=None):
         """Run the prompt ``[B, T]`` through the model, filling ``cache``; returns
-        the last position's logits ``[B, V]``."""
-        logits = self.forward(input_ids, past_key_value=cache, last_only=True)
-        cache.set_length(input_ids.shape[1])
+        the last position's logits ``[B, V]``.  A left-padded batch
+        (``attention_mask [B, T]``, zeros before each row's tokens, as
+        generate pads) caches each row's own tokens and continues at its own
+        position."""
+        mask = padding_mask(attention_mask)
+        if mask is not None and not bool(mask[:, -1].all()):
+            raise ValueError("prefill with a padding mask expects left padding (every row's last token kept)")
+        logits = self.forward(input_ids, attention_mask=mask, past_key_value=cache, last_only=True)
+        if mask is None:
+            cache.set_length(input_ids.shape[1])
+        else:
+            cache.set_lengths(mask.sum(-1))
         return logits
 
     @torch.no_grad()
@@ -218,12 +244,14 @@ class LoGoForCausalLM(nn.Module):
         return step
 
     @torch.no_grad()
-    def greedy_generate(self, input_ids, max_new_tokens: int, cache: Optional[LogoKVCache] = None):
-        """Greedy decoding: returns the generated tokens ``[B, max_new_tokens]``."""
+    def greedy_generate(self, input_ids, max_new_tokens: int, cache: Optional[LogoKVCache] = None,
+                        attention_mask=None):
+        """Greedy decoding: returns the generated tokens ``[B, max_new_tokens]``;
+        ``attention_mask`` for a left-padded prompt batch."""
         B, T = input_ids.shape
         if cache is None:
             cache = self.new_cache(B, T + max_new_tokens, device=input_ids.device)
-        tok = self.prefill(input_ids, cache).argmax(-1)
+        tok = self.prefill(input_ids, cache, attention_mask=attention_mask).argmax(-1)
         out = [tok]
         for _ in range(max_new_tokens - 1):
             tok = self.decode_step(tok, cache).argmax(-1)

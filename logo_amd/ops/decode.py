@@ -153,11 +153,18 @@ class LogoKVCache:
     def get_seq_length(self) -> int:
         return self.seen
 
-    def prefill(self, layer: int, k_local, v_local, k_global, v_global):
+    def prefill(self, layer: int, k_local, v_local, k_global, v_global, keep=None):
         """Store a prompt's K/V (``[B, H, T, D]``) for one layer, at positions
         [0, T).  Only an empty cache takes a prompt: the prefill attends to the
         prompt alone, so a second chunk on top of cached tokens would lose them
-        (``reset()`` empties the cache for a new prompt)."""
+        (``reset()`` empties the cache for a new prompt).
+
+        ``keep`` (bool ``[B, T]``, a padding mask): each row stores its kept
+        tokens only, in order, at positions [0, n_b) -- the reference keeps the
+        padded positions and masks them out of every decode step
+        (logo/layers/logo.py:162-176, :230-244 with logo/layers/utils.py:44-81),
+        which attends the same keys; ``set_lengths`` then records the per-row
+        counts."""
         if self.seen > 0:
             raise ValueError(
                 f"prefill into a cache that already holds {self.seen} tokens: a multi-token forward "
@@ -165,19 +172,32 @@ class LogoKVCache:
         T = k_global.shape[2]
         if T > self.max_len:
             raise ValueError(f"prompt of {T} tokens exceeds the cache's {self.max_len}")
-        self.global_k[layer][:, :, :T].copy_(k_global)
-        self.global_v[layer][:, :, :T].copy_(v_global)
+        if keep is not None:
+            keep = keep.to(k_global.device).bool()
+            for b in range(k_global.shape[0]):
+                idx = torch.nonzero(keep[b]).flatten()
+                self._store_rows(layer, slice(b, b + 1), *(x[b:b + 1].index_select(2, idx)
+                                                          for x in (k_local, v_local, k_global, v_global)))
+            return
+        self._store_rows(layer, slice(None), k_local, v_local, k_global, v_global)
+
+    def _store_rows(self, layer, rows, k_local, v_local, k_global, v_global):
+        """Positions [0, T) of batch ``rows``: the global cache, and the last
+        ``ring`` positions into the local ring at slot ``p % ring``."""
+        T = k_global.shape[2]
+        self.global_k[layer][rows, :, :T].copy_(k_global)
+        self.global_v[layer][rows, :, :T].copy_(v_global)
         lo = max(0, T - self.ring)
         for p0 in range(lo, T, self.ring):
             p1 = min(T, p0 + self.ring)
             s0 = p0 % self.ring
             n = p1 - p0
             first = min(n, self.ring - s0)
-            self.local_k[layer][:, :, s0:s0 + first].copy_(k_local[:, :, p0:p0 + first])
-            self.local_v[layer][:, :, s0:s0 + first].copy_(v_local[:, :, p0:p0 + first])
+            self.local_k[layer][rows, :, s0:s0 + first].copy_(k_local[:, :, p0:p0 + first])
+            self.local_v[layer][rows, :, s0:s0 + first].copy_(v_local[:, :, p0:p0 + first])
             if first < n:
-                self.local_k[layer][:, :, :n - first].copy_(k_local[:, :, p0 + first:p1])
-                self.local_v[layer][:, :, :n - first].copy_(v_local[:, :, p0 + first:p1])
+                self.local_k[layer][rows, :, :n - first].copy_(k_local[:, :, p0 + first:p1])
+                self.local_v[layer][rows, :, :n - first].copy_(v_local[:, :, p0 + first:p1])
 
     def reset(self):
         """Empty the cache (host and device positions back to 0)."""
@@ -187,6 +207,14 @@ class LogoKVCache:
         """Record that ``seen`` tokens are cached (host value; e.g. after a prefill)."""
         self.seen = seen
         self._pos.fill_(seen)
+        self._step += 1
+
+    def set_lengths(self, lengths):
+        """Per-row cached token counts (after a prefill with a padding mask);
+        the host ``seen`` becomes the largest, the bound for kernel grids."""
+        lengths = torch.as_tensor(lengths).to(device=self._pos.device, dtype=torch.int32).reshape(self.batch)
+        self._pos.copy_(lengths)
+        self.seen = int(lengths.max())
         self._step += 1
 
     def advance_device(self):

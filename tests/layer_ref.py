@@ -132,11 +132,16 @@ def _attn(q, k, v, seg, pos, sel, window, round_dtype=None):
     return o
 
 
-def logo_layer_ref(h, p, cfg, sel_bt, cu=None, backend="hip", store_dtype=None):
+def logo_layer_ref(h, p, cfg, sel_bt, cu=None, backend="hip", store_dtype=None, attention_mask=None):
     """``h [B, T, C]`` float64; ``p`` dict of float64 params (reference names);
     ``sel_bt [B, T]`` bool: which tokens pass the gate threshold;
     ``store_dtype``: None (float64 throughout) or the dtype the reference's
-    module chain stores its tensors in (see the module docstring)."""
+    module chain stores its tensors in (see the module docstring);
+    ``attention_mask [B, T]``: a padding mask, with the reference's semantics
+    (logo/layers/utils.py:180-201, logo/modeling_logo.py:421-432): RoPE at
+    generate's positions (kept tokens counted, pads at 1), the local branch
+    and the "flash" global branch over each row's kept tokens (pads give 0),
+    the sparse global branch over the whole padded row."""
     R = _storer(store_dtype)
     h = R(h)  # the layer input is stored too: its gradient is rounded once summed
     B, T, C = h.shape
@@ -165,15 +170,27 @@ def logo_layer_ref(h, p, cfg, sel_bt, cu=None, backend="hip", store_dtype=None):
             pos[cul[s]:cul[s + 1]] = torch.arange(cul[s + 1] - cul[s])
     seg, pos = seg.to(h.device), pos.to(h.device)
     posbt = pos.view(B, T)
+    keep = None
+    if attention_mask is not None:
+        keep = attention_mask.to(h.device).bool().reshape(N)
+        kept_pos = attention_mask.to(h.device).long().cumsum(-1) - 1
+        posbt = kept_pos.masked_fill(~attention_mask.to(h.device).bool(), 1)
+        # kept tokens: row segments with positions among the kept; every pad its
+        # own segment (its output is zeroed below)
+        lseg = torch.where(keep, seg, -1 - torch.arange(N, device=h.device))
+        lpos = kept_pos.reshape(N).clamp_min(0)
     f32 = store_dtype in (torch.bfloat16, torch.float16)  # the reference computes angles in fp32
     q, k = _rope(q, posbt, cfg.rope_theta, R, f32), _rope(k, posbt, cfg.rope_theta, R, f32)
     gq, gk = _rope(gq, posbt, cfg.rope_theta, R, f32), _rope(gk, posbt, cfg.rope_theta, R, f32)
     gate = R(torch.sigmoid(R(h @ p["gate_proj.weight"].T)))  # [B, T, 1]
     sel_bt = sel_bt.to(h.device)
     sel = sel_bt.reshape(N) if backend != "flash" else None
-    local = R(_attn(q.reshape(N, H, D), k.reshape(N, HK, D), v.reshape(N, HK, D), seg, pos, None,
+    lseg, lpos = (seg, pos) if keep is None else (lseg, lpos)
+    local = R(_attn(q.reshape(N, H, D), k.reshape(N, HK, D), v.reshape(N, HK, D), lseg, lpos, keep,
                     cfg.window_size, store_dtype))
-    glob = R(_attn(gq.reshape(N, H, D), gk.reshape(N, HK, D), gv.reshape(N, HK, D), seg, pos, sel, None,
+    gseg, gpos = (lseg, lpos) if backend == "flash" else (seg, pos)
+    gsel = sel if keep is None or backend != "flash" else keep
+    glob = R(_attn(gq.reshape(N, H, D), gk.reshape(N, HK, D), gv.reshape(N, HK, D), gseg, gpos, gsel, None,
                    store_dtype))
     local = _rmsnorm(local, p["context_norm_local.weight"], cfg.rms_norm_eps, R).reshape(B, T, C)
     glob = _rmsnorm(glob, p["context_norm_global.weight"], cfg.rms_norm_eps, R).reshape(B, T, C)

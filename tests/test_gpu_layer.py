@@ -124,3 +124,42 @@ def test_plain_attention_layer_fwd_bwd(gpu, cu, hk):
     _scaled("dh", hg.grad, h64.grad)
     for n, prm in layer.named_parameters():
         assert_close(n, params[n].grad, prm.grad.double().cpu(), 1e-2)
+
+
+@pytest.mark.parametrize("backend", ["hip", "flash"])
+def test_layer_padding_mask_fwd_bwd(gpu, backend):
+    """A left- and middle-padded batch with a 2-D attention_mask: the local
+    branch (and the "flash" global branch) attend each row's kept tokens only,
+    RoPE runs at generate's positions, and the sparse global branch packs the
+    whole padded row, as the reference's (logo/layers/utils.py:180-201,
+    logo/layers/logo.py:188-209, logo/modeling_logo.py:421-432).  Against the
+    float64 restatement given the same gate decisions: outputs, dh and
+    parameter gradients, at the small-layer tolerances."""
+    cfg = LoGoConfig(hidden_size=512, num_attention_heads=4, num_hidden_layers=1,
+                     sparse_full_attn_backend=backend, gate_thres_init=0.5)
+    layer = _make(cfg, gpu, 11)
+    layer.train()
+    B, T = 3, 200
+    mask = torch.ones(B, T, dtype=torch.long)
+    mask[0, :37] = 0          # left padding
+    mask[2, :150] = 0         # a short row: fewer kept tokens than the window
+    mask[1, 60:64] = 0        # a hole
+    g = gen(12)
+    h = torch.randn(B, T, cfg.hidden_size, generator=g).bfloat16().to(gpu).requires_grad_()
+    dout = torch.randn(B, T, cfg.hidden_size, generator=g).bfloat16().to(gpu)
+    pos = (mask.cumsum(-1) - 1).masked_fill(mask == 0, 1)
+    out, _, _ = layer(h, attention_mask=mask.to(gpu), position_ids=pos.to(gpu))
+    out.backward(dout)
+    with torch.no_grad():
+        gate_gpu = torch.sigmoid(layer.gate_proj(h)).view(B, T)
+    params = {n: p.detach().double().cpu().requires_grad_() for n, p in layer.named_parameters()}
+    sel = (gate_gpu >= layer.gate_thres).cpu()
+    h64 = h.detach().double().cpu().requires_grad_()
+    ref = logo_layer_ref(h64, params, cfg, sel, backend=backend, attention_mask=mask)
+    ref.backward(dout.double().cpu())
+    _scaled("out", out, ref)
+    _scaled("dh", h.grad, h64.grad)
+    for name in ("q_proj.weight", "k_proj.weight", "v_proj.weight", "o_proj.weight", "q_global_proj",
+                 "context_norm_local.weight", "context_norm_global.weight"):
+        prm = dict(layer.named_parameters())[name]
+        assert_close(name, params[name].grad, prm.grad.double().cpu(), 1e-2)

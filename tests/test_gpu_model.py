@@ -137,3 +137,49 @@ def test_second_prefill_rejected_and_reset_repeats_first(gpu):
     cache.reset()
     again = m.prefill(ids, cache)
     assert torch.equal(first, again)
+
+
+@pytest.mark.parametrize("backend,thres", [("flash", -1.0), ("hip", 2.0)])
+def test_left_padded_generate_matches_each_row_alone(gpu, backend, thres):
+    """Greedy decoding of a left-padded prompt batch (generate's padding,
+    logo/modeling_logo.py:421-432): the cache keeps each row's own tokens and
+    each row continues at its own position, so every row's logits match those
+    of the same prompt decoded alone without padding.  (Routes where the
+    reference attends padded keys -- its sparse global prefill -- are left
+    out: threshold 2 sends every token to the local branch.)"""
+    from logo_amd.layers import LoGoConfig as Cfg
+
+    cfg = Cfg(vocab_size=512, hidden_size=256, intermediate_size=512, num_hidden_layers=2, num_attention_heads=4,
+              window_size=128, gate_thres_init=thres, sparse_full_attn_backend=backend)
+    m = LoGoForCausalLM(cfg)
+    g = torch.Generator()
+    g.manual_seed(9)
+    m.init_weights(g)
+    with torch.no_grad():
+        for layer in m.model.layers:
+            for p in (layer.self_attn.q_global_proj, layer.self_attn.k_global_proj, layer.self_attn.v_global_proj):
+                p.add_(torch.randn(p.shape, generator=g) * 0.05)
+    m = m.to(device=gpu, dtype=torch.bfloat16).eval()
+    lens, T, steps = [190, 60, 141], 190, 8
+    ids = torch.randint(1, 512, (3, T), generator=g)
+    mask = torch.zeros(3, T, dtype=torch.long)
+    for b, n in enumerate(lens):
+        mask[b, T - n:] = 1
+        ids[b, :T - n] = 0
+    cache = m.new_cache(3, T + steps, device=gpu)
+    logits = m.prefill(ids.to(gpu), cache, attention_mask=mask.to(gpu))
+    assert cache._pos.tolist() == lens
+    toks, outs = [], []
+    for s in range(steps):
+        outs.append(logits.float())
+        tok = logits.argmax(-1)
+        toks.append(tok)
+        logits = m.decode_step(tok, cache)
+    for b, n in enumerate(lens):
+        alone = m.new_cache(1, n + steps, device=gpu)
+        lg = m.prefill(ids[b:b + 1, T - n:].to(gpu), alone)
+        for s in range(steps):
+            err = (lg.float()[0] - outs[s][b]).abs().max().item()
+            scale = outs[s][b].abs().max().item()
+            assert err <= 0.03 * scale + 1e-3, f"row {b} step {s}: max diff {err:.4f} (scale {scale:.3f})"
+            lg = m.decode_step(toks[s][b:b + 1], alone)
