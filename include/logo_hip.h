@@ -147,7 +147,8 @@ int logo_sq_bwd(const void* q, const void* k, const void* v, const void* o,
  * The three backward phases of logo_sq_bwd as separate launches, same
  * arguments: delta and the q_sel / do_sel copies (:124-138, :365-371), dq
  * (:141-228, :424-432), dk/dv (:231-337, :433-445).  Callers time or overlap
- * them one by one; dq and dk/dv read what the delta phase wrote.
+ * them one by one; dq and dk/dv read what the delta phase wrote.  Each phase
+ * needs only the outputs it writes (dq, or dk and dv); the others may be NULL.
  */
 int logo_sq_bwd_delta(const void* q, const void* k, const void* v, const void* o,
     const void* dout, const float* lse, float* delta, void* q_sel, void* do_sel,

@@ -164,7 +164,9 @@ static int bwd_entry(LOGO_BWD_PARAMS, int phase) {
   int rc = check_common(n_tokens, nseq, hq, h, d, v_dim, lanes, dtype);
   if (rc != LOGO_OK) return rc;
   LOGO_REQUIRE(q && k && v && o && dout && lse && delta && meta && cu, "null pointer argument");
-  LOGO_REQUIRE(phase == 0 || (dq && dk && dv), "null gradient pointer");
+  // each phase needs the outputs it writes: dq (phase 1), dk / dv (phase 2)
+  LOGO_REQUIRE((phase == 0 || phase == 2 || dq) && (phase == 0 || phase == 1 || (dk && dv)),
+               "null gradient pointer");
   LOGO_REQUIRE((q_idx == nullptr) == (pos == nullptr), "q_idx and pos must both be set or both be null");
   LOGO_REQUIRE(q_idx == nullptr || (q_sel && do_sel), "sparse backward needs q_sel and do_sel workspaces");
   AttnArgs a = make_args(q, k, v, q_idx, pos, meta, cu, n_tokens, nseq, hq, h, lanes, scale, window);

@@ -11,7 +11,7 @@ from typing import Optional
 
 import torch
 
-from .. import _lib
+from .. import _lib, _torch_ops
 
 __all__ = [
     "SelInfo",
@@ -129,15 +129,7 @@ def compact_selection(selection: torch.Tensor, cu_seqlens: torch.Tensor) -> Devi
     nseq = cu.numel() - 1
     if nseq < 1:
         raise ValueError("cu_seqlens must have at least two entries")
-    lib = _lib.lib()
-    q_idx = torch.empty(lanes, max(n, 1), dtype=torch.int64, device=dev)
-    pos = torch.empty(lanes, max(n, 1), dtype=torch.int32, device=dev)
-    meta = torch.empty(lanes * _lib.meta_stride(nseq), dtype=torch.int32, device=dev)
-    ws_bytes = lib.logo_compact_workspace_bytes(n, lanes)
-    ws = torch.empty((ws_bytes + 3) // 4, dtype=torch.int32, device=dev)
-    sel_u8 = sel.view(torch.uint8)
-    _lib.launch("logo_compact", lib.logo_compact, _lib.ptr(sel_u8), n, lanes, _lib.ptr(cu), nseq,
-                _lib.ptr(q_idx), _lib.ptr(pos), _lib.ptr(meta), _lib.ptr(ws), _lib.stream_of(sel))
+    q_idx, pos, meta = _torch_ops.timed("logo_compact", _torch_ops.ops().compact, sel, cu)
     return DeviceSelection(meta=meta, cu=cu, q_idx=q_idx, pos=pos, n_tokens=n, nseq=nseq, lanes=lanes)
 
 
@@ -145,10 +137,8 @@ def dense_selection(cu_seqlens: torch.Tensor, n_tokens: int, device) -> DeviceSe
     """Metadata for attention over every row (no compaction)."""
     cu = _as_cu(cu_seqlens, device)
     nseq = cu.numel() - 1
-    meta = torch.empty(_lib.meta_stride(nseq), dtype=torch.int32, device=device)
-    lib = _lib.lib()
-    _lib.check(lib.logo_dense_meta(_lib.ptr(cu), nseq, n_tokens, _lib.ptr(meta), _lib.stream_of(cu)),
-               "logo_dense_meta")
+    _lib.require_gpu(cu)
+    meta = _torch_ops.ops().dense_meta(cu, n_tokens)
     return DeviceSelection(meta=meta, cu=cu, q_idx=None, pos=None, n_tokens=n_tokens, nseq=nseq, lanes=1)
 
 

@@ -15,7 +15,7 @@ from typing import Optional
 
 import torch
 
-from .. import _lib
+from .. import _lib, _torch_ops
 
 __all__ = ["decode_attn", "decode_attn_fused", "cache_append", "decode_qkv", "LogoKVCache"]
 
@@ -33,19 +33,12 @@ def decode_attn(q, k_cache, v_cache, lens, gate=None, thres=None, max_len: Optio
         scale = D ** -0.5
     if max_len is None:
         max_len = t_cap
-    qc = q.contiguous()
-    out = torch.empty_like(qc)
-    lib = _lib.lib()
-    ws = torch.empty((lib.logo_decode_workspace_bytes(B, HQ, D, max_len) + 3) // 4, dtype=torch.float32,
-                     device=q.device)
-    th, th_dt = None, _lib.DTYPE_F32
+    th = None
     if gate is not None:
         gate = gate.contiguous().view(B)
-        th, th_dt = _lib.thres_arg(thres)
-    _lib.launch("logo_decode_attn", lib.logo_decode_attn, _lib.ptr(qc), _lib.ptr(k_cache), _lib.ptr(v_cache),
-                _lib.ptr(lens), _lib.ptr(gate), _lib.ptr(th), th_dt, _lib.ptr(out), _lib.ptr(ws), B, HQ, H, D, t_cap,
-                int(max_len), float(scale), _lib.DTYPE_BF16, _lib.stream_of(q))
-    return out
+        th, _ = _lib.thres_arg(thres)
+    return _torch_ops.timed("logo_decode_attn", _torch_ops.ops().decode_attn, q.contiguous(), k_cache, v_cache,
+                            lens, gate, th, int(max_len), float(scale))
 
 
 def decode_attn_fused(q_local, k_local, v_local, lens_local, max_len_local: int, q_global, k_global, v_global,

@@ -9,7 +9,7 @@ pair its backward.
 
 import torch
 
-from .. import _lib
+from .. import _lib, _torch_ops
 
 __all__ = ["logo_epilogue", "LogoEpilogueFunction"]
 
@@ -23,12 +23,9 @@ class LogoEpilogueFunction(torch.autograd.Function):
         Lc = L.contiguous().view(n, H, D)
         Gc = G.contiguous().view(n, H, D)
         gc = gate.contiguous().view(n)
-        th, th_dt = _lib.thres_arg(thres)
-        out = torch.empty(n, H * D, dtype=L.dtype, device=L.device)
-        lib = _lib.lib()
-        _lib.launch("logo_epilogue_fwd", lib.logo_epilogue_fwd, _lib.ptr(Lc), _lib.ptr(Gc), _lib.ptr(gc),
-                    _lib.ptr(th), th_dt, _lib.ptr(w_l), _lib.ptr(w_g), _lib.ptr(out), n, H, D, float(eps),
-                    _lib.DTYPE_BF16, _lib.stream_of(L))
+        th, _ = _lib.thres_arg(thres)
+        out = _torch_ops.timed("logo_epilogue_fwd", _torch_ops.ops().epilogue_fwd, Lc, Gc, gc, th, w_l, w_g,
+                               float(eps))
         # the threshold is read in place; the backward keeps its own copy (the
         # buffer may be stepped by the budget controller in between)
         ctx.save_for_backward(Lc, Gc, gc, th.clone() if any(ctx.needs_input_grad) else th, w_l, w_g)
@@ -41,20 +38,9 @@ class LogoEpilogueFunction(torch.autograd.Function):
         Lc, Gc, gc, th, w_l, w_g = ctx.saved_tensors
         (shape, gshape) = ctx.shapes
         n, H, D = Lc.shape
-        do = dout.contiguous().to(Lc.dtype)
-        dL = torch.empty_like(Lc)
-        dG = torch.empty_like(Gc)
-        dgate = torch.empty_like(gc)
-        dwl = torch.empty_like(w_l)
-        dwg = torch.empty_like(w_g)
-        lib = _lib.lib()
-        ws_bytes = lib.logo_epilogue_bwd_workspace_bytes(n, H, D)
-        ws = torch.empty((ws_bytes + 3) // 4, dtype=torch.float32, device=Lc.device)
-        _lib.launch("logo_epilogue_bwd", lib.logo_epilogue_bwd, _lib.ptr(Lc), _lib.ptr(Gc), _lib.ptr(gc),
-                    _lib.ptr(th), _lib.thres_arg(th)[1], _lib.ptr(w_l), _lib.ptr(w_g), _lib.ptr(do), _lib.ptr(dL),
-                    _lib.ptr(dG),
-                    _lib.ptr(dgate), _lib.ptr(dwl), _lib.ptr(dwg), n, H, D, float(ctx.eps), _lib.ptr(ws),
-                    _lib.DTYPE_BF16, _lib.stream_of(Lc))
+        do = dout.contiguous().to(Lc.dtype).view(n, H * D)
+        dL, dG, dgate, dwl, dwg = _torch_ops.timed("logo_epilogue_bwd", _torch_ops.ops().epilogue_bwd, Lc, Gc, gc,
+                                                   th, w_l, w_g, do, float(ctx.eps))
         return dL.view(shape), dG.view(shape), dgate.view(gshape), None, dwl, dwg, None
 
 

@@ -14,7 +14,7 @@ from typing import Optional
 import torch
 import torch.nn.functional as F
 
-from .. import _lib
+from .. import _lib, _torch_ops
 from .common import DeviceSelection, compact_selection, dense_selection
 
 __all__ = ["sq_full_attn", "swa_attn", "dense_causal_attn", "SQFullAttentionFunction"]
@@ -53,41 +53,19 @@ def _to_kernel(t: torch.Tensor, d: int) -> torch.Tensor:
 
 
 def _fwd(q, k, v, dsel: DeviceSelection, scale: float, window: int):
-    n, hq, d = q.shape
-    h = k.shape[1]
-    o = torch.zeros(n, hq, d, dtype=torch.bfloat16, device=q.device)
-    lse = torch.empty(hq, n, dtype=torch.float32, device=q.device)
-    lib = _lib.lib()
-    _lib.launch("logo_sq_fwd", lib.logo_sq_fwd,
-                _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(o), _lib.ptr(lse),
-                _lib.ptr(dsel.q_idx), _lib.ptr(dsel.pos), _lib.ptr(dsel.meta), _lib.ptr(dsel.cu),
-                n, dsel.nseq, hq, h, d, v.shape[2], dsel.lanes, float(scale), int(window), _lib.DTYPE_BF16,
-                _lib.stream_of(q))
-    return o, lse
+    """o [N, HQ, D] (unselected rows zero) and lse [HQ, N] (log2 domain)."""
+    return _torch_ops.timed("logo_sq_fwd", _torch_ops.ops().sq_fwd, q, k, v, dsel.q_idx, dsel.pos, dsel.meta,
+                            dsel.cu, dsel.lanes, float(scale), int(window))
 
 
 def _bwd(q, k, v, o, lse, do, dsel: DeviceSelection, scale: float, window: int):
-    n, hq, d = q.shape
-    h = k.shape[1]
-    dq = torch.zeros_like(q)
-    dk = torch.empty_like(k)
-    dv = torch.empty_like(v)
-    delta = torch.empty(hq, n, dtype=torch.float32, device=q.device)
-    q_sel = do_sel = None
-    if not dsel.dense:
-        # compacted head-major copies of the selected q / dO rows, filled by
-        # the delta phase and streamed by the dq and dk/dv kernels
-        q_sel = torch.empty(hq, n, d, dtype=torch.bfloat16, device=q.device)
-        do_sel = torch.empty(hq, n, d, dtype=torch.bfloat16, device=q.device)
-    lib = _lib.lib()
-    args = (_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(o), _lib.ptr(do), _lib.ptr(lse),
-            _lib.ptr(delta), _lib.ptr(q_sel), _lib.ptr(do_sel), _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(dv),
-            _lib.ptr(dsel.q_idx), _lib.ptr(dsel.pos), _lib.ptr(dsel.meta), _lib.ptr(dsel.cu),
-            n, dsel.nseq, hq, h, d, v.shape[2], dsel.lanes, float(scale), int(window), _lib.DTYPE_BF16,
-            _lib.stream_of(q))
-    _lib.launch("logo_sq_bwd_delta", lib.logo_sq_bwd_delta, *args)
-    _lib.launch("logo_sq_bwd_dq", lib.logo_sq_bwd_dq, *args)
-    _lib.launch("logo_sq_bwd_dkv", lib.logo_sq_bwd_dkv, *args)
+    """dq (unselected rows zero), dk, dv: the delta phase (with the compacted
+    q / dO copies of sparse mode), then dq, then dk / dv."""
+    ops = _torch_ops.ops()
+    args = (q, k, v, o, lse, do, dsel.q_idx, dsel.pos, dsel.meta, dsel.cu, dsel.lanes, float(scale), int(window))
+    ws = _torch_ops.timed("logo_sq_bwd_delta", ops.sq_bwd_delta, *args)
+    dq = _torch_ops.timed("logo_sq_bwd_dq", ops.sq_bwd_dq, *args, *ws)
+    dk, dv = _torch_ops.timed("logo_sq_bwd_dkv", ops.sq_bwd_dkv, *args, *ws)
     return dq, dk, dv
 
 

@@ -1,0 +1,263 @@
+// TORCH_LIBRARY(logo_hip) registration of the hot-path entry points of
+// liblogo_hip.so, so that torch.library / torch.compile see them as operators
+// with schemas (their fake kernels are registered from logo_amd/_torch_ops.py).
+//
+// Host code only: every operator checks its tensors (device, dtype,
+// contiguity, shapes), allocates its outputs with the caching allocator on the
+// current stream, and calls the C entry point, which launches on that stream.
+// The library's own checks stay the last line (a failure raises with
+// logo_last_error()).  Operators, the C entry point each wraps, and the
+// reference code it replaces:
+//   compact       logo_compact        build_selection, logo/ops/common.py:71-107
+//   dense_meta    logo_dense_meta     all-rows metadata of the dense / SWA branches
+//   sq_fwd        logo_sq_fwd         logo/ops/selected_full_attn.py:33-121, :340-362
+//   sq_bwd_delta  logo_sq_bwd_delta   :124-138, :365-371
+//   sq_bwd_dq     logo_sq_bwd_dq      :141-228, :424-432
+//   sq_bwd_dkv    logo_sq_bwd_dkv     :231-337, :433-445
+//   sq_bwd        the three phases    :124-445 (dq, dk, dv; workspaces internal)
+//   epilogue_fwd  logo_epilogue_fwd   logo/layers/logo.py:180-181, :225-226, :256-258
+//   epilogue_bwd  logo_epilogue_bwd   the autograd of epilogue_fwd
+//   decode_attn   logo_decode_attn    logo/layers/logo.py:228-249
+#include <ATen/ATen.h>
+#include <c10/hip/HIPStream.h>
+#include <torch/library.h>
+
+#include "../../include/logo_hip.h"
+
+namespace {
+
+void* sp() { return reinterpret_cast<void*>(c10::hip::getCurrentHIPStream().stream()); }
+
+void ok(int rc, const char* what) { TORCH_CHECK(rc == LOGO_OK, what, " failed: ", logo_last_error()); }
+
+const void* cptr(const at::Tensor& t) { return t.data_ptr(); }
+void* mptr(at::Tensor& t) { return t.data_ptr(); }
+template <typename T>
+const T* opt_ptr(const std::optional<at::Tensor>& t) {
+  return t.has_value() ? static_cast<const T*>(t->data_ptr()) : nullptr;
+}
+
+void need(const at::Tensor& t, const char* name, at::ScalarType dt) {
+  TORCH_CHECK(t.is_cuda(), "logo_hip: ", name, " must be a ROCm GPU tensor");
+  TORCH_CHECK(t.scalar_type() == dt, "logo_hip: ", name, " must be ", dt, ", got ", t.scalar_type());
+  TORCH_CHECK(t.is_contiguous(), "logo_hip: ", name, " must be contiguous");
+}
+
+// compact(selection bool or u8 [N] or [N, lanes], cu i32 [nseq+1])
+//   -> (q_idx i64 [lanes, N], pos i32 [lanes, N], meta)
+std::tuple<at::Tensor, at::Tensor, at::Tensor> compact(const at::Tensor& sel, const at::Tensor& cu) {
+  need(sel, "selection", sel.scalar_type() == at::kBool ? at::kBool : at::kByte);
+  need(cu, "cu_seqlens", at::kInt);
+  const int64_t n = sel.size(0);
+  const int lanes = sel.dim() == 2 ? (int)sel.size(1) : 1;
+  const int nseq = (int)cu.numel() - 1;
+  auto i32 = cu.options();
+  // entries past each lane's Sq are zero (the kernels write [0, Sq) only)
+  auto q_idx = at::zeros({lanes, std::max<int64_t>(n, 1)}, i32.dtype(at::kLong));
+  auto pos = at::zeros({lanes, std::max<int64_t>(n, 1)}, i32);
+  auto meta = at::empty({lanes * LOGO_META_STRIDE(nseq)}, i32);
+  auto ws = at::empty({(int64_t)logo_compact_workspace_bytes(n, lanes)}, i32.dtype(at::kByte));
+  ok(logo_compact(static_cast<const uint8_t*>(sel.data_ptr()), n, lanes, cu.data_ptr<int32_t>(), nseq,
+                  q_idx.data_ptr<int64_t>(), pos.data_ptr<int32_t>(), meta.data_ptr<int32_t>(), ws.data_ptr(),
+                  sp()),
+     "logo_compact");
+  return {q_idx, pos, meta};
+}
+
+at::Tensor dense_meta(const at::Tensor& cu, int64_t n_tokens) {
+  need(cu, "cu_seqlens", at::kInt);
+  const int nseq = (int)cu.numel() - 1;
+  auto meta = at::empty({LOGO_META_STRIDE(nseq)}, cu.options());
+  ok(logo_dense_meta(cu.data_ptr<int32_t>(), nseq, n_tokens, meta.data_ptr<int32_t>(), sp()), "logo_dense_meta");
+  return meta;
+}
+
+void check_attn(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v) {
+  need(q, "q", at::kBFloat16);
+  need(k, "k", at::kBFloat16);
+  need(v, "v", at::kBFloat16);
+  TORCH_CHECK(q.dim() == 3 && k.dim() == 3 && v.dim() == 3, "logo_hip: q, k, v must be [N, heads, D]");
+  TORCH_CHECK(k.size(0) == q.size(0) && v.sizes() == k.sizes() && k.size(2) == q.size(2),
+              "logo_hip: q [N, HQ, D], k and v [N, H, D] must agree");
+}
+
+std::tuple<at::Tensor, at::Tensor> sq_fwd(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
+                                          const std::optional<at::Tensor>& q_idx,
+                                          const std::optional<at::Tensor>& pos, const at::Tensor& meta,
+                                          const at::Tensor& cu, int64_t lanes, double scale, int64_t window) {
+  check_attn(q, k, v);
+  const int64_t n = q.size(0), hq = q.size(1), h = k.size(1), d = q.size(2);
+  auto o = at::zeros_like(q);
+  auto lse = at::zeros({hq, n}, q.options().dtype(at::kFloat));  // rows past Sq stay zero
+  ok(logo_sq_fwd(cptr(q), cptr(k), cptr(v), mptr(o), lse.data_ptr<float>(), opt_ptr<int64_t>(q_idx),
+                 opt_ptr<int32_t>(pos), meta.data_ptr<int32_t>(), cu.data_ptr<int32_t>(), n, (int)cu.numel() - 1,
+                 (int)hq, (int)h, (int)d, (int)v.size(2), (int)lanes, (float)scale, (int)window, LOGO_DTYPE_BF16,
+                 sp()),
+     "logo_sq_fwd");
+  return {o, lse};
+}
+
+// One backward phase (0 delta, 1 dq, 2 dk/dv) through its C entry point.
+struct Bwd {
+  const at::Tensor &q, &k, &v, &o, &lse, &dout;
+  const std::optional<at::Tensor>&q_idx, &pos;
+  const at::Tensor &meta, &cu;
+  int64_t lanes;
+  double scale;
+  int64_t window;
+  int call(int phase, at::Tensor* delta, at::Tensor* q_sel, at::Tensor* do_sel, at::Tensor* dq, at::Tensor* dk,
+           at::Tensor* dv) const {
+    using F = decltype(&logo_sq_bwd);
+    F fn = phase == 0 ? &logo_sq_bwd_delta : phase == 1 ? &logo_sq_bwd_dq : &logo_sq_bwd_dkv;
+    auto p = [](at::Tensor* t) -> void* { return t && t->numel() ? t->data_ptr() : nullptr; };
+    return fn(cptr(q), cptr(k), cptr(v), cptr(o), cptr(dout), lse.data_ptr<float>(),
+              static_cast<float*>(p(delta)), p(q_sel), p(do_sel), p(dq), p(dk), p(dv), opt_ptr<int64_t>(q_idx),
+              opt_ptr<int32_t>(pos), meta.data_ptr<int32_t>(), cu.data_ptr<int32_t>(), q.size(0),
+              (int)cu.numel() - 1, (int)q.size(1), (int)k.size(1), (int)q.size(2), (int)v.size(2), (int)lanes,
+              (float)scale, (int)window, LOGO_DTYPE_BF16, sp());
+  }
+};
+
+#define LOGO_BWD_SCHEMA_ARGS                                                                                 \
+  const at::Tensor &q, const at::Tensor &k, const at::Tensor &v, const at::Tensor &o, const at::Tensor &lse, \
+      const at::Tensor &dout, const std::optional<at::Tensor>&q_idx, const std::optional<at::Tensor>&pos,    \
+      const at::Tensor &meta, const at::Tensor &cu, int64_t lanes, double scale, int64_t window
+
+// delta [HQ, N] fp32 (rows past Sq zero) and, in sparse mode, the compacted
+// copies q_sel / do_sel [HQ, N, D] (empty in dense mode): workspaces of the
+// dq and dk/dv phases, whose rows past each head's Sq are left unwritten.
+std::tuple<at::Tensor, at::Tensor, at::Tensor> sq_bwd_delta(LOGO_BWD_SCHEMA_ARGS) {
+  check_attn(q, k, v);
+  need(dout, "dout", at::kBFloat16);
+  const bool sparse = q_idx.has_value();
+  auto delta = at::zeros({q.size(1), q.size(0)}, q.options().dtype(at::kFloat));
+  auto q_sel = sparse ? at::empty({q.size(1), q.size(0), q.size(2)}, q.options()) : at::empty({0}, q.options());
+  auto do_sel = sparse ? at::empty_like(q_sel) : at::empty({0}, q.options());
+  Bwd b{q, k, v, o, lse, dout, q_idx, pos, meta, cu, lanes, scale, window};
+  ok(b.call(0, &delta, &q_sel, &do_sel, nullptr, nullptr, nullptr), "logo_sq_bwd_delta");
+  return {delta, q_sel, do_sel};
+}
+
+at::Tensor sq_bwd_dq(LOGO_BWD_SCHEMA_ARGS, const at::Tensor& delta, const at::Tensor& q_sel,
+                     const at::Tensor& do_sel) {
+  check_attn(q, k, v);
+  auto dq = at::zeros_like(q);
+  Bwd b{q, k, v, o, lse, dout, q_idx, pos, meta, cu, lanes, scale, window};
+  auto dl = delta, qs = q_sel, ds = do_sel;
+  ok(b.call(1, &dl, &qs, &ds, &dq, nullptr, nullptr), "logo_sq_bwd_dq");
+  return dq;
+}
+
+std::tuple<at::Tensor, at::Tensor> sq_bwd_dkv(LOGO_BWD_SCHEMA_ARGS, const at::Tensor& delta,
+                                              const at::Tensor& q_sel, const at::Tensor& do_sel) {
+  check_attn(q, k, v);
+  auto dk = at::empty_like(k);
+  auto dv = at::empty_like(v);
+  Bwd b{q, k, v, o, lse, dout, q_idx, pos, meta, cu, lanes, scale, window};
+  auto dl = delta, qs = q_sel, ds = do_sel;
+  ok(b.call(2, &dl, &qs, &ds, nullptr, &dk, &dv), "logo_sq_bwd_dkv");
+  return {dk, dv};
+}
+
+// The whole backward: (dq, dk, dv), its workspaces internal.
+std::tuple<at::Tensor, at::Tensor, at::Tensor> sq_bwd(LOGO_BWD_SCHEMA_ARGS) {
+  auto ws = sq_bwd_delta(q, k, v, o, lse, dout, q_idx, pos, meta, cu, lanes, scale, window);
+  auto dq = sq_bwd_dq(q, k, v, o, lse, dout, q_idx, pos, meta, cu, lanes, scale, window, std::get<0>(ws),
+                      std::get<1>(ws), std::get<2>(ws));
+  auto dkv = sq_bwd_dkv(q, k, v, o, lse, dout, q_idx, pos, meta, cu, lanes, scale, window, std::get<0>(ws),
+                        std::get<1>(ws), std::get<2>(ws));
+  return {dq, std::get<0>(dkv), std::get<1>(dkv)};
+}
+
+int thres_code(const at::Tensor& thres) {
+  TORCH_CHECK(thres.numel() == 1 && (thres.scalar_type() == at::kBFloat16 || thres.scalar_type() == at::kFloat),
+              "logo_hip: the threshold is one bf16 or fp32 value");
+  return thres.scalar_type() == at::kBFloat16 ? LOGO_DTYPE_BF16 : LOGO_DTYPE_F32;
+}
+
+// L, G [n, H, D] bf16, gate [n] bf16 (post-sigmoid), w_l / w_g [D] -> out [n, H * D]
+at::Tensor epilogue_fwd(const at::Tensor& L, const at::Tensor& G, const at::Tensor& gate, const at::Tensor& thres,
+                        const at::Tensor& w_l, const at::Tensor& w_g, double eps) {
+  need(L, "L", at::kBFloat16);
+  need(G, "G", at::kBFloat16);
+  need(gate, "gate", at::kBFloat16);
+  TORCH_CHECK(L.dim() == 3 && G.sizes() == L.sizes() && gate.numel() == L.size(0), "logo_hip: epilogue shapes");
+  auto out = at::empty({L.size(0), L.size(1) * L.size(2)}, L.options());
+  ok(logo_epilogue_fwd(cptr(L), cptr(G), cptr(gate), cptr(thres), thres_code(thres), cptr(w_l), cptr(w_g),
+                       mptr(out), L.size(0), (int)L.size(1), (int)L.size(2), (float)eps, LOGO_DTYPE_BF16, sp()),
+     "logo_epilogue_fwd");
+  return out;
+}
+
+std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor, at::Tensor> epilogue_bwd(
+    const at::Tensor& L, const at::Tensor& G, const at::Tensor& gate, const at::Tensor& thres, const at::Tensor& w_l,
+    const at::Tensor& w_g, const at::Tensor& dout, double eps) {
+  need(L, "L", at::kBFloat16);
+  need(dout, "dout", at::kBFloat16);
+  const int64_t n = L.size(0), H = L.size(1), D = L.size(2);
+  auto dL = at::empty_like(L), dG = at::empty_like(G), dgate = at::empty_like(gate);
+  auto dwl = at::empty_like(w_l), dwg = at::empty_like(w_g);
+  auto ws = at::empty({(int64_t)logo_epilogue_bwd_workspace_bytes(n, (int)H, (int)D)}, L.options().dtype(at::kByte));
+  ok(logo_epilogue_bwd(cptr(L), cptr(G), cptr(gate), cptr(thres), thres_code(thres), cptr(w_l), cptr(w_g),
+                       cptr(dout), mptr(dL), mptr(dG), mptr(dgate), mptr(dwl), mptr(dwg), n, (int)H, (int)D,
+                       (float)eps, ws.data_ptr(), LOGO_DTYPE_BF16, sp()),
+     "logo_epilogue_bwd");
+  return {dL, dG, dgate, dwl, dwg};
+}
+
+// q [B, HQ, D], caches [B, H, T_cap, D], lens i32 [B]; gate [B] with thres, or neither.
+at::Tensor decode_attn(const at::Tensor& q, const at::Tensor& k_cache, const at::Tensor& v_cache,
+                       const at::Tensor& lens, const std::optional<at::Tensor>& gate,
+                       const std::optional<at::Tensor>& thres, int64_t max_len, double scale) {
+  need(q, "q", at::kBFloat16);
+  need(lens, "lens", at::kInt);
+  TORCH_CHECK(gate.has_value() == thres.has_value(), "logo_hip: gate and thres go together");
+  const int64_t B = q.size(0), HQ = q.size(1), D = q.size(2);
+  auto out = at::empty_like(q);
+  auto ws = at::empty({(int64_t)logo_decode_workspace_bytes((int)B, (int)HQ, (int)D, (int)max_len)},
+                      q.options().dtype(at::kByte));
+  ok(logo_decode_attn(cptr(q), cptr(k_cache), cptr(v_cache), lens.data_ptr<int32_t>(),
+                      gate.has_value() ? cptr(*gate) : nullptr, thres.has_value() ? cptr(*thres) : nullptr,
+                      thres.has_value() ? thres_code(*thres) : LOGO_DTYPE_F32, mptr(out), ws.data_ptr(), (int)B,
+                      (int)HQ, (int)k_cache.size(1), (int)D, k_cache.size(2), (int)max_len, (float)scale,
+                      LOGO_DTYPE_BF16, sp()),
+     "logo_decode_attn");
+  return out;
+}
+
+}  // namespace
+
+TORCH_LIBRARY(logo_hip, m) {
+  m.def("compact(Tensor selection, Tensor cu) -> (Tensor, Tensor, Tensor)");
+  m.def("dense_meta(Tensor cu, int n_tokens) -> Tensor");
+  m.def("sq_fwd(Tensor q, Tensor k, Tensor v, Tensor? q_idx, Tensor? pos, Tensor meta, Tensor cu, int lanes, "
+        "float scale, int window) -> (Tensor, Tensor)");
+  m.def("sq_bwd_delta(Tensor q, Tensor k, Tensor v, Tensor o, Tensor lse, Tensor dout, Tensor? q_idx, "
+        "Tensor? pos, Tensor meta, Tensor cu, int lanes, float scale, int window) -> (Tensor, Tensor, Tensor)");
+  m.def("sq_bwd_dq(Tensor q, Tensor k, Tensor v, Tensor o, Tensor lse, Tensor dout, Tensor? q_idx, Tensor? pos, "
+        "Tensor meta, Tensor cu, int lanes, float scale, int window, Tensor delta, Tensor q_sel, Tensor do_sel) "
+        "-> Tensor");
+  m.def("sq_bwd_dkv(Tensor q, Tensor k, Tensor v, Tensor o, Tensor lse, Tensor dout, Tensor? q_idx, "
+        "Tensor? pos, Tensor meta, Tensor cu, int lanes, float scale, int window, Tensor delta, Tensor q_sel, "
+        "Tensor do_sel) -> (Tensor, Tensor)");
+  m.def("sq_bwd(Tensor q, Tensor k, Tensor v, Tensor o, Tensor lse, Tensor dout, Tensor? q_idx, Tensor? pos, "
+        "Tensor meta, Tensor cu, int lanes, float scale, int window) -> (Tensor, Tensor, Tensor)");
+  m.def("epilogue_fwd(Tensor L, Tensor G, Tensor gate, Tensor thres, Tensor w_l, Tensor w_g, float eps) -> Tensor");
+  m.def("epilogue_bwd(Tensor L, Tensor G, Tensor gate, Tensor thres, Tensor w_l, Tensor w_g, Tensor dout, "
+        "float eps) -> (Tensor, Tensor, Tensor, Tensor, Tensor)");
+  m.def("decode_attn(Tensor q, Tensor k_cache, Tensor v_cache, Tensor lens, Tensor? gate, Tensor? thres, "
+        "int max_len, float scale) -> Tensor");
+}
+
+TORCH_LIBRARY_IMPL(logo_hip, CUDA, m) {
+  m.impl("compact", &compact);
+  m.impl("dense_meta", &dense_meta);
+  m.impl("sq_fwd", &sq_fwd);
+  m.impl("sq_bwd_delta", &sq_bwd_delta);
+  m.impl("sq_bwd_dq", &sq_bwd_dq);
+  m.impl("sq_bwd_dkv", &sq_bwd_dkv);
+  m.impl("sq_bwd", &sq_bwd);
+  m.impl("epilogue_fwd", &epilogue_fwd);
+  m.impl("epilogue_bwd", &epilogue_bwd);
+  m.impl("decode_attn", &decode_attn);
+}

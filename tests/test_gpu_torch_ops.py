@@ -1,0 +1,75 @@
+"""torch.library.opcheck of the logo_hip operators on the GPU: schema, fake
+kernel against the real one, and dispatch under AOTAutograd with dynamic
+shapes; plus sq_full_attn under torch.compile matching eager."""
+
+import pytest
+import torch
+
+from logo_amd import _torch_ops
+from logo_amd.ops import sq_full_attn
+from logo_amd.ops.common import compact_selection
+from tests.helpers import gen, randn
+
+pytestmark = pytest.mark.gpu
+
+_CHECKS = ("test_schema", "test_faketensor", "test_aot_dispatch_dynamic")
+
+
+def _inputs(dev, n=700, hq=4, h=2, d=128):
+    g = gen(40)
+    q, k, v, do = (randn((n, x, d), g).to(dev) for x in (hq, h, h, hq))
+    sel = (torch.rand(n, generator=g) < 0.4).to(dev)
+    cu = torch.tensor([0, 300, n], dtype=torch.int32, device=dev)
+    return q, k, v, do, sel, cu
+
+
+def test_opcheck_attention_ops(gpu):
+    ops = _torch_ops.ops()
+    q, k, v, do, sel, cu = _inputs(gpu)
+    dsel = compact_selection(sel, cu)
+    torch.library.opcheck(ops.compact.default, (sel.view(torch.uint8), cu), test_utils=_CHECKS)
+    fwd_args = (q, k, v, dsel.q_idx, dsel.pos, dsel.meta, cu, 1, 0.088, -1)
+    torch.library.opcheck(ops.sq_fwd.default, fwd_args, test_utils=_CHECKS)
+    o, lse = ops.sq_fwd(*fwd_args)
+    bwd_args = (q, k, v, o, lse, do, dsel.q_idx, dsel.pos, dsel.meta, cu, 1, 0.088, -1)
+    torch.library.opcheck(ops.sq_bwd.default, bwd_args, test_utils=_CHECKS)
+    # the per-phase ops pass workspaces whose rows past Sq are unspecified
+    # (q_sel, do_sel): schema and fake kernel only
+    phase = ("test_schema", "test_faketensor")
+    torch.library.opcheck(ops.sq_bwd_delta.default, bwd_args, test_utils=phase)
+    ws = ops.sq_bwd_delta(*bwd_args)
+    torch.library.opcheck(ops.sq_bwd_dq.default, (*bwd_args, *ws), test_utils=phase)
+    torch.library.opcheck(ops.sq_bwd_dkv.default, (*bwd_args, *ws), test_utils=phase)
+    # and the phases give what the whole backward gives
+    dq, dk, dv = ops.sq_bwd(*bwd_args)
+    assert torch.equal(dq, ops.sq_bwd_dq(*bwd_args, *ws))
+    assert all(torch.equal(a, b) for a, b in zip((dk, dv), ops.sq_bwd_dkv(*bwd_args, *ws)))
+
+
+def test_opcheck_epilogue_and_decode(gpu):
+    ops = _torch_ops.ops()
+    g = gen(41)
+    n, hq, d = 257, 4, 128
+    L, G = randn((n, hq, d), g).to(gpu), randn((n, hq, d), g).to(gpu)
+    gate = torch.rand(n, generator=g).bfloat16().to(gpu)
+    th = torch.tensor([0.5], dtype=torch.bfloat16, device=gpu)
+    w = (1 + 0.1 * torch.randn(d, generator=g)).bfloat16().to(gpu)
+    torch.library.opcheck(ops.epilogue_fwd.default, (L, G, gate, th, w, w, 1e-5), test_utils=_CHECKS)
+    dout = randn((n, hq * d), g).to(gpu)
+    torch.library.opcheck(ops.epilogue_bwd.default, (L, G, gate, th, w, w, dout, 1e-5), test_utils=_CHECKS)
+    q = randn((3, hq, d), g).to(gpu)
+    cache = randn((3, 2, 600, d), g).to(gpu)
+    lens = torch.tensor([1, 600, 333], dtype=torch.int32, device=gpu)
+    torch.library.opcheck(ops.decode_attn.default, (q, cache, cache, lens, gate[:3].contiguous(), th, 600, 0.088),
+                          test_utils=_CHECKS)
+
+
+def test_sq_full_attn_under_torch_compile(gpu):
+    q, k, v, do, sel, cu = _inputs(gpu)
+
+    def f(q, k, v):
+        return sq_full_attn(q[None], k[None], v[None], sel[None], cu_seqlens=cu)[0]
+
+    want = f(q, k, v)
+    got = torch.compile(f)(q, k, v)
+    assert torch.equal(got, want)
