@@ -129,7 +129,12 @@ class EventTimer:
 def cpu_baseline(q, k, v, sel_np, cu, do, heads, flops_per_head):
     from oracle.cpu_path import time_fwd_bwd
 
-    threads = min(16, len(os.sched_getaffinity(0)))
+    # every core the process may run on, within the host's CPU share for this
+    # GPU when the environment states it (OMP_NUM_THREADS; 16 on the GPU boxes)
+    threads = len(os.sched_getaffinity(0))
+    share = os.environ.get("OMP_NUM_THREADS", "")
+    if share.isdigit() and int(share) > 0:
+        threads = min(threads, int(share))
     qs = q[:, :heads].float().cpu()
     ks = k[:, :heads].float().cpu()
     vs = v[:, :heads].float().cpu()
@@ -144,7 +149,8 @@ def cpu_baseline(q, k, v, sel_np, cu, do, heads, flops_per_head):
         "sample": (f"reference CPU formulation (logo/ops/dense_full_attn.py:30-69 dense causal SDPA per "
                    f"segment, then selection mask) in torch fp32 autograd fwd+bwd on {heads} of "
                    f"{q.shape[1]} heads of the same T={q.shape[0]} workload; {secs:.2f} s; effective "
-                   f"FLOPs on selected rows as for the GPU value"),
+                   f"FLOPs on selected rows as for the GPU value; {threads} threads = the process's CPU "
+                   f"affinity capped by OMP_NUM_THREADS"),
     }
 
 

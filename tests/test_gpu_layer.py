@@ -163,3 +163,42 @@ def test_layer_padding_mask_fwd_bwd(gpu, backend):
                  "context_norm_local.weight", "context_norm_global.weight"):
         prm = dict(layer.named_parameters())[name]
         assert_close(name, params[name].grad, prm.grad.double().cpu(), 1e-2)
+
+
+@pytest.mark.parametrize("backend", ["hip", "flash"])
+def test_layer_scale_offset_fwd_bwd(gpu, backend):
+    """global_qk_param="scale_offset" (logo/layers/logo.py:80-84): the global
+    q / k / v as per-channel affine maps of the local ones, against the float64
+    restatement: outputs, dh and every parameter gradient, the six scale /
+    offset vectors included.  The k / v offset gradients sum dK / dV over every
+    key: before RoPE, sum_k dK = scale sum_q q sum_k dS_qk = 0 exactly, so
+    d(k_offset) is the small RoPE-weighted residual of large cancelling terms
+    (ill-conditioned like gate_proj's 2048-term dot product), and the offsets
+    take gate_proj's bound, 2e-2."""
+    cfg = LoGoConfig(hidden_size=512, num_attention_heads=4, num_hidden_layers=1, global_qk_param="scale_offset",
+                     sparse_full_attn_backend=backend, gate_thres_init=0.5)
+    layer = _make(cfg, gpu, 21)
+    with torch.no_grad():
+        g0 = torch.Generator(device=gpu).manual_seed(22)
+        for name, prm in layer.named_parameters():
+            if "global_scale" in name or "global_offset" in name:
+                prm.add_((0.1 * torch.randn(prm.shape, generator=g0, device=gpu)).to(prm.dtype))
+    layer.train()
+    B, T = 2, 170
+    g = gen(23)
+    h = torch.randn(B, T, cfg.hidden_size, generator=g).bfloat16().to(gpu).requires_grad_()
+    dout = torch.randn(B, T, cfg.hidden_size, generator=g).bfloat16().to(gpu)
+    out, _, _ = layer(h)
+    out.backward(dout)
+    with torch.no_grad():
+        gate_gpu = torch.sigmoid(layer.gate_proj(h)).view(B, T)
+    params = {n: p.detach().double().cpu().requires_grad_() for n, p in layer.named_parameters()}
+    sel = (gate_gpu >= layer.gate_thres).cpu()
+    h64 = h.detach().double().cpu().requires_grad_()
+    ref = logo_layer_ref(h64, params, cfg, sel, backend=backend)
+    ref.backward(dout.double().cpu())
+    _scaled("out", out, ref)
+    _scaled("dh", h.grad, h64.grad)
+    for name, prm in layer.named_parameters():
+        tol = 2e-2 if name == "gate_proj.weight" or "global_offset" in name else 1e-2
+        assert_close(name, params[name].grad, prm.grad.double().cpu(), tol)
