@@ -47,6 +47,7 @@ extern "C" {
 
 #define LOGO_DTYPE_BF16 0
 #define LOGO_DTYPE_F32 1
+#define LOGO_DTYPE_F16 2
 
 /* Message of the calling thread's last error ("" if none). */
 const char* logo_last_error(void);
@@ -122,6 +123,10 @@ int logo_q_start_blk(const int32_t* pos, const int32_t* cu_q, const int32_t* chu
  * the reference keeps separate (V, :341) and which must equal d here: every
  * kernel strides all of them by d.  The Python op zero-pads other K, V <= 128
  * to 64 or 128 before it calls this.
+ * dtype: LOGO_DTYPE_BF16, or LOGO_DTYPE_F16 in sparse mode without a window
+ * (the reference's dots run in the input dtype, :80 :108); every 16-bit
+ * tensor of the call (q, k, v, o, and for the backward dout, q_sel, do_sel,
+ * dq, dk, dv) holds that type.
  */
 int logo_sq_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
                 const int64_t* q_idx, const int32_t* pos, const int32_t* meta,
@@ -135,7 +140,8 @@ int logo_sq_fwd(const void* q, const void* k, const void* v, void* o, float* lse
  * fused), every row of dk and dv [N, H, D], and the workspaces delta [HQ, N]
  * fp32 and, in sparse mode, q_sel / do_sel [HQ, N, D] bf16: compacted copies
  * of the selected q and dO rows (the reference's q_sel / do_sel, :461 :483),
- * filled by the delta phase.  Dense mode ignores q_sel / do_sel.
+ * filled by the delta phase, of the call's dtype.  Dense mode ignores q_sel /
+ * do_sel.
  */
 int logo_sq_bwd(const void* q, const void* k, const void* v, const void* o,
     const void* dout, const float* lse, float* delta, void* q_sel, void* do_sel,

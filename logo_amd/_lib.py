@@ -69,6 +69,7 @@ BKV = 128
 META_HDR = 8
 DTYPE_BF16 = 0
 DTYPE_F32 = 1
+DTYPE_F16 = 2
 
 
 def thres_arg(thres: torch.Tensor):

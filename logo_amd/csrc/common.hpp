@@ -22,6 +22,10 @@ namespace logo {
 typedef __bf16 bf16;
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16;
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef __fp16 hf16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -31,6 +35,34 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 constexpr int kBQ = 128;   // compacted query rows per workgroup (fwd, dq)
 constexpr int kBKV = 128;  // keys per workgroup (dkv)
 constexpr int kMetaHdr = 8;
+
+typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
+typedef __attribute__((address_space(3))) hf16x4 lds_hf16x4;
+
+// The 16-bit element types the attention kernels compute in: bf16, and fp16
+// for fp16 callers (the reference's dots run in the input dtype,
+// logo/ops/selected_full_attn.py:95-99).  Storage is 16 bits either way, so
+// pointers stay bf16* and only values, MFMAs and conversions change.
+template <typename E>
+struct Elem;
+template <>
+struct Elem<bf16> {
+  using x8 = bf16x8;
+  using x4 = bf16x4;
+  static constexpr bool kHalf = false;
+  __device__ __forceinline__ static f32x16 mfma(x8 a, x8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+};
+template <>
+struct Elem<f16> {
+  using x8 = f16x8;
+  using x4 = f16x4;
+  static constexpr bool kHalf = true;
+  __device__ __forceinline__ static f32x16 mfma(x8 a, x8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+};
 
 // D += A * B (v_mfma_f32_32x32x16_bf16) with D held in AGPRs, for
 // accumulators that only MFMAs touch inside the loop (the other MFMAs of a
@@ -44,6 +76,9 @@ constexpr int kMetaHdr = 8;
 // written it, so the ISA of these kernels is checked for in-loop copies.
 __device__ __forceinline__ void mfma32_agpr(f32x16& d, const bf16x8& a, const bf16x8& b) {
   asm volatile("s_nop 2\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(d) : "v"(a), "v"(b));
+}
+__device__ __forceinline__ void mfma32_agpr(f32x16& d, const f16x8& a, const f16x8& b) {
+  asm volatile("s_nop 2\n\tv_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+a"(d) : "v"(a), "v"(b));
 }
 // Wait states between the last mfma32_agpr and a VALU read of its result
 // (an 8-pass MFMA needs fewer than 32).  The compiler may place its own
@@ -88,12 +123,15 @@ __device__ __forceinline__ float pair_min(float x) {
 // Eight bf16 values times s, each rounded back to bf16 (the pre-scaled query
 // rows of the sparse path: the forward's registers and the backward's
 // compacted copies are made by this same rounding).
-__device__ __forceinline__ bf16x8 scale_bf16x8(const bf16x8 v, float s) {
-  bf16x8 r;
+template <typename V>
+__device__ __forceinline__ V scale8(const V v, float s) {
+  using T = std::remove_cv_t<std::remove_reference_t<decltype(v[0])>>;
+  V r;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) r[e] = (bf16)((float)v[e] * s);
+  for (int e = 0; e < 8; ++e) r[e] = (T)((float)v[e] * s);
   return r;
 }
+__device__ __forceinline__ bf16x8 scale_bf16x8(const bf16x8 v, float s) { return scale8(v, s); }
 
 // Anchors a value at this point of the instruction stream (an empty asm
 // statement that reads and rewrites it): arithmetic on it cannot be hoisted
@@ -115,21 +153,22 @@ __device__ __forceinline__ void static_for(F&& f) {
 
 __device__ __forceinline__ int rowmap(int g, int j) { return 8 * (j >> 2) + 4 * g + (j & 3); }
 
-__device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
-}
+__device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) { return Elem<bf16>::mfma(a, b, c); }
+__device__ __forceinline__ f32x16 mfma32(f16x8 a, f16x8 b, f32x16 c) { return Elem<f16>::mfma(a, b, c); }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 
-// Eight accumulator items (8h .. 8h+7 of a 32x32 tile) as a bf16 operand.
-__device__ __forceinline__ bf16x8 acc_to_bf16(const f32x16& a, int h) {
-  bf16x8 r;
+// Eight accumulator items (8h .. 8h+7 of a 32x32 tile) as a 16-bit operand.
+template <typename E = bf16>
+__device__ __forceinline__ typename Elem<E>::x8 acc_to(const f32x16& a, int h) {
+  typename Elem<E>::x8 r;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) r[e] = (bf16)a[8 * h + e];
+  for (int e = 0; e < 8; ++e) r[e] = (E)a[8 * h + e];
   return r;
 }
+__device__ __forceinline__ bf16x8 acc_to_bf16(const f32x16& a, int h) { return acc_to<bf16>(a, h); }
 
 // LDS tile layouts.  gfx950's LDS serves 64 four-byte banks per cycle:
 // ds_read_b128 16 lanes per cycle, ds_read_b64_tr_b16 32 lanes per cycle.
@@ -278,8 +317,6 @@ struct TileBufDma {
 // above) to land.
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0); }
 
-typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
-
 // LDS reads through a restrict pointer: inlining gives the read
 // alias-scope metadata, without which the compiler's wait-count insertion
 // treats it as possibly reading LDS that an in-flight global->LDS copy (the
@@ -292,6 +329,9 @@ __device__ __attribute__((always_inline)) inline T lds_load(const T* __restrict_
 }
 __device__ __attribute__((always_inline)) inline bf16x4 ds_read_tr(const lds_bf16x4* __restrict__ p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4bf16(const_cast<lds_bf16x4*>(p));
+}
+__device__ __attribute__((always_inline)) inline f16x4 ds_read_tr(const lds_hf16x4* __restrict__ p) {
+  return __builtin_bit_cast(f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4f16(const_cast<lds_hf16x4*>(p)));
 }
 
 // MFMA operand reads from a tile, with every lane-dependent part of the
@@ -334,16 +374,20 @@ struct TileReader {
     }
   }
 
-  __device__ __forceinline__ bf16x8 row(const bf16* tile, int rbase, int ks) const {
+  // E: the element type the tile holds (its storage is addressed as bf16)
+  template <typename E = bf16>
+  __device__ __forceinline__ typename Elem<E>::x8 row(const bf16* tile, int rbase, int ks) const {
     const int o = SWZ ? rbase * Geo::RS + row_off[ks] : rbase * Geo::RS + 16 * ks + row_off[0];
-    return lds_load(reinterpret_cast<const bf16x8*>(tile + o));
+    return lds_load(reinterpret_cast<const typename Elem<E>::x8*>(tile + o));
   }
 
-  __device__ __forceinline__ bf16x8 tr(const bf16* tile, int r0, int dt) const {
+  template <typename E = bf16>
+  __device__ __forceinline__ typename Elem<E>::x8 tr(const bf16* tile, int r0, int dt) const {
+    using L4 = std::conditional_t<Elem<E>::kHalf, lds_hf16x4, lds_bf16x4>;
     const int o0 = SWZ ? r0 * Geo::RS + tr_off[2 * dt] : r0 * Geo::RS + 32 * dt + tr_off[0];
     const int o1 = SWZ ? r0 * Geo::RS + tr_off[2 * dt + 1] : o0 + 8 * Geo::RS;
-    const bf16x4 lo = ds_read_tr((const lds_bf16x4*)(tile + o0));
-    const bf16x4 hi = ds_read_tr((const lds_bf16x4*)(tile + o1));
+    const auto lo = ds_read_tr((const L4*)(tile + o0));
+    const auto hi = ds_read_tr((const L4*)(tile + o1));
     return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
   }
 };

@@ -41,12 +41,13 @@ namespace logo {
 
 // ---------------------------------------------------------------------------
 // Backward preprocess: delta = rowsum(o * dO) per compacted row (fp32); in
-// sparse mode also the compacted copies q_sel = bf16(-scale log2(e) q) and
+// sparse mode also the compacted copies q_sel = round(-scale log2(e) q) and
 // do_sel = -dO, which let the dq and dk/dv kernels start their S and dP
 // accumulators from lse and delta.
 // ---------------------------------------------------------------------------
-template <int D, bool SPARSE>
+template <typename EL, int D, bool SPARSE>
 __global__ __launch_bounds__(256) void sq_delta_kernel(const AttnArgs a) {
+  using E8 = typename Elem<EL>::x8;
   constexpr int LPR = D / 8;          // lanes per row
   constexpr int RPB = 256 / LPR;      // rows per workgroup
   const int hq = blockIdx.y;
@@ -59,20 +60,20 @@ __global__ __launch_bounds__(256) void sq_delta_kernel(const AttnArgs a) {
   if (r < sq) {
     const int64_t t = SPARSE ? a.q_idx[(int64_t)lane_sel * a.n + r] : (int64_t)r;
     const int64_t off = (t * a.hq + hq) * D + 8 * c;
-    const bf16x8 ov = *reinterpret_cast<const bf16x8*>(a.o + off);
-    const bf16x8 dv = *reinterpret_cast<const bf16x8*>(a.dout + off);
+    const E8 ov = *reinterpret_cast<const E8*>(a.o + off);
+    const E8 dv = *reinterpret_cast<const E8*>(a.dout + off);
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc = fmaf((float)ov[e], (float)dv[e], acc);
     if (SPARSE) {
-      // the copies the dq and dk/dv kernels stream: q_sel = bf16(-c q) with
+      // the copies the dq and dk/dv kernels stream: q_sel = round(-c q) with
       // c = scale * log2(e), do_sel = -dO (exact)
       const int64_t soff = ((int64_t)hq * a.n + r) * D + 8 * c;
-      const bf16x8 qv = *reinterpret_cast<const bf16x8*>(a.q + off);
-      bf16x8 dn;
+      const E8 qv = *reinterpret_cast<const E8*>(a.q + off);
+      E8 dn;
 #pragma unroll
       for (int e = 0; e < 8; ++e) dn[e] = -dv[e];
-      *reinterpret_cast<bf16x8*>(a.do_sel + soff) = dn;
-      *reinterpret_cast<bf16x8*>(a.q_sel + soff) = scale_bf16x8(qv, -a.scale_log2);
+      *reinterpret_cast<E8*>(a.do_sel + soff) = dn;
+      *reinterpret_cast<E8*>(a.q_sel + soff) = scale8(qv, -a.scale_log2);
     }
   }
 #pragma unroll
@@ -80,21 +81,23 @@ __global__ __launch_bounds__(256) void sq_delta_kernel(const AttnArgs a) {
   if (r < sq && c == 0) a.delta[(int64_t)hq * a.n + r] = acc;
 }
 
-template <int D, bool SPARSE>
+template <typename EL, int D, bool SPARSE>
 static int launch_delta(const AttnArgs& a, hipStream_t st) {
   constexpr int RPB = 256 / (D / 8);
   dim3 grid((unsigned)((a.n + RPB - 1) / RPB), a.hq);
-  hipLaunchKernelGGL((sq_delta_kernel<D, SPARSE>), grid, dim3(256), 0, st, a);
+  hipLaunchKernelGGL((sq_delta_kernel<EL, D, SPARSE>), grid, dim3(256), 0, st, a);
   LOGO_LAUNCH_CHECK("sq_delta_kernel");
   return LOGO_OK;
 }
 
-int sq_launch_delta(const AttnArgs& a, hipStream_t st, int d, bool sparse) {
-  return d == 128 ? (sparse ? launch_delta<128, true>(a, st) : launch_delta<128, false>(a, st))
-                  : (sparse ? launch_delta<64, true>(a, st) : launch_delta<64, false>(a, st));
+int sq_launch_delta(const AttnArgs& a, hipStream_t st, int d, bool sparse, bool half) {
+  if (half) return d == 128 ? launch_delta<f16, 128, true>(a, st) : launch_delta<f16, 64, true>(a, st);
+  return d == 128 ? (sparse ? launch_delta<bf16, 128, true>(a, st) : launch_delta<bf16, 128, false>(a, st))
+                  : (sparse ? launch_delta<bf16, 64, true>(a, st) : launch_delta<bf16, 64, false>(a, st));
 }
 
-static int check_common(int64_t n, int nseq, int hq, int h, int d, int v_dim, int lanes, int dtype) {
+static int check_common(int64_t n, int nseq, int hq, int h, int d, int v_dim, int lanes, int dtype,
+                        bool sparse, int window) {
   LOGO_REQUIRE(n > 0 && n < ((int64_t)1 << 31), "n_tokens out of range: %lld", (long long)n);
   LOGO_REQUIRE(nseq >= 1, "nseq must be >= 1");
   LOGO_REQUIRE(h >= 1 && hq >= h && hq % h == 0, "HQ (%d) must be a multiple of H (%d)", hq, h);
@@ -102,7 +105,10 @@ static int check_common(int64_t n, int nseq, int hq, int h, int d, int v_dim, in
   // every kernel strides q, k, v, o and the gradients by the one head dim d
   LOGO_REQUIRE(v_dim == d, "value head dim %d must equal the key head dim %d", v_dim, d);
   LOGO_REQUIRE(lanes == 1 || lanes == hq, "lanes must be 1 or HQ");
-  LOGO_REQUIRE(dtype == LOGO_DTYPE_BF16, "only bf16 tensors are supported");
+  LOGO_REQUIRE(dtype == LOGO_DTYPE_BF16 || dtype == LOGO_DTYPE_F16, "dtype %d unsupported (bf16 or fp16)", dtype);
+  // fp16 kernels exist for the query-sparse global branch (no window)
+  LOGO_REQUIRE(dtype == LOGO_DTYPE_BF16 || (sparse && window < 0),
+               "fp16 is supported on the query-sparse path without a window only");
   return LOGO_OK;
 }
 
@@ -138,7 +144,7 @@ extern "C" int logo_sq_fwd(const void* q, const void* k, const void* v, void* o,
                            const int64_t* q_idx, const int32_t* pos, const int32_t* meta,
                            const int32_t* cu, int64_t n_tokens, int nseq, int hq, int h, int d,
                            int v_dim, int lanes, float scale, int window, int dtype, void* stream) {
-  int rc = check_common(n_tokens, nseq, hq, h, d, v_dim, lanes, dtype);
+  int rc = check_common(n_tokens, nseq, hq, h, d, v_dim, lanes, dtype, q_idx != nullptr, window);
   if (rc != LOGO_OK) return rc;
   LOGO_REQUIRE(q && k && v && o && lse && meta && cu, "null pointer argument");
   LOGO_REQUIRE((q_idx == nullptr) == (pos == nullptr), "q_idx and pos must both be set or both be null");
@@ -147,7 +153,7 @@ extern "C" int logo_sq_fwd(const void* q, const void* k, const void* v, void* o,
   a.lse = lse;
   const bool sparse = q_idx != nullptr;
   const bool win = window >= 0;
-  return sq_launch_fwd(a, as_stream(stream), d, sparse, win);
+  return sq_launch_fwd(a, as_stream(stream), d, sparse, win, dtype == LOGO_DTYPE_F16);
 }
 
 #define LOGO_BWD_PARAMS                                                                        \
@@ -161,7 +167,7 @@ extern "C" int logo_sq_fwd(const void* q, const void* k, const void* v, void* o,
       h, d, v_dim, lanes, scale, window, dtype, stream
 
 static int bwd_entry(LOGO_BWD_PARAMS, int phase) {
-  int rc = check_common(n_tokens, nseq, hq, h, d, v_dim, lanes, dtype);
+  int rc = check_common(n_tokens, nseq, hq, h, d, v_dim, lanes, dtype, q_idx != nullptr, window);
   if (rc != LOGO_OK) return rc;
   LOGO_REQUIRE(q && k && v && o && dout && lse && delta && meta && cu, "null pointer argument");
   // each phase needs the outputs it writes: dq (phase 1), dk / dv (phase 2)
@@ -181,16 +187,17 @@ static int bwd_entry(LOGO_BWD_PARAMS, int phase) {
   a.dv = static_cast<bf16*>(dv);
   const bool sparse = q_idx != nullptr;
   const bool win = window >= 0;
+  const bool half = dtype == LOGO_DTYPE_F16;
   hipStream_t st = as_stream(stream);
   if (phase < 0 || phase == 0) {
-    rc = sq_launch_delta(a, st, d, sparse);
+    rc = sq_launch_delta(a, st, d, sparse, half);
     if (rc != LOGO_OK) return rc;
   }
   if (phase < 0 || phase == 1) {
-    rc = sq_launch_dq(a, st, d, sparse, win);
+    rc = sq_launch_dq(a, st, d, sparse, win, half);
     if (rc != LOGO_OK) return rc;
   }
-  if (phase < 0 || phase == 2) rc = sq_launch_dkv(a, st, d, sparse, win);
+  if (phase < 0 || phase == 2) rc = sq_launch_dkv(a, st, d, sparse, win, half);
   return rc;
 }
 

@@ -155,11 +155,12 @@ static inline hipError_t allow_smem(K kernel, size_t bytes) {
 }
 
 // Per-phase launchers (d = 64 or 128; sparse: compacted rows; window: a
-// sliding window is set).  Each returns LOGO_OK or an error code.
-int sq_launch_fwd(const AttnArgs& a, hipStream_t st, int d, bool sparse, bool window);
-int sq_launch_delta(const AttnArgs& a, hipStream_t st, int d, bool sparse);
-int sq_launch_dq(const AttnArgs& a, hipStream_t st, int d, bool sparse, bool window);
-int sq_launch_dkv(const AttnArgs& a, hipStream_t st, int d, bool sparse, bool window);
+// sliding window is set; half: fp16 elements, sparse without a window only,
+// else bf16).  Each returns LOGO_OK or an error code.
+int sq_launch_fwd(const AttnArgs& a, hipStream_t st, int d, bool sparse, bool window, bool half);
+int sq_launch_delta(const AttnArgs& a, hipStream_t st, int d, bool sparse, bool half);
+int sq_launch_dq(const AttnArgs& a, hipStream_t st, int d, bool sparse, bool window, bool half);
+int sq_launch_dkv(const AttnArgs& a, hipStream_t st, int d, bool sparse, bool window, bool half);
 
 // Calls FN<D, SPARSE, WINDOW>(a, st) for the runtime (d, sparse, window).
 #define LOGO_DISPATCH(FN, a, st, d, sparse, window)                                                  \

@@ -19,8 +19,10 @@ constexpr int kDkvStages = 2;
 template <int D>
 constexpr int dkv_stage_bytes() { return 2 * kDkvRows * D * 2 + 3 * kDkvRows * 4; }
 
-template <int D, bool SPARSE, bool WINDOW>
+template <typename EL, int D, bool SPARSE, bool WINDOW>
 __global__ __launch_bounds__(256) LOGO_OCC_DKV void sq_dkv_kernel(const AttnArgs a) {
+  using E8 = typename Elem<EL>::x8;
+  using E4 = typename Elem<EL>::x4;
   constexpr int DS = D / 16, DT = D / 32;
   using GQ = TileGeom<D, kSwz>;  // Q and dO read along rows (S, dP) and transposed (dK, dV)
   char* const smem_b = logo_smem;
@@ -63,13 +65,13 @@ __global__ __launch_bounds__(256) LOGO_OCC_DKV void sq_dkv_kernel(const AttnArgs
   const float dk_mul = NEG ? a.scale / a.scale_log2 : a.scale;
   const float dv_mul = NEG ? -1.f : 1.f;
 
-  bf16x8 kreg[DS], vreg[DS];
+  E8 kreg[DS], vreg[DS];
   {
     const int64_t off = ((int64_t)(bos + key) * a.h + h) * D + 8 * g;
 #pragma unroll
     for (int ds = 0; ds < DS; ++ds) {
-      kreg[ds] = valid_k ? *reinterpret_cast<const bf16x8*>(a.k + off + 16 * ds) : bf16x8{};
-      vreg[ds] = valid_k ? *reinterpret_cast<const bf16x8*>(a.v + off + 16 * ds) : bf16x8{};
+      kreg[ds] = valid_k ? *reinterpret_cast<const E8*>(a.k + off + 16 * ds) : E8{};
+      vreg[ds] = valid_k ? *reinterpret_cast<const E8*>(a.v + off + 16 * ds) : E8{};
     }
   }
   f32x16 dkacc[DT], dvacc[DT];
@@ -169,22 +171,22 @@ __global__ __launch_bounds__(256) LOGO_OCC_DKV void sq_dkv_kernel(const AttnArgs
         constexpr int IPD = 16 / DS;        // dS items per slot (over one block)
         static_assert(IPP * 2 * DS == 16 && IPD * DS == 16, "a half has 16 row items per lane");
         f32x16 sacc[2], pacc[2];
-        bf16x8 pbf[2][2], dbf[2][2];  // [half][hh]
-        bf16x8 opA[NSUB * 2 * NS];    // S/dP operands: Q rows / dO rows
-        bf16x8 opC[NSUB * 2 * NS];    // dV/dK operands: dO^T / Q^T
+        E8 pbf[2][2], dbf[2][2];  // [half][hh]
+        E8 opA[NSUB * 2 * NS];    // S/dP operands: Q rows / dO rows
+        E8 opC[NSUB * 2 * NS];    // dV/dK operands: dO^T / Q^T
         f32x4 l4[NSUB][2][4], d4[NSUB][2][4];
         int4 p4[NSUB][2][4];
         // A operand a of sub-tile u: half a / NS; S (first DS) or dP (next DS), k-step a % DS
         auto load_a = [&](auto u_c, auto a_c) {
           constexpr int U = decltype(u_c)::value, A = decltype(a_c)::value;
           constexpr int QQ = A / NS, KK = A % NS;
-          opA[U * 2 * NS + A] = rd.row(KK >= DS ? ob : qb, 64 * U + 32 * QQ, KK % DS);
+          opA[U * 2 * NS + A] = rd.template row<EL>(KK >= DS ? ob : qb, 64 * U + 32 * QQ, KK % DS);
         };
         // C operand c of sub-tile u: half c / NS; dV (first DS) or dK (next DS); hh, dt
         auto load_c = [&](auto u_c, auto c_c) {
           constexpr int U = decltype(u_c)::value, C = decltype(c_c)::value;
           constexpr int QQ = C / NS, KK = C % NS, HH = (KK % DS) / DT, DTI = KK % DT;
-          opC[U * 2 * NS + C] = rd.tr(KK >= DS ? qb : ob, 64 * U + 16 * (2 * QQ + HH), DTI);
+          opC[U * 2 * NS + C] = rd.template tr<EL>(KK >= DS ? qb : ob, 64 * U + 16 * (2 * QQ + HH), DTI);
         };
         // the operand first used at slot T
         auto load_for_slot = [&](auto t_c) {
@@ -221,7 +223,7 @@ __global__ __launch_bounds__(256) LOGO_OCC_DKV void sq_dkv_kernel(const AttnArgs
         auto mfma_a = [&](auto u_c, auto a_c) {
           constexpr int U = decltype(u_c)::value, A = decltype(a_c)::value;
           constexpr int QQ = A / NS, KK = A % NS;
-          bf16x8 op = opA[U * 2 * NS + A];
+          E8 op = opA[U * 2 * NS + A];
           pin(op);
           if constexpr (KK < DS) {
             const f32x16 c0 = NEG ? cat16(l4[U][QQ]) : f32x16{};
@@ -234,7 +236,7 @@ __global__ __launch_bounds__(256) LOGO_OCC_DKV void sq_dkv_kernel(const AttnArgs
         auto mfma_c = [&](auto u_c, auto c_c) {
           constexpr int U = decltype(u_c)::value, C = decltype(c_c)::value;
           constexpr int QQ = C / NS, KK = C % NS, HH = (KK % DS) / DT, DTI = KK % DT;
-          bf16x8 op = opC[U * 2 * NS + C];
+          E8 op = opC[U * 2 * NS + C];
           pin(op);
           if constexpr (KK < DS) mfma32_agpr(dvacc[DTI], op, pbf[QQ][HH]);
           else mfma32_agpr(dkacc[DTI], op, dbf[QQ][HH]);
@@ -258,8 +260,8 @@ __global__ __launch_bounds__(256) LOGO_OCC_DKV void sq_dkv_kernel(const AttnArgs
           pin(pv);
           sacc[qq][JJ] = pv;
           if constexpr (JJ % 2 == 1) {
-            pbf[qq][JJ / 8][JJ % 8 - 1] = (bf16)sacc[qq][JJ - 1];
-            pbf[qq][JJ / 8][JJ % 8] = (bf16)pv;
+            pbf[qq][JJ / 8][JJ % 8 - 1] = (EL)sacc[qq][JJ - 1];
+            pbf[qq][JJ / 8][JJ % 8] = (EL)pv;
           }
         };
         auto ds_item = [&](auto u_c, int qq, auto jj_c) {
@@ -273,8 +275,8 @@ __global__ __launch_bounds__(256) LOGO_OCC_DKV void sq_dkv_kernel(const AttnArgs
           pin(dsv);
           pacc[qq][JJ] = dsv;
           if constexpr (JJ % 2 == 1) {
-            dbf[qq][JJ / 8][JJ % 8 - 1] = (bf16)pacc[qq][JJ - 1];
-            dbf[qq][JJ / 8][JJ % 8] = (bf16)dsv;
+            dbf[qq][JJ / 8][JJ % 8 - 1] = (EL)pacc[qq][JJ - 1];
+            dbf[qq][JJ / 8][JJ % 8] = (EL)dsv;
           }
         };
         // stats of (sub-tile u, half qq, group m) are read DS/2 slots before
@@ -367,14 +369,14 @@ __global__ __launch_bounds__(256) LOGO_OCC_DKV void sq_dkv_kernel(const AttnArgs
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
       for (int q4 = 0; q4 < 4; ++q4) {
-        bf16x4 kv, vv;
+        E4 kv, vv;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          kv[e] = (bf16)(dkacc[dt][4 * q4 + e] * dk_mul);
-          vv[e] = (bf16)(dvacc[dt][4 * q4 + e] * dv_mul);
+          kv[e] = (EL)(dkacc[dt][4 * q4 + e] * dk_mul);
+          vv[e] = (EL)(dvacc[dt][4 * q4 + e] * dv_mul);
         }
-        *reinterpret_cast<bf16x4*>(a.dk + off + 32 * dt + 8 * q4 + 4 * g) = kv;
-        *reinterpret_cast<bf16x4*>(a.dv + off + 32 * dt + 8 * q4 + 4 * g) = vv;
+        *reinterpret_cast<E4*>(a.dk + off + 32 * dt + 8 * q4 + 4 * g) = kv;
+        *reinterpret_cast<E4*>(a.dv + off + 32 * dt + 8 * q4 + 4 * g) = vv;
       }
   }
 }
@@ -382,18 +384,22 @@ __global__ __launch_bounds__(256) LOGO_OCC_DKV void sq_dkv_kernel(const AttnArgs
 template <int D>
 constexpr size_t dkv_smem() { return (size_t)kDkvStages * dkv_stage_bytes<D>(); }
 
-template <int D, bool SPARSE, bool WINDOW>
+template <typename EL, int D, bool SPARSE, bool WINDOW>
 static int launch_dkv(const AttnArgs& a, hipStream_t st) {
   const int64_t ntmax = (a.n + kBKV - 1) / kBKV + a.nseq;
-  auto kern = sq_dkv_kernel<D, SPARSE, WINDOW>;
+  auto kern = sq_dkv_kernel<EL, D, SPARSE, WINDOW>;
   LOGO_HIP_CHECK(allow_smem(kern, dkv_smem<D>()));
   hipLaunchKernelGGL(kern, dim3((unsigned)(ntmax * a.h)), dim3(256), dkv_smem<D>(), st, a);
   LOGO_LAUNCH_CHECK("sq_dkv_kernel");
   return LOGO_OK;
 }
 
-int sq_launch_dkv(const AttnArgs& a, hipStream_t st, int d, bool sparse, bool window) {
-  return LOGO_DISPATCH(launch_dkv, a, st, d, sparse, window);
+template <int D, bool SPARSE, bool WINDOW>
+static int launch_dkv_bf16(const AttnArgs& a, hipStream_t st) { return launch_dkv<bf16, D, SPARSE, WINDOW>(a, st); }
+
+int sq_launch_dkv(const AttnArgs& a, hipStream_t st, int d, bool sparse, bool window, bool half) {
+  if (half) return d == 128 ? launch_dkv<f16, 128, true, false>(a, st) : launch_dkv<f16, 64, true, false>(a, st);
+  return LOGO_DISPATCH(launch_dkv_bf16, a, st, d, sparse, window);
 }
 
 }  // namespace logo

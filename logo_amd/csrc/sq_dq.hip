@@ -21,8 +21,10 @@ namespace logo {
 // K(t + 1) is copied during step (t, 0), after K(t - 1)'s last read (step
 // (t - 1, 1)); V(t + 2) during step (t, 1), after V(t)'s last read (step
 // (t, 0)).  Every step ends with the copy wait and a barrier.
-template <int D, bool SPARSE, bool WINDOW>
+template <typename EL, int D, bool SPARSE, bool WINDOW>
 __global__ __launch_bounds__(128) LOGO_OCC_DQ64 void sq_dq64_kernel(const AttnArgs a) {
+  using E8 = typename Elem<EL>::x8;
+  using E4 = typename Elem<EL>::x4;
   constexpr int DS = D / 16, DT = D / 32;
   constexpr int NX = 2 * DS;    // X slots: K row operand (even), V row operand (odd)
   constexpr int NY = 2 * DT;    // Y slots: K^T operands (16-key step hh, column block dt)
@@ -46,7 +48,7 @@ __global__ __launch_bounds__(128) LOGO_OCC_DQ64 void sq_dq64_kernel(const AttnAr
     pr[b] = vr[b] ? qt.rv.posn(rr[b]) : -1;
   }
 
-  bf16x8 qreg[2][DS], doreg[2][DS];
+  E8 qreg[2][DS], doreg[2][DS];
   float lse_q[2], delta_q[2];
   {
     const QSide<D, SPARSE> qs(a, a.q_sel, a.q, hq), os(a, a.do_sel, a.dout, hq);
@@ -57,8 +59,8 @@ __global__ __launch_bounds__(128) LOGO_OCC_DQ64 void sq_dq64_kernel(const AttnAr
       const bf16* orow = os.row(rc) + 8 * g;
 #pragma unroll
       for (int ds = 0; ds < DS; ++ds) {
-        qreg[b][ds] = vr[b] ? *reinterpret_cast<const bf16x8*>(qrow + 16 * ds) : bf16x8{};
-        doreg[b][ds] = vr[b] ? *reinterpret_cast<const bf16x8*>(orow + 16 * ds) : bf16x8{};
+        qreg[b][ds] = vr[b] ? *reinterpret_cast<const E8*>(qrow + 16 * ds) : E8{};
+        doreg[b][ds] = vr[b] ? *reinterpret_cast<const E8*>(orow + 16 * ds) : E8{};
       }
       lse_q[b] = vr[b] ? a.lse[(int64_t)hq * a.n + rr[b]] : 0.f;
       delta_q[b] = vr[b] ? a.delta[(int64_t)hq * a.n + rr[b]] : 0.f;
@@ -85,7 +87,7 @@ __global__ __launch_bounds__(128) LOGO_OCC_DQ64 void sq_dq64_kernel(const AttnAr
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) dqacc[b][dt] = f32x16{};
   f32x16 sp[2][2][2];  // [half parity][row block][S, dP]
-  bf16x8 dsb[2][2];    // dS of the current half as B operands [row block][16-key step]
+  E8 dsb[2][2];    // dS of the current half as B operands [row block][16-key step]
 
   TileReader<D, kSwz> rd;
   rd.init();
@@ -128,14 +130,14 @@ __global__ __launch_bounds__(128) LOGO_OCC_DQ64 void sq_dq64_kernel(const AttnAr
       constexpr bool DOX = decltype(dox_tag)::value;    // S / dP of the next half
       constexpr bool DOV = decltype(dov_tag)::value;    // dS and dQ of the current half
       constexpr bool MASK = decltype(mask_tag)::value;  // the current half crosses a mask edge
-      bf16x8 op[NX + NY];
+      E8 op[NX + NY];
       auto load_op = [&](auto s_c) {
         constexpr int S = decltype(s_c)::value;
         if constexpr (S < NX) {
-          if constexpr (DOX) op[S] = rd.row(S % 2 ? vx : kx, XR, S / 2);
+          if constexpr (DOX) op[S] = rd.template row<EL>(S % 2 ? vx : kx, XR, S / 2);
         } else {
           constexpr int Y = S - NX;
-          if constexpr (DOV) op[S] = rd.tr(ky, 32 * H + 16 * (Y / DT), Y % DT);
+          if constexpr (DOV) op[S] = rd.template tr<EL>(ky, 32 * H + 16 * (Y / DT), Y % DT);
         }
       };
       static_for<PF>([&](auto s_c) { load_op(s_c); });
@@ -149,7 +151,7 @@ __global__ __launch_bounds__(128) LOGO_OCC_DQ64 void sq_dq64_kernel(const AttnAr
           // one wave per SIMD issues in order: each MFMA is followed by the
           // VALU items of its row block, which run under it
           constexpr int DSI = S / 2, KIND = S % 2;
-          bf16x8 o;
+          E8 o;
           if constexpr (DOX) {
             o = op[S];
             pin(o);
@@ -158,7 +160,7 @@ __global__ __launch_bounds__(128) LOGO_OCC_DQ64 void sq_dq64_kernel(const AttnAr
             constexpr int B = decltype(b_c)::value;
             if constexpr (B == 1) __builtin_amdgcn_sched_barrier(0);
             if constexpr (DOX) {
-              const bf16x8 bop = KIND ? doreg[B][DSI] : qreg[B][DSI];
+              const E8 bop = KIND ? doreg[B][DSI] : qreg[B][DSI];
               const f32x16 c0 = (NEG && !KIND) ? c_lse[B] : f32x16{};
               sp[H ^ 1][B][KIND] = mfma32(o, bop, DSI == 0 ? c0 : sp[H ^ 1][B][KIND]);
             }
@@ -179,14 +181,14 @@ __global__ __launch_bounds__(128) LOGO_OCC_DQ64 void sq_dq64_kernel(const AttnAr
                 pin(dsv);
                 sp[H][B][0][JJ] = pv;
                 sp[H][B][1][JJ] = dsv;
-                if constexpr (JJ % 8 == 7) dsb[B][JJ / 8] = acc_to_bf16(sp[H][B][1], JJ / 8);
+                if constexpr (JJ % 8 == 7) dsb[B][JJ / 8] = acc_to<EL>(sp[H][B][1], JJ / 8);
               });
             }
           });
         } else {
           constexpr int Y = S - NX;
           if constexpr (DOV) {
-            bf16x8 o = op[S];
+            E8 o = op[S];
             pin(o);
             mfma32_agpr(dqacc[0][Y % DT], o, dsb[0][Y / DT]);
             mfma32_agpr(dqacc[1][Y % DT], o, dsb[1][Y / DT]);
@@ -238,10 +240,10 @@ __global__ __launch_bounds__(128) LOGO_OCC_DQ64 void sq_dq64_kernel(const AttnAr
       for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
         for (int q4 = 0; q4 < 4; ++q4) {
-          bf16x4 v;
+          E4 v;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] = (bf16)(dqacc[b][dt][4 * q4 + e] * dq_mul);
-          *reinterpret_cast<bf16x4*>(dqrow + 32 * dt + 8 * q4 + 4 * g) = v;
+          for (int e = 0; e < 4; ++e) v[e] = (EL)(dqacc[b][dt][4 * q4 + e] * dq_mul);
+          *reinterpret_cast<E4*>(dqrow + 32 * dt + 8 * q4 + 4 * g) = v;
         }
     }
   }
@@ -250,18 +252,22 @@ __global__ __launch_bounds__(128) LOGO_OCC_DQ64 void sq_dq64_kernel(const AttnAr
 template <int D>
 constexpr size_t dq_smem() { return (size_t)4 * TileGeom<D, kSwz>::ELEMS * sizeof(bf16); }
 
-template <int D, bool SPARSE, bool WINDOW>
+template <typename EL, int D, bool SPARSE, bool WINDOW>
 static int launch_dq(const AttnArgs& a, hipStream_t st) {
   const int64_t ntmax = (a.n + kBQ - 1) / kBQ + a.nseq;
-  auto kern = sq_dq64_kernel<D, SPARSE, WINDOW>;
+  auto kern = sq_dq64_kernel<EL, D, SPARSE, WINDOW>;
   LOGO_HIP_CHECK(allow_smem(kern, dq_smem<D>()));
   hipLaunchKernelGGL(kern, dim3((unsigned)(ntmax * a.hq)), dim3(128), dq_smem<D>(), st, a);
   LOGO_LAUNCH_CHECK("sq_dq64_kernel");
   return LOGO_OK;
 }
 
-int sq_launch_dq(const AttnArgs& a, hipStream_t st, int d, bool sparse, bool window) {
-  return LOGO_DISPATCH(launch_dq, a, st, d, sparse, window);
+template <int D, bool SPARSE, bool WINDOW>
+static int launch_dq_bf16(const AttnArgs& a, hipStream_t st) { return launch_dq<bf16, D, SPARSE, WINDOW>(a, st); }
+
+int sq_launch_dq(const AttnArgs& a, hipStream_t st, int d, bool sparse, bool window, bool half) {
+  if (half) return d == 128 ? launch_dq<f16, 128, true, false>(a, st) : launch_dq<f16, 64, true, false>(a, st);
+  return LOGO_DISPATCH(launch_dq_bf16, a, st, d, sparse, window);
 }
 
 }  // namespace logo

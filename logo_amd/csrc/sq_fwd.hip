@@ -31,8 +31,10 @@ namespace logo {
 // Masks compare a compile-time offset per accumulator item with one per-lane
 // bound: key j0 + 32 kk + rowmap(g, jj) is visible iff its offset from
 // j0 + 4 g lies in [hi - W, hi], hi = p - j0 - 4 g.
-template <int D, bool SPARSE, bool WINDOW, int NW>
+template <typename EL, int D, bool SPARSE, bool WINDOW, int NW>
 __global__ __launch_bounds__(64 * NW) LOGO_OCC_FWD void sq_fwd_pipe_kernel(const AttnArgs a) {
+  using E8 = typename Elem<EL>::x8;
+  using E4 = typename Elem<EL>::x4;
   constexpr int DS = D / 16, DT = D / 32;
   constexpr int NX = 2 * DS;   // S MFMAs per tile (two 32-key halves x DS k-steps)
   constexpr int NY = 4 * DT;   // PV MFMAs per tile (DT column blocks x 4 key steps)
@@ -62,13 +64,13 @@ __global__ __launch_bounds__(64 * NW) LOGO_OCC_FWD void sq_fwd_pipe_kernel(const
   // from identical products.  Scores are then in the exp2 domain already,
   // masked scores are +inf and the row statistic is a minimum.
   constexpr bool NEG = SPARSE;
-  bf16x8 qreg[DS];
+  E8 qreg[DS];
   {
     const bf16* qrow = a.q + (qt.t * a.hq + hq) * D + 8 * g;
 #pragma unroll
     for (int ds = 0; ds < DS; ++ds) {
-      const bf16x8 qv = qt.valid ? *reinterpret_cast<const bf16x8*>(qrow + 16 * ds) : bf16x8{};
-      qreg[ds] = NEG ? scale_bf16x8(qv, -a.scale_log2) : qv;
+      const E8 qv = qt.valid ? *reinterpret_cast<const E8*>(qrow + 16 * ds) : E8{};
+      qreg[ds] = NEG ? scale8(qv, -a.scale_log2) : qv;
     }
   }
 
@@ -76,7 +78,7 @@ __global__ __launch_bounds__(64 * NW) LOGO_OCC_FWD void sq_fwd_pipe_kernel(const
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) oacc[dt] = f32x16{};
   f32x16 sbuf[2][2];  // [t & 1][32-key half]: S of the current and the next tile
-  bf16x8 pb[4];       // P(t) as the B operand of PV, one per 16-key step
+  E8 pb[4];       // P(t) as the B operand of PV, one per 16-key step
   float m_run = -INFINITY, l_run = 0.f, base = 0.f;  // m_run: running row max of c s
   // NEG: the S' accumulators start from the row's current base (a splat C
   // operand), so they hold S' + base and P = exp2(-acc) needs no add; when a
@@ -120,13 +122,13 @@ __global__ __launch_bounds__(64 * NW) LOGO_OCC_FWD void sq_fwd_pipe_kernel(const
       constexpr bool MASK = decltype(mask_tag)::value;  // S(t+1) crosses a mask edge
       // slot s < NX: K row operand (half s / DS, k-step s % DS);
       // slot s >= NX: V^T operand (key step (s - NX) / DT, column block (s - NX) % DT)
-      bf16x8 op[NX + NY];
+      E8 op[NX + NY];
       auto load_op = [&](auto s_c) {
         constexpr int S = decltype(s_c)::value;
         if constexpr (S < NX) {
-          if constexpr (DOS) op[S] = rd.row(kb, 32 * (S / DS), S % DS);
+          if constexpr (DOS) op[S] = rd.template row<EL>(kb, 32 * (S / DS), S % DS);
         } else {
-          if constexpr (DOPV) op[S] = rd.tr(vb, 16 * ((S - NX) / DT), (S - NX) % DT);
+          if constexpr (DOPV) op[S] = rd.template tr<EL>(vb, 16 * ((S - NX) / DT), (S - NX) % DT);
         }
       };
       static_for<PF>([&](auto s_c) { load_op(s_c); });
@@ -138,14 +140,14 @@ __global__ __launch_bounds__(64 * NW) LOGO_OCC_FWD void sq_fwd_pipe_kernel(const
         if constexpr (S < NX) {
           if constexpr (DOS) {
             constexpr int KK = S / DS, DSI = S % DS;
-            bf16x8 o = op[S];
+            E8 o = op[S];
             pin(o);
             sbuf[PAR ^ 1][KK] = mfma32(o, qreg[DSI], DSI == 0 ? (NEG ? cbase : f32x16{}) : sbuf[PAR ^ 1][KK]);
           }
         } else {
           constexpr int Y = S - NX;
           if constexpr (DOPV) {
-            bf16x8 o = op[S];
+            E8 o = op[S];
             pin(o);
             oacc[Y % DT] = mfma32(o, pb[Y / DT], oacc[Y % DT]);
           }
@@ -185,7 +187,7 @@ __global__ __launch_bounds__(64 * NW) LOGO_OCC_FWD void sq_fwd_pipe_kernel(const
               sbuf[PAR][KK][JJ] = pv;
               psum += pv;
               pin(psum);
-              if constexpr (IT % 8 == 7) pb[IT / 8] = acc_to_bf16(sbuf[PAR][IT / 16], (IT / 8) & 1);
+              if constexpr (IT % 8 == 7) pb[IT / 8] = acc_to<EL>(sbuf[PAR][IT / 16], (IT / 8) & 1);
             }
           });
         }
@@ -251,10 +253,10 @@ __global__ __launch_bounds__(64 * NW) LOGO_OCC_FWD void sq_fwd_pipe_kernel(const
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
       for (int q4 = 0; q4 < 4; ++q4) {
-        bf16x4 v;
+        E4 v;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = (bf16)(oacc[dt][4 * q4 + e] * inv);
-        *reinterpret_cast<bf16x4*>(orow + 32 * dt + 8 * q4 + 4 * g) = v;
+        for (int e = 0; e < 4; ++e) v[e] = (EL)(oacc[dt][4 * q4 + e] * inv);
+        *reinterpret_cast<E4*>(orow + 32 * dt + 8 * q4 + 4 * g) = v;
       }
     if (g == 0) a.lse[(int64_t)hq * a.n + qt.r] = m_run + log2f(l_tot);
   }
@@ -269,7 +271,7 @@ constexpr size_t fwd_smem() { return (size_t)4 * TileGeom<D, kSwz>::ELEMS * size
 // which give more workgroups where rows are few.
 constexpr int64_t kFwdPairMinTokens = 16384;
 
-template <int D, bool SPARSE, bool WINDOW>
+template <typename EL, int D, bool SPARSE, bool WINDOW>
 static int launch_fwd(const AttnArgs& a, hipStream_t st) {
   const bool paired = a.nseq == 1 && a.n >= kFwdPairMinTokens;
   const int64_t rows = paired ? 2 * kBQ : kBQ;
@@ -277,11 +279,11 @@ static int launch_fwd(const AttnArgs& a, hipStream_t st) {
   const int64_t nblk = ntmax * a.hq;
   LOGO_REQUIRE(nblk < ((int64_t)1 << 31), "grid too large");
   if (paired) {
-    auto kern = sq_fwd_pipe_kernel<D, SPARSE, WINDOW, 8>;
+    auto kern = sq_fwd_pipe_kernel<EL, D, SPARSE, WINDOW, 8>;
     LOGO_HIP_CHECK(allow_smem(kern, fwd_smem<D>()));
     hipLaunchKernelGGL(kern, dim3((unsigned)nblk), dim3(512), fwd_smem<D>(), st, a);
   } else {
-    auto kern = sq_fwd_pipe_kernel<D, SPARSE, WINDOW, 4>;
+    auto kern = sq_fwd_pipe_kernel<EL, D, SPARSE, WINDOW, 4>;
     LOGO_HIP_CHECK(allow_smem(kern, fwd_smem<D>()));
     hipLaunchKernelGGL(kern, dim3((unsigned)nblk), dim3(256), fwd_smem<D>(), st, a);
   }
@@ -289,8 +291,12 @@ static int launch_fwd(const AttnArgs& a, hipStream_t st) {
   return LOGO_OK;
 }
 
-int sq_launch_fwd(const AttnArgs& a, hipStream_t st, int d, bool sparse, bool window) {
-  return LOGO_DISPATCH(launch_fwd, a, st, d, sparse, window);
+template <int D, bool SPARSE, bool WINDOW>
+static int launch_fwd_bf16(const AttnArgs& a, hipStream_t st) { return launch_fwd<bf16, D, SPARSE, WINDOW>(a, st); }
+
+int sq_launch_fwd(const AttnArgs& a, hipStream_t st, int d, bool sparse, bool window, bool half) {
+  if (half) return d == 128 ? launch_fwd<f16, 128, true, false>(a, st) : launch_fwd<f16, 64, true, false>(a, st);
+  return LOGO_DISPATCH(launch_fwd_bf16, a, st, d, sparse, window);
 }
 
 }  // namespace logo

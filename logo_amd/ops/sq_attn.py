@@ -38,18 +38,25 @@ def kernel_head_dim(K: int, V: int) -> int:
     return 64 if max(K, V) <= 64 else 128
 
 
-def _to_kernel(t: torch.Tensor, d: int) -> torch.Tensor:
-    """[B, T, H, X] -> contiguous bf16 [B*T, H, d], zero-padded along X.
+def kernel_dtype(q, k, v, sparse: bool, window: int) -> torch.dtype:
+    """The element type a call computes in (fp32 accumulation either way).
 
-    The kernels compute in bf16 with fp32 accumulation, so fp16 and fp32
-    inputs are rounded to bf16 here (the outputs are cast back to the input
-    dtype).  The reference's Triton dots run in the input dtype
-    (logo/ops/selected_full_attn.py:95-99)."""
+    The reference's Triton dots run in the input dtype
+    (logo/ops/selected_full_attn.py:80, :95-99, :108).  fp16 q, k, v on the
+    query-sparse path (no window) run on the fp16 kernels; everything else
+    runs in bf16, so fp32 or mixed inputs and the dense / sliding-window
+    branches round to bf16 (the outputs are cast back to q's dtype)."""
+    half = sparse and window < 0 and q.dtype == k.dtype == v.dtype == torch.float16
+    return torch.float16 if half else torch.bfloat16
+
+
+def _to_kernel(t: torch.Tensor, d: int, dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    """[B, T, H, X] -> contiguous [B*T, H, d] of ``dtype``, zero-padded along X."""
     B, T, H, X = t.shape
     t = t.reshape(B * T, H, X)
     if X != d:
         t = F.pad(t, (0, d - X))
-    return t.contiguous() if t.dtype == torch.bfloat16 else t.to(torch.bfloat16).contiguous()
+    return t.contiguous() if t.dtype == dtype else t.to(dtype).contiguous()
 
 
 def _fwd(q, k, v, dsel: DeviceSelection, scale: float, window: int):
@@ -80,7 +87,8 @@ class SQFullAttentionFunction(torch.autograd.Function):
         V = v.shape[3]
         d = kernel_head_dim(K, V)
         in_dtypes = (q.dtype, k.dtype, v.dtype)
-        qf, kf, vf = _to_kernel(q, d), _to_kernel(k, d), _to_kernel(v, d)
+        kt = kernel_dtype(q, k, v, dsel.q_idx is not None, window)
+        qf, kf, vf = _to_kernel(q, d, kt), _to_kernel(k, d, kt), _to_kernel(v, d, kt)
         o, lse = _fwd(qf, kf, vf, dsel, scale, window)
         ctx.save_for_backward(qf, kf, vf, o, lse)
         ctx.dsel = dsel
@@ -91,7 +99,7 @@ class SQFullAttentionFunction(torch.autograd.Function):
         out = o.view(B, T, HQ, d)
         if V != d:
             out = out[..., :V].contiguous()
-        return out if q.dtype == torch.bfloat16 else out.to(q.dtype)
+        return out if q.dtype == kt else out.to(q.dtype)
 
     @staticmethod
     @_custom_bwd
@@ -99,7 +107,7 @@ class SQFullAttentionFunction(torch.autograd.Function):
         qf, kf, vf, o, lse = ctx.saved_tensors
         B, T, HQ, H, K, V = ctx.shapes
         d = qf.shape[2]
-        dof = _to_kernel(do, d)
+        dof = _to_kernel(do, d, qf.dtype)
         dq, dk, dv = _bwd(qf, kf, vf, o, lse, dof, ctx.dsel, ctx.scale, ctx.window)
         tq, tk, tv = ctx.in_dtypes
         dq = dq.view(B, T, HQ, d)[..., :K].to(tq)

@@ -72,27 +72,30 @@ at::Tensor dense_meta(const at::Tensor& cu, int64_t n_tokens) {
   return meta;
 }
 
-void check_attn(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v) {
-  need(q, "q", at::kBFloat16);
-  need(k, "k", at::kBFloat16);
-  need(v, "v", at::kBFloat16);
+// q, k, v of one 16-bit type (bf16, or fp16 for the C library's query-sparse
+// kernels, which rejects other fp16 calls itself); returns its dtype code.
+int check_attn(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v) {
+  const at::ScalarType dt = q.scalar_type() == at::kHalf ? at::kHalf : at::kBFloat16;
+  need(q, "q", dt);
+  need(k, "k", dt);
+  need(v, "v", dt);
   TORCH_CHECK(q.dim() == 3 && k.dim() == 3 && v.dim() == 3, "logo_hip: q, k, v must be [N, heads, D]");
   TORCH_CHECK(k.size(0) == q.size(0) && v.sizes() == k.sizes() && k.size(2) == q.size(2),
               "logo_hip: q [N, HQ, D], k and v [N, H, D] must agree");
+  return dt == at::kHalf ? LOGO_DTYPE_F16 : LOGO_DTYPE_BF16;
 }
 
 std::tuple<at::Tensor, at::Tensor> sq_fwd(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
                                           const std::optional<at::Tensor>& q_idx,
                                           const std::optional<at::Tensor>& pos, const at::Tensor& meta,
                                           const at::Tensor& cu, int64_t lanes, double scale, int64_t window) {
-  check_attn(q, k, v);
+  const int dtype = check_attn(q, k, v);
   const int64_t n = q.size(0), hq = q.size(1), h = k.size(1), d = q.size(2);
   auto o = at::zeros_like(q);
   auto lse = at::zeros({hq, n}, q.options().dtype(at::kFloat));  // rows past Sq stay zero
   ok(logo_sq_fwd(cptr(q), cptr(k), cptr(v), mptr(o), lse.data_ptr<float>(), opt_ptr<int64_t>(q_idx),
                  opt_ptr<int32_t>(pos), meta.data_ptr<int32_t>(), cu.data_ptr<int32_t>(), n, (int)cu.numel() - 1,
-                 (int)hq, (int)h, (int)d, (int)v.size(2), (int)lanes, (float)scale, (int)window, LOGO_DTYPE_BF16,
-                 sp()),
+                 (int)hq, (int)h, (int)d, (int)v.size(2), (int)lanes, (float)scale, (int)window, dtype, sp()),
      "logo_sq_fwd");
   return {o, lse};
 }
@@ -107,6 +110,20 @@ struct Bwd {
   int64_t window;
   int call(int phase, at::Tensor* delta, at::Tensor* q_sel, at::Tensor* do_sel, at::Tensor* dq, at::Tensor* dk,
            at::Tensor* dv) const {
+    const int dtype = check_attn(q, k, v);
+    need(o, "o", q.scalar_type());
+    need(dout, "dout", q.scalar_type());
+    TORCH_CHECK(o.sizes() == q.sizes() && dout.sizes() == q.sizes(), "logo_hip: o and dout must be [N, HQ, D]");
+    if (phase > 0) {
+      need(*delta, "delta", at::kFloat);
+      TORCH_CHECK(delta->numel() == q.size(0) * q.size(1), "logo_hip: delta must be [HQ, N]");
+      if (q_idx.has_value()) {
+        need(*q_sel, "q_sel", q.scalar_type());
+        need(*do_sel, "do_sel", q.scalar_type());
+        TORCH_CHECK(q_sel->numel() == q.numel() && do_sel->numel() == q.numel(),
+                    "logo_hip: q_sel and do_sel must be [HQ, N, D]");
+      }
+    }
     using F = decltype(&logo_sq_bwd);
     F fn = phase == 0 ? &logo_sq_bwd_delta : phase == 1 ? &logo_sq_bwd_dq : &logo_sq_bwd_dkv;
     auto p = [](at::Tensor* t) -> void* { return t && t->numel() ? t->data_ptr() : nullptr; };
@@ -114,7 +131,7 @@ struct Bwd {
               static_cast<float*>(p(delta)), p(q_sel), p(do_sel), p(dq), p(dk), p(dv), opt_ptr<int64_t>(q_idx),
               opt_ptr<int32_t>(pos), meta.data_ptr<int32_t>(), cu.data_ptr<int32_t>(), q.size(0),
               (int)cu.numel() - 1, (int)q.size(1), (int)k.size(1), (int)q.size(2), (int)v.size(2), (int)lanes,
-              (float)scale, (int)window, LOGO_DTYPE_BF16, sp());
+              (float)scale, (int)window, dtype, sp());
   }
 };
 
@@ -128,7 +145,6 @@ struct Bwd {
 // dq and dk/dv phases, whose rows past each head's Sq are left unwritten.
 std::tuple<at::Tensor, at::Tensor, at::Tensor> sq_bwd_delta(LOGO_BWD_SCHEMA_ARGS) {
   check_attn(q, k, v);
-  need(dout, "dout", at::kBFloat16);
   const bool sparse = q_idx.has_value();
   auto delta = at::zeros({q.size(1), q.size(0)}, q.options().dtype(at::kFloat));
   auto q_sel = sparse ? at::empty({q.size(1), q.size(0), q.size(2)}, q.options()) : at::empty({0}, q.options());

@@ -48,6 +48,26 @@ def test_fwd_bwd_reject_bad_shapes_without_touching_gpu(d, v_dim, hq, h, lanes, 
         assert msg in lib.logo_last_error().decode()
 
 
+@pytest.mark.parametrize("sparse,window,dtype,msg", [
+    (False, -1, 2, "fp16 is supported on the query-sparse path"),   # dense fp16
+    (True, 128, 2, "fp16 is supported on the query-sparse path"),   # sliding-window fp16
+    (True, -1, 1, "unsupported"),                                    # fp32 tensors
+    (True, -1, 7, "unsupported"),
+])
+def test_fwd_bwd_dtype_checks_without_touching_gpu(sparse, window, dtype, msg):
+    """fp16 runs on the query-sparse kernels without a window only; other
+    dtypes are refused before any HIP call."""
+    lib = _lib.lib()
+    p = ctypes.c_void_p(1)
+    idx = p if sparse else None
+    rc = lib.logo_sq_fwd(p, p, p, p, p, idx, idx, p, p, 128, 1, 4, 4, 128, 128, 1, 0.1, window, dtype, None)
+    assert rc == 1 and msg in lib.logo_last_error().decode()
+    for fn in (lib.logo_sq_bwd, lib.logo_sq_bwd_delta, lib.logo_sq_bwd_dq, lib.logo_sq_bwd_dkv):
+        rc = fn(p, p, p, p, p, p, p, p, p, p, p, p, idx, idx, p, p, 128, 1, 4, 4, 128, 128, 1, 0.1, window,
+                dtype, None)
+        assert rc == 1 and msg in lib.logo_last_error().decode()
+
+
 def test_compact_rejects_bad_arguments():
     lib = _lib.lib()
     p = ctypes.c_void_p(1)

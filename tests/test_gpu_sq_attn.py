@@ -13,7 +13,7 @@ import torch
 
 from logo_amd.ops import dense_causal_attn, sq_full_attn, sq_full_attn_dense_ref, swa_attn
 from oracle import attn
-from tests.helpers import (assert_within, cu_from_lengths, gen, markov_selection, randn,
+from tests.helpers import (assert_within, cu_from_lengths, err_stats, gen, markov_selection, randn,
                            torch_sq_attn, varlen_lengths)
 
 pytestmark = pytest.mark.gpu
@@ -159,6 +159,54 @@ def test_noncontiguous_and_fp32_inputs(gpu):
     assert_within("dq", dq, rdq)
     assert_within("dk", dk, rdk)
     assert_within("dv", dv, rdv)
+
+
+@pytest.mark.parametrize("n,hq,h,d,cu,per_head", [
+    (512, 4, 4, 64, [0, 512], False),
+    (700, 4, 2, 128, [0, 1, 1, 200, 700], False),     # GQA, zero/single-token segments
+    (600, 4, 4, 128, [0, 300, 600], True),            # per-head extension
+    (900, 2, 1, 64, [0, 900], True),                  # per-head GQA
+])
+def test_fp16_inputs_run_in_fp16(gpu, n, hq, h, d, cu, per_head):
+    """fp16 q, k, v run on the fp16 kernels (the reference's dots run in the
+    input dtype, logo/ops/selected_full_attn.py:80 :95-99 :108): fp16 output
+    and gradients against the oracle fed the same fp16 values, within max-abs
+    4e-3 / mean-abs 4e-4 (fp16's 11-bit significand: 8x finer than bf16's,
+    whose north-star bound is 2e-2 / 2e-3), and with a mean error below half
+    of what the bf16 kernels give on the same inputs."""
+    g = gen(300 + n + d)
+    q, k, v = (randn((n, x, d), g, dtype=torch.float16) for x in (hq, h, h))
+    do = randn((n, hq, d), g, dtype=torch.float16)
+    sel = torch.rand((n, hq) if per_head else (n,), generator=g) < 0.5
+    cu = torch.tensor(cu, dtype=torch.int32)
+    print(f"fp16 n={n} hq={hq} h={h} d={d} per_head={per_head}", flush=True)
+    o, grads = _run(q, k, v, sel, cu, gpu, do)
+    assert o.dtype == torch.float16 and all(x.dtype == torch.float16 for x in grads)
+    ro, rgrads = _oracle(q, k, v, sel, cu, do)
+    ob, gb = _run(*(x.bfloat16() for x in (q, k, v)), sel, cu, gpu, do.bfloat16())
+    for name, x, xb, r in zip(("o", "dq", "dk", "dv"), (o, *grads), (ob, *gb), (ro, *rgrads)):
+        _, mean16 = assert_within(name, x, r, max_abs=4e-3, mean_abs=4e-4)
+        _, mean_bf = err_stats(xb, r)
+        assert mean16 < 0.5 * mean_bf, f"{name}: fp16 mean-abs {mean16:.2e} vs bf16 {mean_bf:.2e}"
+
+
+def test_fp16_dense_and_window_paths_round_to_bf16(gpu):
+    """The dense and sliding-window branches have bf16 kernels only: fp16
+    inputs are rounded to bf16 and the outputs cast back to fp16, at the
+    bf16 bound."""
+    n, hq, d = 400, 2, 64
+    g = gen(41)
+    q, k, v = (randn((n, hq, d), g, dtype=torch.float16) for _ in range(3))
+    cu = torch.tensor([0, 150, 400], dtype=torch.int32)
+    for window in (16, None):
+        qg, kg, vg = (x.to(gpu)[None] for x in (q, k, v))
+        if window is None:
+            o = dense_causal_attn(qg, kg, vg, cu.to(gpu))[0]
+        else:
+            o = swa_attn(qg, kg, vg, cu.to(gpu), window=window)[0]
+        assert o.dtype == torch.float16
+        ro, _ = _oracle(q, k, v, None, cu, window=window)
+        assert_within(f"o window={window}", o, ro)
 
 
 @pytest.mark.parametrize("K,V,hq,h", [(128, 64, 4, 2), (64, 128, 2, 2), (96, 96, 4, 4), (48, 32, 2, 1),

@@ -15,17 +15,18 @@ pytestmark = pytest.mark.gpu
 _CHECKS = ("test_schema", "test_faketensor", "test_aot_dispatch_dynamic")
 
 
-def _inputs(dev, n=700, hq=4, h=2, d=128):
+def _inputs(dev, n=700, hq=4, h=2, d=128, dtype=torch.bfloat16):
     g = gen(40)
-    q, k, v, do = (randn((n, x, d), g).to(dev) for x in (hq, h, h, hq))
+    q, k, v, do = (randn((n, x, d), g, dtype=dtype).to(dev) for x in (hq, h, h, hq))
     sel = (torch.rand(n, generator=g) < 0.4).to(dev)
     cu = torch.tensor([0, 300, n], dtype=torch.int32, device=dev)
     return q, k, v, do, sel, cu
 
 
-def test_opcheck_attention_ops(gpu):
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_opcheck_attention_ops(gpu, dtype):
     ops = _torch_ops.ops()
-    q, k, v, do, sel, cu = _inputs(gpu)
+    q, k, v, do, sel, cu = _inputs(gpu, dtype=dtype)
     dsel = compact_selection(sel, cu)
     torch.library.opcheck(ops.compact.default, (sel.view(torch.uint8), cu), test_utils=_CHECKS)
     fwd_args = (q, k, v, dsel.q_idx, dsel.pos, dsel.meta, cu, 1, 0.088, -1)

@@ -129,10 +129,15 @@ def _kernel_listings(tmp_path):
 def test_asm_accumulators_are_not_copied_inside_mfma_loops(tmp_path):
     listings = _kernel_listings(tmp_path)
     kernels = [k for k in listings if "sq_dq64_kernel" in k or "sq_dkv_kernel" in k]
-    assert len(kernels) == 16, sorted(listings)  # {dq, dkv} x D {64, 128} x sparse x window
+    # bf16: {dq, dkv} x D {64, 128} x sparse x window; fp16: {dq, dkv} x D, sparse without window
+    assert len(kernels) == 20, sorted(listings)
     for name in kernels:
         lines = listings[name]
         assert any(_ACC_DST.search(line) for line in lines), f"{name}: no AGPR-accumulator MFMA found"
+        # the element type's MFMA, and no other (an fp16 kernel on the bf16 unit, or the reverse)
+        want = "f16" if "IDF16_" in name else "bf16"
+        ops = {m.group(1) for m in re.finditer(r"v_mfma_f32_32x32x16_(b?f16)", "\n".join(lines))}
+        assert ops == {want}, f"{name}: MFMA types {sorted(ops)}, expected {want}"
         bad = check_accumulators(lines)
         assert not bad, f"{name}: " + "; ".join(f"line {n}: {t[:100]}" for n, t in bad[:5])
 
