@@ -127,11 +127,28 @@ int logo_q_start_blk(const int32_t* pos, const int32_t* cu_q, const int32_t* chu
  * (the reference's dots run in the input dtype, :80 :108); every 16-bit
  * tensor of the call (q, k, v, o, and for the backward dout, q_sel, do_sel,
  * dq, dk, dv) holds that type.
+ * workspace / workspace_bytes (may be NULL / 0): device memory that lets the
+ * forward and dq kernels (no window) cut the key range of each query tile
+ * into pieces when a head has few tiles, so that a grid which would fill the
+ * GPU once is not bound by its heaviest tile (the reference has no
+ * counterpart: its grid is one program per chunk, :348 :413).  Its first
+ * bytes are arrival counters that must be zero when a call starts; every call
+ * leaves them zero, so one zero-fill serves every later call.  Calls that
+ * share a workspace must not overlap.  Too small (or NULL): no split.
  */
 int logo_sq_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
                 const int64_t* q_idx, const int32_t* pos, const int32_t* meta,
                 const int32_t* cu, int64_t n_tokens, int nseq, int hq, int h, int d,
-                int v_dim, int lanes, float scale, int window, int dtype, void* stream);
+                int v_dim, int lanes, float scale, int window, int dtype, void* workspace,
+                size_t workspace_bytes, void* stream);
+
+/*
+ * Bytes of the workspace logo_sq_fwd and logo_sq_bwd_dq need to split tiles
+ * on the current device (0: they never split for this shape), and how many
+ * of them, at its start, are the counters that must be zero.
+ */
+size_t logo_sq_workspace_bytes(int64_t n_tokens, int nseq, int hq, int d);
+size_t logo_sq_workspace_counter_bytes(void);
 
 /*
  * Backward (logo/ops/selected_full_attn.py:124-138 delta, :141-228 dq,
@@ -147,7 +164,8 @@ int logo_sq_bwd(const void* q, const void* k, const void* v, const void* o,
     const void* dout, const float* lse, float* delta, void* q_sel, void* do_sel,
     void* dq, void* dk, void* dv, const int64_t* q_idx, const int32_t* pos,
     const int32_t* meta, const int32_t* cu, int64_t n_tokens, int nseq, int hq,
-    int h, int d, int v_dim, int lanes, float scale, int window, int dtype, void* stream);
+    int h, int d, int v_dim, int lanes, float scale, int window, int dtype, void* workspace,
+    size_t workspace_bytes, void* stream);
 
 /*
  * The three backward phases of logo_sq_bwd as separate launches, same
@@ -160,17 +178,20 @@ int logo_sq_bwd_delta(const void* q, const void* k, const void* v, const void* o
     const void* dout, const float* lse, float* delta, void* q_sel, void* do_sel,
     void* dq, void* dk, void* dv, const int64_t* q_idx, const int32_t* pos,
     const int32_t* meta, const int32_t* cu, int64_t n_tokens, int nseq, int hq,
-    int h, int d, int v_dim, int lanes, float scale, int window, int dtype, void* stream);
+    int h, int d, int v_dim, int lanes, float scale, int window, int dtype, void* workspace,
+    size_t workspace_bytes, void* stream);
 int logo_sq_bwd_dq(const void* q, const void* k, const void* v, const void* o,
     const void* dout, const float* lse, float* delta, void* q_sel, void* do_sel,
     void* dq, void* dk, void* dv, const int64_t* q_idx, const int32_t* pos,
     const int32_t* meta, const int32_t* cu, int64_t n_tokens, int nseq, int hq,
-    int h, int d, int v_dim, int lanes, float scale, int window, int dtype, void* stream);
+    int h, int d, int v_dim, int lanes, float scale, int window, int dtype, void* workspace,
+    size_t workspace_bytes, void* stream);
 int logo_sq_bwd_dkv(const void* q, const void* k, const void* v, const void* o,
     const void* dout, const float* lse, float* delta, void* q_sel, void* do_sel,
     void* dq, void* dk, void* dv, const int64_t* q_idx, const int32_t* pos,
     const int32_t* meta, const int32_t* cu, int64_t n_tokens, int nseq, int hq,
-    int h, int d, int v_dim, int lanes, float scale, int window, int dtype, void* stream);
+    int h, int d, int v_dim, int lanes, float scale, int window, int dtype, void* workspace,
+    size_t workspace_bytes, void* stream);
 
 /*
  * Fused epilogue forward: gate threshold, the two branch context RMSNorms

@@ -34,7 +34,9 @@ SIGNATURES = {
     "logo_dense_meta": ([_P, _I, _I64, _P, _P], _I),
     "logo_chunk_indices": ([_P, _I, _I, _P, _I64, _P, _P, _P], _I),
     "logo_q_start_blk": ([_P, _P, _P, _P, _I64, _I, _P, _P], _I),
-    "logo_sq_fwd": ([_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I, _I, _I, _I, _I, _I, _F, _I, _I, _P], _I),
+    "logo_sq_fwd": ([_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I, _I, _I, _I, _I, _I, _F, _I, _I, _P, _SZ, _P], _I),
+    "logo_sq_workspace_bytes": ([_I64, _I, _I, _I], _SZ),
+    "logo_sq_workspace_counter_bytes": ([], _SZ),
     "logo_epilogue_fwd": ([_P, _P, _P, _P, _I, _P, _P, _P, _I64, _I, _I, _F, _I, _P], _I),
     "logo_epilogue_bwd_workspace_bytes": ([_I64, _I, _I], _SZ),
     "logo_epilogue_bwd": ([_P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I, _I, _F, _P, _I, _P],
@@ -58,8 +60,8 @@ SIGNATURES = {
                          _I, _P],
                         _I),
 }
-_BWD = ([_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I, _I, _I, _I, _I, _I, _F, _I, _I, _P],
-        _I)
+_BWD = ([_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I, _I, _I, _I, _I, _I, _F, _I, _I, _P,
+         _SZ, _P], _I)
 for _name in ("logo_sq_bwd", "logo_sq_bwd_delta", "logo_sq_bwd_dq", "logo_sq_bwd_dkv"):
     SIGNATURES[_name] = _BWD
 

@@ -37,6 +37,9 @@
 // Q^T, dO^T) come from the same row-major tiles through ds_read_b64_tr_b16.
 #include "sq_attn.hpp"
 
+#include <algorithm>
+#include <mutex>
+
 namespace logo {
 
 // ---------------------------------------------------------------------------
@@ -96,6 +99,20 @@ int sq_launch_delta(const AttnArgs& a, hipStream_t st, int d, bool sparse, bool 
                   : (sparse ? launch_delta<bf16, 64, true>(a, st) : launch_delta<bf16, 64, false>(a, st));
 }
 
+int device_cus() {
+  static std::mutex mu;
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  std::lock_guard<std::mutex> lock(mu);
+  if (cache[dev] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cache[dev] = cus;
+  }
+  return cache[dev];
+}
+
 static int check_common(int64_t n, int nseq, int hq, int h, int d, int v_dim, int lanes, int dtype,
                         bool sparse, int window) {
   LOGO_REQUIRE(n > 0 && n < ((int64_t)1 << 31), "n_tokens out of range: %lld", (long long)n);
@@ -140,10 +157,23 @@ static AttnArgs make_args(const void* q, const void* k, const void* v, const int
 
 using namespace logo;
 
+extern "C" size_t logo_sq_workspace_bytes(int64_t n_tokens, int nseq, int hq, int d) {
+  if (n_tokens <= 0 || nseq < 1 || hq < 1 || (d != 64 && d != 128)) return 0;
+  const bool paired = nseq == 1 && n_tokens >= kFwdPairMinTokens;
+  const int cap_f = split_cap_for(hq, paired ? 1 : 2), cap_d = split_cap_for(hq, 2);
+  const size_t fwd = cap_f >= 2 ? (size_t)hq * 2 * cap_f * fwd_part_floats(d, paired ? 8 : 4) : 0;
+  const size_t dq = cap_d >= 2 ? (size_t)hq * 2 * cap_d * dq_part_floats(d) : 0;
+  const size_t part = std::max(fwd, dq) * sizeof(float);
+  return part == 0 ? 0 : split_cnt_bytes() + part;
+}
+
+extern "C" size_t logo_sq_workspace_counter_bytes(void) { return split_cnt_bytes(); }
+
 extern "C" int logo_sq_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
                            const int64_t* q_idx, const int32_t* pos, const int32_t* meta,
                            const int32_t* cu, int64_t n_tokens, int nseq, int hq, int h, int d,
-                           int v_dim, int lanes, float scale, int window, int dtype, void* stream) {
+                           int v_dim, int lanes, float scale, int window, int dtype, void* workspace,
+                           size_t workspace_bytes, void* stream) {
   int rc = check_common(n_tokens, nseq, hq, h, d, v_dim, lanes, dtype, q_idx != nullptr, window);
   if (rc != LOGO_OK) return rc;
   LOGO_REQUIRE(q && k && v && o && lse && meta && cu, "null pointer argument");
@@ -151,6 +181,8 @@ extern "C" int logo_sq_fwd(const void* q, const void* k, const void* v, void* o,
   AttnArgs a = make_args(q, k, v, q_idx, pos, meta, cu, n_tokens, nseq, hq, h, lanes, scale, window);
   a.o = static_cast<bf16*>(o);
   a.lse = lse;
+  a.ws = workspace;
+  a.ws_bytes = workspace ? workspace_bytes : 0;
   const bool sparse = q_idx != nullptr;
   const bool win = window >= 0;
   return sq_launch_fwd(a, as_stream(stream), d, sparse, win, dtype == LOGO_DTYPE_F16);
@@ -160,11 +192,12 @@ extern "C" int logo_sq_fwd(const void* q, const void* k, const void* v, void* o,
   const void *q, const void *k, const void *v, const void *o, const void *dout, const float *lse, \
       float *delta, void *q_sel, void *do_sel, void *dq, void *dk, void *dv, const int64_t *q_idx, \
       const int32_t *pos, const int32_t *meta, const int32_t *cu, int64_t n_tokens, int nseq,      \
-      int hq, int h, int d, int v_dim, int lanes, float scale, int window, int dtype, void *stream
+      int hq, int h, int d, int v_dim, int lanes, float scale, int window, int dtype, void *workspace, \
+      size_t workspace_bytes, void *stream
 
 #define LOGO_BWD_ARGS                                                                             \
   q, k, v, o, dout, lse, delta, q_sel, do_sel, dq, dk, dv, q_idx, pos, meta, cu, n_tokens, nseq, hq, \
-      h, d, v_dim, lanes, scale, window, dtype, stream
+      h, d, v_dim, lanes, scale, window, dtype, workspace, workspace_bytes, stream
 
 static int bwd_entry(LOGO_BWD_PARAMS, int phase) {
   int rc = check_common(n_tokens, nseq, hq, h, d, v_dim, lanes, dtype, q_idx != nullptr, window);
@@ -185,6 +218,8 @@ static int bwd_entry(LOGO_BWD_PARAMS, int phase) {
   a.dq = static_cast<bf16*>(dq);
   a.dk = static_cast<bf16*>(dk);
   a.dv = static_cast<bf16*>(dv);
+  a.ws = workspace;
+  a.ws_bytes = workspace ? workspace_bytes : 0;
   const bool sparse = q_idx != nullptr;
   const bool win = window >= 0;
   const bool half = dtype == LOGO_DTYPE_F16;

@@ -39,7 +39,96 @@ struct AttnArgs {
   float scale;
   float scale_log2;
   int window;
+  // Key-range split of the fwd / dq tiles (no window): a tile is cut into up
+  // to kMaxSplit pieces when its head has few tiles; each piece writes an fp32
+  // partial to `part`, and the last piece of a tile to arrive (per-tile counter
+  // in `cnt`, zero on entry, left zero) combines them.  split_cap: the pieces
+  // per head to aim for (0: no split); the workspace holds 2 split_cap per
+  // head.
+  float* part;
+  int* cnt;
+  int split_cap;
+  // the caller's workspace (host side only: the launchers carve part / cnt
+  // from it when it is large enough for their kernel's split_cap)
+  void* ws;
+  size_t ws_bytes;
 };
+
+constexpr int kMaxSplit = 4;
+
+// Single long sequences take 8-wave forward workgroups of two query tiles,
+// which share each K / V tile copy between 256 rows (half the copy traffic
+// and issue per row); packed or short inputs keep 4-wave single-tile
+// workgroups, which give more workgroups where rows are few.
+constexpr int64_t kFwdPairMinTokens = 16384;
+
+// Compute units of the current device (cached per device).
+int device_cus();
+
+// Pieces per head a split kernel aims for: two rounds of the workgroups the
+// device holds at once (wgs_per_cu per CU), shared by the heads.
+inline int split_cap_for(int hq, int wgs_per_cu) { return 2 * device_cus() * wgs_per_cu / hq; }
+
+// Pieces per tile for a head with nt tiles: none while its tiles alone fill
+// more than three quarters of the target (LPT order balances those), else
+// enough to reach the target, at most kMaxSplit.  nt * nper < 1.75 cap.
+__host__ __device__ inline int split_pieces(int nt, int cap) {
+  if (cap <= 0 || nt <= 0 || 4 * nt > 3 * cap) return 1;
+  const int n = (cap + nt - 1) / nt;
+  return n < kMaxSplit ? n : kMaxSplit;
+}
+
+// Bytes of the arrival counters at the start of the workspace (2 split_cap
+// per head: at most 2 workgroups per CU x 2 rounds x 2), 256-byte aligned.
+inline size_t split_cnt_bytes() { return ((size_t)8 * device_cus() * sizeof(int) + 255) & ~(size_t)255; }
+
+// fp32 partial floats per piece: forward (NW waves: O [DT][16][64] plus m / l
+// [64] per wave), dq (2 waves x 2 row blocks x DT x 16 x 64).
+inline size_t fwd_part_floats(int d, int nw) { return (size_t)nw * ((size_t)(d / 32) * 16 * 64 + 64); }
+inline size_t dq_part_floats(int d) { return (size_t)2 * 2 * (d / 32) * 16 * 64; }
+
+// Enables the split in `a` when its workspace holds the counters and
+// 2 split_cap pieces per head of `floats` each; otherwise split_cap = 0.
+inline void split_setup(AttnArgs& a, int wgs_per_cu, size_t floats) {
+  const int cap = split_cap_for(a.hq, wgs_per_cu);
+  const size_t need = split_cnt_bytes() + (size_t)a.hq * 2 * cap * floats * sizeof(float);
+  if (cap >= 2 && a.ws != nullptr && a.ws_bytes >= need) {
+    a.cnt = static_cast<int*>(a.ws);
+    a.part = reinterpret_cast<float*>(static_cast<char*>(a.ws) + split_cnt_bytes());
+    a.split_cap = cap;
+  } else {
+    a.split_cap = 0;
+  }
+}
+
+// Cross-workgroup exchange of the split partials.  The L2s of the XCDs are
+// not coherent with each other, so partials are stored and loaded with
+// agent-scope atomics (sc1: through to the coherent level, no L2 flush or
+// invalidate), and the stores are complete (vmcnt(0)) before the counter
+// increment that publishes them.
+__device__ __forceinline__ void st_agent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_agent(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Arrival of one piece at its tile's counter (after its partial is stored and
+// complete on every wave).  Returns true in the last piece to arrive, which
+// also resets the counter; flag: 4 bytes of LDS no longer in use.
+__device__ __forceinline__ bool split_arrive(int* cnt, int npieces, int* flag) {
+  wait_stores();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int old = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const bool last = old == npieces - 1;
+    if (last) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *flag = last;
+  }
+  __syncthreads();
+  return *flag != 0;
+}
 
 // Per-lane view of the compaction metadata.
 template <bool SPARSE>
@@ -99,20 +188,27 @@ struct QTile {
   bool wave_active, valid;
   int64_t t;
   RowView<SPARSE> rv;
+  // key-range split: rank = trank * nper + piece; nsplit pieces of this tile
+  // exist (nsplit <= nper; 1: no split)
+  int rank, trank, piece, nper, nsplit;
 
   // rpw: compacted rows per wave (32 or 64); r / t / p / valid describe the
   // lane's row in the wave's first 32-row block (row_at gives the others).
   // paired: the workgroup takes two consecutive kBQ-row tiles (a single
   // segment only, nseq == 1, so both tiles share one key range).
+  // splittable: the tile's keys [kv_lo, kv_hi) may be cut into pieces (a
+  // split_cap > 0, no window); the piece's own range replaces them.
   __device__ __forceinline__ bool init(const AttnArgs& a, int wave, int i, bool window, int rpw = 32,
-                                       bool paired = false) {
-    int rank;
+                                       bool paired = false, bool splittable = false) {
     xcd_remap(blockIdx.x, a.hq, rank, hq);
     lane_sel = a.lanes > 1 ? hq : 0;
     const int32_t* meta = a.meta + (int64_t)lane_sel * a.meta_stride;
     const int nt = paired ? (meta[1] + 1) >> 1 : meta[1];
-    if (rank >= nt) return false;
-    const int tile = nt - 1 - rank;  // heaviest (latest) blocks first
+    nper = splittable ? split_pieces(nt, a.split_cap) : 1;
+    if (rank >= nt * nper) return false;
+    trank = rank / nper;
+    piece = rank - trank * nper;
+    const int tile = nt - 1 - trank;  // heaviest (latest) blocks first
     const int32_t* cu_q = meta + kMetaHdr;
     const int32_t* cu_tq = cu_q + (a.nseq + 1);
     if (paired) {
@@ -138,6 +234,16 @@ struct QTile {
     p = valid ? rv.posn(r) : -1;
     kv_lo = window ? (max(0, rv.posn(r0) - a.window) & ~63) : 0;
     kv_hi = rv.posn(r_end - 1) + 1;
+    nsplit = 1;
+    if (nper > 1) {
+      // 64-key-aligned chunks; nsplit <= nper pieces, none empty
+      const int span = kv_hi - kv_lo;
+      const int chunk = (((span + nper - 1) / nper) + 63) & ~63;
+      nsplit = (span + chunk - 1) / chunk;
+      if (piece >= nsplit) return false;
+      kv_lo += piece * chunk;
+      kv_hi = min(kv_hi, kv_lo + chunk);
+    }
     return true;
   }
 };

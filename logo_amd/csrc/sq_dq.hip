@@ -37,7 +37,7 @@ __global__ __launch_bounds__(128) LOGO_OCC_DQ64 void sq_dq64_kernel(const AttnAr
 
   const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63, i = l & 31, g = l >> 5;
   QTile<SPARSE> qt;
-  if (!qt.init(a, wave, i, WINDOW, 64)) return;
+  if (!qt.init(a, wave, i, WINDOW, 64, false, !WINDOW)) return;
   const int hq = qt.hq, W = a.window;
   int rr[2], pr[2];
   bool vr[2];
@@ -106,7 +106,7 @@ __global__ __launch_bounds__(128) LOGO_OCC_DQ64 void sq_dq64_kernel(const AttnAr
   const int nt = (qt.kv_hi - kv_lo + 63) >> 6;
   int hw_lo = 0, hw_hi = 0;  // 32-key halves this wave's rows can see
   if (qt.wave_active) {
-    hw_hi = ((qt.pmax - kv_lo) >> 5) + 1;
+    hw_hi = min(2 * nt, ((qt.pmax - kv_lo) >> 5) + 1);
     hw_lo = WINDOW ? (max(0, qt.pmin - W - kv_lo) >> 5) : 0;
   }
 
@@ -231,6 +231,41 @@ __global__ __launch_bounds__(128) LOGO_OCC_DQ64 void sq_dq64_kernel(const AttnAr
   }
 
   agpr_acc_drain();
+  if (qt.nsplit > 1) {
+    // Key-range split: partial dQ of this piece as [wave][row block][dt][item]
+    // [lane]; the last piece of the tile to arrive adds the others' to its own.
+    constexpr int PQF = 2 * 2 * DT * 16 * 64;  // floats per piece
+    float* const part0 = a.part + (int64_t)(hq * 2 * a.split_cap + qt.trank * qt.nper) * PQF;
+    {
+      float* pq = part0 + (int64_t)qt.piece * PQF + wave * (2 * DT * 16 * 64);
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) st_agent(pq + ((b * DT + dt) * 16 + e) * 64 + l, dqacc[b][dt][e]);
+    }
+    if (!split_arrive(a.cnt + hq * 2 * a.split_cap + qt.trank, qt.nsplit, reinterpret_cast<int*>(smem))) return;
+    // sum the pieces in piece order from zero, whichever arrived last, so the
+    // result does not depend on the arrival order
+    // (one 16-float block at a time, to keep the registers of the main loop)
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        f32x16 sum = f32x16{};
+        for (int pc = 0; pc < qt.nsplit; ++pc) {
+          if (pc == qt.piece) {
+            sum += dqacc[b][dt];
+          } else {
+            const float* pq = part0 + (int64_t)pc * PQF + wave * (2 * DT * 16 * 64) + (b * DT + dt) * 16 * 64;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) sum[e] += ld_agent(pq + e * 64 + l);
+          }
+        }
+        dqacc[b][dt] = sum;
+      }
+  }
 #pragma unroll
   for (int b = 0; b < 2; ++b) {
     if (vr[b]) {
@@ -253,11 +288,16 @@ template <int D>
 constexpr size_t dq_smem() { return (size_t)4 * TileGeom<D, kSwz>::ELEMS * sizeof(bf16); }
 
 template <typename EL, int D, bool SPARSE, bool WINDOW>
-static int launch_dq(const AttnArgs& a, hipStream_t st) {
+static int launch_dq(const AttnArgs& a_in, hipStream_t st) {
+  AttnArgs a = a_in;
   const int64_t ntmax = (a.n + kBQ - 1) / kBQ + a.nseq;
+  if (WINDOW) a.split_cap = 0;
+  else split_setup(a, 2, dq_part_floats(D));
+  const int64_t nblk = std::max<int64_t>(ntmax, 2 * a.split_cap) * a.hq;
+  LOGO_REQUIRE(nblk < ((int64_t)1 << 31), "grid too large");
   auto kern = sq_dq64_kernel<EL, D, SPARSE, WINDOW>;
   LOGO_HIP_CHECK(allow_smem(kern, dq_smem<D>()));
-  hipLaunchKernelGGL(kern, dim3((unsigned)(ntmax * a.hq)), dim3(128), dq_smem<D>(), st, a);
+  hipLaunchKernelGGL(kern, dim3((unsigned)nblk), dim3(128), dq_smem<D>(), st, a);
   LOGO_LAUNCH_CHECK("sq_dq64_kernel");
   return LOGO_OK;
 }

@@ -55,7 +55,7 @@ __global__ __launch_bounds__(64 * NW) LOGO_OCC_FWD void sq_fwd_pipe_kernel(const
 
   const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63, i = l & 31, g = l >> 5;
   QTile<SPARSE> qt;
-  if (!qt.init(a, wave, i, WINDOW, 32, NW == 8)) return;
+  if (!qt.init(a, wave, i, WINDOW, 32, NW == 8, !WINDOW)) return;
   const int hq = qt.hq, p = qt.p, W = a.window;
 
   // Sparse mode holds q pre-scaled and negated, bf16(-c q) with
@@ -104,7 +104,7 @@ __global__ __launch_bounds__(64 * NW) LOGO_OCC_FWD void sq_fwd_pipe_kernel(const
   const int nt = (qt.kv_hi - kv_lo + 63) >> 6;
   int tw_lo = 0, tw_hi = 0;  // tiles this wave's rows can see
   if (qt.wave_active) {
-    tw_hi = ((qt.pmax - kv_lo) >> 6) + 1;
+    tw_hi = min(nt, ((qt.pmax - kv_lo) >> 6) + 1);
     tw_lo = WINDOW ? (max(0, qt.pmin - W - kv_lo) >> 6) : 0;
   }
 
@@ -245,7 +245,57 @@ __global__ __launch_bounds__(64 * NW) LOGO_OCC_FWD void sq_fwd_pipe_kernel(const
     if (t + 1 < nt) step(BufTag<0>{}, t + 1);
   }
 
-  const float l_tot = pair_sum(l_run);
+  float l_tot = pair_sum(l_run);
+  if (qt.nsplit > 1) {
+    // Key-range split: store this piece's partial (O unnormalised, relative to
+    // its base m_run; per row m_run and l) as [wave][dt][item][lane]; the last
+    // piece of the tile to arrive rescales all of them to the largest base.
+    constexpr int OF = DT * 16 * 64;  // O floats per wave
+    float* const part0 = a.part + (int64_t)(hq * 2 * a.split_cap + qt.trank * qt.nper) * NW * (OF + 64);
+    {
+      float* po = part0 + (int64_t)qt.piece * NW * (OF + 64) + wave * (OF + 64);
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) st_agent(po + (dt * 16 + e) * 64 + l, oacc[dt][e]);
+      st_agent(po + OF + l, g == 0 ? m_run : l_tot);
+    }
+    if (!split_arrive(a.cnt + hq * 2 * a.split_cap + qt.trank, qt.nsplit, reinterpret_cast<int*>(smem))) return;
+    // combine in piece order from zero, whichever arrived last, so the
+    // result does not depend on the arrival order
+    float mc[kMaxSplit], lc[kMaxSplit];
+    float mx = -INFINITY;
+    for (int pc = 0; pc < qt.nsplit; ++pc) {
+      const float* po = part0 + (int64_t)pc * NW * (OF + 64) + wave * (OF + 64);
+      mc[pc] = pc == qt.piece ? m_run : ld_agent(po + OF + i);
+      lc[pc] = pc == qt.piece ? l_tot : ld_agent(po + OF + 32 + i);
+      if (lc[pc] > 0.f) mx = fmaxf(mx, mc[pc]);
+    }
+    f32x16 osum[DT];
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) osum[dt] = f32x16{};
+    float lsum = 0.f;
+    for (int pc = 0; pc < qt.nsplit; ++pc) {
+      const float w = lc[pc] > 0.f ? fast_exp2(mc[pc] - mx) : 0.f;
+      if (pc == qt.piece) {
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) osum[dt][e] = fmaf(w, oacc[dt][e], osum[dt][e]);
+      } else {
+        const float* po = part0 + (int64_t)pc * NW * (OF + 64) + wave * (OF + 64);
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) osum[dt][e] = fmaf(w, ld_agent(po + (dt * 16 + e) * 64 + l), osum[dt][e]);
+      }
+      lsum = fmaf(w, lc[pc], lsum);
+    }
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) oacc[dt] = osum[dt];
+    l_tot = lsum;
+    m_run = mx;
+  }
   if (qt.valid) {
     const float inv = 1.f / l_tot;
     bf16* orow = a.o + (qt.t * a.hq + hq) * D;
@@ -265,18 +315,15 @@ __global__ __launch_bounds__(64 * NW) LOGO_OCC_FWD void sq_fwd_pipe_kernel(const
 template <int D>
 constexpr size_t fwd_smem() { return (size_t)4 * TileGeom<D, kSwz>::ELEMS * sizeof(bf16); }
 
-// Single long sequences take 8-wave workgroups of two query tiles, which
-// share each K / V tile copy between 256 rows (half the copy traffic and
-// issue per row); packed or short inputs keep 4-wave single-tile workgroups,
-// which give more workgroups where rows are few.
-constexpr int64_t kFwdPairMinTokens = 16384;
-
 template <typename EL, int D, bool SPARSE, bool WINDOW>
-static int launch_fwd(const AttnArgs& a, hipStream_t st) {
+static int launch_fwd(const AttnArgs& a_in, hipStream_t st) {
+  AttnArgs a = a_in;
   const bool paired = a.nseq == 1 && a.n >= kFwdPairMinTokens;
   const int64_t rows = paired ? 2 * kBQ : kBQ;
   const int64_t ntmax = (a.n + rows - 1) / rows + a.nseq;
-  const int64_t nblk = ntmax * a.hq;
+  if (WINDOW) a.split_cap = 0;
+  else split_setup(a, paired ? 1 : 2, fwd_part_floats(D, paired ? 8 : 4));
+  const int64_t nblk = std::max<int64_t>(ntmax, 2 * a.split_cap) * a.hq;
   LOGO_REQUIRE(nblk < ((int64_t)1 << 31), "grid too large");
   if (paired) {
     auto kern = sq_fwd_pipe_kernel<EL, D, SPARSE, WINDOW, 8>;

@@ -22,6 +22,8 @@
 #include <c10/hip/HIPStream.h>
 #include <torch/library.h>
 
+#include <cstdlib>
+
 #include "../../include/logo_hip.h"
 
 namespace {
@@ -85,6 +87,20 @@ int check_attn(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v) {
   return dt == at::kHalf ? LOGO_DTYPE_F16 : LOGO_DTYPE_BF16;
 }
 
+// Split workspace of the fwd / dq kernels for this shape (empty: no split):
+// only its counter prefix needs zeroing (the kernels leave it zero).  The
+// environment variable LOGO_SQ_SPLIT=0 turns the split off (A/B timing, and
+// tests that compare kernel variants bit for bit).
+at::Tensor split_workspace(const at::Tensor& q, const at::Tensor& cu) {
+  const char* env = std::getenv("LOGO_SQ_SPLIT");
+  const bool off = env != nullptr && env[0] == '0';
+  const size_t bytes =
+      off ? 0 : logo_sq_workspace_bytes(q.size(0), (int)cu.numel() - 1, (int)q.size(1), (int)q.size(2));
+  auto ws = at::empty({(int64_t)bytes}, q.options().dtype(at::kByte));
+  if (bytes) ws.narrow(0, 0, (int64_t)logo_sq_workspace_counter_bytes()).zero_();
+  return ws;
+}
+
 std::tuple<at::Tensor, at::Tensor> sq_fwd(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
                                           const std::optional<at::Tensor>& q_idx,
                                           const std::optional<at::Tensor>& pos, const at::Tensor& meta,
@@ -93,9 +109,11 @@ std::tuple<at::Tensor, at::Tensor> sq_fwd(const at::Tensor& q, const at::Tensor&
   const int64_t n = q.size(0), hq = q.size(1), h = k.size(1), d = q.size(2);
   auto o = at::zeros_like(q);
   auto lse = at::zeros({hq, n}, q.options().dtype(at::kFloat));  // rows past Sq stay zero
+  auto ws = window < 0 ? split_workspace(q, cu) : at::empty({0}, q.options().dtype(at::kByte));
   ok(logo_sq_fwd(cptr(q), cptr(k), cptr(v), mptr(o), lse.data_ptr<float>(), opt_ptr<int64_t>(q_idx),
                  opt_ptr<int32_t>(pos), meta.data_ptr<int32_t>(), cu.data_ptr<int32_t>(), n, (int)cu.numel() - 1,
-                 (int)hq, (int)h, (int)d, (int)v.size(2), (int)lanes, (float)scale, (int)window, dtype, sp()),
+                 (int)hq, (int)h, (int)d, (int)v.size(2), (int)lanes, (float)scale, (int)window, dtype,
+                 ws.numel() ? ws.data_ptr() : nullptr, (size_t)ws.numel(), sp()),
      "logo_sq_fwd");
   return {o, lse};
 }
@@ -127,11 +145,12 @@ struct Bwd {
     using F = decltype(&logo_sq_bwd);
     F fn = phase == 0 ? &logo_sq_bwd_delta : phase == 1 ? &logo_sq_bwd_dq : &logo_sq_bwd_dkv;
     auto p = [](at::Tensor* t) -> void* { return t && t->numel() ? t->data_ptr() : nullptr; };
+    at::Tensor ws = phase == 1 && window < 0 ? split_workspace(q, cu) : at::empty({0}, q.options().dtype(at::kByte));
     return fn(cptr(q), cptr(k), cptr(v), cptr(o), cptr(dout), lse.data_ptr<float>(),
               static_cast<float*>(p(delta)), p(q_sel), p(do_sel), p(dq), p(dk), p(dv), opt_ptr<int64_t>(q_idx),
               opt_ptr<int32_t>(pos), meta.data_ptr<int32_t>(), cu.data_ptr<int32_t>(), q.size(0),
               (int)cu.numel() - 1, (int)q.size(1), (int)k.size(1), (int)q.size(2), (int)v.size(2), (int)lanes,
-              (float)scale, (int)window, dtype, sp());
+              (float)scale, (int)window, dtype, p(&ws), (size_t)ws.numel(), sp());
   }
 };
 

@@ -22,7 +22,7 @@ def test_header_symbols_are_exported():
 
 def test_abi_version_and_workspace():
     lib = _lib.lib()
-    assert lib.logo_abi_version() == 2
+    assert lib.logo_abi_version() == 3
     assert lib.logo_compact_workspace_bytes(4096, 1) == 4
     assert lib.logo_compact_workspace_bytes(4097, 16) == 2 * 16 * 4
 
@@ -38,12 +38,12 @@ def test_fwd_bwd_reject_bad_shapes_without_touching_gpu(d, v_dim, hq, h, lanes, 
     lib = _lib.lib()
     p = ctypes.c_void_p(1)
     rc = lib.logo_sq_fwd(p, p, p, p, p, None, None, p, p, 128, 1, hq, h, d, v_dim, lanes, 0.1, -1,
-                         _lib.DTYPE_BF16, None)
+                         _lib.DTYPE_BF16, None, 0, None)
     assert rc == 1
     assert msg in lib.logo_last_error().decode()
     for fn in (lib.logo_sq_bwd, lib.logo_sq_bwd_delta, lib.logo_sq_bwd_dq, lib.logo_sq_bwd_dkv):
         rc = fn(p, p, p, p, p, p, p, p, p, p, p, p, None, None, p, p, 128, 1, hq, h, d, v_dim, lanes, 0.1, -1,
-                _lib.DTYPE_BF16, None)
+                _lib.DTYPE_BF16, None, 0, None)
         assert rc == 1
         assert msg in lib.logo_last_error().decode()
 
@@ -60,11 +60,11 @@ def test_fwd_bwd_dtype_checks_without_touching_gpu(sparse, window, dtype, msg):
     lib = _lib.lib()
     p = ctypes.c_void_p(1)
     idx = p if sparse else None
-    rc = lib.logo_sq_fwd(p, p, p, p, p, idx, idx, p, p, 128, 1, 4, 4, 128, 128, 1, 0.1, window, dtype, None)
+    rc = lib.logo_sq_fwd(p, p, p, p, p, idx, idx, p, p, 128, 1, 4, 4, 128, 128, 1, 0.1, window, dtype, None, 0, None)
     assert rc == 1 and msg in lib.logo_last_error().decode()
     for fn in (lib.logo_sq_bwd, lib.logo_sq_bwd_delta, lib.logo_sq_bwd_dq, lib.logo_sq_bwd_dkv):
         rc = fn(p, p, p, p, p, p, p, p, p, p, p, p, idx, idx, p, p, 128, 1, 4, 4, 128, 128, 1, 0.1, window,
-                dtype, None)
+                dtype, None, 0, None)
         assert rc == 1 and msg in lib.logo_last_error().decode()
 
 

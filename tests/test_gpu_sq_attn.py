@@ -248,13 +248,15 @@ def test_deterministic(gpu):
 
 
 @pytest.mark.parametrize("per_head,hq,h,d", [(False, 4, 2, 128), (True, 4, 4, 128), (False, 2, 1, 64)])
-def test_long_single_sequence_paired_forward(gpu, per_head, hq, h, d):
+def test_long_single_sequence_paired_forward(gpu, per_head, hq, h, d, monkeypatch):
     """A single sequence of >= 16K tokens takes the 8-wave two-tile forward
     workgroups; the same tokens as a pack with an extra empty segment take the
-    4-wave one-tile workgroups.  Every row visits the same 64-key tiles in the
-    same order either way, so outputs and gradients are bit-identical; the
-    first case is also checked against the torch fp32 reference (ragged last
-    tile, GQA)."""
+    4-wave one-tile workgroups.  Without the key-range split (which cuts the
+    two kinds of tiles differently) every row visits the same 64-key tiles in
+    the same order either way, so outputs and gradients are bit-identical;
+    the first case is also checked against the torch fp32 reference (ragged
+    last tile, GQA)."""
+    monkeypatch.setenv("LOGO_SQ_SPLIT", "0")
     g = gen(16 + hq + int(per_head) + d)
     n = 16384 + 77
     sel = torch.rand((n, hq) if per_head else (n,), generator=g) < 0.3
