@@ -11,11 +11,13 @@
 // Cache layout is logo/cache.py's: K/V [B, H, T, D] per layer (preallocated to
 // T_cap instead of grown with torch.cat, logo/cache.py:115-118).
 //
-// Split-K: a 256-thread workgroup takes 256 keys of one (b, q-head); each wave
+// Split-K: a 256-thread workgroup takes 256 keys of one (b, kv-head); each wave
 // takes 64 of them with lane l owning key 4s + l/16 (s = 0..15) and the 16-byte
 // column chunk l % 16, so every K/V load is a contiguous 256-byte row per 16
-// lanes.  Waves merge through LDS into one (max, sum, o[D]) partial per
-// workgroup; a combine kernel merges the partials of a row and normalises.
+// lanes.  The keys stay in registers while the workgroup serves every query
+// head of the GQA group in turn (one cache read per group, not per query
+// head).  Per query head, the waves merge through LDS into one (max, sum,
+// o[D]) partial; a combine kernel merges the partials of a row and normalises.
 #include <math.h>
 
 #include "capi.hpp"
@@ -25,6 +27,7 @@ namespace logo {
 
 constexpr int kDecKeysPerWave = 64;
 constexpr int kDecKeysPerWG = 256;
+constexpr int kDecHeadsPerPass = 8;  // query heads merged per barrier (LDS: 8 x 4 x D floats)
 
 struct DecArgs {
   const bf16* q;        // [B, HQ, D]
@@ -45,30 +48,29 @@ __device__ __forceinline__ bool dec_active(const DecArgs& a, int b) {
   return a.gate == nullptr || !((float)a.gate[b] < load_thres(a.thres, a.thres_bf16));
 }
 
-// One workgroup's split: keys [256 split, 256 split + 256) of row bq = b * HQ + hq.
-template <int D>
-__device__ __forceinline__ void dec_split(const DecArgs& a, const int split, const int bq) {
+// One workgroup's split: keys [256 split, 256 split + 256) of kv row
+// bh = b * H + h, for the query heads hq = h * G .. h * G + G - 1 (rows
+// bq = b * HQ + hq).
+// GQA: groups of more than one query head (the keys stay live across the
+// heads; G = 1 lets them die after scoring, for a higher occupancy).
+template <int D, bool GQA>
+__device__ __forceinline__ void dec_split(const DecArgs& a, const int split, const int bh) {
   constexpr int CH = D / 8;                 // 16-byte chunks per row
   constexpr int KPS = 64 / CH;              // keys per load step (4 for D=128)
   constexpr int STEPS = kDecKeysPerWave / KPS;
-  const int b = bq / a.hq, hq = bq % a.hq, h = hq / a.g;
+  const int b = bh / a.h, h = bh % a.h;
   const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63;
   const int len = a.lens[b];
   const int k0 = split * kDecKeysPerWG;
   // a single split writes the output itself (no combine launch)
   if (!dec_active(a, b) || k0 >= len) {
-    if (a.nsplit == 1 && tid < D) a.out[(int64_t)bq * D + tid] = (bf16)0.f;
+    if (a.nsplit == 1 && tid < D)
+      for (int j = 0; j < a.g; ++j) a.out[((int64_t)b * a.hq + h * a.g + j) * D + tid] = (bf16)0.f;
     return;
   }
   const int c = l % CH, kk = l / CH;
   const int kw = k0 + wave * kDecKeysPerWave;
 
-  float qv[8];
-  {
-    const bf16x8 q8 = *reinterpret_cast<const bf16x8*>(a.q + (int64_t)bq * D + 8 * c);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) qv[e] = (float)q8[e] * a.scale_log2;
-  }
   const bf16* kb = a.k + ((int64_t)b * a.h + h) * a.t_cap * D + 8 * c;
   const bf16* vb = a.v + ((int64_t)b * a.h + h) * a.t_cap * D + 8 * c;
 
@@ -84,86 +86,112 @@ __device__ __forceinline__ void dec_split(const DecArgs& a, const int split, con
     const int key = kw + KPS * s + kk;
     vr[s] = key < len ? *reinterpret_cast<const bf16x8*>(vb + (int64_t)key * D) : bf16x8{};
   }
-  float sc[STEPS];
-  float m = -INFINITY;
+  // Query heads in chunks of kDecHeadsPerPass: each head's wave partials go
+  // to LDS, and one barrier later the chunk's rows are merged together; the
+  // next head's q is loaded while the current one is scored.
+  __shared__ float sm[kDecHeadsPerPass][4], sl[kDecHeadsPerPass][4];
+  __shared__ float so[kDecHeadsPerPass][4][D];
+  const bf16* qg = a.q + ((int64_t)b * a.hq + h * a.g) * D + 8 * c;
+  bf16x8 qn = *reinterpret_cast<const bf16x8*>(qg);
+  const int G = GQA ? a.g : 1;
+  for (int j0 = 0; j0 < G; j0 += kDecHeadsPerPass) {
+    const int nj = GQA ? min(kDecHeadsPerPass, G - j0) : 1;
+    if (j0 > 0) __syncthreads();  // the previous chunk's merge has read so / sm / sl
+    for (int jj = 0; jj < nj; ++jj) {
+      // keep the keys and values packed across heads (converting them once
+      // for all heads would hold 8x their registers)
+      if constexpr (GQA) {
 #pragma unroll
-  for (int s = 0; s < STEPS; ++s) {
-    float part = 0.f;
+        for (int s = 0; s < STEPS; ++s) {
+          pin(kr[s]);
+          pin(vr[s]);
+        }
+      }
+      float qv[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) part = fmaf(qv[e], (float)kr[s][e], part);
+      for (int e = 0; e < 8; ++e) qv[e] = (float)qn[e] * a.scale_log2;
+      if (GQA && j0 + jj + 1 < G) qn = *reinterpret_cast<const bf16x8*>(qg + (int64_t)(j0 + jj + 1) * D);
+      float sc[STEPS];
+      float m = -INFINITY;
 #pragma unroll
-    for (int off = CH / 2; off > 0; off >>= 1) part += __shfl_xor(part, off);
-    const int key = kw + KPS * s + kk;
-    sc[s] = key < len ? part : -INFINITY;
-    m = fmaxf(m, sc[s]);
-  }
+      for (int s = 0; s < STEPS; ++s) {
+        float part = 0.f;
 #pragma unroll
-  for (int off = CH; off < 64; off <<= 1) m = fmaxf(m, __shfl_xor(m, off));
-  const float base = m == -INFINITY ? 0.f : m;
-  float lsum = 0.f;
-  float o[8];
+        for (int e = 0; e < 8; ++e) part = fmaf(qv[e], (float)kr[s][e], part);
 #pragma unroll
-  for (int e = 0; e < 8; ++e) o[e] = 0.f;
+        for (int off = CH / 2; off > 0; off >>= 1) part += __shfl_xor(part, off);
+        const int key = kw + KPS * s + kk;
+        sc[s] = key < len ? part : -INFINITY;
+        m = fmaxf(m, sc[s]);
+      }
 #pragma unroll
-  for (int s = 0; s < STEPS; ++s) {
-    const float p = fast_exp2(sc[s] - base);
-    lsum += p;
+      for (int off = CH; off < 64; off <<= 1) m = fmaxf(m, __shfl_xor(m, off));
+      const float base = m == -INFINITY ? 0.f : m;
+      float lsum = 0.f;
+      float o[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) o[e] = fmaf(p, (float)vr[s][e], o[e]);
-  }
+      for (int e = 0; e < 8; ++e) o[e] = 0.f;
 #pragma unroll
-  for (int off = CH; off < 64; off <<= 1) {
-    lsum += __shfl_xor(lsum, off);
+      for (int s = 0; s < STEPS; ++s) {
+        const float p = fast_exp2(sc[s] - base);
+        lsum += p;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) o[e] += __shfl_xor(o[e], off);
-  }
-
-  __shared__ float sm[4], sl[4];
-  __shared__ float so[4][D];
-  if (l < CH) {
+        for (int e = 0; e < 8; ++e) o[e] = fmaf(p, (float)vr[s][e], o[e]);
+      }
 #pragma unroll
-    for (int e = 0; e < 8; ++e) so[wave][8 * c + e] = o[e];
-  }
-  if (l == 0) {
-    sm[wave] = m;
-    sl[wave] = lsum;
-  }
-  __syncthreads();
-  if (tid < D) {
-    float M = -INFINITY;
-    for (int w = 0; w < 4; ++w) M = fmaxf(M, sm[w]);
-    const float Mb = M == -INFINITY ? 0.f : M;
-    float L = 0.f, O = 0.f;
-    for (int w = 0; w < 4; ++w) {
-      const float f = fast_exp2(sm[w] - Mb);
-      L += f * sl[w];
-      O += f * so[w][tid];
+      for (int off = CH; off < 64; off <<= 1) {
+        lsum += __shfl_xor(lsum, off);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] += __shfl_xor(o[e], off);
+      }
+      if (l < CH) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) so[jj][wave][8 * c + e] = o[e];
+      }
+      if (l == 0) {
+        sm[jj][wave] = m;
+        sl[jj][wave] = lsum;
+      }
     }
-    if (a.nsplit == 1) {
-      a.out[(int64_t)bq * D + tid] = (bf16)(L > 0.f ? O / L : 0.f);
-    } else {
-      float* pp = a.part + ((int64_t)bq * a.nsplit + split) * (D + 2);
-      pp[2 + tid] = O;
-      if (tid == 0) {
-        pp[0] = M;
-        pp[1] = L;
+    __syncthreads();
+    for (int idx = tid; idx < nj * D; idx += 256) {
+      const int jj = idx / D, d = idx % D;
+      const int bq = b * a.hq + h * a.g + j0 + jj;
+      float M = -INFINITY;
+      for (int w = 0; w < 4; ++w) M = fmaxf(M, sm[jj][w]);
+      const float Mb = M == -INFINITY ? 0.f : M;
+      float L = 0.f, O = 0.f;
+      for (int w = 0; w < 4; ++w) {
+        const float f = fast_exp2(sm[jj][w] - Mb);
+        L += f * sl[jj][w];
+        O += f * so[jj][w][d];
+      }
+      if (a.nsplit == 1) {
+        a.out[(int64_t)bq * D + d] = (bf16)(L > 0.f ? O / L : 0.f);
+      } else {
+        float* pp = a.part + ((int64_t)bq * a.nsplit + split) * (D + 2);
+        pp[2 + d] = O;
+        if (d == 0) {
+          pp[0] = M;
+          pp[1] = L;
+        }
       }
     }
   }
 }
 
-template <int D>
+template <int D, bool GQA>
 __global__ __launch_bounds__(256) void decode_split_kernel(const DecArgs a) {
-  dec_split<D>(a, blockIdx.x, blockIdx.y);
+  dec_split<D, GQA>(a, blockIdx.x, blockIdx.y);
 }
 
 // Both branches of a decode step in one launch: x < glo.nsplit are the global
 // branch's splits, x == glo.nsplit the local window's single split (at most
 // 256 keys), which writes its output row itself.
-template <int D>
+template <int D, bool GQA>
 __global__ __launch_bounds__(256) void decode_dual_split_kernel(const DecArgs loc, const DecArgs glo) {
-  if ((int)blockIdx.x == glo.nsplit) dec_split<D>(loc, 0, blockIdx.y);
-  else dec_split<D>(glo, blockIdx.x, blockIdx.y);
+  if ((int)blockIdx.x == glo.nsplit) dec_split<D, GQA>(loc, 0, blockIdx.y);
+  else dec_split<D, GQA>(glo, blockIdx.x, blockIdx.y);
 }
 
 // Merge the split partials of one (b, q-head) row: the splits' maxima and
@@ -336,11 +364,14 @@ extern "C" int logo_decode_attn(const void* q, const void* k_cache, const void* 
   const DecArgs a = dec_args(q, k_cache, v_cache, lens, gate, thres, thres_dtype, out, workspace, batch, hq, h, t_cap,
                              max_len, scale);
   hipStream_t st = as_stream(stream);
-  dim3 grid(a.nsplit, batch * hq);
+  dim3 grid(a.nsplit, batch * h);  // one workgroup per (split, kv row): the GQA group shares its keys
+  const bool gqa = a.g > 1;
   if (d == 128)
-    hipLaunchKernelGGL(decode_split_kernel<128>, grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL((gqa ? decode_split_kernel<128, true> : decode_split_kernel<128, false>), grid, dim3(256), 0,
+                       st, a);
   else
-    hipLaunchKernelGGL(decode_split_kernel<64>, grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL((gqa ? decode_split_kernel<64, true> : decode_split_kernel<64, false>), grid, dim3(256), 0,
+                       st, a);
   LOGO_LAUNCH_CHECK("decode_split_kernel");
   if (a.nsplit > 1) {  // a single split wrote the output already
     if (d == 128)
@@ -392,13 +423,15 @@ extern "C" int logo_decode_attn_fused(const void* q_local, const void* k_local, 
   e.out = static_cast<bf16*>(out);
   e.eps = eps;
   hipStream_t st = as_stream(stream);
-  const dim3 grid(glo.nsplit + 1, batch * hq);
+  const dim3 grid(glo.nsplit + 1, batch * h);
   if (d == 128) {
-    hipLaunchKernelGGL(decode_dual_split_kernel<128>, grid, dim3(256), 0, st, loc, glo);
+    hipLaunchKernelGGL((glo.g > 1 ? decode_dual_split_kernel<128, true> : decode_dual_split_kernel<128, false>),
+                       grid, dim3(256), 0, st, loc, glo);
     LOGO_LAUNCH_CHECK("decode_dual_split_kernel");
     hipLaunchKernelGGL(decode_combine_epi_kernel<128>, dim3(batch * hq), dim3(kCombThreads), 0, st, glo, e);
   } else {
-    hipLaunchKernelGGL(decode_dual_split_kernel<64>, grid, dim3(256), 0, st, loc, glo);
+    hipLaunchKernelGGL((glo.g > 1 ? decode_dual_split_kernel<64, true> : decode_dual_split_kernel<64, false>),
+                       grid, dim3(256), 0, st, loc, glo);
     LOGO_LAUNCH_CHECK("decode_dual_split_kernel");
     hipLaunchKernelGGL(decode_combine_epi_kernel<64>, dim3(batch * hq), dim3(kCombThreads), 0, st, glo, e);
   }

@@ -14,6 +14,7 @@ pytestmark = pytest.mark.gpu
 @pytest.mark.parametrize("B,HQ,H,D,lens", [
     (4, 16, 16, 128, [1, 257, 4096, 3000]),
     (3, 8, 2, 64, [5000, 128, 700]),
+    (4, 16, 4, 128, [2000, 1, 256, 9000]),  # GQA groups of 4 share one cache read
 ])
 def test_decode_matches_oracle(gpu, B, HQ, H, D, lens):
     g = gen(B * D)
