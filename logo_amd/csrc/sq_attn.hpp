@@ -268,6 +268,11 @@ int sq_launch_delta(const AttnArgs& a, hipStream_t st, int d, bool sparse, bool 
 int sq_launch_dq(const AttnArgs& a, hipStream_t st, int d, bool sparse, bool window, bool half);
 int sq_launch_dkv(const AttnArgs& a, hipStream_t st, int d, bool sparse, bool window, bool half);
 
+// The dedicated sliding-window forward (dense rows, window <= 128, bf16):
+// whether it serves a call, and its launcher.
+bool swa_fwd_applies(const AttnArgs& a, bool sparse, bool half);
+int swa_launch_fwd(const AttnArgs& a, hipStream_t st, int d);
+
 // Calls FN<D, SPARSE, WINDOW>(a, st) for the runtime (d, sparse, window).
 #define LOGO_DISPATCH(FN, a, st, d, sparse, window)                                                  \
   ((d) == 128 ? ((sparse) ? ((window) ? FN<128, true, true>(a, st) : FN<128, true, false>(a, st))   \

@@ -342,6 +342,7 @@ template <int D, bool SPARSE, bool WINDOW>
 static int launch_fwd_bf16(const AttnArgs& a, hipStream_t st) { return launch_fwd<bf16, D, SPARSE, WINDOW>(a, st); }
 
 int sq_launch_fwd(const AttnArgs& a, hipStream_t st, int d, bool sparse, bool window, bool half) {
+  if (window && swa_fwd_applies(a, sparse, half)) return swa_launch_fwd(a, st, d);
   if (half) return d == 128 ? launch_fwd<f16, 128, true, false>(a, st) : launch_fwd<f16, 64, true, false>(a, st);
   return LOGO_DISPATCH(launch_fwd_bf16, a, st, d, sparse, window);
 }

@@ -107,8 +107,12 @@ std::tuple<at::Tensor, at::Tensor> sq_fwd(const at::Tensor& q, const at::Tensor&
                                           const at::Tensor& cu, int64_t lanes, double scale, int64_t window) {
   const int dtype = check_attn(q, k, v);
   const int64_t n = q.size(0), hq = q.size(1), h = k.size(1), d = q.size(2);
-  auto o = at::zeros_like(q);
-  auto lse = at::zeros({hq, n}, q.options().dtype(at::kFloat));  // rows past Sq stay zero
+  // Sparse mode writes the selected rows only (the others are zero, and lse
+  // past each head's Sq); dense mode writes every row of cu's segments, which
+  // cover the tokens, so it skips the fill.
+  const bool sparse = q_idx.has_value();
+  auto o = sparse ? at::zeros_like(q) : at::empty_like(q);
+  auto lse = sparse ? at::zeros({hq, n}, q.options().dtype(at::kFloat)) : at::empty({hq, n}, q.options().dtype(at::kFloat));
   auto ws = window < 0 ? split_workspace(q, cu) : at::empty({0}, q.options().dtype(at::kByte));
   ok(logo_sq_fwd(cptr(q), cptr(k), cptr(v), mptr(o), lse.data_ptr<float>(), opt_ptr<int64_t>(q_idx),
                  opt_ptr<int32_t>(pos), meta.data_ptr<int32_t>(), cu.data_ptr<int32_t>(), n, (int)cu.numel() - 1,
@@ -165,7 +169,8 @@ struct Bwd {
 std::tuple<at::Tensor, at::Tensor, at::Tensor> sq_bwd_delta(LOGO_BWD_SCHEMA_ARGS) {
   check_attn(q, k, v);
   const bool sparse = q_idx.has_value();
-  auto delta = at::zeros({q.size(1), q.size(0)}, q.options().dtype(at::kFloat));
+  auto delta = sparse ? at::zeros({q.size(1), q.size(0)}, q.options().dtype(at::kFloat))
+                      : at::empty({q.size(1), q.size(0)}, q.options().dtype(at::kFloat));
   auto q_sel = sparse ? at::empty({q.size(1), q.size(0), q.size(2)}, q.options()) : at::empty({0}, q.options());
   auto do_sel = sparse ? at::empty_like(q_sel) : at::empty({0}, q.options());
   Bwd b{q, k, v, o, lse, dout, q_idx, pos, meta, cu, lanes, scale, window};
@@ -176,7 +181,7 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> sq_bwd_delta(LOGO_BWD_SCHEMA_ARGS
 at::Tensor sq_bwd_dq(LOGO_BWD_SCHEMA_ARGS, const at::Tensor& delta, const at::Tensor& q_sel,
                      const at::Tensor& do_sel) {
   check_attn(q, k, v);
-  auto dq = at::zeros_like(q);
+  auto dq = q_idx.has_value() ? at::zeros_like(q) : at::empty_like(q);  // dense: every row written
   Bwd b{q, k, v, o, lse, dout, q_idx, pos, meta, cu, lanes, scale, window};
   auto dl = delta, qs = q_sel, ds = do_sel;
   ok(b.call(1, &dl, &qs, &ds, &dq, nullptr, nullptr), "logo_sq_bwd_dq");

@@ -121,21 +121,28 @@ def test_dense_paths_and_dense_ref(gpu):
     assert_within("dense", o2, ro)
 
 
-@pytest.mark.parametrize("window", [128, 16])
-def test_swa_fwd_bwd_matches_oracle(gpu, window):
-    n, hq, h, d = 900, 4, 2, 128
-    g = gen(7 + window)
+@pytest.mark.parametrize("window,d", [(128, 128), (16, 128), (0, 64), (1, 128), (33, 64), (64, 128), (100, 64),
+                                      (127, 128), (200, 128)])
+def test_swa_fwd_bwd_matches_oracle(gpu, window, d):
+    """Sliding-window attention (keys [p - w, p]) against the oracle: windows
+    up to 128 take the dedicated window forward (whole key window in LDS),
+    200 the generic pipelined one; packed segments of 50, 1 and 849 rows
+    (ragged last blocks, a segment shorter than the window).  Bound: the
+    north-star max-abs 2e-2, scaled by max(1, max |ref|) (with one or two
+    visible keys the probabilities are O(1) and dP = dO.v ~ N(0, D), so
+    |dK| reaches 2-4, where one bf16 ulp is 1.6e-2), and mean-abs 2e-3."""
+    n, hq, h = 900, 4, 2
+    g = gen(7 + window + d)
     q, k, v = randn((n, hq, d), g), randn((n, h, d), g), randn((n, h, d), g)
     do = randn((n, hq, d), g)
     cu = torch.tensor([0, 50, 51, 900], dtype=torch.int32)
+    print(f"swa window={window} d={d}", flush=True)
     qg, kg, vg = (x.to(gpu).requires_grad_() for x in (q, k, v))
     o = swa_attn(qg[None], kg[None], vg[None], cu.to(gpu), window=window)[0]
     o.backward(do.to(gpu))
     ro, (rdq, rdk, rdv) = _oracle(q, k, v, None, cu, do=do, window=window)
-    assert_within("o", o, ro)
-    assert_within("dq", qg.grad, rdq)
-    assert_within("dk", kg.grad, rdk)
-    assert_within("dv", vg.grad, rdv)
+    for name, x, r in (("o", o, ro), ("dq", qg.grad, rdq), ("dk", kg.grad, rdk), ("dv", vg.grad, rdv)):
+        assert_within(name, x, r, max_abs=2e-2 * max(1.0, float(np.abs(r).max())))
 
 
 def test_noncontiguous_and_fp32_inputs(gpu):
