@@ -23,6 +23,9 @@
 #include <torch/library.h>
 
 #include <cstdlib>
+#include <map>
+#include <mutex>
+#include <utility>
 
 #include "../../include/logo_hip.h"
 
@@ -87,17 +90,27 @@ int check_attn(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v) {
   return dt == at::kHalf ? LOGO_DTYPE_F16 : LOGO_DTYPE_BF16;
 }
 
-// Split workspace of the fwd / dq kernels for this shape (empty: no split):
-// only its counter prefix needs zeroing (the kernels leave it zero).  The
-// environment variable LOGO_SQ_SPLIT=0 turns the split off (A/B timing, and
-// tests that compare kernel variants bit for bit).
+// Split workspace of the fwd / dq kernels for this shape (empty: no split).
+// One buffer per (device, stream), kept across calls and grown on demand:
+// the kernels leave its counter prefix zero, so only a new buffer needs the
+// zero-fill, and calls on one stream run in order, so they never overlap on
+// it.  The environment variable LOGO_SQ_SPLIT=0 turns the split off (A/B
+// timing, and tests that compare kernel variants bit for bit).
 at::Tensor split_workspace(const at::Tensor& q, const at::Tensor& cu) {
   const char* env = std::getenv("LOGO_SQ_SPLIT");
   const bool off = env != nullptr && env[0] == '0';
   const size_t bytes =
       off ? 0 : logo_sq_workspace_bytes(q.size(0), (int)cu.numel() - 1, (int)q.size(1), (int)q.size(2));
-  auto ws = at::empty({(int64_t)bytes}, q.options().dtype(at::kByte));
-  if (bytes) ws.narrow(0, 0, (int64_t)logo_sq_workspace_counter_bytes()).zero_();
+  if (bytes == 0) return at::empty({0}, q.options().dtype(at::kByte));
+  static std::mutex mu;
+  static std::map<std::pair<int, void*>, at::Tensor> cache;
+  const auto key = std::make_pair((int)q.get_device(), sp());
+  std::lock_guard<std::mutex> lock(mu);
+  at::Tensor& ws = cache[key];
+  if (!ws.defined() || (size_t)ws.numel() < bytes) {
+    ws = at::empty({(int64_t)bytes}, q.options().dtype(at::kByte));
+    ws.narrow(0, 0, (int64_t)logo_sq_workspace_counter_bytes()).zero_();
+  }
   return ws;
 }
 
