@@ -6,7 +6,14 @@
 // attention kernels use to map a workgroup to (sequence, block), which replace
 // prepare_chunk_indices (logo/ops/common.py:110-124) and its host sync.
 //
-// Three launches, none of them synchronising with the host:
+// Short inputs (at most 4096 tokens) and per-head selections of at most 65536
+// tokens a lane take one launch with one 1024-thread workgroup per lane
+// (compact_small): per-64-token ballot counts in LDS, their exclusive scan, a
+// second ballot pass that writes q_idx / pos, cu_q from the group prefixes,
+// then the tile prefixes (one lane of 32768 tokens takes it in about 24 us,
+// no faster than the three launches below, which spread it over the GPU).
+// Everything else takes three launches, none of them synchronising with the
+// host:
 //   count    : per 4096-token chunk and lane, popcount of wave ballots
 //   scatter  : chunk prefix + wave prefix (LDS) + mbcnt rank -> q_idx, pos
 //   finalize : Sq, cu_q by binary search over q_idx, tile prefixes by block scan
@@ -96,22 +103,127 @@ __global__ __launch_bounds__(256) void compact_scatter(const uint8_t* __restrict
   }
 }
 
-// Exclusive scan over 256 threads; returns this thread's exclusive prefix and
+// Exclusive scan over NT threads; returns this thread's exclusive prefix and
 // writes the block total to *total.
+template <int NT = 256>
 __device__ __forceinline__ int block_exscan(int v, int* buf, int* total) {
   const int tid = threadIdx.x;
   buf[tid] = v;
   __syncthreads();
-  for (int off = 1; off < 256; off <<= 1) {
+  for (int off = 1; off < NT; off <<= 1) {
     int add = tid >= off ? buf[tid - off] : 0;
     __syncthreads();
     buf[tid] += add;
     __syncthreads();
   }
   const int inc = buf[tid];
-  *total = buf[255];
+  *total = buf[NT - 1];
   __syncthreads();
   return inc - v;
+}
+
+// Tile prefixes per sequence (query tiles of LOGO_BQ compacted rows, key
+// tiles of LOGO_BKV tokens) and the header, from cu_q already in meta
+// (written by this workgroup before its last barrier).
+template <int NT>
+__device__ __forceinline__ void meta_tiles(const int32_t* __restrict__ cu, int nseq, int64_t n, int sq,
+                                           int32_t* __restrict__ m, int* buf) {
+  int32_t* cu_q = m + kMetaHdr;
+  int32_t* cu_tq = cu_q + (nseq + 1);
+  int32_t* cu_tk = cu_tq + (nseq + 1);
+  int carry_q = 0, carry_k = 0;
+  for (int s0 = 0; s0 < nseq; s0 += NT) {
+    const int s = s0 + threadIdx.x;
+    int bq = 0, bk = 0;
+    if (s < nseq) {
+      const int cq = cu_q[s + 1] - cu_q[s];
+      const int ck = cu[s + 1] - cu[s];
+      bq = (cq + LOGO_BQ - 1) / LOGO_BQ;
+      bk = (ck + LOGO_BKV - 1) / LOGO_BKV;
+    }
+    int tq, tk;
+    const int eq = block_exscan<NT>(bq, buf, &tq);
+    const int ek = block_exscan<NT>(bk, buf, &tk);
+    if (s < nseq) {
+      cu_tq[s] = carry_q + eq;
+      cu_tk[s] = carry_k + ek;
+    }
+    carry_q += tq;
+    carry_k += tk;
+  }
+  if (threadIdx.x == 0) {
+    cu_tq[nseq] = carry_q;
+    cu_tk[nseq] = carry_k;
+    m[0] = sq;
+    m[1] = carry_q;
+    m[2] = carry_k;
+    m[3] = (int)n;
+    m[4] = nseq;
+    m[5] = m[6] = m[7] = 0;
+  }
+}
+
+// The whole compaction of one lane of at most kSmallMax tokens in one
+// workgroup (same outputs as count + scatter + finalize).
+constexpr int kSmallMax = 65536;
+constexpr int kSmallThreads = 1024;
+__global__ __launch_bounds__(kSmallThreads) void compact_small(const uint8_t* __restrict__ sel, int64_t n,
+                                                               int lanes, const int32_t* __restrict__ cu,
+                                                               int nseq, int64_t* __restrict__ q_idx,
+                                                               int32_t* __restrict__ pos,
+                                                               int32_t* __restrict__ meta) {
+  constexpr int NW = kSmallThreads / 64;
+  __shared__ int gpre[kSmallMax / 64];  // per 64-token group: its count, then its exclusive prefix
+  __shared__ int buf[kSmallThreads];
+  const int lane = blockIdx.x;
+  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63;
+  const int G = (int)((n + 63) >> 6);
+#pragma unroll 8
+  for (int gi = w; gi < G; gi += NW) {
+    const uint64_t msk = __ballot(sel_on(sel, n, lanes, lane, (int64_t)gi * 64 + l));
+    if (l == 0) gpre[gi] = __popcll(msk);
+  }
+  __syncthreads();
+  int sq;
+  {
+    // G <= kSmallThreads groups: thread tid scans group tid
+    const int v = tid < G ? gpre[tid] : 0;
+    const int e = block_exscan<kSmallThreads>(v, buf, &sq);
+    if (tid < G) gpre[tid] = e;
+  }
+  __syncthreads();
+  int64_t* qi = q_idx + (int64_t)lane * n;
+  int32_t* ps = pos + (int64_t)lane * n;
+  const uint64_t below = (l == 0) ? 0ull : (~0ull >> (64 - l));
+#pragma unroll 8
+  for (int gi = w; gi < G; gi += NW) {
+    const int64_t t = (int64_t)gi * 64 + l;
+    const uint64_t msk = __ballot(sel_on(sel, n, lanes, lane, t));
+    if ((msk >> l) & 1ull) {
+      const int rank = gpre[gi] + __popcll(msk & below);
+      const int sg = seg_of(cu, nseq, t);
+      qi[rank] = t;
+      ps[rank] = (int32_t)(t - cu[sg]);
+    }
+  }
+  // cu_q[s] = selected tokens before token cu[s]: the prefix of its group plus
+  // the selected tokens of the group below it
+  int32_t* m = meta + (int64_t)lane * LOGO_META_STRIDE(nseq);
+  for (int s = w; s <= nseq; s += NW) {
+    const int64_t key = cu[s];
+    const int gi = (int)(key >> 6);
+    int v;
+    if (gi >= G) {
+      v = sq;
+    } else {
+      const uint64_t msk = __ballot(sel_on(sel, n, lanes, lane, (int64_t)gi * 64 + l));
+      const int r = (int)(key & 63);
+      v = gpre[gi] + __popcll(r == 0 ? 0ull : (msk & (~0ull >> (64 - r))));
+    }
+    if (l == 0) m[kMetaHdr + s] = v;
+  }
+  __syncthreads();
+  meta_tiles<kSmallThreads>(cu, nseq, n, sq, m, buf);
 }
 
 // One workgroup per lane.  dense != 0: cu_q = cu and Sq = n (no q_idx).
@@ -125,8 +237,6 @@ __global__ __launch_bounds__(256) void compact_finalize(const int32_t* __restric
   const int stride = LOGO_META_STRIDE(nseq);
   int32_t* m = meta + (int64_t)lane * stride;
   int32_t* cu_q = m + kMetaHdr;
-  int32_t* cu_tq = cu_q + (nseq + 1);
-  int32_t* cu_tk = cu_tq + (nseq + 1);
 
   int sq;
   if (dense) {
@@ -154,37 +264,7 @@ __global__ __launch_bounds__(256) void compact_finalize(const int32_t* __restric
     cu_q[s] = v;
   }
   __syncthreads();
-
-  int carry_q = 0, carry_k = 0;
-  for (int s0 = 0; s0 < nseq; s0 += 256) {
-    const int s = s0 + threadIdx.x;
-    int bq = 0, bk = 0;
-    if (s < nseq) {
-      const int cq = cu_q[s + 1] - cu_q[s];
-      const int ck = cu[s + 1] - cu[s];
-      bq = (cq + LOGO_BQ - 1) / LOGO_BQ;
-      bk = (ck + LOGO_BKV - 1) / LOGO_BKV;
-    }
-    int tq, tk;
-    const int eq = block_exscan(bq, buf, &tq);
-    const int ek = block_exscan(bk, buf, &tk);
-    if (s < nseq) {
-      cu_tq[s] = carry_q + eq;
-      cu_tk[s] = carry_k + ek;
-    }
-    carry_q += tq;
-    carry_k += tk;
-  }
-  if (threadIdx.x == 0) {
-    cu_tq[nseq] = carry_q;
-    cu_tk[nseq] = carry_k;
-    m[0] = sq;
-    m[1] = carry_q;
-    m[2] = carry_k;
-    m[3] = (int)n;
-    m[4] = nseq;
-    m[5] = m[6] = m[7] = 0;
-  }
+  meta_tiles<256>(cu, nseq, n, sq, m, buf);
 }
 
 // prepare_chunk_indices for an arbitrary chunk size (parity helper).
@@ -243,6 +323,12 @@ extern "C" size_t logo_compact_workspace_bytes(int64_t n_tokens, int lanes) {
 static int compact_launch(const uint8_t* selection, int64_t n_tokens, int lanes, const int32_t* cu,
                           int nseq, int64_t* q_idx, int32_t* pos, int32_t* meta, int32_t* counts,
                           hipStream_t st) {
+  if (n_tokens <= 4096 || (lanes >= 4 && n_tokens <= kSmallMax)) {
+    hipLaunchKernelGGL(compact_small, dim3(lanes), dim3(kSmallThreads), 0, st, selection, n_tokens, lanes, cu, nseq,
+                       q_idx, pos, meta);
+    LOGO_LAUNCH_CHECK("compact_small");
+    return LOGO_OK;
+  }
   const int nchunk = (int)((n_tokens + kChunk - 1) / kChunk);
   if (nchunk > 0) {
     dim3 grid(nchunk, lanes);

@@ -26,6 +26,9 @@ CASES = [
     ([0, 3000, 3000, 9000, 9001, 12345], 0.3),
     ([0, 8192, 16384, 24576, 32768], 0.25),
     ([0, 70000], 0.5),
+    ([0, 4096], 0.7),             # the largest one-lane input one workgroup compacts alone
+    ([0, 100, 4097], 0.7),        # one token past it: the three-launch path
+    ([0, 63, 64, 65, 130], 0.5),  # segment bounds inside and on 64-token groups
 ]
 
 
@@ -62,7 +65,9 @@ def test_compaction_bit_exact(gpu, cu, ratio):
     _check_lane(dsel, 0, want, cu, n)
 
 
-@pytest.mark.parametrize("cu,ratio", [([0, 512], 0.5), ([0, 5000, 5000, 8192], 0.5)])
+@pytest.mark.parametrize("cu,ratio", [([0, 512], 0.5), ([0, 5000, 5000, 8192], 0.5),
+                                      ([0, 30000, 65536], 0.3),   # per-head: one workgroup a lane
+                                      ([0, 70000], 0.3)])         # past 65536: three launches
 def test_per_head_lanes_bit_exact(gpu, cu, ratio):
     n, hq = cu[-1], 4
     rng = np.random.default_rng(7)

@@ -57,7 +57,8 @@ def _case(n, lanes, lengths, ratio, seed):
 def test_noalloc_matches_compact_twice_second_smaller(gpu):
     cases = [
         (300000, 16, [1, 0, 150000, 149999], 0.3, 1),   # 74 chunks x 16 lanes of counts
-        (5000, 1, [2500, 0, 2500], 0.5, 2),             # smaller: 2 chunks x 1 lane
+        (70000, 1, [35000, 0, 35000], 0.5, 2),          # smaller: 18 chunks x 1 lane (above the
+                                                        # 65536 tokens one workgroup compacts alone)
     ]
     for n, lanes, lengths, ratio, seed in cases:
         print(f"noalloc compaction n={n} lanes={lanes} segments={len(lengths)}", flush=True)
