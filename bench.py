@@ -9,7 +9,9 @@ in HBM.  Effective FLOPs count selected rows only:
 ``F = 3.5 * 4 * D * HQ * sum over selected rows of (p + 1)``.
 
 Prints ONE JSON line.  Per-kernel durations come from HIP events recorded on
-the launch stream around every C-ABI launch inside the timed region; the
+the launch stream around every operator call that launches the kernel inside
+the timed region (the operator's output allocation included, and for the
+forward and dq the zero-fill of unselected rows; dk/dv has none); the
 dominant kernel's roofline is its algorithmic FLOPs over that duration.  The
 CPU baseline times the reference's CPU formulation (dense causal attention per
 segment, then row masking, torch fp32 autograd) on a bounded sample of heads.
@@ -102,7 +104,8 @@ def markov_mask(n, ratio, mean_run, gen):
 
 
 class EventTimer:
-    """Launch hook: HIP events around each C-ABI launch on the current stream."""
+    """Launch hook: HIP events on the current stream around each operator call
+    that launches a kernel (its output allocation and fills included)."""
 
     def __init__(self):
         self.pending = {}
@@ -288,7 +291,7 @@ def layer_cfg4_measurement(dev, iters=5, seed=3):
     gate logits are ~ N(0, 1) and threshold 0.5 selects about half the tokens.
     A step is the layer forward plus the backward of a random upstream
     gradient into the hidden states and every parameter.  The HIP kernels'
-    own durations (HIP events around each C-ABI launch) are listed beside the
+    own durations (HIP events around each launching operator call) are listed beside the
     step time; the remainder is the projections (hipBLASLt through torch)
     and the torch glue (RoPE and norms under autograd)."""
     from logo_amd import _lib
