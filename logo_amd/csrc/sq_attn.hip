@@ -48,45 +48,64 @@ namespace logo {
 // do_sel = -dO, which let the dq and dk/dv kernels start their S and dP
 // accumulators from lse and delta.
 // ---------------------------------------------------------------------------
+// Each thread takes one 16-byte chunk of kDeltaRows rows (RPB apart), all its
+// loads issued before any arithmetic, so a workgroup keeps 4x the bytes in
+// flight of a row-per-thread layout.
+constexpr int kDeltaRows = 4;
+
 template <typename EL, int D, bool SPARSE>
 __global__ __launch_bounds__(256) void sq_delta_kernel(const AttnArgs a) {
   using E8 = typename Elem<EL>::x8;
   constexpr int LPR = D / 8;          // lanes per row
-  constexpr int RPB = 256 / LPR;      // rows per workgroup
+  constexpr int RPB = 256 / LPR;      // rows per workgroup and step
+  constexpr int R = kDeltaRows;
   const int hq = blockIdx.y;
   const int lane_sel = a.lanes > 1 ? hq : 0;
   const int32_t* meta = a.meta + (int64_t)lane_sel * a.meta_stride;
   const int sq = meta[0];
-  const int r = blockIdx.x * RPB + threadIdx.x / LPR;
+  const int r0 = blockIdx.x * RPB * R + threadIdx.x / LPR;
   const int c = threadIdx.x % LPR;
-  float acc = 0.f;
-  if (r < sq) {
-    const int64_t t = SPARSE ? a.q_idx[(int64_t)lane_sel * a.n + r] : (int64_t)r;
-    const int64_t off = (t * a.hq + hq) * D + 8 * c;
-    const E8 ov = *reinterpret_cast<const E8*>(a.o + off);
-    const E8 dv = *reinterpret_cast<const E8*>(a.dout + off);
+  if (blockIdx.x * RPB * R >= sq) return;
+  int64_t off[R];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc = fmaf((float)ov[e], (float)dv[e], acc);
-    if (SPARSE) {
+  for (int k = 0; k < R; ++k) {
+    const int r = r0 + k * RPB;
+    const int64_t t = r < sq ? (SPARSE ? a.q_idx[(int64_t)lane_sel * a.n + r] : (int64_t)r) : 0;
+    off[k] = (t * a.hq + hq) * D + 8 * c;
+  }
+  E8 ov[R], dv[R], qv[R];
+#pragma unroll
+  for (int k = 0; k < R; ++k) {
+    const bool ok = r0 + k * RPB < sq;
+    ov[k] = ok ? *reinterpret_cast<const E8*>(a.o + off[k]) : E8{};
+    dv[k] = ok ? *reinterpret_cast<const E8*>(a.dout + off[k]) : E8{};
+    if (SPARSE) qv[k] = ok ? *reinterpret_cast<const E8*>(a.q + off[k]) : E8{};
+  }
+#pragma unroll
+  for (int k = 0; k < R; ++k) {
+    const int r = r0 + k * RPB;
+    float acc = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc = fmaf((float)ov[k][e], (float)dv[k][e], acc);
+    if (SPARSE && r < sq) {
       // the copies the dq and dk/dv kernels stream: q_sel = round(-c q) with
       // c = scale * log2(e), do_sel = -dO (exact)
       const int64_t soff = ((int64_t)hq * a.n + r) * D + 8 * c;
-      const E8 qv = *reinterpret_cast<const E8*>(a.q + off);
       E8 dn;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) dn[e] = -dv[e];
+      for (int e = 0; e < 8; ++e) dn[e] = -dv[k][e];
       *reinterpret_cast<E8*>(a.do_sel + soff) = dn;
-      *reinterpret_cast<E8*>(a.q_sel + soff) = scale8(qv, -a.scale_log2);
+      *reinterpret_cast<E8*>(a.q_sel + soff) = scale8(qv[k], -a.scale_log2);
     }
-  }
 #pragma unroll
-  for (int off = LPR / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
-  if (r < sq && c == 0) a.delta[(int64_t)hq * a.n + r] = acc;
+    for (int o = LPR / 2; o > 0; o >>= 1) acc += __shfl_xor(acc, o);
+    if (r < sq && c == 0) a.delta[(int64_t)hq * a.n + r] = acc;
+  }
 }
 
 template <typename EL, int D, bool SPARSE>
 static int launch_delta(const AttnArgs& a, hipStream_t st) {
-  constexpr int RPB = 256 / (D / 8);
+  constexpr int RPB = 256 / (D / 8) * kDeltaRows;
   dim3 grid((unsigned)((a.n + RPB - 1) / RPB), a.hq);
   hipLaunchKernelGGL((sq_delta_kernel<EL, D, SPARSE>), grid, dim3(256), 0, st, a);
   LOGO_LAUNCH_CHECK("sq_delta_kernel");
