@@ -194,6 +194,20 @@ int logo_sq_bwd_dkv(const void* q, const void* k, const void* v, const void* o,
     size_t workspace_bytes, void* stream);
 
 /*
+ * The dq and dk/dv phases together (after logo_sq_bwd_delta), same arguments,
+ * dq, dk and dv all required: the two phases above in turn, except for the
+ * local sliding-window branch (dense rows, 0 <= window <= 128, HQ == H, bf16;
+ * logo/layers/utils.py:144-147), which runs one fused pass that computes S
+ * and dP once for all three gradients.  logo_sq_bwd takes the same route.
+ */
+int logo_sq_bwd_dqkv(const void* q, const void* k, const void* v, const void* o,
+    const void* dout, const float* lse, float* delta, void* q_sel, void* do_sel,
+    void* dq, void* dk, void* dv, const int64_t* q_idx, const int32_t* pos,
+    const int32_t* meta, const int32_t* cu, int64_t n_tokens, int nseq, int hq,
+    int h, int d, int v_dim, int lanes, float scale, int window, int dtype, void* workspace,
+    size_t workspace_bytes, void* stream);
+
+/*
  * Fused epilogue forward: gate threshold, the two branch context RMSNorms
  * (one [D] weight each, shared by all heads) and the gated fusion, with the
  * reference's eager bf16 rounding points (logo/modules/layernorm.py:17-22;

@@ -62,7 +62,7 @@ SIGNATURES = {
 }
 _BWD = ([_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I, _I, _I, _I, _I, _I, _F, _I, _I, _P,
          _SZ, _P], _I)
-for _name in ("logo_sq_bwd", "logo_sq_bwd_delta", "logo_sq_bwd_dq", "logo_sq_bwd_dkv"):
+for _name in ("logo_sq_bwd", "logo_sq_bwd_delta", "logo_sq_bwd_dq", "logo_sq_bwd_dkv", "logo_sq_bwd_dqkv"):
     SIGNATURES[_name] = _BWD
 
 # Library constants (include/logo_hip.h).

@@ -66,6 +66,10 @@ def _register_fakes():
     def _(q, k, v, o, lse, dout, q_idx, pos, meta, cu, lanes, scale, window, delta, q_sel, do_sel):
         return torch.empty_like(k), torch.empty_like(v)
 
+    @fake("logo_hip::sq_bwd_dqkv")
+    def _(q, k, v, o, lse, dout, q_idx, pos, meta, cu, lanes, scale, window, delta, q_sel, do_sel):
+        return torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+
     @fake("logo_hip::sq_bwd")
     def _(q, k, v, o, lse, dout, q_idx, pos, meta, cu, lanes, scale, window):
         return torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)

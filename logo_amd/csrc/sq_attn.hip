@@ -247,11 +247,13 @@ static int bwd_entry(LOGO_BWD_PARAMS, int phase) {
     rc = sq_launch_delta(a, st, d, sparse, half);
     if (rc != LOGO_OK) return rc;
   }
-  if (phase < 0 || phase == 1) {
+  // dq, dk and dv together: one pass where the fused window kernel applies
+  if ((phase < 0 || phase == 3) && swa_bwd_applies(a, sparse, half)) return swa_launch_bwd(a, st, d);
+  if (phase < 0 || phase == 1 || phase == 3) {
     rc = sq_launch_dq(a, st, d, sparse, win, half);
     if (rc != LOGO_OK) return rc;
   }
-  if (phase < 0 || phase == 2) rc = sq_launch_dkv(a, st, d, sparse, win, half);
+  if (phase < 0 || phase == 2 || phase == 3) rc = sq_launch_dkv(a, st, d, sparse, win, half);
   return rc;
 }
 
@@ -259,4 +261,5 @@ extern "C" int logo_sq_bwd(LOGO_BWD_PARAMS) { return bwd_entry(LOGO_BWD_ARGS, -1
 extern "C" int logo_sq_bwd_delta(LOGO_BWD_PARAMS) { return bwd_entry(LOGO_BWD_ARGS, 0); }
 extern "C" int logo_sq_bwd_dq(LOGO_BWD_PARAMS) { return bwd_entry(LOGO_BWD_ARGS, 1); }
 extern "C" int logo_sq_bwd_dkv(LOGO_BWD_PARAMS) { return bwd_entry(LOGO_BWD_ARGS, 2); }
+extern "C" int logo_sq_bwd_dqkv(LOGO_BWD_PARAMS) { return bwd_entry(LOGO_BWD_ARGS, 3); }
 

@@ -272,6 +272,10 @@ int sq_launch_dkv(const AttnArgs& a, hipStream_t st, int d, bool sparse, bool wi
 // whether it serves a call, and its launcher.
 bool swa_fwd_applies(const AttnArgs& a, bool sparse, bool half);
 int swa_launch_fwd(const AttnArgs& a, hipStream_t st, int d);
+// The fused sliding-window backward (dq, dk and dv in one pass; dense rows,
+// window <= 128, HQ == H, bf16; delta computed beforehand).
+bool swa_bwd_applies(const AttnArgs& a, bool sparse, bool half);
+int swa_launch_bwd(const AttnArgs& a, hipStream_t st, int d);
 
 // Calls FN<D, SPARSE, WINDOW>(a, st) for the runtime (d, sparse, window).
 #define LOGO_DISPATCH(FN, a, st, d, sparse, window)                                                  \

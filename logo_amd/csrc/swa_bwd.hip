@@ -1,0 +1,531 @@
+// Sliding-window causal attention backward for gfx950: dq, dk and dv of the
+// local branch (flash-attn window_size=(w, w), causal=True over every row, as
+// called by logo/layers/utils.py:144-147, :166-178) in one pass, for windows
+// of at most 128 keys, dense rows, HQ == H.
+//
+// Row p sees keys [p - w, p] of its segment, so a block of 128 keys is seen
+// by rows [128 j, 128 j + 127 + w]: four 64-row steps, two of which the next
+// block sees again.  The generic dq and dk/dv kernels each start one
+// workgroup per tile with its own prologue, epilogue and exposed load
+// latency, read q, dO, K and V twice between them and compute S and dP twice.
+// Here one persistent workgroup per CU walks a contiguous run of key blocks:
+//   * each wave owns 32 keys of the block: V in registers, K in the block's
+//     LDS tile (also dQ's operand), dK and dV in AGPRs, stored once when the
+//     walk leaves the block; the next block's K (global -> LDS) and V
+//     (global -> registers) are loaded during this one;
+//   * the 64-row steps stream through two LDS stages (q, dO, lse, delta),
+//     the next step's copy in flight while this one computes (step r of a
+//     block uses stage r % 2, so every LDS address is a lane register plus
+//     a constant);
+//   * each wave computes S, P, dP and dS for its keys and the step's visible
+//     32-row halves, accumulates dV and dK, and writes dS^T (bf16) to LDS;
+//     after a barrier every wave computes one 32-column slice of dQ = dS K
+//     from dS^T and the block's K tile (both read transposed);
+//   * a step's dQ is finished by the two blocks that see it: the first
+//     leaves its part in AGPRs, the next adds its own and stores.  A
+//     workgroup whose run starts inside a sequence first recomputes the
+//     previous block's part of its first two steps (S, dP, dS and dQ only),
+//     and leaves the last two steps of its run's last block to the workgroup
+//     after it, so every dQ row is stored by exactly one workgroup and no
+//     partial crosses workgroups.
+// Results follow the generic kernels: P = exp2(S c - lse) with the forward's
+// log2-domain lse, dS = P (dP - delta), dV = P^T dO, dK = scale dS^T Q,
+// dQ = scale dS K, fp32 accumulation, bf16 stores.  delta comes from the
+// delta kernel.
+#include "sq_attn.hpp"
+
+namespace logo {
+
+constexpr int kSwbMaxWindow = 128;
+
+// LDS, bytes: q tiles of the two stages, then their dO tiles (all four within
+// the 64 KB reach of the DS instruction offset at D = 128), lse / delta of the
+// stages, two K buffers of 128 keys (64-row kSwz tiles), and dS^T
+// [128 keys][64 rows] in the padded kTr layout (only read transposed).
+template <int D>
+struct SwbLayout {
+  static constexpr int TILE = 64 * D * 2;
+  using GS = TileGeom<64, kTr>;
+  static constexpr int q(int b) { return b * TILE; }
+  static constexpr int dout(int b) { return (2 + b) * TILE; }
+  static constexpr int lse(int b) { return 4 * TILE + b * 512; }
+  static constexpr int delta(int b) { return lse(b) + 256; }
+  static constexpr int kbuf(int b) { return 4 * TILE + 1024 + b * 2 * TILE; }
+  static constexpr int ds() { return 8 * TILE + 1024; }
+  static constexpr int BYTES = ds() + 2 * GS::ELEMS * 2;
+};
+
+// dQ k-steps (16 keys) of step r's half q that a 128-key window can reach:
+// keys [64 r + 32 q - 128, 64 r + 32 q + 31] within the block.
+constexpr int swb_klo(int r, int q) {
+  return (64 * r + 32 * q - kSwbMaxWindow > 0 ? 64 * r + 32 * q - kSwbMaxWindow : 0) >> 4;
+}
+constexpr int swb_khi(int r, int q) { return (64 * r + 32 * q + 31 < 127 ? 64 * r + 32 * q + 31 : 127) >> 4; }
+
+// A key block of the walk: head, block index in its segment, segment start
+// and length (all workgroup-uniform).
+struct SwbBlock {
+  int h, j, bos, seqlen;
+};
+
+__device__ __forceinline__ SwbBlock swb_block(const AttnArgs& a, const int32_t* cu_tk, int ntk, int u) {
+  SwbBlock b;
+  b.h = u / ntk;
+  const int tile = u - b.h * ntk;
+  const int s = seg_of(cu_tk, a.nseq, tile);
+  b.j = tile - cu_tk[s];
+  b.bos = a.cu[s];
+  b.seqlen = a.cu[s + 1] - b.bos;
+  return b;
+}
+
+// Step r (rows 128 j + 64 r ..) of block b exists and sees some key of the
+// block; a warm-up block runs its last two steps only.  The steps present
+// in a block are consecutive.
+__device__ __forceinline__ bool swb_present(const SwbBlock& b, int r, bool warm, int w) {
+  return !(warm && r < 2) && 128 * b.j + 64 * r < b.seqlen && 64 * r <= 127 + w;
+}
+
+// Transposed operand reads (ds_read_b64_tr_b16) of one 32-column group dt,
+// chosen at run time, of 64-row tiles with NC columns in layout KIND: lane
+// (i, g) gets T[r0 + 4g + e][32 dt + i], then T[r0 + 8 + 4g + e][32 dt + i]
+// (the k order of TileReader::tr).
+template <int NC, int KIND>
+struct TrCol {
+  using Geo = TileGeom<NC, KIND>;
+  int o0, o1;  // byte offsets for r0 = 0
+  __device__ __forceinline__ void init(int dt) {
+    const int l = threadIdx.x & 63, g = l >> 5, G = l >> 4, j = l & 15;
+    const int col = 32 * dt + 16 * (G & 1) + 4 * (j & 3);
+    const int row = 4 * g + (j >> 2);
+    o0 = 2 * (Geo::off(row, col >> 3) + (col & 7));
+    o1 = 2 * (Geo::off(row + 8, col >> 3) + (col & 7));
+  }
+  // tile: byte address of the tile; r0 a multiple of 16
+  __device__ __forceinline__ bf16x8 tr(uint32_t tile, int r0) const {
+    using P = const lds_bf16x4*;
+    const auto lo = ds_read_tr((P)(uintptr_t)(tile + 2 * r0 * Geo::RS + o0));
+    const auto hi = ds_read_tr((P)(uintptr_t)(tile + 2 * r0 * Geo::RS + o1));
+    return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+  }
+};
+
+// Sets an AGPR accumulator to zero with an MFMA of zero operands (C = 0):
+// clearing it by register writes would have the compiler keep a 16-register
+// zero vector alive to copy from.  Ordered with the asm MFMAs like one of them.
+__device__ __forceinline__ void zero_acc(f32x16& d, const bf16x8& z) {
+  asm volatile("s_nop 2\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %1, 0" : "=a"(d) : "v"(z));
+}
+
+// Wait states after the last MFMA into these accumulators, tied to them so
+// that every read of theirs follows (the reads cannot be scheduled above it).
+__device__ __forceinline__ void drain_acc(f32x16& x, f32x16& y) {
+  asm volatile("s_nop 15\n\ts_nop 15" : "+a"(x), "+a"(y));
+}
+__device__ __forceinline__ void drain_acc(f32x16& x) { asm volatile("s_nop 15\n\ts_nop 15" : "+a"(x)); }
+
+// This wave's vector memory operations and LDS accesses complete, then the
+// workgroup barrier (__syncthreads() would add a release fence: the same
+// waits, plus an L2 write-back on this multi-L2 part).
+__device__ __forceinline__ void swb_barrier() { asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+__device__ __forceinline__ void swb_lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+template <int D>
+__global__ __launch_bounds__(256) LOGO_OCC_DKV void swa_bwd_kernel(const AttnArgs a) {
+  using L = SwbLayout<D>;
+  using GS = typename L::GS;
+  constexpr int DS = D / 16, DT = D / 32;
+  constexpr int QT = DT / 2;  // dQ tiles per wave and step: 2 halves x DT over 4 waves
+  char* const sm = logo_smem;
+  auto ptr = [&](int off) { return reinterpret_cast<bf16*>(sm + off); };
+  const uint32_t sm_addr = (uint32_t)(uintptr_t)sm;
+
+  // the wave index as a scalar: the per-wave visibility tests are then
+  // uniform branches (a divergent one makes the compiler copy the asm
+  // accumulators through VGPRs at its joins)
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, i = l & 31, g = l >> 5;
+  const int W = a.window;
+  const float c = a.scale_log2;
+  const int32_t* cu_tk = a.meta + kMetaHdr + 2 * (a.nseq + 1);
+  const int ntk = a.meta[2];
+  const int nunits = ntk * a.h;
+  const int u0 = (int)((int64_t)blockIdx.x * nunits / gridDim.x);
+  const int u1 = (int)((int64_t)(blockIdx.x + 1) * nunits / gridDim.x);
+  if (u0 >= u1) return;
+
+  TileReader<D, kSwz> rd;
+  rd.init();
+  // dQ tile t of this wave: rows of half qq_of(t), columns 32 dt_w ..
+  const int dt_w = D == 128 ? wave : (wave & 1);
+  auto qq_of = [&](int t) { return D == 128 ? t : (wave >> 1); };
+  TrCol<D, kSwz> kcol;  // K^T reads, column group dt_w
+  kcol.init(dt_w);
+  TrCol<64, kTr> scol[QT];  // dS^T reads: the rows of each dQ tile are its columns
+#pragma unroll
+  for (int t = 0; t < QT; ++t) scol[t].init(qq_of(t));
+  // this wave's 32 keys in a K buffer (byte offset) and its dS^T row, key 32 wave + i
+  const int kw_off = 2 * ((wave >> 1) * 64 * D + 32 * (wave & 1) * D);
+  const int ds_row = 2 * (32 * wave + i) * GS::RS + 8 * g;
+  TileBufDma<D> dma;
+  dma.init(a.hq * D);
+
+  const bf16x8 zero8 = {};
+  f32x16 dka[DT], dva[DT], dqa[2][QT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) {
+    zero_acc(dka[dt], zero8);
+    zero_acc(dva[dt], zero8);
+  }
+#pragma unroll
+  for (int s = 0; s < 2; ++s)
+#pragma unroll
+    for (int t = 0; t < QT; ++t) zero_acc(dqa[s][t], zero8);
+  bf16x8 vreg[DS], vnext[DS];
+
+  float st_l = 0.f, st_d = 0.f;  // the prefetched step's lse / delta (threads < 64)
+  auto issue_tile = [&](const SwbBlock& b, int r, auto buf_c) __attribute__((always_inline)) {
+    constexpr int B = decltype(buf_c)::value;
+    const int row0 = 128 * b.j + 64 * r;
+    const int last = min(63, b.seqlen - 1 - row0);
+    const int64_t tok = b.bos + row0;
+    const bf16* qr = a.q + (tok * a.hq + b.h) * D;
+    const bf16* dr = a.dout + (tok * a.hq + b.h) * D;
+    if (last == 63) {
+      dma.issue(ptr(L::q(B)), qr);
+      dma.issue(ptr(L::dout(B)), dr);
+    } else {
+      dma.issue_clamped(ptr(L::q(B)), qr, last);
+      dma.issue_clamped(ptr(L::dout(B)), dr, last);
+    }
+    if (tid < 64) {
+      const int64_t t = (int64_t)b.h * a.n + tok + min(tid, last);
+      st_l = a.lse[t];
+      st_d = a.delta[t];
+    }
+  };
+  auto store_stats = [&](auto buf_c) __attribute__((always_inline)) {
+    constexpr int B = decltype(buf_c)::value;
+    if (tid < 64) {
+      reinterpret_cast<float*>(sm + L::lse(B))[tid] = st_l;
+      reinterpret_cast<float*>(sm + L::delta(B))[tid] = st_d;
+    }
+  };
+  // K of the block's 128 keys (two 64-row tiles; keys past the segment are
+  // clamped to its last key, whose scores the causal mask drops)
+  auto issue_k = [&](const SwbBlock& b, int kb) __attribute__((always_inline)) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int start = min(128 * b.j + 64 * t, b.seqlen - 1);
+      const int last = min(63, b.seqlen - 1 - start);
+      const bf16* src = a.k + ((int64_t)(b.bos + start) * a.h + b.h) * D;
+      bf16* dst = ptr(L::kbuf(0) + kb * 2 * L::TILE + t * L::TILE);
+      if (last == 63) dma.issue(dst, src);
+      else dma.issue_clamped(dst, src, last);
+    }
+  };
+  auto load_v = [&](const SwbBlock& b, bf16x8 (&dst)[DS]) __attribute__((always_inline)) {
+    const int key = 128 * b.j + 32 * wave + i;
+    // keys past the segment read its last key (finite; never visible)
+    const bf16* vp = a.v + ((int64_t)(b.bos + min(key, b.seqlen - 1)) * a.h + b.h) * D + 8 * g;
+#pragma unroll
+    for (int ds = 0; ds < DS; ++ds) dst[ds] = *reinterpret_cast<const bf16x8*>(vp + 16 * ds);
+  };
+
+  // One step's S, P, dP, dS for this wave's keys and the step's two 32-row
+  // halves h0, h1 (stage B), dV / dK +=, and dS^T to LDS (zeros when the
+  // wave sees neither half; a wave that sees one computes both, the other
+  // masked to zero, which costs no time: the step's critical path is two
+  // halves).  The MFMAs run in eight blocks of DS slots
+  //   S(h0) | dP(h0) | S(h1) | dP(h1) | dV(h0) | dK(h0) | dV(h1) | dK(h1)
+  // with P = exp2(S c - lse) of h0 under blocks 1-2, dS = P (dP - delta) of
+  // h0 under block 3, P of h1 under 4-5 and dS of h1 under 6; each slot's
+  // LDS operands are read PF slots ahead, and scheduling fences between the
+  // slots keep the VALU work under the MFMAs.  K's rows (the B operand of
+  // S) come from the block's LDS tile kt, V's from registers.
+  auto compute_step = [&](auto buf_c, const SwbBlock& b, int r, const bf16* kt) __attribute__((always_inline)) {
+    constexpr int B = decltype(buf_c)::value;
+    constexpr int NSL = 8 * DS, PF = 6;
+    constexpr int IPP = 16 / (2 * DS), IPD = 16 / DS;  // P / dS items per slot
+    const int R0 = 128 * b.j + 64 * r;
+    const int K0 = 128 * b.j + 32 * wave;
+    const bool see0 = R0 < b.seqlen && R0 <= K0 + 31 + W && R0 + 31 >= K0;
+    const bool see1 = R0 + 32 < b.seqlen && R0 + 32 <= K0 + 31 + W && R0 + 63 >= K0;
+    bf16x8 dbf[2][2] = {};  // dS of the halves as bf16 (zeros where not seen)
+    if (see0 | see1) {
+      const int key = K0 + i;
+      const bf16* qb = ptr(L::q(B));
+      const bf16* ob = ptr(L::dout(B));
+      const f32x4* lb = reinterpret_cast<const f32x4*>(sm + L::lse(B));
+      const f32x4* db = reinterpret_cast<const f32x4*>(sm + L::delta(B));
+      f32x16 sacc[2], pacc[2];
+      bf16x8 pbf[2][2];
+      bf16x8 opA[NSL], opB[2 * DS];
+      f32x4 l4[2][4], d4[2][4];
+      // the LDS operands of slot T
+      auto load_slot = [&](auto t_c) __attribute__((always_inline)) {
+        constexpr int T = decltype(t_c)::value, BLK = T / DS, K = T % DS;
+        if constexpr (BLK == 0 || BLK == 2) {
+          opA[T] = rd.row(qb, 16 * BLK, K);
+          opB[(BLK / 2) * DS + K] = rd.row(kt, 0, K);
+        } else if constexpr (BLK == 1 || BLK == 3) {
+          opA[T] = rd.row(ob, 16 * (BLK - 1), K);
+        } else {
+          constexpr int QQ = (BLK - 4) / 2, HH = K / DT, DTI = K % DT;
+          opA[T] = rd.tr((BLK % 2 == 0) ? ob : qb, 32 * QQ + 16 * HH, DTI);
+        }
+      };
+      auto p_item = [&](auto q_c, auto j_c) __attribute__((always_inline)) {
+        constexpr int QQ = decltype(q_c)::value, JJ = decltype(j_c)::value;
+        const int p = R0 + 32 * QQ + rowmap(g, JJ);
+        const bool vis = (key <= p) & (key >= p - W) & (p < b.seqlen);  // no short circuit: no branch
+        float sv = sacc[QQ][JJ];
+        pin(sv);
+        float pv = fast_exp2(fmaf(sv, c, -l4[QQ][JJ / 4][JJ % 4]));
+        pin(pv);
+        pv = vis ? pv : 0.f;
+        sacc[QQ][JJ] = pv;
+        if constexpr (JJ % 2 == 1) {
+          pbf[QQ][JJ / 8][JJ % 8 - 1] = (bf16)sacc[QQ][JJ - 1];
+          pbf[QQ][JJ / 8][JJ % 8] = (bf16)pv;
+        }
+      };
+      auto ds_item = [&](auto q_c, auto j_c) __attribute__((always_inline)) {
+        constexpr int QQ = decltype(q_c)::value, JJ = decltype(j_c)::value;
+        float pv = sacc[QQ][JJ], dpv = pacc[QQ][JJ];
+        pin(pv);
+        pin(dpv);
+        const float dsv = pv * (dpv - d4[QQ][JJ / 4][JJ % 4]);
+        pacc[QQ][JJ] = dsv;
+        if constexpr (JJ % 2 == 1) {
+          dbf[QQ][JJ / 8][JJ % 8 - 1] = (bf16)pacc[QQ][JJ - 1];
+          dbf[QQ][JJ / 8][JJ % 8] = (bf16)dsv;
+        }
+      };
+      static_for<PF>([&](auto t_c) __attribute__((always_inline)) { load_slot(t_c); });
+      static_for<NSL>([&](auto s_c) __attribute__((always_inline)) {
+        constexpr int S = decltype(s_c)::value, BLK = S / DS, K = S % DS;
+        constexpr int HH = K / DT, DTI = K % DT;
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (BLK == 0 || BLK == 2) {
+          constexpr int QQ = BLK / 2;
+          sacc[QQ] = mfma32(opA[S], opB[QQ * DS + K], K == 0 ? f32x16{} : sacc[QQ]);
+        } else if constexpr (BLK == 1 || BLK == 3) {
+          constexpr int QQ = BLK / 2;
+          pacc[QQ] = mfma32(opA[S], vreg[K], K == 0 ? f32x16{} : pacc[QQ]);
+        } else if constexpr (BLK == 4) {
+          mfma32_agpr(dva[DTI], opA[S], pbf[0][HH]);
+        } else if constexpr (BLK == 5) {
+          mfma32_agpr(dka[DTI], opA[S], dbf[0][HH]);
+        } else if constexpr (BLK == 6) {
+          mfma32_agpr(dva[DTI], opA[S], pbf[1][HH]);
+        } else {
+          mfma32_agpr(dka[DTI], opA[S], dbf[1][HH]);
+        }
+        if constexpr (S + PF < NSL) load_slot(std::integral_constant<int, S + PF>{});
+        // lse / delta of items 4m .. 4m+3 of a half, two slots before the
+        // first of them is needed (P of half q from slot DS (1 + 3q), dS from
+        // slot DS (3 + 3q))
+#pragma unroll
+        for (int q = 0; q < 2; ++q)
+#pragma unroll
+          for (int m = 0; m < 4; ++m) {
+            if (S == DS * (1 + 3 * q) + 4 * m / IPP - 2) l4[q][m] = lds_load(lb + 8 * q + 2 * m + g);
+            if (S == DS * (3 + 3 * q) + 4 * m / IPD - 2) d4[q][m] = lds_load(db + 8 * q + 2 * m + g);
+          }
+        if constexpr (BLK == 1 || BLK == 2 || BLK == 4 || BLK == 5) {
+          constexpr int QQ = BLK >= 4, J0 = (S - DS * (1 + 3 * QQ)) * IPP;
+          static_for<IPP>([&](auto e_c) __attribute__((always_inline)) {
+            p_item(std::integral_constant<int, QQ>{}, std::integral_constant<int, J0 + decltype(e_c)::value>{});
+          });
+        }
+        if constexpr (BLK == 3 || BLK == 6) {
+          constexpr int QQ = BLK == 6, J0 = K * IPD;
+          static_for<IPD>([&](auto e_c) __attribute__((always_inline)) {
+            ds_item(std::integral_constant<int, QQ>{}, std::integral_constant<int, J0 + decltype(e_c)::value>{});
+          });
+        }
+      });
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // dS^T row = key 32 wave + i of the block, columns 32 qq + 8 m + 4 g + e
+    // (written after the branch: an else branch beside the accumulating one
+    // makes the compiler copy the accumulators between registers inside it)
+    char* const st = sm + L::ds() + ds_row;
+#pragma unroll
+    for (int qq = 0; qq < 2; ++qq)
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const bf16x8 src = dbf[qq][m >> 1];
+        *reinterpret_cast<bf16x4*>(st + 64 * qq + 16 * m) =
+            (m & 1) ? __builtin_shufflevector(src, src, 4, 5, 6, 7) : __builtin_shufflevector(src, src, 0, 1, 2, 3);
+      }
+  };
+
+  // dQ of step R's rows += dS K.  The k-steps are those a 128-key window can
+  // reach (keys [row - 128, row + 31] of the half): exact for w = 128, a
+  // superset for smaller windows, whose extra dS^T entries are zeros.
+  // Compile-time bounds keep the MFMA sequence free of branches; operands
+  // are read two MFMAs ahead.
+  auto dq_phase = [&](auto r_c, uint32_t kbuf_addr) __attribute__((always_inline)) {
+    constexpr int R = decltype(r_c)::value, SET = R & 1;
+    // tile 0: half 0 (D = 128) or the wave's half (D = 64: bounds over both)
+    constexpr int LO0 = swb_klo(R, 0), HI0 = swb_khi(R, QT == 2 ? 0 : 1);
+    constexpr int LO1 = swb_klo(R, 1), HI1 = swb_khi(R, 1);
+    constexpr int N0 = HI0 - LO0 + 1, N1 = QT == 2 ? HI1 - LO1 + 1 : 0;
+    constexpr int NM = N0 + N1, PFQ = 2;
+    bf16x8 ka[NM], sb[NM];
+    auto load = [&](auto m_c) __attribute__((always_inline)) {
+      constexpr int M = decltype(m_c)::value, T = M < N0 ? 0 : 1;
+      constexpr int KS = M < N0 ? LO0 + M : LO1 + M - N0;
+      ka[M] = kcol.tr(kbuf_addr + (KS >> 2) * L::TILE, 16 * (KS & 3));
+      sb[M] = scol[T].tr(sm_addr + L::ds() + 2 * (KS >> 2) * GS::ELEMS, 16 * (KS & 3));
+    };
+    static_for<(PFQ < NM ? PFQ : NM)>([&](auto m_c) __attribute__((always_inline)) { load(m_c); });
+    static_for<NM>([&](auto m_c) __attribute__((always_inline)) {
+      constexpr int M = decltype(m_c)::value, T = M < N0 ? 0 : 1;
+      __builtin_amdgcn_sched_barrier(0);
+      mfma32_agpr(dqa[SET][T], ka[M], sb[M]);
+      if constexpr (M + PFQ < NM) load(std::integral_constant<int, M + PFQ>{});
+    });
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  // store the finished dQ rows of step R, then clear its accumulators
+  auto store_dq = [&](auto r_c, const SwbBlock& b) __attribute__((always_inline)) {
+    constexpr int R = decltype(r_c)::value, SET = R & 1;
+    if constexpr (QT == 2) drain_acc(dqa[SET][0], dqa[SET][1]);
+    else drain_acc(dqa[SET][0]);
+#pragma unroll
+    for (int t = 0; t < QT; ++t) {
+      const int row = 128 * b.j + 64 * R + 32 * qq_of(t) + i;
+      if (row < b.seqlen) {
+        bf16* dst = a.dq + ((int64_t)(b.bos + row) * a.hq + b.h) * D + 32 * dt_w + 4 * g;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          bf16x4 v;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = (bf16)(dqa[SET][t][4 * m + e] * a.scale);
+          *reinterpret_cast<bf16x4*>(dst + 8 * m) = v;
+        }
+      }
+      zero_acc(dqa[SET][t], zero8);
+    }
+  };
+  // store dK / dV of the block (keep: not a warm-up block, whose sums are
+  // only cleared), then clear them
+  auto store_kv = [&](const SwbBlock& b, bool keep) __attribute__((always_inline)) {
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) drain_acc(dka[dt], dva[dt]);
+    const int key = 128 * b.j + 32 * wave + i;
+    if (keep && key < b.seqlen) {
+      const int64_t off = ((int64_t)(b.bos + key) * a.h + b.h) * D + 4 * g;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          bf16x4 kv, vv;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            kv[e] = (bf16)(dka[dt][4 * m + e] * a.scale);
+            vv[e] = (bf16)dva[dt][4 * m + e];
+          }
+          *reinterpret_cast<bf16x4*>(a.dk + off + 32 * dt + 8 * m) = kv;
+          *reinterpret_cast<bf16x4*>(a.dv + off + 32 * dt + 8 * m) = vv;
+        }
+    }
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      zero_acc(dka[dt], zero8);
+      zero_acc(dva[dt], zero8);
+    }
+  };
+
+  // The walk: a warm-up block (the one before u0: S, dP, dS and dQ of its
+  // last two steps) when the run starts inside a sequence and the window
+  // reaches back.
+  SwbBlock cur = swb_block(a, cu_tk, ntk, u0);
+  const bool warm = cur.j > 0 && W >= 1;
+  int u = u0;
+  if (warm) {
+    cur.j -= 1;
+    u = u0 - 1;
+  }
+  issue_k(cur, 0);
+  load_v(cur, vnext);
+  issue_tile(cur, warm ? 2 : 0, std::integral_constant<int, 0>{});  // step 0 or 2: stage 0
+  wait_vmem();
+  store_stats(std::integral_constant<int, 0>{});
+  swb_barrier();
+  int kb = 0;
+
+  for (; u < u1; ++u) {
+    const bool wblk = u < u0;
+    const bool has_nxt = u + 1 < u1;
+    const SwbBlock nxt = has_nxt ? swb_block(a, cu_tk, ntk, u + 1) : cur;
+#pragma unroll
+    for (int ds = 0; ds < DS; ++ds) vreg[ds] = vnext[ds];
+    if (has_nxt) {
+      issue_k(nxt, kb ^ 1);
+      load_v(nxt, vnext);
+    }
+    const uint32_t kbuf_addr = sm_addr + L::kbuf(0) + kb * 2 * L::TILE;
+    const bf16* kt = reinterpret_cast<const bf16*>(sm + L::kbuf(0) + kb * 2 * L::TILE + kw_off);
+    static_for<4>([&](auto r_c) __attribute__((always_inline)) {
+      constexpr int R = decltype(r_c)::value, B = R & 1;
+      using Cur = std::integral_constant<int, B>;
+      using Nxt = std::integral_constant<int, B ^ 1>;
+      if (!swb_present(cur, R, wblk, W)) return;
+      // prefetch the next step into the other stage: step R + 1 of this
+      // block, or step 0 (stage 0) of the next block when this is stage 1;
+      // after an even last step that copy waits for the end of the step
+      const bool pf_here = R < 3 && swb_present(cur, R + 1, wblk, W);
+      const bool pf_next = !pf_here && has_nxt && B == 1;
+      if (pf_here) issue_tile(cur, R + 1, Nxt{});
+      else if (pf_next) issue_tile(nxt, 0, Nxt{});
+      // (steps 2, 3 of the run's last block are finished by the next
+      // workgroup: what this one sums for them is never stored)
+      compute_step(Cur{}, cur, R, kt);
+      swb_lds_barrier();  // dS^T complete
+      dq_phase(r_c, kbuf_addr);
+      if (pf_here || pf_next) {
+        wait_vmem();
+        store_stats(Nxt{});
+      }
+      swb_barrier();  // next stage landed; this stage, dS^T and K free
+      // rows of steps 0, 1 are finished (the previous block's part came first)
+      if (R < 2 && !wblk) store_dq(r_c, cur);
+      if (!pf_here && has_nxt && B == 0) {
+        issue_tile(nxt, 0, std::integral_constant<int, 0>{});
+        wait_vmem();
+        store_stats(std::integral_constant<int, 0>{});
+        swb_barrier();
+      }
+    });
+    store_kv(cur, !wblk);
+    kb ^= 1;
+    cur = nxt;
+  }
+}
+
+template <int D>
+static int launch_swa_bwd(const AttnArgs& a, hipStream_t st) {
+  const int64_t ntmax = (a.n + kBKV - 1) / kBKV + a.nseq;
+  const int cus = device_cus();
+  LOGO_REQUIRE(cus > 0, "device query failed");
+  const int64_t units = ntmax * a.h;
+  const unsigned grid = (unsigned)(units < cus ? units : cus);
+  auto kern = swa_bwd_kernel<D>;
+  LOGO_HIP_CHECK(allow_smem(kern, (size_t)SwbLayout<D>::BYTES));
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(256), (size_t)SwbLayout<D>::BYTES, st, a);
+  LOGO_LAUNCH_CHECK("swa_bwd_kernel");
+  return LOGO_OK;
+}
+
+bool swa_bwd_applies(const AttnArgs& a, bool sparse, bool half) {
+  return !sparse && !half && a.g == 1 && a.window >= 0 && a.window <= kSwbMaxWindow;
+}
+
+int swa_launch_bwd(const AttnArgs& a, hipStream_t st, int d) {
+  return d == 128 ? launch_swa_bwd<128>(a, st) : launch_swa_bwd<64>(a, st);
+}
+
+}  // namespace logo

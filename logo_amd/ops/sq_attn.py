@@ -67,10 +67,15 @@ def _fwd(q, k, v, dsel: DeviceSelection, scale: float, window: int):
 
 def _bwd(q, k, v, o, lse, do, dsel: DeviceSelection, scale: float, window: int):
     """dq (unselected rows zero), dk, dv: the delta phase (with the compacted
-    q / dO copies of sparse mode), then dq, then dk / dv."""
+    q / dO copies of sparse mode), then dq and dk / dv as two launches, or
+    as the one fused pass of the sliding-window branch (dense rows, window
+    <= 128, HQ == H; the library picks the kernels, this only keeps the two
+    launches separately timed where they are separate)."""
     ops = _torch_ops.ops()
     args = (q, k, v, o, lse, do, dsel.q_idx, dsel.pos, dsel.meta, dsel.cu, dsel.lanes, float(scale), int(window))
     ws = _torch_ops.timed("logo_sq_bwd_delta", ops.sq_bwd_delta, *args)
+    if dsel.q_idx is None and 0 <= window <= 128 and q.shape[1] == k.shape[1]:
+        return _torch_ops.timed("logo_sq_bwd_dqkv", ops.sq_bwd_dqkv, *args, *ws)
     dq = _torch_ops.timed("logo_sq_bwd_dq", ops.sq_bwd_dq, *args, *ws)
     dk, dv = _torch_ops.timed("logo_sq_bwd_dkv", ops.sq_bwd_dkv, *args, *ws)
     return dq, dk, dv

@@ -14,7 +14,9 @@
 //   sq_bwd_delta  logo_sq_bwd_delta   :124-138, :365-371
 //   sq_bwd_dq     logo_sq_bwd_dq      :141-228, :424-432
 //   sq_bwd_dkv    logo_sq_bwd_dkv     :231-337, :433-445
-//   sq_bwd        the three phases    :124-445 (dq, dk, dv; workspaces internal)
+//   sq_bwd_dqkv   logo_sq_bwd_dqkv    dq and dk/dv together (one fused pass for
+//                                     the sliding window, logo/layers/utils.py:144-147)
+//   sq_bwd        delta, then dqkv    :124-445 (dq, dk, dv; workspaces internal)
 //   epilogue_fwd  logo_epilogue_fwd   logo/layers/logo.py:180-181, :225-226, :256-258
 //   epilogue_bwd  logo_epilogue_bwd   the autograd of epilogue_fwd
 //   decode_attn   logo_decode_attn    logo/layers/logo.py:228-249
@@ -160,9 +162,11 @@ struct Bwd {
       }
     }
     using F = decltype(&logo_sq_bwd);
-    F fn = phase == 0 ? &logo_sq_bwd_delta : phase == 1 ? &logo_sq_bwd_dq : &logo_sq_bwd_dkv;
+    F fn = phase == 0 ? &logo_sq_bwd_delta : phase == 1 ? &logo_sq_bwd_dq : phase == 2 ? &logo_sq_bwd_dkv
+                                                                                  : &logo_sq_bwd_dqkv;
     auto p = [](at::Tensor* t) -> void* { return t && t->numel() ? t->data_ptr() : nullptr; };
-    at::Tensor ws = phase == 1 && window < 0 ? split_workspace(q, cu) : at::empty({0}, q.options().dtype(at::kByte));
+    at::Tensor ws = (phase == 1 || phase == 3) && window < 0 ? split_workspace(q, cu)
+                                                            : at::empty({0}, q.options().dtype(at::kByte));
     return fn(cptr(q), cptr(k), cptr(v), cptr(o), cptr(dout), lse.data_ptr<float>(),
               static_cast<float*>(p(delta)), p(q_sel), p(do_sel), p(dq), p(dk), p(dv), opt_ptr<int64_t>(q_idx),
               opt_ptr<int32_t>(pos), meta.data_ptr<int32_t>(), cu.data_ptr<int32_t>(), q.size(0),
@@ -212,14 +216,24 @@ std::tuple<at::Tensor, at::Tensor> sq_bwd_dkv(LOGO_BWD_SCHEMA_ARGS, const at::Te
   return {dk, dv};
 }
 
+// dq, dk and dv after the delta phase (one fused pass for the sliding window).
+std::tuple<at::Tensor, at::Tensor, at::Tensor> sq_bwd_dqkv(LOGO_BWD_SCHEMA_ARGS, const at::Tensor& delta,
+                                                           const at::Tensor& q_sel, const at::Tensor& do_sel) {
+  check_attn(q, k, v);
+  auto dq = q_idx.has_value() ? at::zeros_like(q) : at::empty_like(q);
+  auto dk = at::empty_like(k);
+  auto dv = at::empty_like(v);
+  Bwd b{q, k, v, o, lse, dout, q_idx, pos, meta, cu, lanes, scale, window};
+  auto dl = delta, qs = q_sel, ds = do_sel;
+  ok(b.call(3, &dl, &qs, &ds, &dq, &dk, &dv), "logo_sq_bwd_dqkv");
+  return {dq, dk, dv};
+}
+
 // The whole backward: (dq, dk, dv), its workspaces internal.
 std::tuple<at::Tensor, at::Tensor, at::Tensor> sq_bwd(LOGO_BWD_SCHEMA_ARGS) {
   auto ws = sq_bwd_delta(q, k, v, o, lse, dout, q_idx, pos, meta, cu, lanes, scale, window);
-  auto dq = sq_bwd_dq(q, k, v, o, lse, dout, q_idx, pos, meta, cu, lanes, scale, window, std::get<0>(ws),
-                      std::get<1>(ws), std::get<2>(ws));
-  auto dkv = sq_bwd_dkv(q, k, v, o, lse, dout, q_idx, pos, meta, cu, lanes, scale, window, std::get<0>(ws),
-                        std::get<1>(ws), std::get<2>(ws));
-  return {dq, std::get<0>(dkv), std::get<1>(dkv)};
+  return sq_bwd_dqkv(q, k, v, o, lse, dout, q_idx, pos, meta, cu, lanes, scale, window, std::get<0>(ws),
+                     std::get<1>(ws), std::get<2>(ws));
 }
 
 int thres_code(const at::Tensor& thres) {
@@ -293,6 +307,9 @@ TORCH_LIBRARY(logo_hip, m) {
   m.def("sq_bwd_dkv(Tensor q, Tensor k, Tensor v, Tensor o, Tensor lse, Tensor dout, Tensor? q_idx, "
         "Tensor? pos, Tensor meta, Tensor cu, int lanes, float scale, int window, Tensor delta, Tensor q_sel, "
         "Tensor do_sel) -> (Tensor, Tensor)");
+  m.def("sq_bwd_dqkv(Tensor q, Tensor k, Tensor v, Tensor o, Tensor lse, Tensor dout, Tensor? q_idx, "
+        "Tensor? pos, Tensor meta, Tensor cu, int lanes, float scale, int window, Tensor delta, Tensor q_sel, "
+        "Tensor do_sel) -> (Tensor, Tensor, Tensor)");
   m.def("sq_bwd(Tensor q, Tensor k, Tensor v, Tensor o, Tensor lse, Tensor dout, Tensor? q_idx, Tensor? pos, "
         "Tensor meta, Tensor cu, int lanes, float scale, int window) -> (Tensor, Tensor, Tensor)");
   m.def("epilogue_fwd(Tensor L, Tensor G, Tensor gate, Tensor thres, Tensor w_l, Tensor w_g, float eps) -> Tensor");
@@ -309,6 +326,7 @@ TORCH_LIBRARY_IMPL(logo_hip, CUDA, m) {
   m.impl("sq_bwd_delta", &sq_bwd_delta);
   m.impl("sq_bwd_dq", &sq_bwd_dq);
   m.impl("sq_bwd_dkv", &sq_bwd_dkv);
+  m.impl("sq_bwd_dqkv", &sq_bwd_dqkv);
   m.impl("sq_bwd", &sq_bwd);
   m.impl("epilogue_fwd", &epilogue_fwd);
   m.impl("epilogue_bwd", &epilogue_bwd);

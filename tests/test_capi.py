@@ -22,7 +22,7 @@ def test_header_symbols_are_exported():
 
 def test_abi_version_and_workspace():
     lib = _lib.lib()
-    assert lib.logo_abi_version() == 3
+    assert lib.logo_abi_version() == 4
     assert lib.logo_compact_workspace_bytes(4096, 1) == 4
     assert lib.logo_compact_workspace_bytes(4097, 16) == 2 * 16 * 4
 

@@ -82,6 +82,82 @@ def check_accumulators(lines):
     return bad
 
 
+_ADDR = re.compile(r"//\s*([0-9A-Fa-f]+):")
+_UNCOND = ("s_branch", "s_setpc_b64", "s_endpgm")
+
+
+def _flow(lines):
+    """(code, predecessors) per line of a kernel listing: the instruction
+    text, and the indices of the lines control can come from (the line
+    before unless it ends in an unconditional jump, and every branch whose
+    target, PC + 4 + 4 * simm16, is this line's address).  Listings without
+    addresses (the synthetic ones below) fall through line by line."""
+    code = [line.split("//")[0].split() for line in lines]
+    addr = {}
+    for n, line in enumerate(lines):
+        m = _ADDR.search(line)
+        if m:
+            addr[int(m.group(1), 16)] = n
+    preds = [[] for _ in lines]
+    for n, c in enumerate(code):
+        if n + 1 < len(lines) and not (c and c[0] in _UNCOND):
+            preds[n + 1].append(n)
+        if c and c[0].startswith(("s_branch", "s_cbranch")) and len(c) > 1:
+            m = _ADDR.search(lines[n])
+            try:
+                imm = int(c[1]) if not c[1].startswith("0x") else int(c[1], 16)
+            except ValueError:
+                continue
+            if imm >= 1 << 15:
+                imm -= 1 << 16
+            tgt = addr.get(int(m.group(1), 16) + 4 + 4 * imm) if m else None
+            if tgt is not None:
+                preds[tgt].append(n)
+    return code, preds
+
+
+def check_accumulators_drained(lines):
+    """Violations of the rule for kernels that also read or clear their
+    accumulators between MFMA phases (the fused window backward stores dQ
+    rows inside its walk): on every control-flow path into an instruction
+    that touches registers an accumulator MFMA writes, a drain (two s_nop 15)
+    lies between it and the nearest MFMA whose accumulator overlaps them
+    (the asm MFMA's result is not written yet when it issues; MFMAs into
+    other accumulators do not matter)."""
+    acc = set()
+    dst = []
+    for line in lines:
+        m = _ACC_DST.search(line)
+        r = set(range(int(m.group(1)), int(m.group(2)) + 1)) if m else set()
+        acc |= r
+        dst.append(r)
+    code, preds = _flow(lines)
+    bad = []
+    for n, c in enumerate(code):
+        if not c or c[0].startswith("v_mfma"):
+            continue
+        touched = set().union(*(_regs(t) for t in c[1:])) & acc
+        if not touched:
+            continue
+        # backward search over (line, consecutive s_nop 15 seen after it)
+        stack, seen, hit = [(p, 0) for p in preds[n]], set(), False
+        while stack and not hit:
+            k, nops = stack.pop()
+            if (k, nops) in seen:
+                continue
+            seen.add((k, nops))
+            if dst[k] & touched:
+                hit = True
+                break
+            nops = nops + 1 if code[k] == ["s_nop", "15"] else 0
+            if nops == 2:
+                continue
+            stack.extend((p, nops) for p in preds[k])
+        if hit:
+            bad.append((n, "accumulator touched with no drain after an MFMA: " + lines[n].strip()))
+    return bad
+
+
 def _gfx950_objects(lib_path, tmp_path):
     section = tmp_path / "hip_fatbin.bin"
     subprocess.run([f"{LLVM}/llvm-objcopy", "-O", "binary", "--only-section=.hip_fatbin", lib_path, str(section)],
@@ -107,7 +183,7 @@ def _gfx950_objects(lib_path, tmp_path):
 def _kernel_listings(tmp_path):
     listings = {}
     for j, obj in enumerate(_gfx950_objects(LIB, tmp_path)):
-        if b"sq_dkv_kernel" not in obj and b"sq_dq64_kernel" not in obj:
+        if b"sq_dkv_kernel" not in obj and b"sq_dq64_kernel" not in obj and b"swa_bwd_kernel" not in obj:
             continue
         path = tmp_path / f"co{j}.o"
         path.write_bytes(obj)
@@ -142,6 +218,19 @@ def test_asm_accumulators_are_not_copied_inside_mfma_loops(tmp_path):
         assert not bad, f"{name}: " + "; ".join(f"line {n}: {t[:100]}" for n, t in bad[:5])
 
 
+@pytest.mark.skipif(not (os.path.exists(LIB) and shutil.which(f"{LLVM}/llvm-objdump")),
+                    reason="needs the built library and ROCm's llvm-objdump")
+def test_window_backward_accumulators_are_drained_before_use(tmp_path):
+    listings = _kernel_listings(tmp_path)
+    kernels = [k for k in listings if "swa_bwd_kernel" in k]
+    assert len(kernels) == 2, sorted(listings)  # D = 64, 128
+    for name in kernels:
+        lines = listings[name]
+        assert any(_ACC_DST.search(line) for line in lines), f"{name}: no AGPR-accumulator MFMA found"
+        bad = check_accumulators_drained(lines)
+        assert not bad, f"{name}: " + "; ".join(f"line {n}: {t[:100]}" for n, t in bad[:5])
+
+
 _GOOD = """\
 	v_accvgpr_write_b32 a0, 0
 	s_nop 2
@@ -170,3 +259,21 @@ def test_checker_flags_a_read_without_drain():
     bad = [line for line in _GOOD if "s_nop 15" not in line]
     found = check_accumulators(bad)
     assert found and "no drain" in found[0][1]
+
+
+def test_drain_checker_accepts_reads_and_clears_after_a_drain():
+    assert check_accumulators_drained(_GOOD) == []
+    mid = _GOOD[:6] + ["\ts_nop 15", "\ts_nop 15", "\tv_accvgpr_read_b32 v41, a2", "\tv_accvgpr_write_b32 a2, 0"]
+    assert check_accumulators_drained(mid + _GOOD[6:]) == []
+
+
+def test_drain_checker_flags_a_clear_right_after_an_mfma():
+    bad = _GOOD[:6] + ["\tv_accvgpr_write_b32 a2, 0"] + _GOOD[6:]
+    found = check_accumulators_drained(bad)
+    assert found and "no drain" in found[0][1]
+
+
+def test_drain_checker_ignores_other_accumulators():
+    ok = _GOOD[:6] + ["\tv_accvgpr_write_b32 a16, v3", "\ts_nop 2",
+                      "\tv_mfma_f32_32x32x16_bf16 a[16:31], v[2:5], v[6:9], a[16:31]"] + _GOOD[6:]
+    assert check_accumulators_drained(ok) == []
