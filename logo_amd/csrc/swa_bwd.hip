@@ -41,19 +41,25 @@ constexpr int kSwbMaxWindow = 128;
 // LDS, bytes: q tiles of the two stages, then their dO tiles (all four within
 // the 64 KB reach of the DS instruction offset at D = 128), lse / delta of the
 // stages, two K buffers of 128 keys (64-row kSwz tiles), and dS^T
-// [128 keys][64 rows] in the padded kTr layout (only read transposed).
+// [128 keys][64 rows] (128-byte rows, swizzled as below).
 template <int D>
 struct SwbLayout {
   static constexpr int TILE = 64 * D * 2;
-  using GS = TileGeom<64, kTr>;
   static constexpr int q(int b) { return b * TILE; }
   static constexpr int dout(int b) { return (2 + b) * TILE; }
   static constexpr int lse(int b) { return 4 * TILE + b * 512; }
   static constexpr int delta(int b) { return lse(b) + 256; }
   static constexpr int kbuf(int b) { return 4 * TILE + 1024 + b * 2 * TILE; }
   static constexpr int ds() { return 8 * TILE + 1024; }
-  static constexpr int BYTES = ds() + 2 * GS::ELEMS * 2;
+  static constexpr int BYTES = ds() + 128 * 64 * 2;
 };
+
+// dS^T swizzle: the 8-byte chunk c of row r is stored at chunk c ^ swb_dsw(r).
+// Writes (a wave's 32 rows, one chunk each, 32 lanes a cycle): the 16 rows of
+// one parity take 16 distinct chunks, so the 32 lanes hit 64 distinct banks.
+// Transposed reads (rows 4a .. 4a+3, 8 consecutive chunks each): the two
+// rows of each parity land in opposite 8-chunk halves, again 64 banks.
+__device__ __forceinline__ int swb_dsw(int r) { return ((r >> 2) & 7) | (((r >> 1) & 1) << 3); }
 
 // dQ k-steps (16 keys) of step r's half q that a 128-key window can reach:
 // keys [64 r + 32 q - 128, 64 r + 32 q + 31] within the block.
@@ -62,10 +68,10 @@ constexpr int swb_klo(int r, int q) {
 }
 constexpr int swb_khi(int r, int q) { return (64 * r + 32 * q + 31 < 127 ? 64 * r + 32 * q + 31 : 127) >> 4; }
 
-// A key block of the walk: head, block index in its segment, segment start
-// and length (all workgroup-uniform).
+// A key block of the walk: head, block index in its segment and the
+// segment's block count, start and length (all workgroup-uniform).
 struct SwbBlock {
-  int h, j, bos, seqlen;
+  int h, j, nt, bos, seqlen;
 };
 
 __device__ __forceinline__ SwbBlock swb_block(const AttnArgs& a, const int32_t* cu_tk, int ntk, int u) {
@@ -74,10 +80,33 @@ __device__ __forceinline__ SwbBlock swb_block(const AttnArgs& a, const int32_t* 
   const int tile = u - b.h * ntk;
   const int s = seg_of(cu_tk, a.nseq, tile);
   b.j = tile - cu_tk[s];
+  b.nt = cu_tk[s + 1] - cu_tk[s];
   b.bos = a.cu[s];
   b.seqlen = a.cu[s + 1] - b.bos;
   return b;
 }
+
+// The block after b (unit u + 1): the next block of the segment needs no
+// memory reads; only a new segment or head searches the tile prefixes.
+__device__ __forceinline__ SwbBlock swb_next(const AttnArgs& a, const int32_t* cu_tk, int ntk, int u,
+                                             const SwbBlock& b) {
+  if (b.j + 1 < b.nt) {
+    SwbBlock n = b;
+    n.j += 1;
+    return n;
+  }
+  return swb_block(a, cu_tk, ntk, u + 1);
+}
+
+// 64 lanes x 4 bytes global -> LDS (buffer_load_dword ... lds), as
+// buf_load_lds16 in common.hpp.
+__device__ __forceinline__ void buf_load_lds4(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 4, voff, 0, 0, 0);
+}
+
+// Keeps memory accesses on their side of this point (the vmcnt accounting
+// below relies on the issue order of the copies, loads and stores).
+__device__ __forceinline__ void mem_fence_compiler() { asm volatile("" ::: "memory"); }
 
 // Step r (rows 128 j + 64 r ..) of block b exists and sees some key of the
 // block; a warm-up block runs its last two steps only.  The steps present
@@ -117,6 +146,30 @@ __device__ __forceinline__ void zero_acc(f32x16& d, const bf16x8& z) {
   asm volatile("s_nop 2\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %1, 0" : "=a"(d) : "v"(z));
 }
 
+// Transposed reads (ds_read_b64_tr_b16) of column group dt (32 rows of the
+// step) of the dS^T tile: lane (i, g) gets T[r0 + 4g + e][32 dt + i], then
+// T[r0 + 8 + 4g + e][32 dt + i] (the k order of TileReader::tr).  With r0 a
+// multiple of 16, swb_dsw(r0 + x) = swb_dsw(x) ^ 4 (r0 / 16 & 1), which flips
+// bit 5 of the lane's byte offset for odd r0 / 16.
+struct SwbDsCol {
+  int o0, o1;  // byte offsets for r0 = 0
+  __device__ __forceinline__ void init(int dt) {
+    const int l = threadIdx.x & 63, g = l >> 5, G = l >> 4, j = l & 15;
+    const int c = 8 * dt + 4 * (G & 1) + (j & 3);
+    const int r = 4 * g + (j >> 2);
+    o0 = 128 * r + 8 * (c ^ swb_dsw(r));
+    o1 = 128 * (r + 8) + 8 * (c ^ swb_dsw(r + 8));
+  }
+  template <int R0>
+  __device__ __forceinline__ bf16x8 tr(uint32_t tile) const {
+    constexpr int F = (R0 / 16 & 1) ? 32 : 0;
+    using P = const lds_bf16x4*;
+    const auto lo = ds_read_tr((P)(uintptr_t)(tile + 128 * R0 + (o0 ^ F)));
+    const auto hi = ds_read_tr((P)(uintptr_t)(tile + 128 * R0 + (o1 ^ F)));
+    return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+  }
+};
+
 // Wait states after the last MFMA into these accumulators, tied to them so
 // that every read of theirs follows (the reads cannot be scheduled above it).
 __device__ __forceinline__ void drain_acc(f32x16& x, f32x16& y) {
@@ -128,12 +181,16 @@ __device__ __forceinline__ void drain_acc(f32x16& x) { asm volatile("s_nop 15\n\
 // workgroup barrier (__syncthreads() would add a release fence: the same
 // waits, plus an L2 write-back on this multi-L2 part).
 __device__ __forceinline__ void swb_barrier() { asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+// The same with up to N vector-memory operations (the youngest) still in flight.
+template <int N>
+__device__ __forceinline__ void swb_barrier_vm() {
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
 __device__ __forceinline__ void swb_lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 template <int D>
 __global__ __launch_bounds__(256) LOGO_OCC_DKV void swa_bwd_kernel(const AttnArgs a) {
   using L = SwbLayout<D>;
-  using GS = typename L::GS;
   constexpr int DS = D / 16, DT = D / 32;
   constexpr int QT = DT / 2;  // dQ tiles per wave and step: 2 halves x DT over 4 waves
   char* const sm = logo_smem;
@@ -160,12 +217,14 @@ __global__ __launch_bounds__(256) LOGO_OCC_DKV void swa_bwd_kernel(const AttnArg
   auto qq_of = [&](int t) { return D == 128 ? t : (wave >> 1); };
   TrCol<D, kSwz> kcol;  // K^T reads, column group dt_w
   kcol.init(dt_w);
-  TrCol<64, kTr> scol[QT];  // dS^T reads: the rows of each dQ tile are its columns
+  SwbDsCol scol[QT];  // dS^T reads: the rows of each dQ tile are its columns
 #pragma unroll
   for (int t = 0; t < QT; ++t) scol[t].init(qq_of(t));
-  // this wave's 32 keys in a K buffer (byte offset) and its dS^T row, key 32 wave + i
+  // this wave's 32 keys in a K buffer (byte offset); its dS^T row (key
+  // 32 wave + i) and the lane's part of the swizzled chunk index
   const int kw_off = 2 * ((wave >> 1) * 64 * D + 32 * (wave & 1) * D);
-  const int ds_row = 2 * (32 * wave + i) * GS::RS + 8 * g;
+  const int ds_row = 128 * (32 * wave + i);
+  const int ds_x = g ^ swb_dsw(32 * wave + i);
   TileBufDma<D> dma;
   dma.init(a.hq * D);
 
@@ -182,7 +241,9 @@ __global__ __launch_bounds__(256) LOGO_OCC_DKV void swa_bwd_kernel(const AttnArg
     for (int t = 0; t < QT; ++t) zero_acc(dqa[s][t], zero8);
   bf16x8 vreg[DS], vnext[DS];
 
-  float st_l = 0.f, st_d = 0.f;  // the prefetched step's lse / delta (threads < 64)
+  // Step r of block b into stage B: q and dO rows (two 64-row tiles) and the
+  // rows' lse (wave 0) and delta (wave 1), all global -> LDS copies, rows
+  // past the segment clamped to its last row (masked).
   auto issue_tile = [&](const SwbBlock& b, int r, auto buf_c) __attribute__((always_inline)) {
     constexpr int B = decltype(buf_c)::value;
     const int row0 = 128 * b.j + 64 * r;
@@ -197,17 +258,11 @@ __global__ __launch_bounds__(256) LOGO_OCC_DKV void swa_bwd_kernel(const AttnArg
       dma.issue_clamped(ptr(L::q(B)), qr, last);
       dma.issue_clamped(ptr(L::dout(B)), dr, last);
     }
-    if (tid < 64) {
-      const int64_t t = (int64_t)b.h * a.n + tok + min(tid, last);
-      st_l = a.lse[t];
-      st_d = a.delta[t];
-    }
-  };
-  auto store_stats = [&](auto buf_c) __attribute__((always_inline)) {
-    constexpr int B = decltype(buf_c)::value;
-    if (tid < 64) {
-      reinterpret_cast<float*>(sm + L::lse(B))[tid] = st_l;
-      reinterpret_cast<float*>(sm + L::delta(B))[tid] = st_d;
+    if (wave < 2) {
+      const float* src = (wave == 0 ? a.lse : a.delta) + (int64_t)b.h * a.n + tok;
+      const auto rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(src), (short)0, (last + 1) * 4,
+                                                        kBufRsrcWord3);
+      buf_load_lds4(rs, sm + (wave == 0 ? L::lse(B) : L::delta(B)), (uint32_t)min(l, last) * 4);
     }
   };
   // K of the block's 128 keys (two 64-row tiles; keys past the segment are
@@ -347,16 +402,17 @@ __global__ __launch_bounds__(256) LOGO_OCC_DKV void swa_bwd_kernel(const AttnArg
       });
       __builtin_amdgcn_sched_barrier(0);
     }
-    // dS^T row = key 32 wave + i of the block, columns 32 qq + 8 m + 4 g + e
-    // (written after the branch: an else branch beside the accumulating one
-    // makes the compiler copy the accumulators between registers inside it)
+    // dS^T row = key 32 wave + i of the block, columns 32 qq + 8 m + 4 g + e:
+    // 8-byte chunk 8 qq + 2 m + g, swizzled (written after the branch: an
+    // else branch beside the accumulating one makes the compiler copy the
+    // accumulators between registers inside it)
     char* const st = sm + L::ds() + ds_row;
 #pragma unroll
     for (int qq = 0; qq < 2; ++qq)
 #pragma unroll
       for (int m = 0; m < 4; ++m) {
         const bf16x8 src = dbf[qq][m >> 1];
-        *reinterpret_cast<bf16x4*>(st + 64 * qq + 16 * m) =
+        *reinterpret_cast<bf16x4*>(st + 8 * ((8 * qq + 2 * m) ^ ds_x)) =
             (m & 1) ? __builtin_shufflevector(src, src, 4, 5, 6, 7) : __builtin_shufflevector(src, src, 0, 1, 2, 3);
       }
   };
@@ -378,7 +434,7 @@ __global__ __launch_bounds__(256) LOGO_OCC_DKV void swa_bwd_kernel(const AttnArg
       constexpr int M = decltype(m_c)::value, T = M < N0 ? 0 : 1;
       constexpr int KS = M < N0 ? LO0 + M : LO1 + M - N0;
       ka[M] = kcol.tr(kbuf_addr + (KS >> 2) * L::TILE, 16 * (KS & 3));
-      sb[M] = scol[T].tr(sm_addr + L::ds() + 2 * (KS >> 2) * GS::ELEMS, 16 * (KS & 3));
+      sb[M] = scol[T].template tr<16 * (KS & 3)>(sm_addr + L::ds() + (KS >> 2) * 64 * 128);
     };
     static_for<(PFQ < NM ? PFQ : NM)>([&](auto m_c) __attribute__((always_inline)) { load(m_c); });
     static_for<NM>([&](auto m_c) __attribute__((always_inline)) {
@@ -452,21 +508,17 @@ __global__ __launch_bounds__(256) LOGO_OCC_DKV void swa_bwd_kernel(const AttnArg
   issue_k(cur, 0);
   load_v(cur, vnext);
   issue_tile(cur, warm ? 2 : 0, std::integral_constant<int, 0>{});  // step 0 or 2: stage 0
-  wait_vmem();
-  store_stats(std::integral_constant<int, 0>{});
   swb_barrier();
+#pragma unroll
+  for (int ds = 0; ds < DS; ++ds) vreg[ds] = vnext[ds];
   int kb = 0;
+  // vector-memory loads a wave issues for the next block (K copies, V rows)
+  constexpr int N_KV = 2 * TileBufDma<D>::BLOCKS + DS;
 
   for (; u < u1; ++u) {
     const bool wblk = u < u0;
     const bool has_nxt = u + 1 < u1;
-    const SwbBlock nxt = has_nxt ? swb_block(a, cu_tk, ntk, u + 1) : cur;
-#pragma unroll
-    for (int ds = 0; ds < DS; ++ds) vreg[ds] = vnext[ds];
-    if (has_nxt) {
-      issue_k(nxt, kb ^ 1);
-      load_v(nxt, vnext);
-    }
+    const SwbBlock nxt = has_nxt ? swb_next(a, cu_tk, ntk, u, cur) : cur;
     const uint32_t kbuf_addr = sm_addr + L::kbuf(0) + kb * 2 * L::TILE;
     const bf16* kt = reinterpret_cast<const bf16*>(sm + L::kbuf(0) + kb * 2 * L::TILE + kw_off);
     static_for<4>([&](auto r_c) __attribute__((always_inline)) {
@@ -474,32 +526,53 @@ __global__ __launch_bounds__(256) LOGO_OCC_DKV void swa_bwd_kernel(const AttnArg
       using Cur = std::integral_constant<int, B>;
       using Nxt = std::integral_constant<int, B ^ 1>;
       if (!swb_present(cur, R, wblk, W)) return;
-      // prefetch the next step into the other stage: step R + 1 of this
-      // block, or step 0 (stage 0) of the next block when this is stage 1;
-      // after an even last step that copy waits for the end of the step
+      // Issue order (vector memory): the previous step's stores (already
+      // issued), this step's prefetch, then on the block's first step the
+      // next block's K / V.  Loads complete in issue order, so the end of
+      // the step waits until only those K / V loads may be outstanding
+      // (vmcnt(N_KV)); stores in between do not matter (the younger loads
+      // alone keep the count above N_KV while the prefetch is in flight).
+      // Prefetch into the other stage: step R + 1 of this block, or step 0
+      // (stage 0) of the next block when this is stage 1; after an even last
+      // step that copy waits for the end of the step.
       const bool pf_here = R < 3 && swb_present(cur, R + 1, wblk, W);
       const bool pf_next = !pf_here && has_nxt && B == 1;
+      mem_fence_compiler();
       if (pf_here) issue_tile(cur, R + 1, Nxt{});
       else if (pf_next) issue_tile(nxt, 0, Nxt{});
+      mem_fence_compiler();
+      const bool kv = R == (wblk ? 2 : 0) && has_nxt;
+      if (kv) {
+        issue_k(nxt, kb ^ 1);
+        load_v(nxt, vnext);
+      }
+      mem_fence_compiler();
       // (steps 2, 3 of the run's last block are finished by the next
       // workgroup: what this one sums for them is never stored)
       compute_step(Cur{}, cur, R, kt);
       swb_lds_barrier();  // dS^T complete
       dq_phase(r_c, kbuf_addr);
-      if (pf_here || pf_next) {
-        wait_vmem();
-        store_stats(Nxt{});
-      }
-      swb_barrier();  // next stage landed; this stage, dS^T and K free
+      // next stage landed; this stage, dS^T and K free.  The block's last
+      // step waits for everything (the next block's K is read next).
+      if (kv && pf_here) swb_barrier_vm<N_KV>();
+      else swb_barrier();
       // rows of steps 0, 1 are finished (the previous block's part came first)
       if (R < 2 && !wblk) store_dq(r_c, cur);
       if (!pf_here && has_nxt && B == 0) {
+        mem_fence_compiler();
         issue_tile(nxt, 0, std::integral_constant<int, 0>{});
-        wait_vmem();
-        store_stats(std::integral_constant<int, 0>{});
         swb_barrier();
       }
     });
+    // the next block's V: its loads completed at the last step's barrier, so
+    // the wait the compiler places on them here is free; after the stores
+    // below it would wait for those stores too (anchored here, the copy
+    // cannot sink below them)
+#pragma unroll
+    for (int ds = 0; ds < DS; ++ds) {
+      vreg[ds] = vnext[ds];
+      pin(vreg[ds]);
+    }
     store_kv(cur, !wblk);
     kb ^= 1;
     cur = nxt;
