@@ -452,28 +452,54 @@ __global__ __launch_bounds__(256) LOGO_OCC_DKV void swa_bwd_kernel(const AttnArg
     else drain_acc(dqa[SET][0]);
 #pragma unroll
     for (int t = 0; t < QT; ++t) {
+      // Lane (i, g) holds columns 32 dt + 8 m + 4 g + e of row i.  For each
+      // pair m, m + 1 the two lanes of a row trade one half (permlane32
+      // swap), so lane g = 0 stores columns 8 m .. 8 m + 7 and lane g = 1
+      // columns 8 m + 8 .. 8 m + 15: 16 bytes a lane, 32 contiguous bytes a
+      // row per store.
       const int row = 128 * b.j + 64 * R + 32 * qq_of(t) + i;
-      if (row < b.seqlen) {
-        bf16* dst = a.dq + ((int64_t)(b.bos + row) * a.hq + b.h) * D + 32 * dt_w + 4 * g;
+      bf16* dst = a.dq + ((int64_t)(b.bos + min(row, b.seqlen - 1)) * a.hq + b.h) * D + 32 * dt_w + 8 * g;
 #pragma unroll
-        for (int m = 0; m < 4; ++m) {
-          bf16x4 v;
+      for (int m = 0; m < 4; m += 2) {
+        bf16x4 lo, hi;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] = (bf16)(dqa[SET][t][4 * m + e] * a.scale);
-          *reinterpret_cast<bf16x4*>(dst + 8 * m) = v;
+        for (int e = 0; e < 4; ++e) {
+          lo[e] = (bf16)(dqa[SET][t][4 * m + e] * a.scale);
+          hi[e] = (bf16)(dqa[SET][t][4 * m + 4 + e] * a.scale);
         }
+        const u32x2 lo2 = __builtin_bit_cast(u32x2, lo), hi2 = __builtin_bit_cast(u32x2, hi);
+        // g = 0 gives its columns 8 m + 8 .. (hi), g = 1 its 8 m + 4 .. (lo)
+        u32x2 x = g ? lo2 : hi2, y;
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+          const auto r = __builtin_amdgcn_permlane32_swap(x[k], x[k], false, false);
+          y[k] = g ? r[0] : r[1];
+        }
+        const u32x4 v = g ? u32x4{y[0], y[1], hi2[0], hi2[1]} : u32x4{lo2[0], lo2[1], y[0], y[1]};
+        if (row < b.seqlen) *reinterpret_cast<u32x4*>(dst + 8 * m) = v;
       }
       zero_acc(dqa[SET][t], zero8);
     }
   };
-  // store dK / dV of the block (keep: not a warm-up block, whose sums are
-  // only cleared), then clear them
-  auto store_kv = [&](const SwbBlock& b, bool keep) __attribute__((always_inline)) {
+  // Store dK / dV of the block (keep: not a warm-up block, whose sums are
+  // only cleared), then clear them.  The bf16 tiles go through LDS that is
+  // free at the block's end (its K buffer: dK; stage 1's q and dO tiles:
+  // dV), so that each global store writes 16 contiguous bytes a lane and a
+  // whole 256-byte row per 16 lanes; stored straight from the MFMA layout,
+  // every store instruction wrote 16-byte pieces of 32 rows.
+  auto store_kv = [&](const SwbBlock& b, bool keep, int kbuf) __attribute__((always_inline)) {
+    using G = TileGeom<D, kSwz>;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) drain_acc(dka[dt], dva[dt]);
-    const int key = 128 * b.j + 32 * wave + i;
-    if (keep && key < b.seqlen) {
-      const int64_t off = ((int64_t)(b.bos + key) * a.h + b.h) * D + 4 * g;
+    if (keep) {
+      // lane indices anchored here: the offsets below are recomputed per
+      // block instead of being hoisted out of the walk (registers held
+      // through every step)
+      int lane = tid;
+      pin(lane);
+      const int row = 32 * (wave & 1) + (lane & 31), gl = (lane >> 5) & 1;
+      bf16* const kt2 = ptr(L::kbuf(0) + kbuf * 2 * L::TILE + (wave >> 1) * L::TILE);
+      bf16* const vt2 = ptr((wave >> 1) == 0 ? L::q(1) : L::dout(1));
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
@@ -484,9 +510,28 @@ __global__ __launch_bounds__(256) LOGO_OCC_DKV void swa_bwd_kernel(const AttnArg
             kv[e] = (bf16)(dka[dt][4 * m + e] * a.scale);
             vv[e] = (bf16)dva[dt][4 * m + e];
           }
-          *reinterpret_cast<bf16x4*>(a.dk + off + 32 * dt + 8 * m) = kv;
-          *reinterpret_cast<bf16x4*>(a.dv + off + 32 * dt + 8 * m) = vv;
+          *reinterpret_cast<bf16x4*>(kt2 + G::off(row, 4 * dt + m) + 4 * gl) = kv;
+          *reinterpret_cast<bf16x4*>(vt2 + G::off(row, 4 * dt + m) + 4 * gl) = vv;
+          __builtin_amdgcn_sched_barrier(0);
         }
+      swb_lds_barrier();
+      constexpr int CH = D / 8, RPT = 64 * CH / 256;
+      const int c = lane % CH, r0 = lane / CH;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const bf16* src = t < 2 ? ptr(L::kbuf(0) + kbuf * 2 * L::TILE + t * L::TILE) : ptr(t == 2 ? L::q(1) : L::dout(1));
+        bf16* const dst = t < 2 ? a.dk : a.dv;
+#pragma unroll
+        for (int k = 0; k < RPT; ++k) {
+          const int r = r0 + (256 / CH) * k;
+          const int key = 128 * b.j + 64 * (t & 1) + r;
+          const u32x4 val = lds_load(reinterpret_cast<const u32x4*>(src + G::off(r, c)));
+          if (key < b.seqlen)
+            *reinterpret_cast<u32x4*>(dst + ((int64_t)(b.bos + key) * a.h + b.h) * D + 8 * c) = val;
+        }
+        __builtin_amdgcn_sched_barrier(0);  // a tile at a time: few registers live
+      }
+      swb_lds_barrier();  // the LDS is read: the next block's copies may land there
     }
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
@@ -573,7 +618,7 @@ __global__ __launch_bounds__(256) LOGO_OCC_DKV void swa_bwd_kernel(const AttnArg
       vreg[ds] = vnext[ds];
       pin(vreg[ds]);
     }
-    store_kv(cur, !wblk);
+    store_kv(cur, !wblk, kb);
     kb ^= 1;
     cur = nxt;
   }
