@@ -82,6 +82,9 @@ def parse():
     ap.add_argument("--layer", action="store_true",
                     help="run only the config-4 LoGoAttention layer forward + backward measurement and "
                          "print its result")
+    ap.add_argument("--swa", action="store_true",
+                    help="run only the config-4 sliding-window (local branch) forward and "
+                         "forward + backward measurement and print its result")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run one 1 GiB device-to-device copy before the workload (the reference kernel "
                          "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters to bytes)")
@@ -171,6 +174,29 @@ def _time_ms(fn, iters, warmup=2):
     return a.elapsed_time(b) / iters
 
 
+def swa_cfg4_measurement(q, k, v, do, iters=10):
+    """The local branch at the cfg4 shape: sliding window 128 over
+    [1, 4 x 8192, 16, 128] (four packed sequences), forward alone and
+    forward + backward through swa_attn.  Bandwidths are algorithmic bytes:
+    forward q, k, v read and o written; backward q, k, v, o, dO read and dq,
+    dk, dv written (bf16), over the backward's share of the time."""
+    from logo_amd.ops import swa_attn
+    N4, H, D = 4 * 8192, q.shape[2], q.shape[3]
+    dev = q.device
+    cu4 = torch.arange(0, N4 + 1, 8192, dtype=torch.int32, device=dev)
+    q4, k4, v4 = (x[:, :N4].detach().requires_grad_() for x in (q, k, v))
+    with torch.no_grad():
+        tsf = _time_ms(lambda: swa_attn(q4, k4, v4, cu4, window=128), iters)
+
+    def swa_fb():
+        o = swa_attn(q4, k4, v4, cu4, window=128)
+        torch.autograd.grad(o, (q4, k4, v4), do[:, :N4])
+    tsb = _time_ms(swa_fb, max(iters // 2, 1))
+    io = 4 * N4 * H * D * 2
+    return {"fwd_ms": round(tsf, 4), "fwd_gbs": round(io / tsf / 1e6, 1), "fwd_bwd_ms": round(tsb, 4),
+            "bwd_ms": round(tsb - tsf, 4), "bwd_gbs": round(2 * io / (tsb - tsf) / 1e6, 1)}
+
+
 def extra_measurements(dev):
     """Secondary rows: speed-up vs global ratio, cfg2 forward, cfg3 varlen
     fwd+bwd, SWA and epilogue at cfg4 shapes, gate-aware decode at cfg5 shape.
@@ -233,20 +259,8 @@ def extra_measurements(dev):
     f3 = 3.5 * 4 * D * H * float((pos3 + 1).sum())
     out["cfg3_fwd_bwd_varlen"] = {"lens": lens, "ms": round(t3, 3), "tflops": round(f3 / t3 / 1e9, 1)}
 
-    # SWA (window 128) fwd+bwd at cfg4 shape: [1, 4*8192, 16, 128]
+    out["swa_w128_cfg4"] = swa_cfg4_measurement(q, k, v, do)
     N4 = 4 * 8192
-    cu4 = torch.arange(0, N4 + 1, 8192, dtype=torch.int32, device=dev)
-    q4, k4, v4 = (x[:, :N4].detach().requires_grad_() for x in (q, k, v))
-    with torch.no_grad():
-        tsf = _time_ms(lambda: swa_attn(q4, k4, v4, cu4, window=128), 10)
-
-    def swa_fb():
-        o = swa_attn(q4, k4, v4, cu4, window=128)
-        torch.autograd.grad(o, (q4, k4, v4), do[:, :N4])
-    tsb = _time_ms(swa_fb, 5)
-    io = 4 * N4 * H * D * 2  # q, k, v read + o written, bf16
-    out["swa_w128_cfg4"] = {"fwd_ms": round(tsf, 4), "fwd_gbs": round(io / tsf / 1e6, 1),
-                            "fwd_bwd_ms": round(tsb, 4)}
 
     # fused epilogue at cfg4 shape: L, G [32768, 16, 128], gate [32768]
     L = (torch.randn(N4, H, D, generator=gen)).bfloat16().to(dev).requires_grad_()
@@ -494,6 +508,14 @@ def main():
         return
     if args.layer:
         print(json.dumps(layer_cfg4_measurement(dev)), flush=True)
+        return
+    if args.swa:
+        g = torch.Generator()
+        g.manual_seed(args.seed)
+        q, k, v = ((torch.randn(1, 4 * 8192, 16, 128, generator=g) * 0.5).to(torch.bfloat16).to(dev)
+                   for _ in range(3))
+        do = torch.randn(1, 4 * 8192, 16, 128, generator=g).to(torch.bfloat16).to(dev)
+        print(json.dumps(swa_cfg4_measurement(q, k, v, do, iters=20)), flush=True)
         return
     T, H, D = args.seq_len, args.heads, args.head_dim
     gen = torch.Generator()
