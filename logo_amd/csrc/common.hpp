@@ -80,6 +80,18 @@ __device__ __forceinline__ void mfma32_agpr(f32x16& d, const bf16x8& a, const bf
 __device__ __forceinline__ void mfma32_agpr(f32x16& d, const f16x8& a, const f16x8& b) {
   asm volatile("s_nop 2\n\tv_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+a"(d) : "v"(a), "v"(b));
 }
+// mfma32_agpr without the leading wait states, for schedules in which no VALU
+// instruction writes A or B within the three instructions before the MFMA
+// (the operands are LDS reads, or packed several MFMA slots earlier).  The
+// leading s_nop costs three issue cycles per MFMA, which one wave per SIMD
+// pays in full (dk/dv: 4% of the kernel).  The ISA test checks the operand
+// distance in every kernel that uses it.
+__device__ __forceinline__ void mfma32_agpr_ready(f32x16& d, const bf16x8& a, const bf16x8& b) {
+  asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(d) : "v"(a), "v"(b));
+}
+__device__ __forceinline__ void mfma32_agpr_ready(f32x16& d, const f16x8& a, const f16x8& b) {
+  asm volatile("v_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+a"(d) : "v"(a), "v"(b));
+}
 // Wait states between the last mfma32_agpr and a VALU read of its result
 // (an 8-pass MFMA needs fewer than 32).  The compiler may place its own
 // copies out of the AGPRs ahead of this operand-less asm, so kernels also run

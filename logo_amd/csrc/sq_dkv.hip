@@ -238,8 +238,15 @@ __global__ __launch_bounds__(256) LOGO_OCC_DKV void sq_dkv_kernel(const AttnArgs
           constexpr int QQ = C / NS, KK = C % NS, HH = (KK % DS) / DT, DTI = KK % DT;
           E8 op = opC[U * 2 * NS + C];
           pin(op);
-          if constexpr (KK < DS) mfma32_agpr(dvacc[DTI], op, pbf[QQ][HH]);
-          else mfma32_agpr(dkacc[DTI], op, dbf[QQ][HH]);
+          // D = 128: P and dS are packed at least four slots before their MFMAs
+          // read them; D = 64 (four-slot blocks) keeps the leading wait states
+          if constexpr (DS >= 8) {
+            if constexpr (KK < DS) mfma32_agpr_ready(dvacc[DTI], op, pbf[QQ][HH]);
+            else mfma32_agpr_ready(dkacc[DTI], op, dbf[QQ][HH]);
+          } else {
+            if constexpr (KK < DS) mfma32_agpr(dvacc[DTI], op, pbf[QQ][HH]);
+            else mfma32_agpr(dkacc[DTI], op, dbf[QQ][HH]);
+          }
         };
         // row item jj of half qq: items 4m..4m+3 are query rows 32qq + 8m + 4g + e.
         // P items leave P in sacc (fp32) and pack pairs into pbf; dS items leave

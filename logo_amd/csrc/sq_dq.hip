@@ -190,8 +190,8 @@ __global__ __launch_bounds__(128) LOGO_OCC_DQ64 void sq_dq64_kernel(const AttnAr
           if constexpr (DOV) {
             E8 o = op[S];
             pin(o);
-            mfma32_agpr(dqacc[0][Y % DT], o, dsb[0][Y / DT]);
-            mfma32_agpr(dqacc[1][Y % DT], o, dsb[1][Y / DT]);
+            mfma32_agpr_ready(dqacc[0][Y % DT], o, dsb[0][Y / DT]);
+            mfma32_agpr_ready(dqacc[1][Y % DT], o, dsb[1][Y / DT]);
           }
         }
         if constexpr (S + PF < NX + NY) load_op(std::integral_constant<int, S + PF>{});

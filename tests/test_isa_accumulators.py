@@ -82,6 +82,47 @@ def check_accumulators(lines):
     return bad
 
 
+def _vregs(tok):
+    tok = tok.rstrip(",")
+    m = re.fullmatch(r"-?v\[(\d+):(\d+)\]", tok)
+    if m:
+        return set(range(int(m.group(1)), int(m.group(2)) + 1))
+    m = re.fullmatch(r"-?v(\d+)", tok)
+    return {int(m.group(1))} if m else set()
+
+
+# A VALU write of an MFMA's A or B operand needs wait states before the MFMA
+# (two on the gfx9 MFMA parts; three are required here).  The compiler adds
+# them for its own MFMAs but not for the inline-asm accumulator MFMAs without
+# a leading s_nop (mfma32_agpr_ready), so for those the distance is checked.
+OPERAND_WAIT_STATES = 3
+
+
+def check_operand_distance(lines):
+    """Violations (line index, text): an accumulator MFMA whose A or B
+    VGPRs a VALU instruction wrote within OPERAND_WAIT_STATES wait states
+    before it (each instruction is one wait state, s_nop N is N + 1; the walk
+    follows the listing, as the slot schedules are straight-line code)."""
+    code = [line.split("//")[0].split() for line in lines]
+    bad = []
+    for n, c in enumerate(code):
+        if not (c and c[0].startswith("v_mfma") and len(c) >= 4 and _ACC_DST.search(lines[n])):
+            continue
+        srcs = _vregs(c[2]) | _vregs(c[3])
+        waits, k = 0, n - 1
+        while k >= 0 and waits < OPERAND_WAIT_STATES:
+            p = code[k]
+            k -= 1
+            if not p or p[0].startswith((".", ";")) or p[0].endswith(":"):
+                continue
+            if p[0].startswith("v_") and not p[0].startswith(("v_mfma", "v_accvgpr_write")) and len(p) > 1:
+                if _vregs(p[1]) & srcs:
+                    bad.append((n, "operand written %d wait state(s) before: %s" % (waits, lines[k + 1].strip())))
+                    break
+            waits += int(p[1]) + 1 if p[0] == "s_nop" and len(p) > 1 else 1
+    return bad
+
+
 _ADDR = re.compile(r"//\s*([0-9A-Fa-f]+):")
 _UNCOND = ("s_branch", "s_setpc_b64", "s_endpgm")
 
@@ -216,6 +257,8 @@ def test_asm_accumulators_are_not_copied_inside_mfma_loops(tmp_path):
         assert ops == {want}, f"{name}: MFMA types {sorted(ops)}, expected {want}"
         bad = check_accumulators(lines)
         assert not bad, f"{name}: " + "; ".join(f"line {n}: {t[:100]}" for n, t in bad[:5])
+        bad = check_operand_distance(lines)
+        assert not bad, f"{name}: " + "; ".join(f"line {n}: {t[:100]}" for n, t in bad[:5])
 
 
 @pytest.mark.skipif(not (os.path.exists(LIB) and shutil.which(f"{LLVM}/llvm-objdump")),
@@ -277,3 +320,21 @@ def test_drain_checker_ignores_other_accumulators():
     ok = _GOOD[:6] + ["\tv_accvgpr_write_b32 a16, v3", "\ts_nop 2",
                       "\tv_mfma_f32_32x32x16_bf16 a[16:31], v[2:5], v[6:9], a[16:31]"] + _GOOD[6:]
     assert check_accumulators_drained(ok) == []
+
+
+def test_operand_checker_accepts_distant_writes():
+    ok = ["\tv_cvt_pk_bf16_f32 v6, v40, v41", "\tds_read_b128 v[2:5], v90", "\ts_waitcnt lgkmcnt(0)",
+          "\tv_exp_f32_e64 v50, -v51", "\tv_mfma_f32_32x32x16_bf16 a[0:15], v[2:5], v[6:9], a[0:15]"]
+    assert check_operand_distance(ok) == []
+    assert check_operand_distance(["\tv_cvt_pk_bf16_f32 v6, v40, v41", "\ts_nop 2",
+                                   "\tv_mfma_f32_32x32x16_bf16 a[0:15], v[2:5], v[6:9], a[0:15]"]) == []
+
+
+def test_operand_checker_flags_a_recent_valu_write():
+    bad = ["\tv_cvt_pk_bf16_f32 v7, v40, v41", "\ts_waitcnt lgkmcnt(0)",
+           "\tv_mfma_f32_32x32x16_bf16 a[0:15], v[2:5], v[6:9], a[0:15]"]
+    found = check_operand_distance(bad)
+    assert found and "operand written" in found[0][1]
+    # a VGPR-result MFMA is the compiler's to protect, and is not checked
+    assert check_operand_distance(["\tv_cvt_pk_bf16_f32 v7, v40, v41",
+                                   "\tv_mfma_f32_32x32x16_bf16 v[20:35], v[2:5], v[6:9], 0"]) == []
