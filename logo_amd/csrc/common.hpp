@@ -479,6 +479,26 @@ __device__ __forceinline__ int lower_bound_i32(const int32_t* arr, int lo, int h
   return lo;
 }
 
+// lower_bound_i32 by a whole wave, 64 probes per round (about log64 of the
+// range in dependent loads instead of log2): every lane must call it with the
+// same arguments, and every lane gets the result.
+__device__ __forceinline__ int wave_lower_bound(const int32_t* arr, int lo, int hi, int x) {
+  const int lane = threadIdx.x & 63;
+  while (hi - lo > 64) {
+    const int stride = (hi - lo + 63) >> 6;
+    const int idx = lo + stride * (lane + 1) - 1;  // the last element of chunk `lane`
+    const bool ge = idx >= hi || arr[idx] >= x;
+    const unsigned long long m = __ballot(ge);
+    if (m == 0) return hi;
+    const int j0 = __builtin_ctzll(m);  // the first chunk whose last element is >= x
+    lo += stride * j0;
+    hi = min(hi, lo + stride);
+  }
+  const bool ge = lo + lane < hi && arr[lo + lane] >= x;
+  const unsigned long long m = __ballot(ge);
+  return m == 0 ? hi : lo + __builtin_ctzll(m);
+}
+
 // Workgroup id -> (rank, head) so that the workgroups of one head land on one
 // XCD (workgroups are dispatched round-robin over the 8 XCDs), keeping that
 // head's K/V in one L2.  Ranks are visited in launch order.

@@ -97,13 +97,21 @@ __global__ __launch_bounds__(256) LOGO_OCC_DKV void sq_dkv_kernel(const AttnArgs
     const RowView<SPARSE> rv = row_view<SPARSE>(a, lane_sel, bos);
     const QSide<D, SPARSE> qs(a, a.q_sel, a.q, hq), os(a, a.do_sel, a.dout, hq);
     const int q_lo = cu_q[s], q_hi = cu_q[s + 1];
-    int rq0, rq_end;
-    if (SPARSE) {
-      rq0 = lower_bound_i32(rv.ps, q_lo, q_hi, k0);
-      rq_end = WINDOW ? lower_bound_i32(rv.ps, rq0, q_hi, k_last + W + 1) : q_hi;
-    } else {
-      rq0 = min(q_lo + k0, q_hi);
-      rq_end = WINDOW ? min(q_hi, q_lo + k_last + W + 1) : q_hi;
+    // first row in [lo, hi) whose position is >= x (rows ascend by position;
+    // dense rows are the positions themselves)
+    auto lb_pos = [&](int lo, int hi, int x) {
+      return SPARSE ? wave_lower_bound(rv.ps, lo, hi, x) : min(max(q_lo + x, lo), hi);
+    };
+    const int rq0 = lb_pos(q_lo, q_hi, k0);
+    const int rq_end = WINDOW ? lb_pos(rq0, q_hi, k_last + W + 1) : q_hi;
+    // This wave's keys kw0 .. kw_last: rows before lb0 see none of them,
+    // rows from lb1 on see all of them (causally), rows from lb2 on are past
+    // the window of the last one.
+    int lb0 = rq_end, lb1 = rq_end, lb2 = rq_end;
+    if (wave_active && rq0 < rq_end) {
+      lb0 = lb_pos(rq0, rq_end, kw0);
+      lb1 = lb_pos(lb0, rq_end, kw_last);
+      if (WINDOW) lb2 = lb_pos(lb1, rq_end, kw_last + W + 1);
     }
     const float* lse_h = a.lse + (int64_t)hq * a.n;
     const float* delta_h = a.delta + (int64_t)hq * a.n;
@@ -150,8 +158,6 @@ __global__ __launch_bounds__(256) LOGO_OCC_DKV void sq_dkv_kernel(const AttnArgs
       const float* dlb = sDelta(B);
       const int* pob = sPos(B);
       const int last = min(rt + RS - 1, rq_end - 1);
-      const int p_first = pob[0];
-      const int p_last = pob[last - rt];
       // Each 64-row sub-tile as two 32-row halves h0, h1, its MFMAs in eight
       // blocks of DS slots (one wave per SIMD):
       //   S(h0) | dP(h0) | S(h1) | dP(h1) | dV(h0) | dK(h0) | dV(h1) | dK(h1)
@@ -345,9 +351,12 @@ __global__ __launch_bounds__(256) LOGO_OCC_DKV void sq_dkv_kernel(const AttnArgs
         });
         __builtin_amdgcn_sched_barrier(0);
       };
-      const bool skip = !wave_active || p_last < kw0 || (WINDOW && p_first > kw_last + W);
+      // the step's last row is before lb0 (sees none of the wave's keys) or
+      // its first row is past lb2 (past the window); rows before lb1, the
+      // window and clamped rows past rq_end need the mask
+      const bool skip = !wave_active || last < lb0 || (WINDOW && rt >= lb2);
       if (!skip) {
-        const bool need_mask = WINDOW || (p_first < kw_last) || (rt + RS > rq_end);
+        const bool need_mask = WINDOW || rt < lb1 || (rt + RS > rq_end);
         if (need_mask) compute(std::true_type{});
         else compute(std::false_type{});
       }
