@@ -140,9 +140,17 @@ __global__ __launch_bounds__(256) void swa_fwd_kernel(const AttnArgs a) {
     }
   }
 
-  if (qt.valid) {
-    const float inv = 1.f / l_tot;
-    bf16* orow = a.o + (qt.t * a.hq + hq) * D;
+  // O leaves through LDS as whole rows: each wave writes its 32 rows (8-byte
+  // pieces, swizzled chunks) over the V tiles, then 16 lanes store one row's
+  // D * 2 bytes together.  Stored from the accumulators directly, every
+  // 8-byte piece would touch its own row (32 rows per store instruction).
+  const float inv = qt.valid ? 1.f / l_tot : 0.f;
+  __syncthreads();  // every wave is done with V's tiles
+  bf16* const ot = tile(0);  // 128 rows x D (two 64-row swizzled tiles)
+  {
+    const int row = 32 * wave + i;
+    bf16* const orow = ot + (row >> 6) * GT::ELEMS;
+    const int rr = row & 63;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
@@ -150,9 +158,25 @@ __global__ __launch_bounds__(256) void swa_fwd_kernel(const AttnArgs a) {
         bf16x4 v;
 #pragma unroll
         for (int e = 0; e < 4; ++e) v[e] = (bf16)(oacc[dt][4 * q4 + e] * inv);
-        *reinterpret_cast<bf16x4*>(orow + 32 * dt + 8 * q4 + 4 * g) = v;
+        // d = 32 dt + 8 q4 + 4 g: half g of chunk 4 dt + q4
+        *reinterpret_cast<bf16x4*>(orow + GT::off(rr, 4 * dt + q4) + 4 * g) = v;
       }
-    if (g == 0) a.lse[(int64_t)hq * a.n + qt.r] = base + log2f(l_tot);
+  }
+  if (qt.valid && g == 0) a.lse[(int64_t)hq * a.n + qt.r] = base + log2f(l_tot);
+  __syncthreads();
+  {
+    constexpr int CHR = D / 8;               // 16-byte chunks per row
+    constexpr int RPP = 256 / CHR;           // rows per pass
+    const int ch = tid % CHR;
+    const int nrow = qt.r_end - qt.r0;
+#pragma unroll
+    for (int r = tid / CHR; r < 128; r += RPP) {
+      if (r < nrow) {
+        const u32x4 v = *reinterpret_cast<const u32x4*>(ot + (r >> 6) * GT::ELEMS + GT::off(r & 63, ch));
+        // dense rows: row r0 + r is the token
+        *reinterpret_cast<u32x4*>(a.o + ((int64_t)(qt.r0 + r) * a.hq + hq) * D + 8 * ch) = v;
+      }
+    }
   }
 }
 
