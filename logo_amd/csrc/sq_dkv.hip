@@ -379,8 +379,17 @@ __global__ __launch_bounds__(256) LOGO_OCC_DKV void sq_dkv_kernel(const AttnArgs
   }
 
   agpr_acc_drain();
-  if (valid_k) {
-    const int64_t off = ((int64_t)(bos + key) * a.h + h) * D;
+  // dK and dV leave through LDS (free after the last step's barrier) as whole
+  // rows: each wave writes its 32 keys' rows (8-byte pieces into swizzled
+  // chunks), then 16 lanes store one row's D * 2 bytes together.  Stored from
+  // the accumulators directly, every 8-byte piece would touch its own row.
+  {
+    using GT = TileGeom<D, kSwz>;
+    bf16* const blk_k = reinterpret_cast<bf16*>(smem_b);  // 128 rows: two 64-row tiles
+    bf16* const blk_v = blk_k + 2 * GT::ELEMS;
+    const int row = 32 * wave + i, rr = row & 63;
+    bf16* const rk = blk_k + (row >> 6) * GT::ELEMS;
+    bf16* const rv_ = blk_v + (row >> 6) * GT::ELEMS;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
@@ -391,9 +400,21 @@ __global__ __launch_bounds__(256) LOGO_OCC_DKV void sq_dkv_kernel(const AttnArgs
           kv[e] = (EL)(dkacc[dt][4 * q4 + e] * dk_mul);
           vv[e] = (EL)(dvacc[dt][4 * q4 + e] * dv_mul);
         }
-        *reinterpret_cast<E4*>(a.dk + off + 32 * dt + 8 * q4 + 4 * g) = kv;
-        *reinterpret_cast<E4*>(a.dv + off + 32 * dt + 8 * q4 + 4 * g) = vv;
+        // d = 32 dt + 8 q4 + 4 g: half g of chunk 4 dt + q4
+        *reinterpret_cast<E4*>(rk + GT::off(rr, 4 * dt + q4) + 4 * g) = kv;
+        *reinterpret_cast<E4*>(rv_ + GT::off(rr, 4 * dt + q4) + 4 * g) = vv;
       }
+    __syncthreads();
+    constexpr int CHR = D / 8;      // 16-byte chunks per row
+    constexpr int RPP = 256 / CHR;  // rows per pass
+    const int ch = tid % CHR;
+    const int nkey = min(kBKV, seqlen - k0);
+    for (int r = tid / CHR; r < nkey; r += RPP) {
+      const int64_t off = ((int64_t)(bos + k0 + r) * a.h + h) * D + 8 * ch;
+      const int lo = (r >> 6) * GT::ELEMS + GT::off(r & 63, ch);
+      *reinterpret_cast<u32x4*>(a.dk + off) = *reinterpret_cast<const u32x4*>(blk_k + lo);
+      *reinterpret_cast<u32x4*>(a.dv + off) = *reinterpret_cast<const u32x4*>(blk_v + lo);
+    }
   }
 }
 
