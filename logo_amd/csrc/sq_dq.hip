@@ -266,11 +266,17 @@ __global__ __launch_bounds__(128) LOGO_OCC_DQ64 void sq_dq64_kernel(const AttnAr
         dqacc[b][dt] = sum;
       }
   }
+  // dQ leaves through LDS as whole rows: each wave writes its 64 rows (8-byte
+  // pieces into swizzled chunks) over the K / V tiles, then 16 lanes store
+  // one row's D * 2 bytes together (rows are scattered tokens, each row
+  // contiguous).  Stored from the accumulators directly, every 8-byte piece
+  // would touch its own row.
+  {
+    using GT = TileGeom<D, kSwz>;
+    __syncthreads();  // every wave is done with the K / V tiles
 #pragma unroll
-  for (int b = 0; b < 2; ++b) {
-    if (vr[b]) {
-      const int64_t tok = qt.rv.token(rr[b]);
-      bf16* dqrow = a.dq + (tok * a.hq + hq) * D;
+    for (int b = 0; b < 2; ++b) {
+      const int rr_ = 32 * b + i;
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
@@ -278,8 +284,19 @@ __global__ __launch_bounds__(128) LOGO_OCC_DQ64 void sq_dq64_kernel(const AttnAr
           E4 v;
 #pragma unroll
           for (int e = 0; e < 4; ++e) v[e] = (EL)(dqacc[b][dt][4 * q4 + e] * dq_mul);
-          *reinterpret_cast<E4*>(dqrow + 32 * dt + 8 * q4 + 4 * g) = v;
+          // d = 32 dt + 8 q4 + 4 g: half g of chunk 4 dt + q4
+          *reinterpret_cast<E4*>(smem + wave * GT::ELEMS + GT::off(rr_, 4 * dt + q4) + 4 * g) = v;
         }
+    }
+    __syncthreads();
+    constexpr int CHR = D / 8;        // 16-byte chunks per row
+    constexpr int RPP = 128 / CHR;    // rows per pass (128 threads)
+    const int ch = threadIdx.x % CHR;
+    const int nrow = qt.r_end - qt.r0;
+    for (int r = threadIdx.x / CHR; r < nrow; r += RPP) {
+      const int64_t tok = qt.rv.token(qt.r0 + r);
+      const u32x4 v = *reinterpret_cast<const u32x4*>(smem + (r >> 6) * GT::ELEMS + GT::off(r & 63, ch));
+      *reinterpret_cast<u32x4*>(a.dq + (tok * a.hq + hq) * D + 8 * ch) = v;
     }
   }
 }

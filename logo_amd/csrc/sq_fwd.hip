@@ -296,9 +296,20 @@ __global__ __launch_bounds__(64 * NW) LOGO_OCC_FWD void sq_fwd_pipe_kernel(const
     l_tot = lsum;
     m_run = mx;
   }
-  if (qt.valid) {
-    const float inv = 1.f / l_tot;
-    bf16* orow = a.o + (qt.t * a.hq + hq) * D;
+  // O leaves through LDS as whole rows: each wave writes its 32 rows (8-byte
+  // pieces into swizzled chunks) over the K / V tiles, then 16 lanes store
+  // one row's D * 2 bytes together (the rows are scattered tokens, but each
+  // row is contiguous).  Stored from the accumulators directly, every 8-byte
+  // piece would touch its own row.
+  {
+    using GT = TileGeom<D, kSwz>;
+    const float inv = qt.valid ? 1.f / l_tot : 0.f;
+    if (qt.valid && g == 0) a.lse[(int64_t)hq * a.n + qt.r] = m_run + log2f(l_tot);
+    __syncthreads();  // every wave is done with the K / V tiles
+    bf16* const blk = reinterpret_cast<bf16*>(smem);  // NW * 32 rows in 64-row tiles
+    const int row = 32 * wave + i;
+    bf16* const orow = blk + (row >> 6) * GT::ELEMS;
+    const int rr = row & 63;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
@@ -306,9 +317,19 @@ __global__ __launch_bounds__(64 * NW) LOGO_OCC_FWD void sq_fwd_pipe_kernel(const
         E4 v;
 #pragma unroll
         for (int e = 0; e < 4; ++e) v[e] = (EL)(oacc[dt][4 * q4 + e] * inv);
-        *reinterpret_cast<E4*>(orow + 32 * dt + 8 * q4 + 4 * g) = v;
+        // d = 32 dt + 8 q4 + 4 g: half g of chunk 4 dt + q4
+        *reinterpret_cast<E4*>(orow + GT::off(rr, 4 * dt + q4) + 4 * g) = v;
       }
-    if (g == 0) a.lse[(int64_t)hq * a.n + qt.r] = m_run + log2f(l_tot);
+    __syncthreads();
+    constexpr int CHR = D / 8;           // 16-byte chunks per row
+    constexpr int RPP = NW * 64 / CHR;   // rows per pass
+    const int ch = threadIdx.x % CHR;
+    const int nrow = qt.r_end - qt.r0;
+    for (int r = threadIdx.x / CHR; r < nrow; r += RPP) {
+      const int64_t tok = qt.rv.token(qt.r0 + r);
+      const u32x4 v = *reinterpret_cast<const u32x4*>(blk + (r >> 6) * GT::ELEMS + GT::off(r & 63, ch));
+      *reinterpret_cast<u32x4*>(a.o + (tok * a.hq + hq) * D + 8 * ch) = v;
+    }
   }
 }
 
