@@ -22,9 +22,11 @@
  *   [8 +   (nseq+1) ...]         prefix of ceil(count_s / LOGO_BQ)
  *   [8 + 2*(nseq+1) ...]         prefix of ceil(len_s / LOGO_BKV)
  * Row lists: q_idx int64 [lanes, N], pos int32 [lanes, N]; entries
- * [0, Sq) of each lane are valid (logo/ops/common.py:90-93).
+ * [0, Sq) of each lane are the rows (logo/ops/common.py:90-93), entries
+ * [Sq, N) are written zero.
  * lse / delta: float32 [HQ, N] indexed by compacted row (log2 domain lse,
- * logo/ops/selected_full_attn.py:118-119).
+ * logo/ops/selected_full_attn.py:118-119); the forward writes zero to the lse
+ * rows past the lane's rows, delta rows past Sq are left unwritten.
  */
 #ifndef LOGO_HIP_H_
 #define LOGO_HIP_H_
@@ -115,8 +117,9 @@ int logo_q_start_blk(const int32_t* pos, const int32_t* cu_q, const int32_t* chu
  * Query-sparse causal attention forward on selected rows
  * (sq_full_attn_fwd_kernel + _fwd, logo/ops/selected_full_attn.py:33-121,
  * :340-362, with the q gather :461 and output scatter :469-471 fused).
- * Writes o[t] for selected rows t only (the caller zero-fills o) and lse per
- * compacted row.  q_idx/pos == NULL selects dense mode (every row, meta from
+ * Writes every row of o: o[t] for selected tokens t, zero for the others
+ * (the reference's zero-initialised output, :469-470; no fill by the caller),
+ * and lse per compacted row.  q_idx/pos == NULL selects dense mode (every row, meta from
  * logo_dense_meta).  window < 0: full causal; window >= 0: keys
  * [p - window, p] (logo/layers/utils.py:144-147).
  * d is the head dim of q and k (64 or 128); v_dim is that of v and o, which
@@ -152,9 +155,10 @@ size_t logo_sq_workspace_counter_bytes(void);
 
 /*
  * Backward (logo/ops/selected_full_attn.py:124-138 delta, :141-228 dq,
- * :231-337 dk/dv, :444-445 GQA sum).  o and dout are [N, HQ, D]; writes dq
- * rows of selected tokens (caller zero-fills dq; the scatter :487-488 is
- * fused), every row of dk and dv [N, H, D], and the workspaces delta [HQ, N]
+ * :231-337 dk/dv, :444-445 GQA sum).  o and dout are [N, HQ, D]; writes
+ * every row of dq (zero for unselected tokens, as the zero-initialised dq of
+ * the scatter :487-488, which is fused; no fill by the caller), every row of
+ * dk and dv [N, H, D], and the workspaces delta [HQ, N]
  * fp32 and, in sparse mode, q_sel / do_sel [HQ, N, D] bf16: compacted copies
  * of the selected q and dO rows (the reference's q_sel / do_sel, :461 :483),
  * filled by the delta phase, of the call's dtype.  Dense mode ignores q_sel /

@@ -16,6 +16,7 @@
 // host:
 //   count    : per 4096-token chunk and lane, popcount of wave ballots
 //   scatter  : chunk prefix + wave prefix (LDS) + mbcnt rank -> q_idx, pos
+//              (and zeros in entries [Sq, N), one per unselected token)
 //   finalize : Sq, cu_q by binary search over q_idx, tile prefixes by block scan
 #include <mutex>
 
@@ -69,9 +70,14 @@ __global__ __launch_bounds__(256) void compact_scatter(const uint8_t* __restrict
   const int chunk = blockIdx.x;
   const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
 
-  int part = 0;
-  for (int c = threadIdx.x; c < chunk; c += 256) part += counts[lane * nchunk + c];
+  int part = 0, all = 0;
+  for (int c = threadIdx.x; c < nchunk; c += 256) {
+    const int v = counts[lane * nchunk + c];
+    all += v;
+    if (c < chunk) part += v;
+  }
   const int prefix = block_sum(part, red);
+  const int sq = block_sum(all, red);
 
   const int64_t base = (int64_t)chunk * kChunk + w * 1024;
   uint64_t masks[16];
@@ -92,12 +98,17 @@ __global__ __launch_bounds__(256) void compact_scatter(const uint8_t* __restrict
 #pragma unroll
   for (int s = 0; s < 16; ++s) {
     const uint64_t m = masks[s];
+    const int rank = run + __popcll(m & below);  // selected tokens before t
+    const int64_t t = base + s * 64 + l;
     if ((m >> l) & 1ull) {
-      const int rank = run + __popcll(m & below);
-      const int64_t t = base + s * 64 + l;
       const int sg = seg_of(cu, nseq, t);
       qi[rank] = t;
       ps[rank] = (int32_t)(t - cu[sg]);
+    } else if (t < n) {
+      // entries [Sq, N) are zero: unselected token t fills entry Sq + (the
+      // unselected tokens before it)
+      qi[sq + (t - rank)] = 0;
+      ps[sq + (t - rank)] = 0;
     }
     run += __popcll(m);
   }
@@ -199,11 +210,14 @@ __global__ __launch_bounds__(kSmallThreads) void compact_small(const uint8_t* __
   for (int gi = w; gi < G; gi += NW) {
     const int64_t t = (int64_t)gi * 64 + l;
     const uint64_t msk = __ballot(sel_on(sel, n, lanes, lane, t));
+    const int rank = gpre[gi] + __popcll(msk & below);  // selected tokens before t
     if ((msk >> l) & 1ull) {
-      const int rank = gpre[gi] + __popcll(msk & below);
       const int sg = seg_of(cu, nseq, t);
       qi[rank] = t;
       ps[rank] = (int32_t)(t - cu[sg]);
+    } else if (t < n) {
+      qi[sq + (t - rank)] = 0;  // entries [Sq, N) are zero, as in compact_scatter
+      ps[sq + (t - rank)] = 0;
     }
   }
   // cu_q[s] = selected tokens before token cu[s]: the prefix of its group plus

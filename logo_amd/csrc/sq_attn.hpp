@@ -185,6 +185,9 @@ template <bool SPARSE>
 struct QTile {
   int hq, h, lane_sel, s, r0, r_end, bos, seqlen;
   int pmin, pmax, r, p, kv_lo, kv_hi;
+  // the lane's rows in all segments (cu_q[nseq]) and its tiles (paired
+  // tiles counted once); set before init can return false
+  int q_end, ntile;
   bool wave_active, valid;
   int64_t t;
   RowView<SPARSE> rv;
@@ -204,13 +207,15 @@ struct QTile {
     lane_sel = a.lanes > 1 ? hq : 0;
     const int32_t* meta = a.meta + (int64_t)lane_sel * a.meta_stride;
     const int nt = paired ? (meta[1] + 1) >> 1 : meta[1];
+    const int32_t* cu_q = meta + kMetaHdr;
+    const int32_t* cu_tq = cu_q + (a.nseq + 1);
+    q_end = cu_q[a.nseq];
+    ntile = nt;
     nper = splittable ? split_pieces(nt, a.split_cap) : 1;
     if (rank >= nt * nper) return false;
     trank = rank / nper;
     piece = rank - trank * nper;
     const int tile = nt - 1 - trank;  // heaviest (latest) blocks first
-    const int32_t* cu_q = meta + kMetaHdr;
-    const int32_t* cu_tq = cu_q + (a.nseq + 1);
     if (paired) {
       s = 0;
       r0 = cu_q[0] + tile * 2 * kBQ;
@@ -247,6 +252,103 @@ struct QTile {
     return true;
   }
 };
+
+// Sparse mode: the rows of tokens that no compacted row writes are zero in
+// the outputs o and dq ([N, HQ, D]), written by the fwd and dq kernels
+// themselves instead of a separate fill of the whole tensor.  The lane's rows
+// ascend by token over all its segments (t_0 < t_1 < ... < t_{q_end-1}), so
+// the tokens to zero are the gaps (t_{r-1}, t_r) for 0 < r < q_end, the
+// leading range [0, t_0) and the trailing range (t_{q_end-1}, N).  Gap r goes
+// to the tile that holds row r (the tiles partition [0, q_end)); the leading
+// and trailing ranges are cut into one slice per tile, so that a long
+// unselected span is spread over the grid instead of one workgroup.  A lane
+// without rows has no tiles: then every workgroup of the head's grid zeroes
+// one slice of [0, N).  Only piece 0 of a split tile zeroes.  The forward
+// also zeroes the head's lse rows [q_end, N), the same way.
+// 16 bytes a lane, CHR = D / 8 lanes a row; tokens fit in int (N < 2^31).
+template <int D>
+__device__ __forceinline__ void zero_row(bf16* out, int tok, int hq_n, int hq, int c16) {
+  *reinterpret_cast<u32x4*>(out + ((int64_t)tok * hq_n + hq) * D + 8 * c16) = u32x4{0u, 0u, 0u, 0u};
+}
+
+// Slice k of nslice of [lo, hi): ceil((hi - lo) / nslice) items a slice.
+__device__ __forceinline__ void slice_of(int lo, int hi, int k, int nslice, int& s0, int& s1) {
+  const int span = hi - lo;
+  const int chunk = (span + nslice - 1) / nslice;
+  s0 = lo + (int)min((int64_t)chunk * k, (int64_t)span);
+  s1 = lo + (int)min((int64_t)chunk * (k + 1), (int64_t)span);
+}
+
+// Slice k of nslice of the tokens [lo, hi), by the workgroup's nthreads.
+template <int D>
+__device__ __forceinline__ void zero_slice(bf16* out, int hq_n, int hq, int lo, int hi, int k, int nslice,
+                                           int nthreads) {
+  constexpr int CHR = D / 8;
+  const int grp = threadIdx.x / CHR, ngrp = nthreads / CHR, c16 = threadIdx.x % CHR;
+  int s0, s1;
+  slice_of(lo, hi, k, nslice, s0, s1);
+  for (int u = s0 + grp; u < s1; u += ngrp) zero_row<D>(out, u, hq_n, hq, c16);
+}
+
+// Gaps of the tile's rows [r0, r_end): wave w takes rows r0 + 64 w + lane,
+// stepping 64 nw; each gap found (ballot) is zeroed by the wave's 64 / CHR
+// row groups in turn.
+template <int D>
+__device__ __forceinline__ void zero_gaps(bf16* out, int hq_n, int hq, const RowView<true>& rv, int r0, int r_end,
+                                          int nthreads) {
+  constexpr int CHR = D / 8, GPW = 64 / CHR;
+  const int l = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = nthreads >> 6;
+  const int grp = l / CHR, c16 = l % CHR;
+  for (int rb = r0 + 64 * wave; rb < r_end; rb += 64 * nw) {
+    const int r = rb + l;
+    int lo = 0, hi = 0;
+    if (r > 0 && r < r_end) {
+      lo = (int)rv.token(r - 1) + 1;
+      hi = (int)rv.token(r);
+    }
+    unsigned long long m = __ballot(hi > lo);
+    while (m != 0) {
+      const int j = __builtin_ctzll(m);
+      m &= m - 1;
+      const int a0 = __shfl(lo, j), a1 = __shfl(hi, j);
+      for (int u = a0 + grp; u < a1; u += GPW) zero_row<D>(out, u, hq_n, hq, c16);
+    }
+  }
+}
+
+// Slice k of nslice of the floats [lo, hi) of p (the forward's lse rows past
+// the lane's q_end, which no tile writes, are zero too).
+__device__ __forceinline__ void zero_slice_f32(float* p, int lo, int hi, int k, int nslice, int nthreads) {
+  int s0, s1;
+  slice_of(lo, hi, k, nslice, s0, s1);
+  for (int u = s0 + threadIdx.x; u < s1; u += nthreads) p[u] = 0.f;
+}
+
+// Everything a tile's workgroup (piece 0) zeroes: its rows' gaps and its
+// slices (tile rank k of ntile) of the leading and trailing ranges; lse
+// (forward only, else nullptr): its slice of the head's rows [q_end, N).
+template <int D>
+__device__ __forceinline__ void zero_unselected(const AttnArgs& a, bf16* out, float* lse, const QTile<true>& qt,
+                                                int nthreads) {
+  const int n = (int)a.n;
+  zero_gaps<D>(out, a.hq, qt.hq, qt.rv, qt.r0, qt.r_end, nthreads);
+  const int first = (int)qt.rv.token(0), last = (int)qt.rv.token(qt.q_end - 1);
+  zero_slice<D>(out, a.hq, qt.hq, 0, first, qt.trank, qt.ntile, nthreads);
+  zero_slice<D>(out, a.hq, qt.hq, last + 1, n, qt.trank, qt.ntile, nthreads);
+  if (lse != nullptr) zero_slice_f32(lse + (int64_t)qt.hq * n, qt.q_end, n, qt.trank, qt.ntile, nthreads);
+}
+
+// A workgroup for which init returned false: in a lane without rows, its
+// slice (grid rank of the head's gridDim.x / HQ) of every token (and of the
+// head's lse rows).
+template <int D>
+__device__ __forceinline__ void zero_empty_lane(const AttnArgs& a, bf16* out, float* lse, const QTile<true>& qt,
+                                                int nthreads) {
+  if (qt.q_end != 0) return;
+  const int n = (int)a.n, nslice = (int)(gridDim.x / a.hq);
+  zero_slice<D>(out, a.hq, qt.hq, 0, n, qt.rank, nslice, nthreads);
+  if (lse != nullptr) zero_slice_f32(lse + (int64_t)qt.hq * n, 0, n, qt.rank, nslice, nthreads);
+}
 
 // ---------------------------------------------------------------------------
 // Forward

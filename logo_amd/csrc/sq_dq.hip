@@ -37,7 +37,10 @@ __global__ __launch_bounds__(128) LOGO_OCC_DQ64 void sq_dq64_kernel(const AttnAr
 
   const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63, i = l & 31, g = l >> 5;
   QTile<SPARSE> qt;
-  if (!qt.init(a, wave, i, WINDOW, 64, false, !WINDOW)) return;
+  if (!qt.init(a, wave, i, WINDOW, 64, false, !WINDOW)) {
+    if constexpr (SPARSE) zero_empty_lane<D>(a, a.dq, nullptr, qt, 128);
+    return;
+  }
   const int hq = qt.hq, W = a.window;
   int rr[2], pr[2];
   bool vr[2];
@@ -231,6 +234,8 @@ __global__ __launch_bounds__(128) LOGO_OCC_DQ64 void sq_dq64_kernel(const AttnAr
   }
 
   agpr_acc_drain();
+  if constexpr (SPARSE)
+    if (qt.piece == 0) zero_unselected<D>(a, a.dq, nullptr, qt, 128);
   if (qt.nsplit > 1) {
     // Key-range split: partial dQ of this piece as [wave][row block][dt][item]
     // [lane]; the last piece of the tile to arrive adds the others' to its own.

@@ -55,7 +55,10 @@ __global__ __launch_bounds__(64 * NW) LOGO_OCC_FWD void sq_fwd_pipe_kernel(const
 
   const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63, i = l & 31, g = l >> 5;
   QTile<SPARSE> qt;
-  if (!qt.init(a, wave, i, WINDOW, 32, NW == 8, !WINDOW)) return;
+  if (!qt.init(a, wave, i, WINDOW, 32, NW == 8, !WINDOW)) {
+    if constexpr (SPARSE) zero_empty_lane<D>(a, a.o, a.lse, qt, 64 * NW);
+    return;
+  }
   const int hq = qt.hq, p = qt.p, W = a.window;
 
   // Sparse mode holds q pre-scaled and negated, bf16(-c q) with
@@ -246,6 +249,8 @@ __global__ __launch_bounds__(64 * NW) LOGO_OCC_FWD void sq_fwd_pipe_kernel(const
   }
 
   float l_tot = pair_sum(l_run);
+  if constexpr (SPARSE)
+    if (qt.piece == 0) zero_unselected<D>(a, a.o, a.lse, qt, 64 * NW);
   if (qt.nsplit > 1) {
     // Key-range split: store this piece's partial (O unnormalised, relative to
     // its base m_run; per row m_run and l) as [wave][dt][item][lane]; the last

@@ -59,9 +59,10 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> compact(const at::Tensor& sel, co
   const int lanes = sel.dim() == 2 ? (int)sel.size(1) : 1;
   const int nseq = (int)cu.numel() - 1;
   auto i32 = cu.options();
-  // entries past each lane's Sq are zero (the kernels write [0, Sq) only)
-  auto q_idx = at::zeros({lanes, std::max<int64_t>(n, 1)}, i32.dtype(at::kLong));
-  auto pos = at::zeros({lanes, std::max<int64_t>(n, 1)}, i32);
+  // entries past each lane's Sq: zero, written by the compaction itself
+  // (n == 0 keeps one zero entry per lane)
+  auto q_idx = n > 0 ? at::empty({lanes, n}, i32.dtype(at::kLong)) : at::zeros({lanes, 1}, i32.dtype(at::kLong));
+  auto pos = n > 0 ? at::empty({lanes, n}, i32) : at::zeros({lanes, 1}, i32);
   auto meta = at::empty({lanes * LOGO_META_STRIDE(nseq)}, i32);
   auto ws = at::empty({(int64_t)logo_compact_workspace_bytes(n, lanes)}, i32.dtype(at::kByte));
   ok(logo_compact(static_cast<const uint8_t*>(sel.data_ptr()), n, lanes, cu.data_ptr<int32_t>(), nseq,
@@ -122,12 +123,10 @@ std::tuple<at::Tensor, at::Tensor> sq_fwd(const at::Tensor& q, const at::Tensor&
                                           const at::Tensor& cu, int64_t lanes, double scale, int64_t window) {
   const int dtype = check_attn(q, k, v);
   const int64_t n = q.size(0), hq = q.size(1), h = k.size(1), d = q.size(2);
-  // Sparse mode writes the selected rows only (the others are zero, and lse
-  // past each head's Sq); dense mode writes every row of cu's segments, which
-  // cover the tokens, so it skips the fill.
-  const bool sparse = q_idx.has_value();
-  auto o = sparse ? at::zeros_like(q) : at::empty_like(q);
-  auto lse = sparse ? at::zeros({hq, n}, q.options().dtype(at::kFloat)) : at::empty({hq, n}, q.options().dtype(at::kFloat));
+  // Every row of o and lse is written (sparse mode: zero for unselected
+  // tokens and for lse rows past each lane's rows, by the kernel).
+  auto o = at::empty_like(q);
+  auto lse = at::empty({hq, n}, q.options().dtype(at::kFloat));
   auto ws = window < 0 ? split_workspace(q, cu) : at::empty({0}, q.options().dtype(at::kByte));
   ok(logo_sq_fwd(cptr(q), cptr(k), cptr(v), mptr(o), lse.data_ptr<float>(), opt_ptr<int64_t>(q_idx),
                  opt_ptr<int32_t>(pos), meta.data_ptr<int32_t>(), cu.data_ptr<int32_t>(), n, (int)cu.numel() - 1,
@@ -180,14 +179,13 @@ struct Bwd {
       const at::Tensor &dout, const std::optional<at::Tensor>&q_idx, const std::optional<at::Tensor>&pos,    \
       const at::Tensor &meta, const at::Tensor &cu, int64_t lanes, double scale, int64_t window
 
-// delta [HQ, N] fp32 (rows past Sq zero) and, in sparse mode, the compacted
+// delta [HQ, N] fp32 (rows past Sq unwritten) and, in sparse mode, the compacted
 // copies q_sel / do_sel [HQ, N, D] (empty in dense mode): workspaces of the
 // dq and dk/dv phases, whose rows past each head's Sq are left unwritten.
 std::tuple<at::Tensor, at::Tensor, at::Tensor> sq_bwd_delta(LOGO_BWD_SCHEMA_ARGS) {
   check_attn(q, k, v);
   const bool sparse = q_idx.has_value();
-  auto delta = sparse ? at::zeros({q.size(1), q.size(0)}, q.options().dtype(at::kFloat))
-                      : at::empty({q.size(1), q.size(0)}, q.options().dtype(at::kFloat));
+  auto delta = at::empty({q.size(1), q.size(0)}, q.options().dtype(at::kFloat));
   auto q_sel = sparse ? at::empty({q.size(1), q.size(0), q.size(2)}, q.options()) : at::empty({0}, q.options());
   auto do_sel = sparse ? at::empty_like(q_sel) : at::empty({0}, q.options());
   Bwd b{q, k, v, o, lse, dout, q_idx, pos, meta, cu, lanes, scale, window};
@@ -198,7 +196,7 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> sq_bwd_delta(LOGO_BWD_SCHEMA_ARGS
 at::Tensor sq_bwd_dq(LOGO_BWD_SCHEMA_ARGS, const at::Tensor& delta, const at::Tensor& q_sel,
                      const at::Tensor& do_sel) {
   check_attn(q, k, v);
-  auto dq = q_idx.has_value() ? at::zeros_like(q) : at::empty_like(q);  // dense: every row written
+  auto dq = at::empty_like(q);  // every row written (sparse: unselected rows zero)
   Bwd b{q, k, v, o, lse, dout, q_idx, pos, meta, cu, lanes, scale, window};
   auto dl = delta, qs = q_sel, ds = do_sel;
   ok(b.call(1, &dl, &qs, &ds, &dq, nullptr, nullptr), "logo_sq_bwd_dq");
@@ -220,7 +218,7 @@ std::tuple<at::Tensor, at::Tensor> sq_bwd_dkv(LOGO_BWD_SCHEMA_ARGS, const at::Te
 std::tuple<at::Tensor, at::Tensor, at::Tensor> sq_bwd_dqkv(LOGO_BWD_SCHEMA_ARGS, const at::Tensor& delta,
                                                            const at::Tensor& q_sel, const at::Tensor& do_sel) {
   check_attn(q, k, v);
-  auto dq = q_idx.has_value() ? at::zeros_like(q) : at::empty_like(q);
+  auto dq = at::empty_like(q);
   auto dk = at::empty_like(k);
   auto dv = at::empty_like(v);
   Bwd b{q, k, v, o, lse, dout, q_idx, pos, meta, cu, lanes, scale, window};
