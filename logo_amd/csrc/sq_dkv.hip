@@ -172,7 +172,7 @@ __global__ __launch_bounds__(256) LOGO_OCC_DKV void sq_dkv_kernel(const AttnArgs
         constexpr bool MASK = decltype(mask_tag)::value;
         constexpr int NS = 2 * DS;  // MFMAs per half and pass: S and dP over D / 16 k-steps
         constexpr int SPT = 4 * NS; // slots per sub-tile
-        constexpr int PF = 6;       // operand prefetch distance, in slots
+        constexpr int PF = 4;       // operand prefetch distance, in slots
         constexpr int IPP = 16 / (2 * DS);  // P items per slot (over two blocks)
         constexpr int IPD = 16 / DS;        // dS items per slot (over one block)
         static_assert(IPP * 2 * DS == 16 && IPD * DS == 16, "a half has 16 row items per lane");

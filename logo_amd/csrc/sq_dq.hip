@@ -29,7 +29,7 @@ __global__ __launch_bounds__(128) LOGO_OCC_DQ64 void sq_dq64_kernel(const AttnAr
   constexpr int NX = 2 * DS;    // X slots: K row operand (even), V row operand (odd)
   constexpr int NY = 2 * DT;    // Y slots: K^T operands (16-key step hh, column block dt)
   constexpr int IX = 16 / NX;   // VALU items per X slot and row block (16 per half)
-  constexpr int PF = 3;         // operand prefetch distance, in slots
+  constexpr int PF = 2;         // operand prefetch distance, in slots
   using GT = TileGeom<D, kSwz>;
   bf16* const smem = dyn_smem();
   auto tileK = [&](int b) { return smem + b * GT::ELEMS; };
