@@ -10,8 +10,8 @@ in HBM.  Effective FLOPs count selected rows only:
 
 Prints ONE JSON line.  Per-kernel durations come from HIP events recorded on
 the launch stream around every operator call that launches the kernel inside
-the timed region (the operator's output allocation included, and for the
-forward and dq the zero-fill of unselected rows; dk/dv has none); the
+the timed region (the operator's output allocation included; the forward and
+dq kernels write the zero rows of unselected tokens themselves); the
 dominant kernel's roofline is its algorithmic FLOPs over that duration.  The
 CPU baseline times the reference's CPU formulation (dense causal attention per
 segment, then row masking, torch fp32 autograd) on a bounded sample of heads.
