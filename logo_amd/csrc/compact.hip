@@ -8,10 +8,11 @@
 //
 // Short inputs (at most 4096 tokens) and per-head selections of at most 65536
 // tokens a lane take one launch with one 1024-thread workgroup per lane
-// (compact_small): per-64-token ballot counts in LDS, their exclusive scan, a
-// second ballot pass that writes q_idx / pos, cu_q from the group prefixes,
-// then the tile prefixes (one lane of 32768 tokens takes it in about 24 us,
-// no faster than the three launches below, which spread it over the GPU).
+// (compact_small): per-64-token ballots and counts in LDS, the counts'
+// exclusive scan, a pass over the kept ballots that writes q_idx / pos, cu_q
+// from the group prefixes, then the tile prefixes (one lane of 32768 tokens
+// takes it in about 24 us, no faster than the three launches below, which
+// spread it over the GPU).
 // Everything else takes three launches, none of them synchronising with the
 // host:
 //   count    : per 4096-token chunk and lane, popcount of wave ballots
@@ -115,22 +116,33 @@ __global__ __launch_bounds__(256) void compact_scatter(const uint8_t* __restrict
 }
 
 // Exclusive scan over NT threads; returns this thread's exclusive prefix and
-// writes the block total to *total.
+// writes the block total to *total.  Each wave scans its 64 values with
+// shuffles, the wave totals go through LDS (buf[0, NT / 64)), and every
+// thread adds those of the waves before its own: three barriers in all (the
+// first keeps a previous call's readers of buf ahead of the new writes).
 template <int NT = 256>
 __device__ __forceinline__ int block_exscan(int v, int* buf, int* total) {
-  const int tid = threadIdx.x;
-  buf[tid] = v;
-  __syncthreads();
-  for (int off = 1; off < NT; off <<= 1) {
-    int add = tid >= off ? buf[tid - off] : 0;
-    __syncthreads();
-    buf[tid] += add;
-    __syncthreads();
+  constexpr int NW = NT / 64;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  int x = v;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_up(x, off);
+    if (lane >= off) x += y;
   }
-  const int inc = buf[tid];
-  *total = buf[NT - 1];
   __syncthreads();
-  return inc - v;
+  if (lane == 63) buf[w] = x;
+  __syncthreads();
+  int before = 0, all = 0;
+#pragma unroll
+  for (int i = 0; i < NW; ++i) {
+    const int t = buf[i];
+    before += i < w ? t : 0;
+    all += t;
+  }
+  *total = all;
+  __syncthreads();
+  return before + x - v;
 }
 
 // Tile prefixes per sequence (query tiles of LOGO_BQ compacted rows, key
@@ -185,14 +197,18 @@ __global__ __launch_bounds__(kSmallThreads) void compact_small(const uint8_t* __
                                                                int32_t* __restrict__ meta) {
   constexpr int NW = kSmallThreads / 64;
   __shared__ int gpre[kSmallMax / 64];  // per 64-token group: its count, then its exclusive prefix
-  __shared__ int buf[kSmallThreads];
+  __shared__ uint64_t gmask[kSmallMax / 64];  // per 64-token group: its selection ballot
+  __shared__ int buf[NW];
   const int lane = blockIdx.x;
   const int tid = threadIdx.x, w = tid >> 6, l = tid & 63;
   const int G = (int)((n + 63) >> 6);
 #pragma unroll 8
   for (int gi = w; gi < G; gi += NW) {
     const uint64_t msk = __ballot(sel_on(sel, n, lanes, lane, (int64_t)gi * 64 + l));
-    if (l == 0) gpre[gi] = __popcll(msk);
+    if (l == 0) {
+      gpre[gi] = __popcll(msk);
+      gmask[gi] = msk;
+    }
   }
   __syncthreads();
   int sq;
@@ -209,7 +225,7 @@ __global__ __launch_bounds__(kSmallThreads) void compact_small(const uint8_t* __
 #pragma unroll 8
   for (int gi = w; gi < G; gi += NW) {
     const int64_t t = (int64_t)gi * 64 + l;
-    const uint64_t msk = __ballot(sel_on(sel, n, lanes, lane, t));
+    const uint64_t msk = gmask[gi];
     const int rank = gpre[gi] + __popcll(msk & below);  // selected tokens before t
     if ((msk >> l) & 1ull) {
       const int sg = seg_of(cu, nseq, t);
@@ -230,7 +246,7 @@ __global__ __launch_bounds__(kSmallThreads) void compact_small(const uint8_t* __
     if (gi >= G) {
       v = sq;
     } else {
-      const uint64_t msk = __ballot(sel_on(sel, n, lanes, lane, (int64_t)gi * 64 + l));
+      const uint64_t msk = gmask[gi];
       const int r = (int)(key & 63);
       v = gpre[gi] + __popcll(r == 0 ? 0ull : (msk & (~0ull >> (64 - r))));
     }
