@@ -40,10 +40,12 @@ __global__ __launch_bounds__(64 * NW) LOGO_OCC_FWD void sq_fwd_pipe_kernel(const
   constexpr int NY = 4 * DT;   // PV MFMAs per tile (DT column blocks x 4 key steps)
   constexpr int IY = 32 / NY;  // mask / max items per Y slot
   // The 32 P items of a tile (per lane) are spread evenly over the X slots and
-  // the first three quarters of Y: PV runs key-step major (Y slot y: key step
-  // y / DT, column block y % DT), so pb[k] is first read at Y slot DT k, and
-  // the softmax work is split between both phases instead of crowding X.
-  constexpr int NPS = NX + 3 * DT;  // slots that carry P items
+  // the first three quarters of Y (the 8-wave form: the first half, measured
+  // 0.8% faster there; its 4-wave form would spill): PV runs key-step major
+  // (Y slot y: key step y / DT, column block y % DT), so pb[k] is first read at
+  // Y slot DT k, and the softmax work is split between both phases instead of
+  // crowding X.
+  constexpr int NPS = NX + (NW == 8 ? 2 : 3) * DT;  // slots that carry P items
   constexpr auto pslot = [](int it) constexpr { return it * NPS / 32; };
   static_assert(pslot(7) < NX && pslot(15) < NX + DT && pslot(23) < NX + 2 * DT && pslot(31) < NX + 3 * DT,
                 "each group of eight P items is packed before its PV MFMAs");
