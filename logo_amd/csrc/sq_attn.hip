@@ -49,9 +49,10 @@ namespace logo {
 // accumulators from lse and delta.
 // ---------------------------------------------------------------------------
 // Each thread takes one 16-byte chunk of kDeltaRows rows (RPB apart), all its
-// loads issued before any arithmetic, so a workgroup keeps 4x the bytes in
-// flight of a row-per-thread layout.
-constexpr int kDeltaRows = 4;
+// loads issued before any arithmetic, so a workgroup keeps 2x the bytes in
+// flight of a row-per-thread layout (2 rows: 31 us at the T = 32K, r = 0.25
+// workload; 4 rows 33 us, 8 rows 35 us, as fewer workgroups share the rows).
+constexpr int kDeltaRows = 2;
 
 template <typename EL, int D, bool SPARSE>
 __global__ __launch_bounds__(256) void sq_delta_kernel(const AttnArgs a) {
