@@ -106,6 +106,21 @@ def markov_mask(n, ratio, mean_run, gen):
     return out
 
 
+def headline_inputs(T, H, D, ratio, seed):
+    """The timed step's synthetic input on the host: the selection (Markov
+    spans, mean run 8, token 0 selected), then q, k, v ~ N(0, 1) * 0.5 and
+    dO ~ N(0, 1) in bf16, [T, H, D], all from one generator seeded ``seed``."""
+    gen = torch.Generator()
+    gen.manual_seed(seed)
+    sel_np = markov_mask(T, ratio, 8, gen)
+    sel_np[0] = True
+    q = (torch.randn(T, H, D, generator=gen) * 0.5).to(torch.bfloat16)
+    k = (torch.randn(T, H, D, generator=gen) * 0.5).to(torch.bfloat16)
+    v = (torch.randn(T, H, D, generator=gen) * 0.5).to(torch.bfloat16)
+    do = torch.randn(T, H, D, generator=gen).to(torch.bfloat16)
+    return q, k, v, do, sel_np
+
+
 class EventTimer:
     """Launch hook: HIP events on the current stream around each operator call
     that launches a kernel (its output allocation and fills included)."""
@@ -518,14 +533,7 @@ def main():
         print(json.dumps(swa_cfg4_measurement(q, k, v, do, iters=20)), flush=True)
         return
     T, H, D = args.seq_len, args.heads, args.head_dim
-    gen = torch.Generator()
-    gen.manual_seed(args.seed)
-    sel_np = markov_mask(T, args.ratio, 8, gen)
-    sel_np[0] = True
-    q = (torch.randn(T, H, D, generator=gen) * 0.5).to(torch.bfloat16)
-    k = (torch.randn(T, H, D, generator=gen) * 0.5).to(torch.bfloat16)
-    v = (torch.randn(T, H, D, generator=gen) * 0.5).to(torch.bfloat16)
-    do = torch.randn(T, H, D, generator=gen).to(torch.bfloat16)
+    q, k, v, do, sel_np = headline_inputs(T, H, D, args.ratio, args.seed)
     pos = np.flatnonzero(sel_np)
     pairs_per_head = float((pos + 1).sum())  # single sequence: p = token index
     f_fwd = 4.0 * D * H * pairs_per_head

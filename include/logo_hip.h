@@ -77,8 +77,10 @@ int logo_compact(const uint8_t* selection, int64_t n_tokens, int lanes,
  * fixed device array of LOGO_COMPACT_SCRATCH_INTS int32 (256 KB, held by each
  * GPU the library runs on until the process ends), so lanes *
  * ceil(n_tokens / 4096) must not exceed it (LOGO_EINVAL otherwise, e.g. up to
- * 16.7M tokens with 16 lanes).  Every call on one GPU shares that array:
- * calls that overlap on one GPU (different streams, or threads) race.
+ * 16.7M tokens with 16 lanes).  Every call on one GPU shares that array, so
+ * only one call per GPU may be in flight at a time: calls that overlap on
+ * one GPU (different streams, or threads) race and corrupt each other's
+ * q_idx.  Calls queued on one stream run in order and do not overlap.
  * Outputs and their meaning are those of logo_compact.
  */
 #define LOGO_COMPACT_SCRATCH_INTS 65536

@@ -66,7 +66,8 @@ def build_torch_shim(verbose: bool = False) -> str:
     cmd += ["-I", "/opt/rocm/include", TORCH_SHIM_SRC]
     for lib_dir in library_paths():
         cmd += ["-L", lib_dir]
-    cmd += ["-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_hip", "-L", HERE, "-llogo_hip",
+    cmd += ["-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_hip", "-L", "/opt/rocm/lib", "-lamdhip64",
+            "-L", HERE, "-llogo_hip",
             "-Wl,-rpath,$ORIGIN", "-o", TORCH_SHIM + ".tmp"]
     if verbose:
         print(" ".join(cmd), flush=True)

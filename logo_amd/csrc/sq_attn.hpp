@@ -106,6 +106,31 @@ inline void split_setup(AttnArgs& a, int wgs_per_cu, size_t floats) {
 // agent-scope atomics (sc1: through to the coherent level, no L2 flush or
 // invalidate), and the stores are complete (vmcnt(0)) before the counter
 // increment that publishes them.
+//
+// Why this is ordered on gfx950 without release / acquire fences (an
+// agent-scope release or acquire compiles to a write-back or invalidate of
+// the whole XCD L2 here, which is what the sc1 accesses avoid):
+//  1. Each partial store is an agent-scope atomic store, so it writes
+//     through the XCD's L2 to the memory-side coherence point.  On gfx9
+//     parts vmcnt counts stores as well as loads, and a store is counted
+//     until the coherence point acknowledges it: after wait_stores()
+//     (s_waitcnt vmcnt(0)) this wave's partials are visible to any
+//     agent-scope load.
+//  2. __syncthreads() after that wait means every wave of the piece has
+//     completed its stores before thread 0 issues the counter add, and the
+//     add is itself an agent-scope atomic performed at the coherence point.
+//     So when a piece's add returns npieces - 1, every other piece's
+//     partials were complete before their adds.
+//  3. The last piece's loads of the partials cannot issue early: they are
+//     control-dependent on the add's returned value, which reaches the
+//     other waves only through the LDS flag after a second __syncthreads();
+//     and they are agent-scope atomic loads, which read at the coherence
+//     point rather than from a possibly stale L2 line.
+// What the compiler must keep: the "memory" clobber of wait_stores() and the
+// barriers (both stop it from moving the stores below, or the loads above,
+// these points), and the agent scope on every store and load of `part`.
+// Plain loads or stores of the partials, or loads moved above the flag
+// test, would break the exchange silently.
 __device__ __forceinline__ void st_agent(float* p, float v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }

@@ -24,10 +24,13 @@
 #include <c10/hip/HIPStream.h>
 #include <torch/library.h>
 
+#include <hip/hip_runtime_api.h>
+
+#include <algorithm>
 #include <cstdlib>
-#include <map>
 #include <mutex>
 #include <utility>
+#include <vector>
 
 #include "../../include/logo_hip.h"
 
@@ -94,22 +97,50 @@ int check_attn(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v) {
 }
 
 // Split workspace of the fwd / dq kernels for this shape (empty: no split).
-// One buffer per (device, stream), kept across calls and grown on demand:
-// the kernels leave its counter prefix zero, so only a new buffer needs the
-// zero-fill, and calls on one stream run in order, so they never overlap on
-// it.  The environment variable LOGO_SQ_SPLIT=0 turns the split off (A/B
-// timing, and tests that compare kernel variants bit for bit).
+// Its size depends only on the device's CU count, HQ and D (the pieces a
+// split aims for fill the device twice, whatever N is): at most 136 MB at
+// D = 128 on MI355X.
+//  * Outside graph capture: one buffer per (device, stream), kept across
+//    calls and grown on demand.  The kernels leave its counter prefix zero,
+//    so only a new buffer needs the zero fill, and calls on one stream run in
+//    order, so they never overlap on it.  At most kMaxCachedStreams buffers
+//    are kept; beyond that the oldest entry is dropped (its memory returns to
+//    the caching allocator on its own stream, after the work queued there).
+//  * Under capture (hipStreamIsCapturing): a fresh buffer per call from the
+//    caching allocator, its counters cleared by a fill kernel recorded in the
+//    graph.  The graph's memory pool keeps the buffer for the graph's
+//    lifetime, so a later eager call that regrows the cached buffer cannot
+//    free memory a replay still uses, and a replay never depends on counters
+//    that eager calls left behind.
+// The environment variable LOGO_SQ_SPLIT=0 turns the split off (A/B timing,
+// and tests that compare kernel variants bit for bit).
+constexpr size_t kMaxCachedStreams = 16;
+
 at::Tensor split_workspace(const at::Tensor& q, const at::Tensor& cu) {
   const char* env = std::getenv("LOGO_SQ_SPLIT");
   const bool off = env != nullptr && env[0] == '0';
   const size_t bytes =
       off ? 0 : logo_sq_workspace_bytes(q.size(0), (int)cu.numel() - 1, (int)q.size(1), (int)q.size(2));
   if (bytes == 0) return at::empty({0}, q.options().dtype(at::kByte));
+  hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+  TORCH_CHECK(hipStreamIsCapturing(static_cast<hipStream_t>(sp()), &status) == hipSuccess,
+              "logo_hip: hipStreamIsCapturing failed");
+  if (status != hipStreamCaptureStatusNone) {
+    auto ws = at::empty({(int64_t)bytes}, q.options().dtype(at::kByte));
+    ws.narrow(0, 0, (int64_t)logo_sq_workspace_counter_bytes()).zero_();
+    return ws;
+  }
   static std::mutex mu;
-  static std::map<std::pair<int, void*>, at::Tensor> cache;
+  static std::vector<std::pair<std::pair<int, void*>, at::Tensor>> cache;  // oldest first
   const auto key = std::make_pair((int)q.get_device(), sp());
   std::lock_guard<std::mutex> lock(mu);
-  at::Tensor& ws = cache[key];
+  auto it = std::find_if(cache.begin(), cache.end(), [&](const auto& e) { return e.first == key; });
+  if (it == cache.end()) {
+    if (cache.size() >= kMaxCachedStreams) cache.erase(cache.begin());
+    cache.emplace_back(key, at::Tensor());
+    it = cache.end() - 1;
+  }
+  at::Tensor& ws = it->second;
   if (!ws.defined() || (size_t)ws.numel() < bytes) {
     ws = at::empty({(int64_t)bytes}, q.options().dtype(at::kByte));
     ws.narrow(0, 0, (int64_t)logo_sq_workspace_counter_bytes()).zero_();

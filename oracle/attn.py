@@ -155,10 +155,6 @@ def swa_fwd(q, k, v, cu_seqlens, window=128, scale=None, dtype=np.float64):
     return sq_attn_fwd(q, k, v, None, cu_seqlens, scale=scale, window=window, dtype=dtype)
 
 
-def swa_bwd(q, k, v, o, do, cu_seqlens, window=128, scale=None, dtype=np.float64):
-    return sq_attn_bwd(q, k, v, o, do, None, cu_seqlens, scale=scale, window=window, dtype=dtype)
-
-
 def sq_flops_fwd(selection, cu_seqlens, n_heads, head_dim):
     """Algorithmic forward FLOPs counted on selected rows only.
 

@@ -1,3 +1,4 @@
+import json
 import os
 import sys
 
@@ -22,3 +23,27 @@ def gpu():
     assert torch.cuda.is_available(), "GPU tests need a ROCm GPU"
     _lib.lib()
     return torch.device("cuda", 0)
+
+
+@pytest.fixture(autouse=True)
+def _margin_test_id(request):
+    """Names the running test in the parity-margin records of tests/helpers.py."""
+    from tests import helpers
+
+    helpers.CURRENT_TEST["id"] = request.node.nodeid
+    yield
+    helpers.CURRENT_TEST["id"] = None
+
+
+def pytest_sessionfinish(session, exitstatus):
+    """With LOGO_PARITY_LOG set, append every recorded comparison (max-abs and
+    mean-abs error against its bound) to that file as JSON lines."""
+    path = os.environ.get("LOGO_PARITY_LOG")
+    if not path:
+        return
+    from tests import helpers
+
+    os.makedirs(os.path.dirname(os.path.abspath(path)), exist_ok=True)
+    with open(path, "a") as f:
+        for rec in helpers.MARGINS:
+            f.write(json.dumps(rec) + "\n")

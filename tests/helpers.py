@@ -1,11 +1,20 @@
-"""Shared test inputs, tolerances and a chunked torch fp32 attention reference.
+"""Shared test inputs, tolerances and chunked torch fp32 references.
 
 Inputs follow the benchmark configurations of BASELINE.json (seeded
-``torch.Generator``).  ``torch_sq_attn`` is a plain-PyTorch fp32 restatement of
-the same semantics as ``oracle.attn`` used where the numpy oracle would be too
-slow (full-size cases on the GPU); it is itself pinned against the oracle on
-the CPU in tests/test_oracle_attn.py.
+``torch.Generator``).  ``torch_sq_attn`` and ``torch_decode_attn`` are
+plain-PyTorch fp32 restatements of the same semantics as ``oracle.attn`` and
+``oracle.decode``, used where the numpy oracle would be too slow (full-size
+cases on the GPU); they are themselves pinned against the oracle on the CPU
+(tests/test_oracle_attn.py, tests/test_oracle_decode.py).
+
+Every comparison made through ``assert_within`` or ``record`` is kept in
+``MARGINS`` (test, tensor, max-abs and mean-abs error, the bounds); with the
+environment variable ``LOGO_PARITY_LOG`` set, tests/conftest.py writes them as
+JSON lines to that file when the session ends (tests/parity_margins.py renders
+the table).
 """
+
+import os
 
 import numpy as np
 import torch
@@ -16,13 +25,31 @@ MAX_ABS = 2e-2
 MEAN_ABS = 2e-3
 
 
+MARGINS = []
+CURRENT_TEST = {"id": None}
+
+
+def record(name, max_err, mean_err, max_bound, mean_bound, kind="abs"):
+    """Keep one comparison's errors and bounds for the parity-margin log."""
+    MARGINS.append({"test": CURRENT_TEST["id"], "tensor": name, "kind": kind, "max": float(max_err),
+                    "mean": float(mean_err), "max_bound": max_bound, "mean_bound": mean_bound})
+
+
 def err_stats(x, ref):
-    d = (x.detach().double().cpu() - torch.as_tensor(ref).double().cpu()).abs()
+    """max-abs and mean-abs of x - ref, in float64 on x's device (no host copy
+    of full-size tensors)."""
+    x = x.detach()
+    ref = torch.as_tensor(ref)
+    dev = x.device if x.is_cuda else ref.device
+    d = (x.to(dev).double() - ref.to(dev).double()).abs()
     return d.max().item(), d.mean().item()
 
 
 def assert_within(name, x, ref, max_abs=MAX_ABS, mean_abs=MEAN_ABS):
     mx, mn = err_stats(x, ref)
+    record(name, mx, mn, max_abs, mean_abs)
+    if os.environ.get("LOGO_PARITY_VERBOSE"):
+        print(f"  {name}: max-abs {mx:.3e} mean-abs {mn:.3e}", flush=True)
     assert mx <= max_abs and mn <= mean_abs, f"{name}: max-abs {mx:.3e} (<= {max_abs}), mean-abs {mn:.3e} (<= {mean_abs})"
     return mx, mn
 
@@ -122,3 +149,24 @@ def torch_sq_attn(q, k, v, sel_rows, cu, scale=None, window=None, do=None, row_c
     if grads:
         return o, (dq, dk, dv)
     return o
+
+
+def torch_decode_attn(q, k, v, lens, active=None, scale=None):
+    """fp32 decode attention on the tensors' device: ``q [B, HQ, D]``,
+    ``k/v [B, H, T, D]`` (row b valid on ``[0, lens[b])``); inactive rows are
+    zero (the semantics of oracle.decode.decode_attn)."""
+    B, HQ, D = q.shape
+    G = HQ // k.shape[1]
+    if scale is None:
+        scale = D ** -0.5
+    out = torch.zeros(B, HQ, v.shape[3], dtype=torch.float32, device=q.device)
+    for b in range(B):
+        if active is not None and not bool(active[b]):
+            continue
+        n = int(lens[b])
+        K = k[b, :, :n].float().repeat_interleave(G, 0).contiguous()  # [HQ, n, D]
+        V = v[b, :, :n].float().repeat_interleave(G, 0).contiguous()
+        s = torch.bmm(K, q[b].float()[:, :, None].contiguous())[..., 0] * scale
+        p = torch.softmax(s, -1)
+        out[b] = torch.bmm(p[:, None, :].contiguous(), V)[:, 0]
+    return out

@@ -74,3 +74,48 @@ def test_sq_full_attn_under_torch_compile(gpu):
     want = f(q, k, v)
     got = torch.compile(f)(q, k, v)
     assert torch.equal(got, want)
+
+
+def test_split_workspace_under_graph_capture(gpu):
+    """sq_fwd and sq_bwd_dq on a shape whose key ranges split, captured in a
+    HIP graph and replayed, with eager calls of the same ops (which use the
+    per-stream cached workspace) before, between and after the replays: every
+    replay and every eager call gives the first eager call's results bit for
+    bit.  Under capture the operator takes a fresh workspace from the graph's
+    pool with its counters cleared by a recorded fill kernel, so neither side
+    depends on the other's buffer or counters."""
+    ops = _torch_ops.ops()
+    g = gen(45)
+    n, hq, h, d = 16384, 4, 4, 128
+    q, k, v, do = (randn((n, x, d), g, 0.5).to(gpu) for x in (hq, h, h, hq))
+    sel = (torch.rand(n, generator=g) < 0.03).to(gpu)
+    sel[0] = True
+    cu = torch.tensor([0, n], dtype=torch.int32, device=gpu)
+    dsel = compact_selection(sel, cu)
+    fwd_args = (q, k, v, dsel.q_idx, dsel.pos, dsel.meta, cu, 1, d ** -0.5, -1)
+    o_ref, lse_ref = ops.sq_fwd(*fwd_args)
+    bwd_args = (q, k, v, o_ref, lse_ref, do, dsel.q_idx, dsel.pos, dsel.meta, cu, 1, d ** -0.5, -1)
+    ws = ops.sq_bwd_delta(*bwd_args)
+    dq_ref = ops.sq_bwd_dq(*bwd_args, *ws)
+    torch.cuda.synchronize()
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):  # warm-up on the capture stream (cached workspace)
+        ops.sq_fwd(*fwd_args)
+        ops.sq_bwd_dq(*bwd_args, *ws)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        o_c, lse_c = ops.sq_fwd(*fwd_args)
+        dq_c = ops.sq_bwd_dq(*bwd_args, *ws)
+    for rep in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(o_c, o_ref) and torch.equal(lse_c, lse_ref), f"forward replay {rep}"
+        assert torch.equal(dq_c, dq_ref), f"dq replay {rep}"
+        o_e, lse_e = ops.sq_fwd(*fwd_args)
+        dq_e = ops.sq_bwd_dq(*bwd_args, *ws)
+        torch.cuda.synchronize()
+        assert torch.equal(o_e, o_ref) and torch.equal(dq_e, dq_ref), f"eager call after replay {rep}"

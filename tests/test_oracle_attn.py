@@ -175,6 +175,27 @@ def test_flops_formula_closed_form():
     assert f == 4 * D * H * T * (T + 1) // 2
 
 
+def test_flops_formula_per_head_and_segments_brute_force():
+    """Per-head selection [N, HQ] over packed segments: each head counts its
+    own rows' visible keys (position within the segment + 1), by brute force
+    over every (row, key) pair; a shared [N] mask is every head counting the
+    same rows."""
+    rng = np.random.default_rng(9)
+    cu = [0, 13, 13, 40, 61]
+    N, HQ, D = 61, 3, 16
+    sel = rng.random((N, HQ)) < 0.4
+    want = 0
+    for s in range(len(cu) - 1):
+        for hq in range(HQ):
+            for t in range(cu[s], cu[s + 1]):
+                if sel[t, hq]:
+                    want += sum(1 for key in range(cu[s], cu[s + 1]) if key <= t)
+    assert attn.sq_flops_fwd(sel, cu, HQ, D) == 4 * D * want
+    shared = sel[:, 0]
+    want1 = sum(t - cu[s] + 1 for s in range(len(cu) - 1) for t in range(cu[s], cu[s + 1]) if shared[t])
+    assert attn.sq_flops_fwd(shared, cu, HQ, D) == 4 * D * HQ * want1
+
+
 @pytest.mark.parametrize("K,V", [(8, 5), (6, 12)])
 def test_value_dim_differs_from_key_dim(K, V):
     """V != K (the reference's V is its own constexpr, selected_full_attn.py:341):

@@ -6,8 +6,6 @@ second must not see).  Also: a size above the fixed scratch is refused with
 LOGO_EINVAL before any launch.
 """
 
-import ctypes
-
 import numpy as np
 import pytest
 import torch
@@ -18,6 +16,7 @@ from oracle import compact as oc
 pytestmark = pytest.mark.gpu
 
 SENTINEL = -7
+LOGO_COMPACT_SCRATCH_INTS = 65536  # include/logo_hip.h
 
 
 def _outputs(n, lanes, nseq, dev):
@@ -81,9 +80,18 @@ def test_noalloc_matches_compact_twice_second_smaller(gpu):
 
 
 def test_noalloc_refuses_more_than_its_scratch(gpu):
+    """One token in 65537 lanes needs 65537 counts, one more than the scratch
+    holds.  Every buffer is real and sized for that call, so a regression of
+    the guard would launch on valid memory rather than fault."""
     lib = _lib.lib()
-    p = ctypes.c_void_p(1)
-    n = 65536 * 4096 // 16 + 1  # 16 lanes x 4097 chunks of 4096 tokens > 65536 counts
-    rc = lib.logo_compact_noalloc(p, n, 16, p, 1, p, p, p, None)
+    n, lanes = 1, LOGO_COMPACT_SCRATCH_INTS + 1
+    sel = torch.ones(n, lanes, dtype=torch.uint8, device=gpu)
+    cu = torch.tensor([0, n], dtype=torch.int32, device=gpu)
+    q_idx = torch.zeros(lanes, n, dtype=torch.int64, device=gpu)
+    pos = torch.zeros(lanes, n, dtype=torch.int32, device=gpu)
+    meta = torch.zeros(lanes * _lib.meta_stride(1), dtype=torch.int32, device=gpu)
+    rc = lib.logo_compact_noalloc(_lib.ptr(sel), n, lanes, _lib.ptr(cu), 1, _lib.ptr(q_idx), _lib.ptr(pos),
+                                  _lib.ptr(meta), _lib.stream_of(sel))
+    torch.cuda.synchronize()
     assert rc == 1
     assert "scratch" in lib.logo_last_error().decode()
