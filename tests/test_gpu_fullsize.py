@@ -176,8 +176,11 @@ def test_decode_fused_cfg5_full_size(gpu):
                             q_g, k_g, v_g, torch.tensor(lens_g, dtype=torch.int32, device=gpu), max(lens_g),
                             gate, thres, w_l, w_g, eps)
     active = (gate >= thres).cpu()
-    local = torch_decode_attn(q_l, k_l, v_l, lens_l).cpu().numpy()
-    glob = torch_decode_attn(q_g, k_g, v_g, lens_g, active).cpu().numpy()
+    # each branch's attention output is stored in bf16 before the epilogue,
+    # as the reference's branches return it (flash-attn and sq_full_attn
+    # outputs in the input dtype, logo/layers/logo.py:228-249)
+    local = torch_decode_attn(q_l, k_l, v_l, lens_l).bfloat16().float().cpu().numpy()
+    glob = torch_decode_attn(q_g, k_g, v_g, lens_g, active).bfloat16().float().cpu().numpy()
     f = lambda t: t.float().cpu().numpy()  # noqa: E731
     ref = oepi.epilogue_fwd(local, glob, f(gate), float(thres.float()), f(w_l), f(w_g), eps)
     print(f"cfg5 fused decode: active={int(active.sum())}", flush=True)
