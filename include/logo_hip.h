@@ -54,7 +54,7 @@ extern "C" {
 /* Message of the calling thread's last error ("" if none). */
 const char* logo_last_error(void);
 
-/* ABI version of this library. */
+/* ABI version of this library (5: head dim 256, fp32, logo_sq_generic). */
 int logo_abi_version(void);
 
 /* Bytes of workspace logo_compact needs. */
@@ -124,14 +124,16 @@ int logo_q_start_blk(const int32_t* pos, const int32_t* cu_q, const int32_t* chu
  * and lse per compacted row.  q_idx/pos == NULL selects dense mode (every row, meta from
  * logo_dense_meta).  window < 0: full causal; window >= 0: keys
  * [p - window, p] (logo/layers/utils.py:144-147).
- * d is the head dim of q and k (64 or 128); v_dim is that of v and o, which
- * the reference keeps separate (V, :341) and which must equal d here: every
- * kernel strides all of them by d.  The Python op zero-pads other K, V <= 128
- * to 64 or 128 before it calls this.
- * dtype: LOGO_DTYPE_BF16, or LOGO_DTYPE_F16 in sparse mode without a window
- * (the reference's dots run in the input dtype, :80 :108); every 16-bit
- * tensor of the call (q, k, v, o, and for the backward dout, q_sel, do_sel,
- * dq, dk, dv) holds that type.
+ * d is the head dim of q and k (64, 128 or 256); v_dim is that of v and o,
+ * which the reference keeps separate (V, :341) and which must equal d here:
+ * every kernel strides all of them by d.  The Python op zero-pads other
+ * K, V <= 256 to 64, 128 or 256 before it calls this (the reference takes
+ * K <= 256 in one block, :344).
+ * dtype: LOGO_DTYPE_BF16; LOGO_DTYPE_F16 or LOGO_DTYPE_F32 in sparse mode
+ * without a window (the reference's dots run in the input dtype, :80 :93-99
+ * :108).  Every element tensor of the call (q, k, v, o, and for the backward
+ * dout, q_sel, do_sel, dq, dk, dv) holds that type.  d = 256 and fp32 run on
+ * generic kernels (logo_sq_generic); the others on the tuned ones.
  * workspace / workspace_bytes (may be NULL / 0): device memory that lets the
  * forward and dq kernels (no window) cut the key range of each query tile
  * into pieces when a head has few tiles, so that a grid which would fill the
@@ -154,6 +156,15 @@ int logo_sq_fwd(const void* q, const void* k, const void* v, void* o, float* lse
  */
 size_t logo_sq_workspace_bytes(int64_t n_tokens, int nseq, int hq, int d);
 size_t logo_sq_workspace_counter_bytes(void);
+
+/*
+ * 1 when calls with head dim d and element type dtype run on the generic
+ * attention kernels (d = 256, or LOGO_DTYPE_F32), 0 for the tuned ones (no
+ * counterpart in the reference, whose Triton kernels take every size).  The
+ * generic kernels take no split workspace, and their sparse backward reads q
+ * and dout in place: q_sel and do_sel may be NULL.
+ */
+int logo_sq_generic(int d, int dtype);
 
 /*
  * Backward (logo/ops/selected_full_attn.py:124-138 delta, :141-228 dq,

@@ -55,7 +55,8 @@ def _register_fakes():
 
     @fake("logo_hip::sq_bwd_delta")
     def _(q, k, v, o, lse, dout, q_idx, pos, meta, cu, lanes, scale, window):
-        sel = (q.shape[1], q.shape[0], q.shape[2]) if q_idx is not None else (0,)
+        copies = q_idx is not None and not generic_kernels(q.shape[2], q.dtype)
+        sel = (q.shape[1], q.shape[0], q.shape[2]) if copies else (0,)
         return q.new_empty((q.shape[1], q.shape[0]), dtype=torch.float32), q.new_empty(sel), q.new_empty(sel)
 
     @fake("logo_hip::sq_bwd_dq")
@@ -86,6 +87,13 @@ def _register_fakes():
     @fake("logo_hip::decode_attn")
     def _(q, k_cache, v_cache, lens, gate, thres, max_len, scale):
         return torch.empty_like(q)
+
+
+def generic_kernels(d: int, dtype: torch.dtype) -> bool:
+    """Whether head dim ``d`` and element type ``dtype`` run on the library's
+    generic attention kernels (``logo_sq_generic``: d = 256 or fp32)."""
+    code = {torch.float16: _lib.DTYPE_F16, torch.float32: _lib.DTYPE_F32}.get(dtype, _lib.DTYPE_BF16)
+    return bool(_lib.lib().logo_sq_generic(int(d), code))
 
 
 def timed(name: str, fn, *args):

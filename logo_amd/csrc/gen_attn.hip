@@ -1,0 +1,648 @@
+// Generic query-sparse / dense causal attention, forward and backward, for
+// the calls the tuned kernels do not cover:
+//   * head dims in (128, 256] (run at D = 256, K and V zero-padded by the
+//     caller): the reference takes any K <= 256 in one block
+//     (logo/ops/selected_full_attn.py:344, logo/ops/common.py:127-168);
+//   * fp32 q, k, v on the query-sparse path, computed in fp32 throughout:
+//     the reference's dots run in the input dtype, P kept in fp32 for PV
+//     (logo/ops/selected_full_attn.py:93-99) and the output in v's dtype
+//     (:349).
+// Semantics are those of the tuned kernels (sq_fwd.hip, sq_dq.hip,
+// sq_dkv.hip): selected (compacted) rows attend causally within their packed
+// segment, optionally within a sliding window (keys [p - w, p]); the
+// backward recomputes P from the log2-domain lse with delta = rowsum(o * dO)
+// (:124-138); dk / dv of a GQA group are summed over its query heads
+// (:444-445); rows of unselected tokens are zero in o and dq.
+//
+// Unlike the tuned kernels these compute the scores the reference's way:
+// S = q.k accumulated in fp32 from the unscaled inputs, then scaled by
+// scale * log2(e) in fp32 (:93); P and dS are rounded to the input type
+// before their products (:99, :206-207), which for fp32 means no rounding.
+//
+// Structure (simple, one LDS buffer, no software pipelining):
+//   16x16 MFMA tiles with a 16-deep k step for every element type:
+//   v_mfma_f32_16x16x16_bf16 / _f16 (one per k step) and
+//   v_mfma_f32_16x16x4_f32 (four per k step).  Lane l = 16 G + i holds
+//   elements 4G .. 4G+3 of the k step for row / column i of an operand, and
+//   accumulator items j = 0..3 of row 4G + j, column i, so an accumulator
+//   read row-major is directly the B operand of the next product (its rows
+//   are the k index).
+//   fwd, dq : 4 waves x 16 compacted rows = 64 rows per workgroup (half of a
+//             128-row tile of the compaction's tile list); q (and dO) in
+//             registers; 32-key K / V tiles through LDS; S^T = K Q^T, so each
+//             lane's query is its column i and row statistics reduce over
+//             the four lanes i, i+16, i+32, i+48.
+//   dk/dv   : 4 waves x 16 keys = 64 keys per workgroup (half of a 128-key
+//             tile); K, V and the dK^T / dV^T accumulators in registers; the
+//             query heads of the GQA group looped inside; 16-row steps of
+//             q, dO, lse, delta and positions through LDS.
+// Tiles in LDS are row-major with 16-byte chunks XOR-swizzled by row, so the
+// row reads of 16 consecutive rows fall in distinct banks.
+#include "sq_attn.hpp"
+
+namespace logo {
+namespace gen {
+
+// ---------------------------------------------------------------------------
+// MFMA per element type: 16x16 output, 16-deep k step, 4 elements per lane
+// ---------------------------------------------------------------------------
+template <typename T>
+struct Mma;
+template <>
+struct Mma<bf16> {
+  using Op = bf16x4;
+  __device__ __forceinline__ static f32x4 mma(Op a, Op b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+  }
+};
+template <>
+struct Mma<f16> {
+  using Op = f16x4;
+  __device__ __forceinline__ static f32x4 mma(Op a, Op b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+  }
+};
+template <>
+struct Mma<float> {
+  using Op = f32x4;
+  // k slot G of MFMA s is element s of lane group G: k = 4 G + s, the same
+  // k as the 16-bit forms' element s of lane group G.
+  __device__ __forceinline__ static f32x4 mma(Op a, Op b, f32x4 c) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s], b[s], c, 0, 0, 0);
+    return c;
+  }
+};
+
+// Four accumulator values as an operand of type T (the reference's
+// `.to(q.dtype)` before a product; exact for fp32).
+template <typename T>
+__device__ __forceinline__ typename Mma<T>::Op to_op(const f32x4 v) {
+  typename Mma<T>::Op r;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) r[e] = (T)v[e];
+  return r;
+}
+
+// ---------------------------------------------------------------------------
+// LDS tiles: rows of D elements of T, 16-byte chunks XOR-swizzled by row
+// ---------------------------------------------------------------------------
+template <typename T, int D>
+struct GTile {
+  static constexpr int RB = D * (int)sizeof(T);  // bytes per row (>= 128)
+  static constexpr int CH = RB / 16;             // 16-byte chunks per row
+  static constexpr int SW = CH < 16 ? CH - 1 : 15;
+  __device__ __forceinline__ static int off(int r, int ch) { return r * RB + 16 * (ch ^ (r & SW)); }
+  // byte offset of element (r, c); four elements from c = 4m stay in one chunk
+  __device__ __forceinline__ static int eoff(int r, int c) {
+    const int b = c * (int)sizeof(T);
+    return off(r, b >> 4) + (b & 15);
+  }
+  // Row operand: lane (i, G) gets elements 16 ks + 4 G .. + 3 of row r.
+  __device__ __forceinline__ static typename Mma<T>::Op row(const char* t, int r, int ks, int G) {
+    return *reinterpret_cast<const typename Mma<T>::Op*>(t + eoff(r, 16 * ks + 4 * G));
+  }
+  // Transposed operand: lane (i, G) gets column c of rows rb + 4 G .. + 3.
+  __device__ __forceinline__ static typename Mma<T>::Op tr(const char* t, int rb, int c, int G) {
+    typename Mma<T>::Op v;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = *reinterpret_cast<const T*>(t + eoff(rb + 4 * G + e, c));
+    return v;
+  }
+  // Rows [0, R) by NT threads; rowptr(r) is a valid row for every r.
+  template <int R, int NT, typename F>
+  __device__ __forceinline__ static void load(char* t, F rowptr) {
+#pragma unroll
+    for (int k = 0; k < (R * CH + NT - 1) / NT; ++k) {
+      const int c = threadIdx.x + NT * k;
+      if (R * CH % NT == 0 || c < R * CH) {
+        const int r = c / CH, ch = c % CH;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(rowptr(r)) + 16 * ch);
+        *reinterpret_cast<u32x4*>(t + off(r, ch)) = v;
+      }
+    }
+  }
+};
+
+// Sum / max over the four lanes of a query column (i, i+16, i+32, i+48).
+__device__ __forceinline__ float col_sum(float x) {
+  x += __shfl_xor(x, 16);
+  return x + __shfl_xor(x, 32);
+}
+__device__ __forceinline__ float col_max(float x) {
+  x = fmaxf(x, __shfl_xor(x, 16));
+  return fmaxf(x, __shfl_xor(x, 32));
+}
+
+constexpr int kRowsWG = 64;  // compacted rows per fwd / dq workgroup (half a kBQ tile)
+constexpr int kKT = 32;      // keys per K / V tile (fwd, dq)
+constexpr int kKeysWG = 64;  // keys per dk/dv workgroup (half a kBKV tile)
+constexpr int kQS = 16;      // query rows per dk/dv step
+
+// The rows of a fwd / dq workgroup: half (sub) of a kBQ-row tile of the
+// compaction's tile list.  qt describes the whole tile for the zero-row
+// helpers shared with the tuned kernels (rank: the workgroup's rank in its
+// head's grid; trank / ntile: the tile's).
+template <bool SPARSE>
+struct GenRows {
+  QTile<SPARSE> qt;
+  int r0, r_end, sub;
+
+  __device__ __forceinline__ bool init(const AttnArgs& a) {
+    int rank, hq;
+    xcd_remap(blockIdx.x, a.hq, rank, hq);
+    qt.rank = rank;
+    qt.hq = hq;
+    qt.lane_sel = a.lanes > 1 ? hq : 0;
+    const int32_t* meta = a.meta + (int64_t)qt.lane_sel * a.meta_stride;
+    const int nt = meta[1];
+    const int32_t* cu_q = meta + kMetaHdr;
+    const int32_t* cu_tq = cu_q + (a.nseq + 1);
+    qt.q_end = cu_q[a.nseq];
+    qt.ntile = nt;
+    qt.trank = rank >> 1;
+    sub = rank & 1;
+    if (qt.trank >= nt) return false;
+    const int tile = nt - 1 - qt.trank;  // latest (heaviest) tiles first
+    qt.s = seg_of(cu_tq, a.nseq, tile);
+    qt.r0 = cu_q[qt.s] + (tile - cu_tq[qt.s]) * kBQ;
+    qt.r_end = min(qt.r0 + kBQ, cu_q[qt.s + 1]);
+    qt.bos = a.cu[qt.s];
+    qt.seqlen = a.cu[qt.s + 1] - qt.bos;
+    qt.h = hq / a.g;
+    qt.rv = row_view<SPARSE>(a, qt.lane_sel, qt.bos);
+    r0 = qt.r0 + kRowsWG * sub;
+    r_end = min(r0 + kRowsWG, qt.r_end);
+    return true;
+  }
+};
+
+// Zero rows of unselected tokens (sparse mode), by the first half of each
+// tile, and the whole-lane slices of a lane without rows.  Rows are DB
+// bf16-sized units long (D * sizeof(T) / 2).
+template <typename T, int D, bool SPARSE>
+__device__ __forceinline__ void gen_zero(const AttnArgs& a, void* out, float* lse, const GenRows<SPARSE>& gr,
+                                         bool have_rows) {
+  if constexpr (SPARSE) {
+    constexpr int DB = D * (int)sizeof(T) / 2;
+    bf16* o = static_cast<bf16*>(out);
+    if (!have_rows) zero_empty_lane<DB>(a, o, lse, gr.qt, 256);
+    else if (gr.sub == 0) zero_unselected<DB>(a, o, lse, gr.qt, 256);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Forward
+// ---------------------------------------------------------------------------
+template <typename T, int D, bool SPARSE>
+__global__ __launch_bounds__(256) void gen_fwd_kernel(const AttnArgs a) {
+  using M = Mma<T>;
+  using Op = typename M::Op;
+  using TL = GTile<T, D>;
+  constexpr int KS = D / 16;  // k steps over the head dim; also 16-column blocks of O
+  char* const tK = logo_smem;
+  char* const tV = logo_smem + kKT * TL::RB;
+  const T* q = reinterpret_cast<const T*>(a.q);
+  const T* k = reinterpret_cast<const T*>(a.k);
+  const T* v = reinterpret_cast<const T*>(a.v);
+  T* o = reinterpret_cast<T*>(a.o);
+
+  GenRows<SPARSE> gr;
+  if (!gr.init(a)) {
+    gen_zero<T, D, SPARSE>(a, a.o, a.lse, gr, false);
+    return;
+  }
+  gen_zero<T, D, SPARSE>(a, a.o, a.lse, gr, true);
+  if (gr.r0 >= gr.r_end) return;  // the second half of a short tile
+  const QTile<SPARSE>& qt = gr.qt;
+  const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63, i = l & 15, G = l >> 4;
+  const int hq = qt.hq, h = qt.h, W = a.window;
+  const bool win = W >= 0;
+  const int rw0 = gr.r0 + 16 * wave;
+  const bool wave_active = rw0 < gr.r_end;
+  const int r = rw0 + i;
+  const bool valid = r < gr.r_end;
+  const int64_t t = valid ? qt.rv.token(r) : 0;
+  const int p = valid ? qt.rv.posn(r) : -1;
+  const int pw_lo = wave_active ? qt.rv.posn(rw0) : 0;
+  const int pw_hi = wave_active ? qt.rv.posn(min(rw0 + 15, gr.r_end - 1)) : -1;
+  const int kv_lo = win ? (max(0, qt.rv.posn(gr.r0) - W) & ~(kKT - 1)) : 0;
+  const int kv_hi = qt.rv.posn(gr.r_end - 1) + 1;
+  const float c = a.scale_log2;
+
+  Op qreg[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks)
+    qreg[ks] = valid ? *reinterpret_cast<const Op*>(q + (t * a.hq + hq) * D + 16 * ks + 4 * G) : Op{};
+  f32x4 oacc[KS];
+#pragma unroll
+  for (int dt = 0; dt < KS; ++dt) oacc[dt] = f32x4{};
+  float m_run = -INFINITY, l_run = 0.f;
+
+  const int last_key = qt.seqlen - 1;
+  for (int kt = kv_lo; kt < kv_hi; kt += kKT) {
+    __syncthreads();  // the previous tile's readers are done
+    TL::template load<kKT, 256>(tK, [&](int rr) {
+      return k + ((int64_t)(qt.bos + min(kt + rr, last_key)) * a.h + h) * D;
+    });
+    TL::template load<kKT, 256>(tV, [&](int rr) {
+      return v + ((int64_t)(qt.bos + min(kt + rr, last_key)) * a.h + h) * D;
+    });
+    __syncthreads();
+    if (!wave_active || kt > pw_hi || (win && kt + kKT - 1 < pw_lo - W)) continue;
+    f32x4 sacc[kKT / 16];
+#pragma unroll
+    for (int kb = 0; kb < kKT / 16; ++kb) {
+      sacc[kb] = f32x4{};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) sacc[kb] = M::mma(TL::row(tK, 16 * kb + i, ks, G), qreg[ks], sacc[kb]);
+    }
+    // scores in the log2 domain; item j of block kb is key kt + 16 kb + 4 G + j
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < kKT / 16; ++kb)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int key = kt + 16 * kb + 4 * G + j;
+        const bool vis = key <= p && (!win || key >= p - W);
+        sacc[kb][j] = vis ? sacc[kb][j] * c : -INFINITY;
+        mx = fmaxf(mx, sacc[kb][j]);
+      }
+    mx = col_max(mx);
+    const float m_new = fmaxf(m_run, mx);
+    // A query with no visible key so far keeps m = -inf: its P, O and l stay
+    // zero through base 0 (arithmetic, no branch: the MFMAs below run on
+    // every lane of the wave).
+    const float base = m_new == -INFINITY ? 0.f : m_new;
+    const float alpha = exp2f(m_run - base);
+    float ls = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < kKT / 16; ++kb)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        sacc[kb][j] = exp2f(sacc[kb][j] - base);
+        ls += sacc[kb][j];
+      }
+    l_run = l_run * alpha + col_sum(ls);
+    m_run = m_new;
+#pragma unroll
+    for (int dt = 0; dt < KS; ++dt) oacc[dt] *= alpha;
+#pragma unroll
+    for (int kb = 0; kb < kKT / 16; ++kb) {
+      const Op pb = to_op<T>(sacc[kb]);
+#pragma unroll
+      for (int dt = 0; dt < KS; ++dt) oacc[dt] = M::mma(TL::tr(tV, 16 * kb, 16 * dt + i, G), pb, oacc[dt]);
+    }
+  }
+  if (!valid) return;
+  const float inv = 1.f / l_run;
+  if (G == 0) a.lse[(int64_t)hq * a.n + r] = m_run + log2f(l_run);
+  T* orow = o + (t * a.hq + hq) * D + 4 * G;
+#pragma unroll
+  for (int dt = 0; dt < KS; ++dt) {
+    Op ov;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) ov[j] = (T)(oacc[dt][j] * inv);
+    *reinterpret_cast<Op*>(orow + 16 * dt) = ov;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// delta = rowsum(o * dO) per compacted row, fp32 (:124-138)
+// ---------------------------------------------------------------------------
+template <typename T, int D, bool SPARSE>
+__global__ __launch_bounds__(256) void gen_delta_kernel(const AttnArgs a) {
+  const int hq = blockIdx.y;
+  const int lane_sel = a.lanes > 1 ? hq : 0;
+  const int32_t* meta = a.meta + (int64_t)lane_sel * a.meta_stride;
+  const int sq = meta[0];
+  const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int l = threadIdx.x & 63;
+  if (r >= sq) return;
+  const int64_t t = SPARSE ? a.q_idx[(int64_t)lane_sel * a.n + r] : (int64_t)r;
+  const T* o = reinterpret_cast<const T*>(a.o) + (t * a.hq + hq) * D;
+  const T* dout = reinterpret_cast<const T*>(a.dout) + (t * a.hq + hq) * D;
+  float acc = 0.f;
+#pragma unroll
+  for (int e = l; e < D; e += 64) acc = fmaf((float)o[e], (float)dout[e], acc);
+#pragma unroll
+  for (int s = 32; s > 0; s >>= 1) acc += __shfl_xor(acc, s);
+  if (l == 0) a.delta[(int64_t)hq * a.n + r] = acc;
+}
+
+// ---------------------------------------------------------------------------
+// dq: dS^T = P^T (dP^T - delta), dQ^T += K^T dS^T (:141-228)
+// ---------------------------------------------------------------------------
+template <typename T, int D, bool SPARSE>
+__global__ __launch_bounds__(256) void gen_dq_kernel(const AttnArgs a) {
+  using M = Mma<T>;
+  using Op = typename M::Op;
+  using TL = GTile<T, D>;
+  constexpr int KS = D / 16;
+  char* const tK = logo_smem;
+  char* const tV = logo_smem + kKT * TL::RB;
+  const T* q = reinterpret_cast<const T*>(a.q);
+  const T* k = reinterpret_cast<const T*>(a.k);
+  const T* v = reinterpret_cast<const T*>(a.v);
+  const T* dout = reinterpret_cast<const T*>(a.dout);
+  T* dq = reinterpret_cast<T*>(a.dq);
+
+  GenRows<SPARSE> gr;
+  if (!gr.init(a)) {
+    gen_zero<T, D, SPARSE>(a, a.dq, nullptr, gr, false);
+    return;
+  }
+  gen_zero<T, D, SPARSE>(a, a.dq, nullptr, gr, true);
+  if (gr.r0 >= gr.r_end) return;
+  const QTile<SPARSE>& qt = gr.qt;
+  const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63, i = l & 15, G = l >> 4;
+  const int hq = qt.hq, h = qt.h, W = a.window;
+  const bool win = W >= 0;
+  const int rw0 = gr.r0 + 16 * wave;
+  const bool wave_active = rw0 < gr.r_end;
+  const int r = rw0 + i;
+  const bool valid = r < gr.r_end;
+  const int64_t t = valid ? qt.rv.token(r) : 0;
+  const int p = valid ? qt.rv.posn(r) : -1;
+  const int pw_lo = wave_active ? qt.rv.posn(rw0) : 0;
+  const int pw_hi = wave_active ? qt.rv.posn(min(rw0 + 15, gr.r_end - 1)) : -1;
+  const int kv_lo = win ? (max(0, qt.rv.posn(gr.r0) - W) & ~(kKT - 1)) : 0;
+  const int kv_hi = qt.rv.posn(gr.r_end - 1) + 1;
+  const float c = a.scale_log2;
+  const float lse = valid ? a.lse[(int64_t)hq * a.n + r] : 0.f;
+  const float dlt = valid ? a.delta[(int64_t)hq * a.n + r] : 0.f;
+
+  Op qreg[KS], dreg[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    const int64_t off = (t * a.hq + hq) * D + 16 * ks + 4 * G;
+    qreg[ks] = valid ? *reinterpret_cast<const Op*>(q + off) : Op{};
+    dreg[ks] = valid ? *reinterpret_cast<const Op*>(dout + off) : Op{};
+  }
+  f32x4 dqacc[KS];
+#pragma unroll
+  for (int dt = 0; dt < KS; ++dt) dqacc[dt] = f32x4{};
+
+  const int last_key = qt.seqlen - 1;
+  for (int kt = kv_lo; kt < kv_hi; kt += kKT) {
+    __syncthreads();
+    TL::template load<kKT, 256>(tK, [&](int rr) {
+      return k + ((int64_t)(qt.bos + min(kt + rr, last_key)) * a.h + h) * D;
+    });
+    TL::template load<kKT, 256>(tV, [&](int rr) {
+      return v + ((int64_t)(qt.bos + min(kt + rr, last_key)) * a.h + h) * D;
+    });
+    __syncthreads();
+    if (!wave_active || kt > pw_hi || (win && kt + kKT - 1 < pw_lo - W)) continue;
+#pragma unroll
+    for (int kb = 0; kb < kKT / 16; ++kb) {
+      f32x4 s = f32x4{}, dp = f32x4{};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        s = M::mma(TL::row(tK, 16 * kb + i, ks, G), qreg[ks], s);
+        dp = M::mma(TL::row(tV, 16 * kb + i, ks, G), dreg[ks], dp);
+      }
+      f32x4 ds;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int key = kt + 16 * kb + 4 * G + j;
+        const bool vis = key <= p && (!win || key >= p - W);
+        const float pr = vis ? exp2f(s[j] * c - lse) : 0.f;
+        ds[j] = pr * (dp[j] - dlt);
+      }
+      const Op db = to_op<T>(ds);
+#pragma unroll
+      for (int dt = 0; dt < KS; ++dt) dqacc[dt] = M::mma(TL::tr(tK, 16 * kb, 16 * dt + i, G), db, dqacc[dt]);
+    }
+  }
+  if (!valid) return;
+  T* drow = dq + (t * a.hq + hq) * D + 4 * G;
+#pragma unroll
+  for (int dt = 0; dt < KS; ++dt) {
+    Op dv;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) dv[j] = (T)(dqacc[dt][j] * a.scale);
+    *reinterpret_cast<Op*>(drow + 16 * dt) = dv;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dk / dv: S = Q K^T, P, dP = dO V^T, dS; dV^T += dO^T P, dK^T += Q^T dS,
+// summed over the query heads of the GQA group (:231-337, :444-445)
+// ---------------------------------------------------------------------------
+template <typename T, int D>
+constexpr size_t gen_dkv_smem() {
+  return (size_t)2 * kQS * GTile<T, D>::RB + 3 * kQS * sizeof(float);
+}
+
+template <typename T, int D, bool SPARSE>
+__global__ __launch_bounds__(256) void gen_dkv_kernel(const AttnArgs a) {
+  using M = Mma<T>;
+  using Op = typename M::Op;
+  using TL = GTile<T, D>;
+  constexpr int KS = D / 16;
+  char* const tQ = logo_smem;
+  char* const tO = logo_smem + kQS * TL::RB;
+  float* const sLse = reinterpret_cast<float*>(logo_smem + 2 * kQS * TL::RB);
+  float* const sDelta = sLse + kQS;
+  int* const sPos = reinterpret_cast<int*>(sDelta + kQS);
+  const T* q = reinterpret_cast<const T*>(a.q);
+  const T* k = reinterpret_cast<const T*>(a.k);
+  const T* v = reinterpret_cast<const T*>(a.v);
+  const T* dout = reinterpret_cast<const T*>(a.dout);
+
+  int rank, h;
+  xcd_remap(blockIdx.x, a.h, rank, h);
+  const int32_t* meta0 = a.meta;
+  const int ntk = meta0[2];
+  const int tile = rank >> 1, sub = rank & 1;
+  if (tile >= ntk) return;
+  const int32_t* cu_tk = meta0 + kMetaHdr + 2 * (a.nseq + 1);
+  const int s = seg_of(cu_tk, a.nseq, tile);
+  const int bos = a.cu[s];
+  const int seqlen = a.cu[s + 1] - bos;
+  const int k0 = (tile - cu_tk[s]) * kBKV + kKeysWG * sub;
+  if (k0 >= seqlen) return;
+  const int k_last = min(k0 + kKeysWG, seqlen) - 1;
+
+  const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63, i = l & 15, G = l >> 4;
+  const int key = k0 + 16 * wave + i;
+  const bool valid_k = key < seqlen;
+  const int W = a.window;
+  const bool win = W >= 0;
+  const float c = a.scale_log2;
+
+  Op kreg[KS], vreg[KS];
+  {
+    const int64_t off = ((int64_t)(bos + key) * a.h + h) * D + 4 * G;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      kreg[ks] = valid_k ? *reinterpret_cast<const Op*>(k + off + 16 * ks) : Op{};
+      vreg[ks] = valid_k ? *reinterpret_cast<const Op*>(v + off + 16 * ks) : Op{};
+    }
+  }
+  f32x4 dkacc[KS], dvacc[KS];
+#pragma unroll
+  for (int dt = 0; dt < KS; ++dt) {
+    dkacc[dt] = f32x4{};
+    dvacc[dt] = f32x4{};
+  }
+
+  for (int gg = 0; gg < a.g; ++gg) {
+    const int hq = h * a.g + gg;
+    const int lane_sel = a.lanes > 1 ? hq : 0;
+    const int32_t* cu_q = a.meta + (int64_t)lane_sel * a.meta_stride + kMetaHdr;
+    const RowView<SPARSE> rv = row_view<SPARSE>(a, lane_sel, bos);
+    const int q_lo = cu_q[s], q_hi = cu_q[s + 1];
+    // rows ascend by position within the segment (dense rows: position = row - bos)
+    auto lb_pos = [&](int lo, int hi, int x) {
+      return SPARSE ? wave_lower_bound(rv.ps, lo, hi, x) : min(max(q_lo + x, lo), hi);
+    };
+    const int rq0 = lb_pos(q_lo, q_hi, k0);
+    const int rq_end = win ? lb_pos(rq0, q_hi, k_last + W + 1) : q_hi;
+    const float* lse_h = a.lse + (int64_t)hq * a.n;
+    const float* delta_h = a.delta + (int64_t)hq * a.n;
+    for (int rs = rq0; rs < rq_end; rs += kQS) {
+      __syncthreads();  // the previous step's readers are done
+      const int last = rq_end - 1;
+      TL::template load<kQS, 256>(tQ, [&](int rr) { return q + (rv.token(min(rs + rr, last)) * a.hq + hq) * D; });
+      TL::template load<kQS, 256>(tO, [&](int rr) {
+        return dout + (rv.token(min(rs + rr, last)) * a.hq + hq) * D;
+      });
+      if (tid < kQS) {
+        const int rr = rs + tid;
+        const int rc = min(rr, last);
+        sLse[tid] = lse_h[rc];
+        sDelta[tid] = delta_h[rc];
+        sPos[tid] = rr < rq_end ? rv.posn(rr) : -1;  // rows past the end see no key
+      }
+      __syncthreads();
+      if (16 * wave + k0 > k_last) continue;  // this wave's keys are past the segment
+      f32x4 sacc = f32x4{}, dpacc = f32x4{};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        sacc = M::mma(TL::row(tQ, i, ks, G), kreg[ks], sacc);
+        dpacc = M::mma(TL::row(tO, i, ks, G), vreg[ks], dpacc);
+      }
+      // item j: query row rs + 4 G + j, key `key`
+      f32x4 pr, ds;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int rj = 4 * G + j;
+        const int pq = sPos[rj];
+        const bool vis = valid_k && key <= pq && (!win || key >= pq - W);
+        pr[j] = vis ? exp2f(sacc[j] * c - sLse[rj]) : 0.f;
+        ds[j] = pr[j] * (dpacc[j] - sDelta[rj]);
+      }
+      const Op pb = to_op<T>(pr), db = to_op<T>(ds);
+#pragma unroll
+      for (int dt = 0; dt < KS; ++dt) {
+        dvacc[dt] = M::mma(TL::tr(tO, 0, 16 * dt + i, G), pb, dvacc[dt]);
+        dkacc[dt] = M::mma(TL::tr(tQ, 0, 16 * dt + i, G), db, dkacc[dt]);
+      }
+    }
+  }
+  if (!valid_k) return;
+  // lane (i, G) holds columns 16 dt + 4 G .. + 3 of key `key`
+  const int64_t off = ((int64_t)(bos + key) * a.h + h) * D + 4 * G;
+  T* dk = reinterpret_cast<T*>(a.dk) + off;
+  T* dv = reinterpret_cast<T*>(a.dv) + off;
+#pragma unroll
+  for (int dt = 0; dt < KS; ++dt) {
+    Op kv, vv;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      kv[j] = (T)(dkacc[dt][j] * a.scale);
+      vv[j] = (T)dvacc[dt][j];
+    }
+    *reinterpret_cast<Op*>(dk + 16 * dt) = kv;
+    *reinterpret_cast<Op*>(dv + 16 * dt) = vv;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Launchers
+// ---------------------------------------------------------------------------
+template <typename T, int D>
+constexpr size_t gen_kv_smem() { return (size_t)2 * kKT * GTile<T, D>::RB; }
+
+// fwd / dq grid: two workgroups per 128-row tile (worst case over the lanes),
+// per query head.
+inline int64_t gen_row_grid(const AttnArgs& a) { return 2 * ((a.n + kBQ - 1) / kBQ + a.nseq) * a.hq; }
+
+template <typename T, int D, bool SPARSE>
+int launch_fwd(const AttnArgs& a, hipStream_t st) {
+  const int64_t nblk = gen_row_grid(a);
+  LOGO_REQUIRE(nblk < ((int64_t)1 << 31), "grid too large");
+  auto kern = gen_fwd_kernel<T, D, SPARSE>;
+  const size_t smem = gen_kv_smem<T, D>();
+  LOGO_HIP_CHECK(allow_smem(kern, smem));
+  hipLaunchKernelGGL(kern, dim3((unsigned)nblk), dim3(256), smem, st, a);
+  LOGO_LAUNCH_CHECK("gen_fwd_kernel");
+  return LOGO_OK;
+}
+
+template <typename T, int D, bool SPARSE>
+int launch_delta(const AttnArgs& a, hipStream_t st) {
+  dim3 grid((unsigned)((a.n + 3) / 4), a.hq);
+  hipLaunchKernelGGL((gen_delta_kernel<T, D, SPARSE>), grid, dim3(256), 0, st, a);
+  LOGO_LAUNCH_CHECK("gen_delta_kernel");
+  return LOGO_OK;
+}
+
+template <typename T, int D, bool SPARSE>
+int launch_dq(const AttnArgs& a, hipStream_t st) {
+  const int64_t nblk = gen_row_grid(a);
+  LOGO_REQUIRE(nblk < ((int64_t)1 << 31), "grid too large");
+  auto kern = gen_dq_kernel<T, D, SPARSE>;
+  const size_t smem = gen_kv_smem<T, D>();
+  LOGO_HIP_CHECK(allow_smem(kern, smem));
+  hipLaunchKernelGGL(kern, dim3((unsigned)nblk), dim3(256), smem, st, a);
+  LOGO_LAUNCH_CHECK("gen_dq_kernel");
+  return LOGO_OK;
+}
+
+template <typename T, int D, bool SPARSE>
+int launch_dkv(const AttnArgs& a, hipStream_t st) {
+  // two workgroups per 128-key tile (worst case), per kv head
+  const int64_t nblk = 2 * ((a.n + kBKV - 1) / kBKV + a.nseq) * a.h;
+  LOGO_REQUIRE(nblk < ((int64_t)1 << 31), "grid too large");
+  auto kern = gen_dkv_kernel<T, D, SPARSE>;
+  const size_t smem = gen_dkv_smem<T, D>();
+  LOGO_HIP_CHECK(allow_smem(kern, smem));
+  hipLaunchKernelGGL(kern, dim3((unsigned)nblk), dim3(256), smem, st, a);
+  LOGO_LAUNCH_CHECK("gen_dkv_kernel");
+  return LOGO_OK;
+}
+
+// The instantiations that exist: sparse bf16 / fp16 at D = 256, sparse fp32
+// at D = 64, 128, 256, dense (with or without a window) bf16 at D = 256.
+#define LOGO_GEN_DISPATCH(FN, a, st, d, dtype, sparse)                                                  \
+  do {                                                                                                  \
+    if (dtype == LOGO_DTYPE_F32 && sparse)                                                              \
+      return d == 64 ? FN<float, 64, true>(a, st) : d == 128 ? FN<float, 128, true>(a, st)              \
+                                                             : FN<float, 256, true>(a, st);             \
+    if (d == 256 && dtype == LOGO_DTYPE_F16 && sparse) return FN<f16, 256, true>(a, st);               \
+    if (d == 256 && dtype == LOGO_DTYPE_BF16) return sparse ? FN<bf16, 256, true>(a, st)                \
+                                                            : FN<bf16, 256, false>(a, st);              \
+    LOGO_REQUIRE(false, "no generic attention kernel for d=%d dtype=%d sparse=%d", d, dtype, (int)sparse); \
+  } while (0)
+
+}  // namespace gen
+
+bool gen_applies(int d, int dtype) { return d == 256 || dtype == LOGO_DTYPE_F32; }
+
+int gen_launch_fwd(const AttnArgs& a, hipStream_t st, int d, int dtype, bool sparse) {
+  LOGO_GEN_DISPATCH(gen::launch_fwd, a, st, d, dtype, sparse);
+}
+int gen_launch_delta(const AttnArgs& a, hipStream_t st, int d, int dtype, bool sparse) {
+  LOGO_GEN_DISPATCH(gen::launch_delta, a, st, d, dtype, sparse);
+}
+int gen_launch_dq(const AttnArgs& a, hipStream_t st, int d, int dtype, bool sparse) {
+  LOGO_GEN_DISPATCH(gen::launch_dq, a, st, d, dtype, sparse);
+}
+int gen_launch_dkv(const AttnArgs& a, hipStream_t st, int d, int dtype, bool sparse) {
+  LOGO_GEN_DISPATCH(gen::launch_dkv, a, st, d, dtype, sparse);
+}
+
+}  // namespace logo

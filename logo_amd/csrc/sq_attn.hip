@@ -138,14 +138,15 @@ static int check_common(int64_t n, int nseq, int hq, int h, int d, int v_dim, in
   LOGO_REQUIRE(n > 0 && n < ((int64_t)1 << 31), "n_tokens out of range: %lld", (long long)n);
   LOGO_REQUIRE(nseq >= 1, "nseq must be >= 1");
   LOGO_REQUIRE(h >= 1 && hq >= h && hq % h == 0, "HQ (%d) must be a multiple of H (%d)", hq, h);
-  LOGO_REQUIRE(d == 64 || d == 128, "head dim %d unsupported (64 or 128)", d);
+  LOGO_REQUIRE(d == 64 || d == 128 || d == 256, "head dim %d unsupported (64, 128 or 256)", d);
   // every kernel strides q, k, v, o and the gradients by the one head dim d
   LOGO_REQUIRE(v_dim == d, "value head dim %d must equal the key head dim %d", v_dim, d);
   LOGO_REQUIRE(lanes == 1 || lanes == hq, "lanes must be 1 or HQ");
-  LOGO_REQUIRE(dtype == LOGO_DTYPE_BF16 || dtype == LOGO_DTYPE_F16, "dtype %d unsupported (bf16 or fp16)", dtype);
-  // fp16 kernels exist for the query-sparse global branch (no window)
+  LOGO_REQUIRE(dtype == LOGO_DTYPE_BF16 || dtype == LOGO_DTYPE_F16 || dtype == LOGO_DTYPE_F32,
+               "dtype %d unsupported (bf16, fp16 or fp32)", dtype);
+  // fp16 and fp32 kernels exist for the query-sparse global branch (no window)
   LOGO_REQUIRE(dtype == LOGO_DTYPE_BF16 || (sparse && window < 0),
-               "fp16 is supported on the query-sparse path without a window only");
+               "fp16 and fp32 are supported on the query-sparse path without a window only");
   return LOGO_OK;
 }
 
@@ -205,8 +206,11 @@ extern "C" int logo_sq_fwd(const void* q, const void* k, const void* v, void* o,
   a.ws_bytes = workspace ? workspace_bytes : 0;
   const bool sparse = q_idx != nullptr;
   const bool win = window >= 0;
+  if (gen_applies(d, dtype)) return gen_launch_fwd(a, as_stream(stream), d, dtype, sparse);
   return sq_launch_fwd(a, as_stream(stream), d, sparse, win, dtype == LOGO_DTYPE_F16);
 }
+
+extern "C" int logo_sq_generic(int d, int dtype) { return gen_applies(d, dtype) ? 1 : 0; }
 
 #define LOGO_BWD_PARAMS                                                                        \
   const void *q, const void *k, const void *v, const void *o, const void *dout, const float *lse, \
@@ -227,7 +231,9 @@ static int bwd_entry(LOGO_BWD_PARAMS, int phase) {
   LOGO_REQUIRE((phase == 0 || phase == 2 || dq) && (phase == 0 || phase == 1 || (dk && dv)),
                "null gradient pointer");
   LOGO_REQUIRE((q_idx == nullptr) == (pos == nullptr), "q_idx and pos must both be set or both be null");
-  LOGO_REQUIRE(q_idx == nullptr || (q_sel && do_sel), "sparse backward needs q_sel and do_sel workspaces");
+  const bool generic = gen_applies(d, dtype);
+  LOGO_REQUIRE(q_idx == nullptr || generic || (q_sel && do_sel),
+               "sparse backward needs q_sel and do_sel workspaces");
   AttnArgs a = make_args(q, k, v, q_idx, pos, meta, cu, n_tokens, nseq, hq, h, lanes, scale, window);
   a.o = const_cast<bf16*>(static_cast<const bf16*>(o));
   a.dout = static_cast<const bf16*>(dout);
@@ -244,6 +250,18 @@ static int bwd_entry(LOGO_BWD_PARAMS, int phase) {
   const bool win = window >= 0;
   const bool half = dtype == LOGO_DTYPE_F16;
   hipStream_t st = as_stream(stream);
+  if (generic) {  // the generic kernels read q and dO in place (no compacted copies)
+    if (phase < 0 || phase == 0) {
+      rc = gen_launch_delta(a, st, d, dtype, sparse);
+      if (rc != LOGO_OK) return rc;
+    }
+    if (phase < 0 || phase == 1 || phase == 3) {
+      rc = gen_launch_dq(a, st, d, dtype, sparse);
+      if (rc != LOGO_OK) return rc;
+    }
+    if (phase < 0 || phase == 2 || phase == 3) rc = gen_launch_dkv(a, st, d, dtype, sparse);
+    return rc;
+  }
   if (phase < 0 || phase == 0) {
     rc = sq_launch_delta(a, st, d, sparse, half);
     if (rc != LOGO_OK) return rc;

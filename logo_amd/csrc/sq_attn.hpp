@@ -404,6 +404,16 @@ int swa_launch_fwd(const AttnArgs& a, hipStream_t st, int d);
 bool swa_bwd_applies(const AttnArgs& a, bool sparse, bool half);
 int swa_launch_bwd(const AttnArgs& a, hipStream_t st, int d);
 
+// The generic kernels (gen_attn.hip): head dim 256 (bf16, and fp16 in sparse
+// mode) and fp32 in sparse mode (d = 64, 128, 256).  gen_applies: whether a
+// call with head dim d and element type dtype runs on them (the entry points
+// route such calls there before any tuned kernel).
+bool gen_applies(int d, int dtype);
+int gen_launch_fwd(const AttnArgs& a, hipStream_t st, int d, int dtype, bool sparse);
+int gen_launch_delta(const AttnArgs& a, hipStream_t st, int d, int dtype, bool sparse);
+int gen_launch_dq(const AttnArgs& a, hipStream_t st, int d, int dtype, bool sparse);
+int gen_launch_dkv(const AttnArgs& a, hipStream_t st, int d, int dtype, bool sparse);
+
 // Calls FN<D, SPARSE, WINDOW>(a, st) for the runtime (d, sparse, window).
 #define LOGO_DISPATCH(FN, a, st, d, sparse, window)                                                  \
   ((d) == 128 ? ((sparse) ? ((window) ? FN<128, true, true>(a, st) : FN<128, true, false>(a, st))   \

@@ -23,31 +23,39 @@ _custom_fwd = functools.partial(torch.amp.custom_fwd, device_type="cuda")
 _custom_bwd = functools.partial(torch.amp.custom_bwd, device_type="cuda")
 
 
-# Head dims the gfx950 kernels are compiled for.  A call with other K, V <= 128
-# (V != K included, as the reference allows: its V is a separate constexpr,
-# logo/ops/selected_full_attn.py:341-351) runs on the next compiled dim with
-# q, k and v zero-padded: zero columns add nothing to q.k, and they give zero
-# output and gradient columns, which are sliced off.
-KERNEL_HEAD_DIMS = (64, 128)
+# Head dims the gfx950 kernels are compiled for: 64 and 128 on the tuned
+# kernels, 256 on the generic ones.  A call with other K, V <= 256 (V != K
+# included, as the reference allows: its V is a separate constexpr and K fits
+# one block of <= 256, logo/ops/selected_full_attn.py:341-351, :344) runs on
+# the next compiled dim with q, k and v zero-padded: zero columns add nothing
+# to q.k, and they give zero output and gradient columns, which are sliced off.
+KERNEL_HEAD_DIMS = (64, 128, 256)
 
 
 def kernel_head_dim(K: int, V: int) -> int:
     """The compiled head dim a call with key dim K and value dim V runs on."""
     assert K <= 256, "K must fit in a single block (<=256)"
-    assert 0 < K <= 128 and 0 < V <= 128, "the gfx950 kernels take head dims K, V in [1, 128]"
-    return 64 if max(K, V) <= 64 else 128
+    assert 0 < K and 0 < V <= 256, "the gfx950 kernels take head dims K, V in [1, 256]"
+    m = max(K, V)
+    return 64 if m <= 64 else 128 if m <= 128 else 256
 
 
 def kernel_dtype(q, k, v, sparse: bool, window: int) -> torch.dtype:
     """The element type a call computes in (fp32 accumulation either way).
 
     The reference's Triton dots run in the input dtype
-    (logo/ops/selected_full_attn.py:80, :95-99, :108).  fp16 q, k, v on the
-    query-sparse path (no window) run on the fp16 kernels; everything else
-    runs in bf16, so fp32 or mixed inputs and the dense / sliding-window
-    branches round to bf16 (the outputs are cast back to q's dtype)."""
-    half = sparse and window < 0 and q.dtype == k.dtype == v.dtype == torch.float16
-    return torch.float16 if half else torch.bfloat16
+    (logo/ops/selected_full_attn.py:80, :93-99, :108).  On the query-sparse
+    path (no window): fp32 inputs (any of q, k, v) run on the fp32 kernels,
+    all three in fp32 (the others are widened, exactly), and fp16 q, k, v on
+    the fp16 kernels.  Everything else runs in bf16: bf16 inputs, mixed 16-bit
+    inputs, and the dense / sliding-window branches (the reference's flash-attn
+    branches take 16-bit inputs only); outputs are cast back to v's dtype."""
+    if sparse and window < 0:
+        if torch.float32 in (q.dtype, k.dtype, v.dtype):
+            return torch.float32
+        if q.dtype == k.dtype == v.dtype == torch.float16:
+            return torch.float16
+    return torch.bfloat16
 
 
 def _to_kernel(t: torch.Tensor, d: int, dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
@@ -104,7 +112,8 @@ class SQFullAttentionFunction(torch.autograd.Function):
         out = o.view(B, T, HQ, d)
         if V != d:
             out = out[..., :V].contiguous()
-        return out if q.dtype == kt else out.to(q.dtype)
+        # the output has v's dtype (logo/ops/selected_full_attn.py:349)
+        return out if v.dtype == kt else out.to(v.dtype)
 
     @staticmethod
     @_custom_bwd

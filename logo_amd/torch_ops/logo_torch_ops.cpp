@@ -83,18 +83,23 @@ at::Tensor dense_meta(const at::Tensor& cu, int64_t n_tokens) {
   return meta;
 }
 
-// q, k, v of one 16-bit type (bf16, or fp16 for the C library's query-sparse
-// kernels, which rejects other fp16 calls itself); returns its dtype code.
+// q, k, v of one element type (bf16; fp16 or fp32 for the C library's
+// query-sparse kernels, which rejects other fp16 / fp32 calls itself);
+// returns its dtype code.
 int check_attn(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v) {
-  const at::ScalarType dt = q.scalar_type() == at::kHalf ? at::kHalf : at::kBFloat16;
+  const at::ScalarType qt = q.scalar_type();
+  const at::ScalarType dt = qt == at::kHalf || qt == at::kFloat ? qt : at::kBFloat16;
   need(q, "q", dt);
   need(k, "k", dt);
   need(v, "v", dt);
   TORCH_CHECK(q.dim() == 3 && k.dim() == 3 && v.dim() == 3, "logo_hip: q, k, v must be [N, heads, D]");
   TORCH_CHECK(k.size(0) == q.size(0) && v.sizes() == k.sizes() && k.size(2) == q.size(2),
               "logo_hip: q [N, HQ, D], k and v [N, H, D] must agree");
-  return dt == at::kHalf ? LOGO_DTYPE_F16 : LOGO_DTYPE_BF16;
+  return dt == at::kHalf ? LOGO_DTYPE_F16 : dt == at::kFloat ? LOGO_DTYPE_F32 : LOGO_DTYPE_BF16;
 }
+
+// Whether the call runs on the generic kernels (no compacted copies, no split).
+bool generic_path(const at::Tensor& q, int dtype) { return logo_sq_generic((int)q.size(2), dtype) != 0; }
 
 // Split workspace of the fwd / dq kernels for this shape (empty: no split).
 // Its size depends only on the device's CU count, HQ and D (the pieces a
@@ -116,9 +121,9 @@ int check_attn(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v) {
 // and tests that compare kernel variants bit for bit).
 constexpr size_t kMaxCachedStreams = 16;
 
-at::Tensor split_workspace(const at::Tensor& q, const at::Tensor& cu) {
+at::Tensor split_workspace(const at::Tensor& q, const at::Tensor& cu, int dtype) {
   const char* env = std::getenv("LOGO_SQ_SPLIT");
-  const bool off = env != nullptr && env[0] == '0';
+  const bool off = (env != nullptr && env[0] == '0') || generic_path(q, dtype);
   const size_t bytes =
       off ? 0 : logo_sq_workspace_bytes(q.size(0), (int)cu.numel() - 1, (int)q.size(1), (int)q.size(2));
   if (bytes == 0) return at::empty({0}, q.options().dtype(at::kByte));
@@ -158,7 +163,7 @@ std::tuple<at::Tensor, at::Tensor> sq_fwd(const at::Tensor& q, const at::Tensor&
   // tokens and for lse rows past each lane's rows, by the kernel).
   auto o = at::empty_like(q);
   auto lse = at::empty({hq, n}, q.options().dtype(at::kFloat));
-  auto ws = window < 0 ? split_workspace(q, cu) : at::empty({0}, q.options().dtype(at::kByte));
+  auto ws = window < 0 ? split_workspace(q, cu, dtype) : at::empty({0}, q.options().dtype(at::kByte));
   ok(logo_sq_fwd(cptr(q), cptr(k), cptr(v), mptr(o), lse.data_ptr<float>(), opt_ptr<int64_t>(q_idx),
                  opt_ptr<int32_t>(pos), meta.data_ptr<int32_t>(), cu.data_ptr<int32_t>(), n, (int)cu.numel() - 1,
                  (int)hq, (int)h, (int)d, (int)v.size(2), (int)lanes, (float)scale, (int)window, dtype,
@@ -184,7 +189,7 @@ struct Bwd {
     if (phase > 0) {
       need(*delta, "delta", at::kFloat);
       TORCH_CHECK(delta->numel() == q.size(0) * q.size(1), "logo_hip: delta must be [HQ, N]");
-      if (q_idx.has_value()) {
+      if (q_idx.has_value() && !generic_path(q, dtype)) {
         need(*q_sel, "q_sel", q.scalar_type());
         need(*do_sel, "do_sel", q.scalar_type());
         TORCH_CHECK(q_sel->numel() == q.numel() && do_sel->numel() == q.numel(),
@@ -195,7 +200,7 @@ struct Bwd {
     F fn = phase == 0 ? &logo_sq_bwd_delta : phase == 1 ? &logo_sq_bwd_dq : phase == 2 ? &logo_sq_bwd_dkv
                                                                                   : &logo_sq_bwd_dqkv;
     auto p = [](at::Tensor* t) -> void* { return t && t->numel() ? t->data_ptr() : nullptr; };
-    at::Tensor ws = (phase == 1 || phase == 3) && window < 0 ? split_workspace(q, cu)
+    at::Tensor ws = (phase == 1 || phase == 3) && window < 0 ? split_workspace(q, cu, dtype)
                                                             : at::empty({0}, q.options().dtype(at::kByte));
     return fn(cptr(q), cptr(k), cptr(v), cptr(o), cptr(dout), lse.data_ptr<float>(),
               static_cast<float*>(p(delta)), p(q_sel), p(do_sel), p(dq), p(dk), p(dv), opt_ptr<int64_t>(q_idx),
@@ -210,12 +215,12 @@ struct Bwd {
       const at::Tensor &dout, const std::optional<at::Tensor>&q_idx, const std::optional<at::Tensor>&pos,    \
       const at::Tensor &meta, const at::Tensor &cu, int64_t lanes, double scale, int64_t window
 
-// delta [HQ, N] fp32 (rows past Sq unwritten) and, in sparse mode, the compacted
-// copies q_sel / do_sel [HQ, N, D] (empty in dense mode): workspaces of the
-// dq and dk/dv phases, whose rows past each head's Sq are left unwritten.
+// delta [HQ, N] fp32 (rows past Sq unwritten) and, in sparse mode on the tuned
+// kernels, the compacted copies q_sel / do_sel [HQ, N, D] (empty in dense mode
+// and on the generic kernels, which read q and dout in place): workspaces of
+// the dq and dk/dv phases, whose rows past each head's Sq are left unwritten.
 std::tuple<at::Tensor, at::Tensor, at::Tensor> sq_bwd_delta(LOGO_BWD_SCHEMA_ARGS) {
-  check_attn(q, k, v);
-  const bool sparse = q_idx.has_value();
+  const bool sparse = q_idx.has_value() && !generic_path(q, check_attn(q, k, v));
   auto delta = at::empty({q.size(1), q.size(0)}, q.options().dtype(at::kFloat));
   auto q_sel = sparse ? at::empty({q.size(1), q.size(0), q.size(2)}, q.options()) : at::empty({0}, q.options());
   auto do_sel = sparse ? at::empty_like(q_sel) : at::empty({0}, q.options());

@@ -22,13 +22,21 @@ def test_header_symbols_are_exported():
 
 def test_abi_version_and_workspace():
     lib = _lib.lib()
-    assert lib.logo_abi_version() == 4
+    assert lib.logo_abi_version() == 5
+    # the generic kernels serve d = 256 and fp32; they never split
+    assert [lib.logo_sq_generic(d, t) for d in (64, 128, 256) for t in (_lib.DTYPE_BF16, _lib.DTYPE_F16)] == \
+        [0, 0, 0, 0, 1, 1]
+    assert all(lib.logo_sq_generic(d, _lib.DTYPE_F32) == 1 for d in (64, 128, 256))
+    assert lib.logo_sq_workspace_bytes(32768, 1, 16, 256) == 0
     assert lib.logo_compact_workspace_bytes(4096, 1) == 4
     assert lib.logo_compact_workspace_bytes(4097, 16) == 2 * 16 * 4
 
 
 @pytest.mark.parametrize("d,v_dim,hq,h,lanes,msg", [
     (96, 96, 4, 4, 1, "head dim"),
+    (192, 192, 4, 4, 1, "head dim"),
+    (512, 512, 4, 4, 1, "head dim"),
+    (256, 128, 4, 4, 1, "value head dim"),
     (128, 128, 6, 4, 1, "multiple"),
     (128, 128, 4, 4, 2, "lanes"),
     (128, 64, 4, 4, 1, "value head dim"),
@@ -49,14 +57,15 @@ def test_fwd_bwd_reject_bad_shapes_without_touching_gpu(d, v_dim, hq, h, lanes, 
 
 
 @pytest.mark.parametrize("sparse,window,dtype,msg", [
-    (False, -1, 2, "fp16 is supported on the query-sparse path"),   # dense fp16
-    (True, 128, 2, "fp16 is supported on the query-sparse path"),   # sliding-window fp16
-    (True, -1, 1, "unsupported"),                                    # fp32 tensors
+    (False, -1, 2, "fp16 and fp32 are supported on the query-sparse path"),   # dense fp16
+    (True, 128, 2, "fp16 and fp32 are supported on the query-sparse path"),   # sliding-window fp16
+    (False, -1, 1, "fp16 and fp32 are supported on the query-sparse path"),   # dense fp32
+    (True, 64, 1, "fp16 and fp32 are supported on the query-sparse path"),    # sliding-window fp32
     (True, -1, 7, "unsupported"),
 ])
 def test_fwd_bwd_dtype_checks_without_touching_gpu(sparse, window, dtype, msg):
-    """fp16 runs on the query-sparse kernels without a window only; other
-    dtypes are refused before any HIP call."""
+    """fp16 and fp32 run on the query-sparse kernels without a window only;
+    other dtypes are refused before any HIP call."""
     lib = _lib.lib()
     p = ctypes.c_void_p(1)
     idx = p if sparse else None
@@ -116,9 +125,9 @@ class _LaunchCounter:
 
 
 @pytest.mark.parametrize("qshape,kshape,vshape,msg", [
-    ((1, 8, 2, 128), (1, 8, 2, 128), (1, 8, 2, 192), "head dims K, V"),
-    ((1, 8, 2, 192), (1, 8, 2, 192), (1, 8, 2, 64), "head dims K, V"),
+    ((1, 8, 2, 128), (1, 8, 2, 128), (1, 8, 2, 320), "head dims K, V"),
     ((1, 8, 2, 320), (1, 8, 2, 320), (1, 8, 2, 64), "single block"),
+    ((1, 8, 2, 257), (1, 8, 2, 257), (1, 8, 2, 257), "single block"),
     ((1, 8, 2, 128), (1, 8, 2, 64), (1, 8, 2, 128), "same head dim K"),
     ((1, 8, 4, 128), (1, 8, 2, 128), (1, 8, 1, 128), "same number of heads"),
     ((1, 8, 2, 128), (1, 9, 2, 128), (1, 9, 2, 128), "share"),
@@ -147,10 +156,13 @@ def test_unsupported_shapes_are_rejected_before_any_launch(qshape, kshape, vshap
 
 
 @pytest.mark.parametrize("K,V,d", [(128, 128, 128), (64, 64, 64), (96, 96, 128), (128, 64, 128),
-                                   (64, 128, 128), (48, 32, 64), (1, 1, 64)])
+                                   (64, 128, 128), (48, 32, 64), (1, 1, 64), (256, 256, 256), (192, 160, 256),
+                                   (128, 192, 256), (129, 8, 256)])
 def test_supported_head_dims_map_to_a_compiled_dim(K, V, d):
-    """K, V <= 128 (V != K included) run on the compiled dim 64 or 128; the
-    GPU parity of the padded calls is in tests/test_gpu_sq_attn.py."""
+    """K, V <= 256 (V != K included, as the reference's single K block of
+    <= 256 allows) run on the compiled dim 64, 128 or 256; the GPU parity of
+    the padded calls is in tests/test_gpu_sq_attn.py and
+    tests/test_gpu_generic.py."""
     import torch
 
     from logo_amd.ops import sq_full_attn

@@ -146,10 +146,10 @@ def test_swa_fwd_bwd_matches_oracle(gpu, window, d):
 
 
 def test_noncontiguous_and_fp32_inputs(gpu):
-    """fp32 inputs (cfg1's dtype) compute in bf16 with fp32 accumulation; the
-    result is compared with the oracle fed the *unrounded* fp32 inputs, at
-    the north-star tolerance (max-abs 2e-2, mean-abs 2e-3), for the output
-    and all three gradients."""
+    """fp32 inputs (cfg1's dtype), q a non-contiguous view: computed in fp32
+    on the generic kernels, fp32 outputs and gradients, compared with the
+    oracle fed the same fp32 inputs at the fp32 bound of
+    tests/test_gpu_generic.py (max-abs 1e-3, mean-abs 1e-4)."""
     n, hq, d = 512, 4, 64
     g = gen(9)
     base = torch.randn(n, d, hq, generator=g)
@@ -162,10 +162,8 @@ def test_noncontiguous_and_fp32_inputs(gpu):
     o, (dq, dk, dv) = _run(q, k, v, sel, cu, gpu, do)
     assert o.dtype == dq.dtype == dk.dtype == dv.dtype == torch.float32
     ro, (rdq, rdk, rdv) = _oracle(q, k, v, sel, cu, do)
-    assert_within("o", o, ro)
-    assert_within("dq", dq, rdq)
-    assert_within("dk", dk, rdk)
-    assert_within("dv", dv, rdv)
+    for name, x, r in (("o", o, ro), ("dq", dq, rdq), ("dk", dk, rdk), ("dv", dv, rdv)):
+        assert_within(name, x, r, max_abs=1e-3, mean_abs=1e-4)
 
 
 @pytest.mark.parametrize("n,hq,h,d,cu,per_head", [
