@@ -212,6 +212,43 @@ def swa_cfg4_measurement(q, k, v, do, iters=10):
             "bwd_ms": round(tsb - tsf, 4), "bwd_gbs": round(2 * io / (tsb - tsf) / 1e6, 1)}
 
 
+def generic_measurement(dev, gen):
+    """The generic kernels (head dim 256; fp32 inputs) on the query-sparse
+    path: fwd+bwd effective TFLOP/s (selected rows only, as the headline) at
+    T=8192, H=16, Markov r=0.25, for K=V=256 in bf16 and for D=128 in fp32
+    (against the fp32 MFMA peak), and config 1 (B=1, H=4, T=512, D=64, fp32,
+    Bernoulli 0.5) in ms."""
+    from logo_amd.ops import sq_full_attn
+    out = {}
+    T, H = 8192, 16
+    sel_np = markov_mask(T, 0.25, 8, gen)
+    sel_np[0] = True
+    pairs = float((np.flatnonzero(sel_np) + 1).sum()) * H
+    sel = torch.from_numpy(sel_np).to(dev)[None]
+    cu = torch.tensor([0, T], dtype=torch.int32, device=dev)
+    for name, D, dt in (("d256_bf16", 256, torch.bfloat16), ("d128_fp32", 128, torch.float32)):
+        q, k, v = ((torch.randn(1, T, H, D, generator=gen) * 0.5).to(dt).to(dev).requires_grad_() for _ in range(3))
+        do = torch.randn(1, T, H, D, generator=gen).to(dt).to(dev)
+
+        def fb():
+            o = sq_full_attn(q, k, v, sel, cu_seqlens=cu)
+            torch.autograd.grad(o, (q, k, v), do)
+        t = _time_ms(fb, 5)
+        out[f"{name}_T8192_r0.25_fwd_bwd"] = {"ms": round(t, 3), "tflops": round(3.5 * 4 * D * pairs / t / 1e9, 1)}
+        del q, k, v, do
+    n1, h1, d1 = 512, 4, 64
+    q, k, v = (torch.randn(1, n1, h1, d1, generator=gen).to(dev).requires_grad_() for _ in range(3))
+    do = torch.randn(1, n1, h1, d1, generator=gen).to(dev)
+    sel1 = (torch.rand(1, n1, generator=gen) < 0.5).to(dev)
+    cu1 = torch.tensor([0, n1], dtype=torch.int32, device=dev)
+
+    def fb1():
+        o = sq_full_attn(q, k, v, sel1, cu_seqlens=cu1)
+        torch.autograd.grad(o, (q, k, v), do)
+    out["cfg1_fp32_fwd_bwd_ms"] = round(_time_ms(fb1, 20), 4)
+    return out
+
+
 def extra_measurements(dev):
     """Secondary rows: speed-up vs global ratio, cfg2 forward, cfg3 varlen
     fwd+bwd, SWA and epilogue at cfg4 shapes, gate-aware decode at cfg5 shape.
@@ -275,6 +312,7 @@ def extra_measurements(dev):
     out["cfg3_fwd_bwd_varlen"] = {"lens": lens, "ms": round(t3, 3), "tflops": round(f3 / t3 / 1e9, 1)}
 
     out["swa_w128_cfg4"] = swa_cfg4_measurement(q, k, v, do)
+    out["generic_kernels"] = generic_measurement(dev, gen)
     N4 = 4 * 8192
 
     # fused epilogue at cfg4 shape: L, G [32768, 16, 128], gate [32768]

@@ -89,6 +89,7 @@ __device__ __forceinline__ typename Mma<T>::Op to_op(const f32x4 v) {
 // ---------------------------------------------------------------------------
 template <typename T, int D>
 struct GTile {
+  using Op = typename Mma<T>::Op;
   static constexpr int RB = D * (int)sizeof(T);  // bytes per row (>= 128)
   static constexpr int CH = RB / 16;             // 16-byte chunks per row
   static constexpr int SW = CH < 16 ? CH - 1 : 15;
@@ -99,29 +100,78 @@ struct GTile {
     return off(r, b >> 4) + (b & 15);
   }
   // Row operand: lane (i, G) gets elements 16 ks + 4 G .. + 3 of row r.
-  __device__ __forceinline__ static typename Mma<T>::Op row(const char* t, int r, int ks, int G) {
-    return *reinterpret_cast<const typename Mma<T>::Op*>(t + eoff(r, 16 * ks + 4 * G));
+  // (LDS reads go through the restrict wrappers of common.hpp, so the
+  // compiler does not make them wait for the next tile's copy in flight.)
+  __device__ __forceinline__ static Op row(const char* t, int r, int ks, int G) {
+    return lds_load(reinterpret_cast<const Op*>(t + eoff(r, 16 * ks + 4 * G)));
   }
-  // Transposed operand: lane (i, G) gets column c of rows rb + 4 G .. + 3.
-  __device__ __forceinline__ static typename Mma<T>::Op tr(const char* t, int rb, int c, int G) {
-    typename Mma<T>::Op v;
+  // Transposed operand: lane l = 16 G + i gets column c0 + i of rows
+  // rb + 4 G .. rb + 4 G + 3 (c0 a multiple of 16).
+  __device__ __forceinline__ static Op tr(const char* t, int rb, int c0, int l) {
+    const int G = l >> 4, i = l & 15;
+    if constexpr (sizeof(T) == 2) {
+      // ds_read_b64_tr_b16: lane 16G + 4a + b receives element b of the
+      // 8-byte chunks addressed by lanes 16G + a + 4e (e = 0..3) as its
+      // elements e.  Lane 16G + j addresses row rb + 4G + j/4 at columns
+      // c0 + 4(j%4) .. + 3, so lane 16G + i receives rows rb + 4G + e of
+      // column c0 + i.
+      using L4 = std::conditional_t<Elem<T>::kHalf, lds_hf16x4, lds_bf16x4>;
+      return ds_read_tr((const L4*)(t + eoff(rb + 4 * G + (i >> 2), c0 + 4 * (i & 3))));
+    } else {
+      Op v;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) v[e] = *reinterpret_cast<const T*>(t + eoff(rb + 4 * G + e, c));
-    return v;
+      for (int e = 0; e < 4; ++e) v[e] = lds_load(reinterpret_cast<const T*>(t + eoff(rb + 4 * G + e, c0 + i)));
+      return v;
+    }
   }
-  // Rows [0, R) by NT threads; rowptr(r) is a valid row for every r.
-  template <int R, int NT, typename F>
-  __device__ __forceinline__ static void load(char* t, F rowptr) {
+  // Rows [0, R) global -> LDS by NT threads with buffer_load ... lds (no
+  // registers): row r is read from row0 + min(r, last) * stride (elements);
+  // each wave instruction fills 1 KB of the tile, lane j the 16 bytes at
+  // offset 16 j, which belong to physical chunk pc of row r and so to
+  // logical chunk pc ^ swz(r).  The buffer's extent ends at row `last`, so
+  // no lane reads past it.  The caller waits (vmcnt) and barriers before
+  // the tile is read.
+  template <int R, int NT>
+  __device__ __forceinline__ static void dma(char* t, const T* row0, int stride, int last) {
+    static_assert(R * RB % 1024 == 0, "tiles are whole 1 KB blocks");
+    constexpr int LOADS = R * RB / 1024, NWV = NT / 64;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), j = threadIdx.x & 63;
+    const int extent = (last * stride) * (int)sizeof(T) + RB;
+    const auto rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(row0), (short)0, extent, kBufRsrcWord3);
 #pragma unroll
-    for (int k = 0; k < (R * CH + NT - 1) / NT; ++k) {
-      const int c = threadIdx.x + NT * k;
-      if (R * CH % NT == 0 || c < R * CH) {
-        const int r = c / CH, ch = c % CH;
-        const u32x4 v = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(rowptr(r)) + 16 * ch);
-        *reinterpret_cast<u32x4*>(t + off(r, ch)) = v;
+    for (int k = 0; k < (LOADS + NWV - 1) / NWV; ++k) {
+      const int b = wave + NWV * k;
+      if (LOADS % NWV == 0 || b < LOADS) {
+        const int o = 1024 * b + 16 * j;
+        const int r = o / RB, pc = (o % RB) >> 4;
+        const uint32_t voff = (uint32_t)(min(r, last) * stride * (int)sizeof(T) + 16 * (pc ^ (r & SW)));
+        buf_load_lds16(rsrc, reinterpret_cast<bf16*>(t + 1024 * b), voff);
       }
     }
   }
+  // Register staging of gathered rows (the dk/dv kernel's q and dO rows):
+  // thread tid holds chunks tid, tid + NT, ... of rows [0, R).
+  template <int R, int NT>
+  struct Staged {
+    static constexpr int N = (R * CH + NT - 1) / NT;
+    u32x4 v[N];
+    template <typename F>
+    __device__ __forceinline__ void fetch(F rowptr) {
+#pragma unroll
+      for (int k = 0; k < N; ++k) {
+        const int c = threadIdx.x + NT * k;
+        if (R * CH % NT == 0 || c < R * CH)
+          v[k] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(rowptr(c / CH)) + 16 * (c % CH));
+      }
+    }
+    __device__ __forceinline__ void stash(char* t) const {
+#pragma unroll
+      for (int k = 0; k < N; ++k) {
+        const int c = threadIdx.x + NT * k;
+        if (R * CH % NT == 0 || c < R * CH) *reinterpret_cast<u32x4*>(t + off(c / CH, c % CH)) = v[k];
+      }
+    }
+  };
 };
 
 // Sum / max over the four lanes of a query column (i, i+16, i+32, i+48).
@@ -200,11 +250,10 @@ __global__ __launch_bounds__(256) void gen_fwd_kernel(const AttnArgs a) {
   using Op = typename M::Op;
   using TL = GTile<T, D>;
   constexpr int KS = D / 16;  // k steps over the head dim; also 16-column blocks of O
-  char* const tK = logo_smem;
-  char* const tV = logo_smem + kKT * TL::RB;
+  // two stages of [K tile][V tile], 32 keys each
+  auto tK = [](int b) { return logo_smem + b * 2 * kKT * TL::RB; };
+  auto tV = [](int b) { return logo_smem + (b * 2 + 1) * kKT * TL::RB; };
   const T* q = reinterpret_cast<const T*>(a.q);
-  const T* k = reinterpret_cast<const T*>(a.k);
-  const T* v = reinterpret_cast<const T*>(a.v);
   T* o = reinterpret_cast<T*>(a.o);
 
   GenRows<SPARSE> gr;
@@ -229,6 +278,17 @@ __global__ __launch_bounds__(256) void gen_fwd_kernel(const AttnArgs a) {
   const int kv_lo = win ? (max(0, qt.rv.posn(gr.r0) - W) & ~(kKT - 1)) : 0;
   const int kv_hi = qt.rv.posn(gr.r_end - 1) + 1;
   const float c = a.scale_log2;
+  const int stride = a.h * D;
+  const T* k0 = reinterpret_cast<const T*>(a.k) + ((int64_t)qt.bos * a.h + h) * D;
+  const T* v0 = reinterpret_cast<const T*>(a.v) + ((int64_t)qt.bos * a.h + h) * D;
+  const int last_key = qt.seqlen - 1;
+  auto issue = [&](int kt, int b) {  // keys past the segment read its last key (masked)
+    const int last = min(kKT - 1, last_key - kt);
+    TL::template dma<kKT, 256>(tK(b), k0 + (int64_t)kt * stride, stride, last);
+    TL::template dma<kKT, 256>(tV(b), v0 + (int64_t)kt * stride, stride, last);
+  };
+  const int ntl = (kv_hi - kv_lo + kKT - 1) / kKT;
+  issue(kv_lo, 0);
 
   Op qreg[KS];
 #pragma unroll
@@ -239,34 +299,31 @@ __global__ __launch_bounds__(256) void gen_fwd_kernel(const AttnArgs a) {
   for (int dt = 0; dt < KS; ++dt) oacc[dt] = f32x4{};
   float m_run = -INFINITY, l_run = 0.f;
 
-  const int last_key = qt.seqlen - 1;
-  for (int kt = kv_lo; kt < kv_hi; kt += kKT) {
-    __syncthreads();  // the previous tile's readers are done
-    TL::template load<kKT, 256>(tK, [&](int rr) {
-      return k + ((int64_t)(qt.bos + min(kt + rr, last_key)) * a.h + h) * D;
-    });
-    TL::template load<kKT, 256>(tV, [&](int rr) {
-      return v + ((int64_t)(qt.bos + min(kt + rr, last_key)) * a.h + h) * D;
-    });
-    __syncthreads();
+  for (int it = 0; it < ntl; ++it) {
+    const int kt = kv_lo + kKT * it, b = it & 1;
+    wait_vmem();
+    __syncthreads();  // tile it has landed; every wave is done with stage b ^ 1
+    if (it + 1 < ntl) issue(kt + kKT, b ^ 1);
     if (!wave_active || kt > pw_hi || (win && kt + kKT - 1 < pw_lo - W)) continue;
+    const char* kb = tK(b);
+    const char* vb = tV(b);
     f32x4 sacc[kKT / 16];
 #pragma unroll
-    for (int kb = 0; kb < kKT / 16; ++kb) {
-      sacc[kb] = f32x4{};
+    for (int kb16 = 0; kb16 < kKT / 16; ++kb16) {
+      sacc[kb16] = f32x4{};
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) sacc[kb] = M::mma(TL::row(tK, 16 * kb + i, ks, G), qreg[ks], sacc[kb]);
+      for (int ks = 0; ks < KS; ++ks) sacc[kb16] = M::mma(TL::row(kb, 16 * kb16 + i, ks, G), qreg[ks], sacc[kb16]);
     }
-    // scores in the log2 domain; item j of block kb is key kt + 16 kb + 4 G + j
+    // scores in the log2 domain; item j of block kb16 is key kt + 16 kb16 + 4 G + j
     float mx = -INFINITY;
 #pragma unroll
-    for (int kb = 0; kb < kKT / 16; ++kb)
+    for (int kb16 = 0; kb16 < kKT / 16; ++kb16)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int key = kt + 16 * kb + 4 * G + j;
+        const int key = kt + 16 * kb16 + 4 * G + j;
         const bool vis = key <= p && (!win || key >= p - W);
-        sacc[kb][j] = vis ? sacc[kb][j] * c : -INFINITY;
-        mx = fmaxf(mx, sacc[kb][j]);
+        sacc[kb16][j] = vis ? sacc[kb16][j] * c : -INFINITY;
+        mx = fmaxf(mx, sacc[kb16][j]);
       }
     mx = col_max(mx);
     const float m_new = fmaxf(m_run, mx);
@@ -277,21 +334,21 @@ __global__ __launch_bounds__(256) void gen_fwd_kernel(const AttnArgs a) {
     const float alpha = exp2f(m_run - base);
     float ls = 0.f;
 #pragma unroll
-    for (int kb = 0; kb < kKT / 16; ++kb)
+    for (int kb16 = 0; kb16 < kKT / 16; ++kb16)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        sacc[kb][j] = exp2f(sacc[kb][j] - base);
-        ls += sacc[kb][j];
+        sacc[kb16][j] = exp2f(sacc[kb16][j] - base);
+        ls += sacc[kb16][j];
       }
     l_run = l_run * alpha + col_sum(ls);
     m_run = m_new;
 #pragma unroll
     for (int dt = 0; dt < KS; ++dt) oacc[dt] *= alpha;
 #pragma unroll
-    for (int kb = 0; kb < kKT / 16; ++kb) {
-      const Op pb = to_op<T>(sacc[kb]);
+    for (int kb16 = 0; kb16 < kKT / 16; ++kb16) {
+      const Op pb = to_op<T>(sacc[kb16]);
 #pragma unroll
-      for (int dt = 0; dt < KS; ++dt) oacc[dt] = M::mma(TL::tr(tV, 16 * kb, 16 * dt + i, G), pb, oacc[dt]);
+      for (int dt = 0; dt < KS; ++dt) oacc[dt] = M::mma(TL::tr(vb, 16 * kb16, 16 * dt, l), pb, oacc[dt]);
     }
   }
   if (!valid) return;
@@ -339,11 +396,9 @@ __global__ __launch_bounds__(256) void gen_dq_kernel(const AttnArgs a) {
   using Op = typename M::Op;
   using TL = GTile<T, D>;
   constexpr int KS = D / 16;
-  char* const tK = logo_smem;
-  char* const tV = logo_smem + kKT * TL::RB;
+  auto tK = [](int b) { return logo_smem + b * 2 * kKT * TL::RB; };
+  auto tV = [](int b) { return logo_smem + (b * 2 + 1) * kKT * TL::RB; };
   const T* q = reinterpret_cast<const T*>(a.q);
-  const T* k = reinterpret_cast<const T*>(a.k);
-  const T* v = reinterpret_cast<const T*>(a.v);
   const T* dout = reinterpret_cast<const T*>(a.dout);
   T* dq = reinterpret_cast<T*>(a.dq);
 
@@ -369,9 +424,20 @@ __global__ __launch_bounds__(256) void gen_dq_kernel(const AttnArgs a) {
   const int kv_lo = win ? (max(0, qt.rv.posn(gr.r0) - W) & ~(kKT - 1)) : 0;
   const int kv_hi = qt.rv.posn(gr.r_end - 1) + 1;
   const float c = a.scale_log2;
+  const int stride = a.h * D;
+  const T* k0 = reinterpret_cast<const T*>(a.k) + ((int64_t)qt.bos * a.h + h) * D;
+  const T* v0 = reinterpret_cast<const T*>(a.v) + ((int64_t)qt.bos * a.h + h) * D;
+  const int last_key = qt.seqlen - 1;
+  auto issue = [&](int kt, int b) {
+    const int last = min(kKT - 1, last_key - kt);
+    TL::template dma<kKT, 256>(tK(b), k0 + (int64_t)kt * stride, stride, last);
+    TL::template dma<kKT, 256>(tV(b), v0 + (int64_t)kt * stride, stride, last);
+  };
+  const int ntl = (kv_hi - kv_lo + kKT - 1) / kKT;
+  issue(kv_lo, 0);
+
   const float lse = valid ? a.lse[(int64_t)hq * a.n + r] : 0.f;
   const float dlt = valid ? a.delta[(int64_t)hq * a.n + r] : 0.f;
-
   Op qreg[KS], dreg[KS];
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) {
@@ -383,36 +449,33 @@ __global__ __launch_bounds__(256) void gen_dq_kernel(const AttnArgs a) {
 #pragma unroll
   for (int dt = 0; dt < KS; ++dt) dqacc[dt] = f32x4{};
 
-  const int last_key = qt.seqlen - 1;
-  for (int kt = kv_lo; kt < kv_hi; kt += kKT) {
+  for (int it = 0; it < ntl; ++it) {
+    const int kt = kv_lo + kKT * it, b = it & 1;
+    wait_vmem();
     __syncthreads();
-    TL::template load<kKT, 256>(tK, [&](int rr) {
-      return k + ((int64_t)(qt.bos + min(kt + rr, last_key)) * a.h + h) * D;
-    });
-    TL::template load<kKT, 256>(tV, [&](int rr) {
-      return v + ((int64_t)(qt.bos + min(kt + rr, last_key)) * a.h + h) * D;
-    });
-    __syncthreads();
+    if (it + 1 < ntl) issue(kt + kKT, b ^ 1);
     if (!wave_active || kt > pw_hi || (win && kt + kKT - 1 < pw_lo - W)) continue;
+    const char* kb = tK(b);
+    const char* vb = tV(b);
 #pragma unroll
-    for (int kb = 0; kb < kKT / 16; ++kb) {
+    for (int kb16 = 0; kb16 < kKT / 16; ++kb16) {
       f32x4 s = f32x4{}, dp = f32x4{};
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        s = M::mma(TL::row(tK, 16 * kb + i, ks, G), qreg[ks], s);
-        dp = M::mma(TL::row(tV, 16 * kb + i, ks, G), dreg[ks], dp);
+        s = M::mma(TL::row(kb, 16 * kb16 + i, ks, G), qreg[ks], s);
+        dp = M::mma(TL::row(vb, 16 * kb16 + i, ks, G), dreg[ks], dp);
       }
       f32x4 ds;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int key = kt + 16 * kb + 4 * G + j;
+        const int key = kt + 16 * kb16 + 4 * G + j;
         const bool vis = key <= p && (!win || key >= p - W);
         const float pr = vis ? exp2f(s[j] * c - lse) : 0.f;
         ds[j] = pr * (dp[j] - dlt);
       }
       const Op db = to_op<T>(ds);
 #pragma unroll
-      for (int dt = 0; dt < KS; ++dt) dqacc[dt] = M::mma(TL::tr(tK, 16 * kb, 16 * dt + i, G), db, dqacc[dt]);
+      for (int dt = 0; dt < KS; ++dt) dqacc[dt] = M::mma(TL::tr(kb, 16 * kb16, 16 * dt, l), db, dqacc[dt]);
     }
   }
   if (!valid) return;
@@ -430,8 +493,9 @@ __global__ __launch_bounds__(256) void gen_dq_kernel(const AttnArgs a) {
 // dk / dv: S = Q K^T, P, dP = dO V^T, dS; dV^T += dO^T P, dK^T += Q^T dS,
 // summed over the query heads of the GQA group (:231-337, :444-445)
 // ---------------------------------------------------------------------------
+// LDS: two stages of [Q rows][dO rows][lse][delta][pos], kQS rows each.
 template <typename T, int D>
-constexpr size_t gen_dkv_smem() {
+constexpr size_t gen_dkv_stage() {
   return (size_t)2 * kQS * GTile<T, D>::RB + 3 * kQS * sizeof(float);
 }
 
@@ -441,11 +505,9 @@ __global__ __launch_bounds__(256) void gen_dkv_kernel(const AttnArgs a) {
   using Op = typename M::Op;
   using TL = GTile<T, D>;
   constexpr int KS = D / 16;
-  char* const tQ = logo_smem;
-  char* const tO = logo_smem + kQS * TL::RB;
-  float* const sLse = reinterpret_cast<float*>(logo_smem + 2 * kQS * TL::RB);
-  float* const sDelta = sLse + kQS;
-  int* const sPos = reinterpret_cast<int*>(sDelta + kQS);
+  auto tQ = [](int b) { return logo_smem + b * gen_dkv_stage<T, D>(); };
+  auto tO = [](int b) { return logo_smem + b * gen_dkv_stage<T, D>() + kQS * TL::RB; };
+  auto sF = [](int b) { return reinterpret_cast<float*>(logo_smem + b * gen_dkv_stage<T, D>() + 2 * kQS * TL::RB); };
   const T* q = reinterpret_cast<const T*>(a.q);
   const T* k = reinterpret_cast<const T*>(a.k);
   const T* v = reinterpret_cast<const T*>(a.v);
@@ -468,6 +530,7 @@ __global__ __launch_bounds__(256) void gen_dkv_kernel(const AttnArgs a) {
   const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63, i = l & 15, G = l >> 4;
   const int key = k0 + 16 * wave + i;
   const bool valid_k = key < seqlen;
+  const bool wave_keys = 16 * wave + k0 <= k_last;  // this wave has keys in the segment
   const int W = a.window;
   const bool win = W >= 0;
   const float c = a.scale_log2;
@@ -488,6 +551,9 @@ __global__ __launch_bounds__(256) void gen_dkv_kernel(const AttnArgs a) {
     dvacc[dt] = f32x4{};
   }
 
+  typename TL::template Staged<kQS, 256> sq, so;
+  float st_lse = 0.f, st_delta = 0.f;
+  int st_pos = -1;
   for (int gg = 0; gg < a.g; ++gg) {
     const int hq = h * a.g + gg;
     const int lane_sel = a.lanes > 1 ? hq : 0;
@@ -500,46 +566,70 @@ __global__ __launch_bounds__(256) void gen_dkv_kernel(const AttnArgs a) {
     };
     const int rq0 = lb_pos(q_lo, q_hi, k0);
     const int rq_end = win ? lb_pos(rq0, q_hi, k_last + W + 1) : q_hi;
+    if (rq0 >= rq_end) continue;  // (uniform) no row of this head sees these keys
     const float* lse_h = a.lse + (int64_t)hq * a.n;
     const float* delta_h = a.delta + (int64_t)hq * a.n;
-    for (int rs = rq0; rs < rq_end; rs += kQS) {
-      __syncthreads();  // the previous step's readers are done
-      const int last = rq_end - 1;
-      TL::template load<kQS, 256>(tQ, [&](int rr) { return q + (rv.token(min(rs + rr, last)) * a.hq + hq) * D; });
-      TL::template load<kQS, 256>(tO, [&](int rr) {
-        return dout + (rv.token(min(rs + rr, last)) * a.hq + hq) * D;
-      });
+    const int last = rq_end - 1;
+    // q / dO rows of a step through registers (gathered rows); rows past the
+    // end read the last row and get position -1 (they see no key)
+    auto fetch = [&](int rs) {
+      sq.fetch([&](int rr) { return q + (rv.token(min(rs + rr, last)) * a.hq + hq) * D; });
+      so.fetch([&](int rr) { return dout + (rv.token(min(rs + rr, last)) * a.hq + hq) * D; });
       if (tid < kQS) {
-        const int rr = rs + tid;
-        const int rc = min(rr, last);
-        sLse[tid] = lse_h[rc];
-        sDelta[tid] = delta_h[rc];
-        sPos[tid] = rr < rq_end ? rv.posn(rr) : -1;  // rows past the end see no key
+        const int rr = rs + tid, rc = min(rr, last);
+        st_lse = lse_h[rc];
+        st_delta = delta_h[rc];
+        st_pos = rr < rq_end ? rv.posn(rr) : -1;
       }
+    };
+    auto stash = [&](int b) {
+      sq.stash(tQ(b));
+      so.stash(tO(b));
+      if (tid < kQS) {
+        sF(b)[tid] = st_lse;
+        sF(b)[kQS + tid] = st_delta;
+        reinterpret_cast<int*>(sF(b))[2 * kQS + tid] = st_pos;
+      }
+    };
+    __syncthreads();  // the previous head's last step is done with both stages
+    fetch(rq0);
+    stash(0);
+    __syncthreads();
+    int b = 0;
+    for (int rs = rq0; rs < rq_end; rs += kQS, b ^= 1) {
+      const bool more = rs + kQS < rq_end;
+      if (more) fetch(rs + kQS);  // in flight during this step's products
+      if (wave_keys) {
+        const char* qb = tQ(b);
+        const char* ob = tO(b);
+        const float* sLse = sF(b);
+        const float* sDelta = sLse + kQS;
+        const int* sPos = reinterpret_cast<const int*>(sLse + 2 * kQS);
+        f32x4 sacc = f32x4{}, dpacc = f32x4{};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          sacc = M::mma(TL::row(qb, i, ks, G), kreg[ks], sacc);
+          dpacc = M::mma(TL::row(ob, i, ks, G), vreg[ks], dpacc);
+        }
+        // item j: query row rs + 4 G + j, key `key`
+        f32x4 pr, ds;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int rj = 4 * G + j;
+          const int pq = sPos[rj];
+          const bool vis = valid_k && key <= pq && (!win || key >= pq - W);
+          pr[j] = vis ? exp2f(sacc[j] * c - sLse[rj]) : 0.f;
+          ds[j] = pr[j] * (dpacc[j] - sDelta[rj]);
+        }
+        const Op pb = to_op<T>(pr), db = to_op<T>(ds);
+#pragma unroll
+        for (int dt = 0; dt < KS; ++dt) {
+          dvacc[dt] = M::mma(TL::tr(ob, 0, 16 * dt, l), pb, dvacc[dt]);
+          dkacc[dt] = M::mma(TL::tr(qb, 0, 16 * dt, l), db, dkacc[dt]);
+        }
+      }
+      if (more) stash(b ^ 1);  // stage b ^ 1 was last read in the previous step
       __syncthreads();
-      if (16 * wave + k0 > k_last) continue;  // this wave's keys are past the segment
-      f32x4 sacc = f32x4{}, dpacc = f32x4{};
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        sacc = M::mma(TL::row(tQ, i, ks, G), kreg[ks], sacc);
-        dpacc = M::mma(TL::row(tO, i, ks, G), vreg[ks], dpacc);
-      }
-      // item j: query row rs + 4 G + j, key `key`
-      f32x4 pr, ds;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int rj = 4 * G + j;
-        const int pq = sPos[rj];
-        const bool vis = valid_k && key <= pq && (!win || key >= pq - W);
-        pr[j] = vis ? exp2f(sacc[j] * c - sLse[rj]) : 0.f;
-        ds[j] = pr[j] * (dpacc[j] - sDelta[rj]);
-      }
-      const Op pb = to_op<T>(pr), db = to_op<T>(ds);
-#pragma unroll
-      for (int dt = 0; dt < KS; ++dt) {
-        dvacc[dt] = M::mma(TL::tr(tO, 0, 16 * dt + i, G), pb, dvacc[dt]);
-        dkacc[dt] = M::mma(TL::tr(tQ, 0, 16 * dt + i, G), db, dkacc[dt]);
-      }
     }
   }
   if (!valid_k) return;
@@ -563,8 +653,9 @@ __global__ __launch_bounds__(256) void gen_dkv_kernel(const AttnArgs a) {
 // ---------------------------------------------------------------------------
 // Launchers
 // ---------------------------------------------------------------------------
+// fwd / dq: two stages of a K and a V tile of kKT keys
 template <typename T, int D>
-constexpr size_t gen_kv_smem() { return (size_t)2 * kKT * GTile<T, D>::RB; }
+constexpr size_t gen_kv_smem() { return (size_t)4 * kKT * GTile<T, D>::RB; }
 
 // fwd / dq grid: two workgroups per 128-row tile (worst case over the lanes),
 // per query head.
@@ -608,7 +699,7 @@ int launch_dkv(const AttnArgs& a, hipStream_t st) {
   const int64_t nblk = 2 * ((a.n + kBKV - 1) / kBKV + a.nseq) * a.h;
   LOGO_REQUIRE(nblk < ((int64_t)1 << 31), "grid too large");
   auto kern = gen_dkv_kernel<T, D, SPARSE>;
-  const size_t smem = gen_dkv_smem<T, D>();
+  const size_t smem = 2 * gen_dkv_stage<T, D>();
   LOGO_HIP_CHECK(allow_smem(kern, smem));
   hipLaunchKernelGGL(kern, dim3((unsigned)nblk), dim3(256), smem, st, a);
   LOGO_LAUNCH_CHECK("gen_dkv_kernel");
