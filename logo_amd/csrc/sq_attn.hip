@@ -38,6 +38,7 @@
 #include "sq_attn.hpp"
 
 #include <algorithm>
+#include <cstdlib>
 #include <mutex>
 
 namespace logo {
@@ -150,6 +151,16 @@ static int check_common(int64_t n, int nseq, int hq, int h, int d, int v_dim, in
   return LOGO_OK;
 }
 
+// Compacted rows a head has in flight in one round of fwd / dq workgroups
+// (CUs * 256 / HQ for every form of those kernels), which sets their key walk
+// order (QTile::desc); the environment variable LOGO_SQ_DESC=0 keeps every
+// walk ascending (A/B timing).
+static int walk_round_rows(int hq) {
+  const char* env = std::getenv("LOGO_SQ_DESC");
+  if (env != nullptr && env[0] == '0') return 0;
+  return device_cus() * 256 / hq;
+}
+
 static AttnArgs make_args(const void* q, const void* k, const void* v, const int64_t* q_idx,
                           const int32_t* pos, const int32_t* meta, const int32_t* cu, int64_t n,
                           int nseq, int hq, int h, int lanes, float scale, int window) {
@@ -171,6 +182,7 @@ static AttnArgs make_args(const void* q, const void* k, const void* v, const int
   a.scale = scale;
   a.scale_log2 = scale * 1.4426950408889634f;
   a.window = window;
+  a.round_rows = window < 0 ? walk_round_rows(hq) : 0;
   return a;
 }
 

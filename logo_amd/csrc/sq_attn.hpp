@@ -52,6 +52,11 @@ struct AttnArgs {
   // from it when it is large enough for their kernel's split_cap)
   void* ws;
   size_t ws_bytes;
+  // Key walk order of the fwd / dq tiles (no window): compacted rows a head
+  // has in flight at once (one round of its workgroups, the same for the
+  // 8-wave and 4-wave forward and for dq: CUs * 256 / HQ); 0 keeps every tile
+  // ascending.  See QTile::desc.
+  int round_rows;
 };
 
 constexpr int kMaxSplit = 4;
@@ -219,6 +224,18 @@ struct QTile {
   // key-range split: rank = trank * nper + piece; nsplit pieces of this tile
   // exist (nsplit <= nper; 1: no split)
   int rank, trank, piece, nper, nsplit;
+  // Walk the key tiles from the last to the first.  The tiles of a head run
+  // heaviest first; those of the first round start together at key 0 and
+  // walk in step, so each K / V tile is fetched into the XCD's L2 once for
+  // all of them.  Tiles of later rounds start one by one, as earlier tiles of
+  // different lengths finish: walking up from key 0 each would fetch its
+  // keys alone.  Walking down instead, a tile that starts later starts lower,
+  // where the tiles that started before it have just arrived, so the tiles of
+  // a round converge and share their K / V again.  Rounds alternate: odd
+  // rounds walk down.  Rounds are counted in pairs of 128-row tiles (the
+  // 8-wave forward's tiles), so the 4-wave forward and dq tiles of the same
+  // rows walk the same way (the forms stay bit-identical).
+  bool desc;
 
   // rpw: compacted rows per wave (32 or 64); r / t / p / valid describe the
   // lane's row in the wave's first 32-row block (row_at gives the others).
@@ -240,6 +257,12 @@ struct QTile {
     if (rank >= nt * nper) return false;
     trank = rank / nper;
     piece = rank - trank * nper;
+    {
+      // rank of the tile's pair of 128-row tiles, heaviest first
+      const int pr = paired ? trank : ((nt + 1) >> 1) - 1 - ((nt - 1 - trank) >> 1);
+      const int pairs_per_round = a.round_rows >> 8;
+      desc = !window && pairs_per_round > 0 && ((pr / pairs_per_round) & 1);
+    }
     const int tile = nt - 1 - trank;  // heaviest (latest) blocks first
     if (paired) {
       s = 0;

@@ -107,7 +107,11 @@ __global__ __launch_bounds__(128) LOGO_OCC_DQ64 void sq_dq64_kernel(const AttnAr
 
   const int kv_lo = qt.kv_lo;
   const int nt = (qt.kv_hi - kv_lo + 63) >> 6;
-  int hw_lo = 0, hw_hi = 0;  // 32-key halves this wave's rows can see
+  // step t of the walk takes key tile ph(t): ascending, or from the last
+  // tile down (qt.desc); the two 32-key halves of a tile go in key order
+  const bool desc = qt.desc;
+  auto ph = [&](int t) { return desc ? nt - 1 - t : t; };
+  int hw_lo = 0, hw_hi = 0;  // 32-key halves (in key order) this wave's rows can see
   if (qt.wave_active) {
     hw_hi = min(2 * nt, ((qt.pmax - kv_lo) >> 5) + 1);
     hw_lo = WINDOW ? (max(0, qt.pmin - W - kv_lo) >> 5) : 0;
@@ -117,16 +121,19 @@ __global__ __launch_bounds__(128) LOGO_OCC_DQ64 void sq_dq64_kernel(const AttnAr
   auto step = [&](auto par_tag, auto h_tag, int t) {
     constexpr int PAR = decltype(par_tag)::value, H = decltype(h_tag)::value;
     if (H == 0) {
-      if (t + 1 < nt) load_one(tileK(PAR ^ 1), kbase, kv_lo + 64 * (t + 1));
+      if (t + 1 < nt) load_one(tileK(PAR ^ 1), kbase, kv_lo + 64 * ph(t + 1));
     } else {
-      if (t + 2 < nt) load_one(tileV(PAR), vbase, kv_lo + 64 * (t + 2));
+      if (t + 2 < nt) load_one(tileV(PAR), vbase, kv_lo + 64 * ph(t + 2));
     }
     // X reads the next half: rows 32 of tile t (H = 0) or rows 0 of tile t + 1
     const bf16* kx = tileK(H == 0 ? PAR : PAR ^ 1);
     const bf16* vx = tileV(H == 0 ? PAR : PAR ^ 1);
     constexpr int XR = H == 0 ? 32 : 0;
     const bf16* ky = tileK(PAR);  // K^T of the current half, rows 32 H
-    const int hx = 2 * t + H;     // current half
+    // the current half and the next one, as halves in key order (t = -1:
+    // only the next half, the first of the walk)
+    const int hx = t >= 0 ? 2 * ph(t) + H : -1;
+    const int hn = H == 0 ? (t >= 0 ? 2 * ph(t) + 1 : -1) : (t + 1 < nt ? 2 * ph(t + 1) : -1);
     const int j0h = kv_lo + 32 * hx;
 
     auto body = [&](auto dox_tag, auto dov_tag, auto mask_tag) {
@@ -203,8 +210,8 @@ __global__ __launch_bounds__(128) LOGO_OCC_DQ64 void sq_dq64_kernel(const AttnAr
     };
     using T_ = std::true_type;
     using F_ = std::false_type;
-    const bool dox = hx + 1 >= hw_lo && hx + 1 < hw_hi;
-    const bool dov = hx >= hw_lo && hx < hw_hi;
+    const bool dox = hn >= 0 && hn >= hw_lo && hn < hw_hi;
+    const bool dov = hx >= 0 && hx >= hw_lo && hx < hw_hi;
     const bool mask = (j0h + 31 > qt.pmin) || (WINDOW && j0h < qt.pmax - W);
     if (dox && dov) {
       if (mask) body(T_{}, T_{}, T_{});
@@ -218,8 +225,8 @@ __global__ __launch_bounds__(128) LOGO_OCC_DQ64 void sq_dq64_kernel(const AttnAr
     __syncthreads();
   };
 
-  load_one(tileK(0), kbase, kv_lo);
-  load_one(tileV(0), vbase, kv_lo);
+  load_one(tileK(0), kbase, kv_lo + 64 * ph(0));
+  load_one(tileV(0), vbase, kv_lo + 64 * ph(0));
   wait_vmem();
   __syncthreads();
   step(BufTag<1>{}, BufTag<1>{}, -1);  // S / dP of half (0, 0); copies V(1)

@@ -107,19 +107,28 @@ __global__ __launch_bounds__(64 * NW) LOGO_OCC_FWD void sq_fwd_pipe_kernel(const
 
   const int kv_lo = qt.kv_lo;
   const int nt = (qt.kv_hi - kv_lo + 63) >> 6;
-  int tw_lo = 0, tw_hi = 0;  // tiles this wave's rows can see
+  // step t of the walk takes key tile ph(t): ascending, or from the last
+  // tile down (qt.desc)
+  const bool desc = qt.desc;
+  auto ph = [&](int t) { return desc ? nt - 1 - t : t; };
+  int tw_lo = 0, tw_hi = 0;  // steps whose tiles this wave's rows can see
   if (qt.wave_active) {
     tw_hi = min(nt, ((qt.pmax - kv_lo) >> 6) + 1);
     tw_lo = WINDOW ? (max(0, qt.pmin - W - kv_lo) >> 6) : 0;
+    if (desc) {
+      const int lo = nt - tw_hi;
+      tw_hi = nt - tw_lo;
+      tw_lo = lo;
+    }
   }
 
   auto step = [&](auto par_tag, int t) {
     constexpr int PAR = decltype(par_tag)::value;  // t & 1
-    if (t + 2 < nt) load_one(tileK(PAR), kbase, kv_lo + 64 * (t + 2));
-    if (t + 1 < nt) load_one(tileV(PAR ^ 1), vbase, kv_lo + 64 * (t + 1));
+    if (t + 2 < nt) load_one(tileK(PAR), kbase, kv_lo + 64 * ph(t + 2));
+    if (t + 1 < nt) load_one(tileV(PAR ^ 1), vbase, kv_lo + 64 * ph(t + 1));
     const bf16* kb = tileK(PAR ^ 1);
     const bf16* vb = tileV(PAR);
-    const int j0n = kv_lo + 64 * (t + 1);
+    const int j0n = kv_lo + 64 * ph(t + 1);
 
     auto body = [&](auto dos_tag, auto dopv_tag, auto mask_tag) {
       constexpr bool DOS = decltype(dos_tag)::value;    // S(t+1) and its statistics
@@ -242,7 +251,7 @@ __global__ __launch_bounds__(64 * NW) LOGO_OCC_FWD void sq_fwd_pipe_kernel(const
     __syncthreads();
   };
 
-  load_one(tileK(0), kbase, kv_lo);
+  load_one(tileK(0), kbase, kv_lo + 64 * ph(0));
   wait_vmem();
   __syncthreads();
   for (int t = -1; t < nt; t += 2) {
