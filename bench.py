@@ -342,10 +342,13 @@ def extra_measurements(dev):
     td = _time_ms(lambda: decode_attn(q5, kc, vc, lens5, gate5, thres, max_len=ctx), 20)
     bytes_active = (B5 // 2) * H * ctx * D * 2 * 2
     td_all = _time_ms(lambda: decode_attn(q5, kc, vc, lens5, max_len=ctx), 20)
+    del kc, vc
+    ceiling = read_ceiling_gbs(dev, bytes_active)["best_gbs"]
     out["decode_global_cfg5_layer"] = {
         "active_rows": B5 // 2, "ms": round(td, 4), "gbs": round(bytes_active / td / 1e6, 1),
         "all_rows_ms": round(td_all, 4), "all_rows_gbs": round(2 * bytes_active / td_all / 1e6, 1),
-        "hbm_peak_gbs": HBM_PEAK_GBS}
+        "hbm_peak_gbs": HBM_PEAK_GBS, "read_ceiling_gbs": ceiling,
+        "of_read_ceiling": round(bytes_active / td / 1e6 / ceiling, 4)}
     return out
 
 
@@ -444,9 +447,30 @@ def decode_layer_only(dev, calls=10):
     lens = torch.full((B,), ctx, dtype=torch.int32, device=dev)
     ms = _time_ms(lambda: decode_attn(q, kc, vc, lens, gate, thres, max_len=ctx), calls)
     nbytes = (B // 2) * H * ctx * D * 2 * 2
+    ceiling = read_ceiling_gbs(dev, nbytes)
     print(json.dumps({"workload": "cfg5 global decode branch, one layer, 16 of 32 rows active",
                       "ms": round(ms, 4), "algorithmic_bytes": nbytes, "gbs": round(nbytes / ms / 1e6, 1),
-                      "hbm_peak_gbs": HBM_PEAK_GBS}), flush=True)
+                      "hbm_peak_gbs": HBM_PEAK_GBS, "read_ceiling_gbs": ceiling,
+                      "of_read_ceiling": round(nbytes / ms / 1e6 / ceiling["best_gbs"], 4)}), flush=True)
+
+
+def read_ceiling_gbs(dev, nbytes, calls=10):
+    """The read bandwidth this part delivers in practice: the library's
+    streaming-read calibration kernel (logo_read_calibration) over a buffer
+    of ``nbytes``, at several grid sizes; best and per-grid GB/s."""
+    from logo_amd import _lib
+    lib = _lib.lib()
+    buf = torch.ones(nbytes // 2, dtype=torch.bfloat16, device=dev)
+    sink = torch.zeros(65536, dtype=torch.int32, device=dev)
+    st = _lib.stream_of(buf)
+    per = {}
+    for grid in (2048, 8192, 16384):
+        def run():
+            _lib.check(lib.logo_read_calibration(_lib.ptr(buf), nbytes, _lib.ptr(sink), grid, st),
+                       "logo_read_calibration")
+        per[grid] = round(nbytes / _time_ms(run, calls) / 1e6, 1)
+    del buf
+    return {"best_gbs": max(per.values()), "per_grid_gbs": per}
 
 
 def decode_model_measurement(dev, batch=32, prompt=16384, steps=256, seed=4):

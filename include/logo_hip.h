@@ -57,6 +57,16 @@ const char* logo_last_error(void);
 /* ABI version of this library (5: head dim 256, fp32, logo_sq_generic). */
 int logo_abi_version(void);
 
+/*
+ * Streaming-read calibration (no counterpart in the reference): reads `bytes`
+ * (a multiple of 16) of the 16-byte aligned device buffer `buf` once with a
+ * grid of `grid` 256-thread workgroups, for timing the read bandwidth the
+ * part delivers in practice (the ceiling the decode kernel's bandwidth is
+ * compared with).  `sink` is device memory of at least grid * 4 bytes, which
+ * it leaves unchanged unless a workgroup's XOR of its words hits a sentinel.
+ */
+int logo_read_calibration(const void* buf, size_t bytes, void* sink, int grid, void* stream);
+
 /* Bytes of workspace logo_compact needs. */
 size_t logo_compact_workspace_bytes(int64_t n_tokens, int lanes);
 
