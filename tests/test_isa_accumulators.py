@@ -101,25 +101,34 @@ OPERAND_WAIT_STATES = 3
 def check_operand_distance(lines):
     """Violations (line index, text): an accumulator MFMA whose A or B
     VGPRs a VALU instruction wrote within OPERAND_WAIT_STATES wait states
-    before it (each instruction is one wait state, s_nop N is N + 1; the walk
-    follows the listing, as the slot schedules are straight-line code)."""
-    code = [line.split("//")[0].split() for line in lines]
+    before it, on any control-flow path into it (each instruction is one
+    wait state, s_nop N is N + 1).  The walk follows _flow's predecessors,
+    so a write at the end of a loop body that reaches an MFMA at the loop
+    head through the back edge is seen too."""
+    code, preds = _flow(lines)
     bad = []
     for n, c in enumerate(code):
         if not (c and c[0].startswith("v_mfma") and len(c) >= 4 and _ACC_DST.search(lines[n])):
             continue
         srcs = _vregs(c[2]) | _vregs(c[3])
-        waits, k = 0, n - 1
-        while k >= 0 and waits < OPERAND_WAIT_STATES:
+        # backward search over (line, wait states between it and the MFMA)
+        stack, seen = [(k, 0) for k in preds[n]], set()
+        while stack:
+            k, waits = stack.pop()
+            if (k, waits) in seen:
+                continue
+            seen.add((k, waits))
             p = code[k]
-            k -= 1
             if not p or p[0].startswith((".", ";")) or p[0].endswith(":"):
+                stack.extend((q, waits) for q in preds[k])
                 continue
             if p[0].startswith("v_") and not p[0].startswith(("v_mfma", "v_accvgpr_write")) and len(p) > 1:
                 if _vregs(p[1]) & srcs:
-                    bad.append((n, "operand written %d wait state(s) before: %s" % (waits, lines[k + 1].strip())))
+                    bad.append((n, "operand written %d wait state(s) before: %s" % (waits, lines[k].strip())))
                     break
             waits += int(p[1]) + 1 if p[0] == "s_nop" and len(p) > 1 else 1
+            if waits < OPERAND_WAIT_STATES:
+                stack.extend((q, waits) for q in preds[k])
     return bad
 
 
@@ -338,3 +347,26 @@ def test_operand_checker_flags_a_recent_valu_write():
     # a VGPR-result MFMA is the compiler's to protect, and is not checked
     assert check_operand_distance(["\tv_cvt_pk_bf16_f32 v7, v40, v41",
                                    "\tv_mfma_f32_32x32x16_bf16 v[20:35], v[2:5], v[6:9], 0"]) == []
+
+
+# A loop with addresses: the MFMA at the loop head (0x10) is reached from the
+# line before it and, through the back edge (s_cbranch_scc1 at 0x1c, simm16
+# -4: 0x1c + 4 - 16 = 0x10), from the end of the loop body.
+_LOOP = """\
+	v_mov_b32 v8, 0 // 000000000008: 0
+	s_nop 4 // 00000000000C: 0
+	v_mfma_f32_32x32x16_bf16 a[0:15], v[2:5], v[6:9], a[0:15] // 000000000010: 0
+	s_add_i32 s4, s4, 1 // 000000000014: 0
+	{last} // 000000000018: 0
+	s_cbranch_scc1 65532 // 00000000001C: 0
+	s_endpgm // 000000000020: 0
+"""
+
+
+def test_operand_checker_follows_the_loop_back_edge():
+    # the write at the loop end is one wait state before the loop head's MFMA
+    found = check_operand_distance(_LOOP.format(last="v_cvt_pk_bf16_f32 v7, v40, v41").splitlines())
+    assert found and "operand written 1 wait state" in found[0][1]
+    # a write to another register there is fine, and so is the straight-line
+    # entry (s_nop 4 between the v8 write and the MFMA)
+    assert check_operand_distance(_LOOP.format(last="v_cvt_pk_bf16_f32 v70, v40, v41").splitlines()) == []
