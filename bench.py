@@ -85,6 +85,9 @@ def parse():
     ap.add_argument("--swa", action="store_true",
                     help="run only the config-4 sliding-window (local branch) forward and "
                          "forward + backward measurement and print its result")
+    ap.add_argument("--generic", action="store_true",
+                    help="run only the generic-kernel measurement (head dim 256 in bf16, fp32 at D=128, "
+                         "config 1 in fp32) and print its result")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run one 1 GiB device-to-device copy before the workload (the reference kernel "
                          "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters to bytes)")
@@ -585,6 +588,11 @@ def main():
         return
     if args.layer:
         print(json.dumps(layer_cfg4_measurement(dev)), flush=True)
+        return
+    if args.generic:
+        g = torch.Generator()
+        g.manual_seed(7)
+        print(json.dumps(generic_measurement(dev, g)), flush=True)
         return
     if args.swa:
         g = torch.Generator()
