@@ -11,6 +11,8 @@ large-logit regime.
   (too many tiles per head); the same generator at r=0.125 gives few enough
   tiles that both split, so that case checks the split path against the
   reference at full size.
+* A single sequence of 262,144 tokens with GQA: long row searches, many
+  key tiles per row and split key ranges at 8x the headline's length.
 * Large logits: a few q / k feature dims of magnitude ~9, so that the scaled
   scores span about +-45 in log2 units and attention is peaked.  The sparse
   kernels round the pre-scaled query ``-scale * log2(e) * q`` to bf16 before
@@ -168,3 +170,37 @@ def test_large_logits_against_oracle(gpu):
             failures.append(f"{name}: scaled max {scaled:.3e} (<= {max_bound:.3e}), mean {err.mean().item():.3e} "
                             f"(<= {mean_bound:.3e})")
     assert not failures, "; ".join(failures)
+
+
+def test_long_sequence_256k_tokens(gpu):
+    """One sequence of 262,144 tokens (8x the headline), GQA (HQ=4, H=2),
+    D=128, Markov selection at r=0.03: rows that see up to 4096 key tiles,
+    lower-bound searches over ~8K rows per lane, a forward and dq with few
+    tiles per head (so both split their key ranges).  o, dq, dk and dv against the fp32 torch reference at the
+    north-star bound."""
+    from bench import markov_mask
+
+    T, hq, h, d = 262144, 4, 2, 128
+    g = torch.Generator()
+    g.manual_seed(11)
+    sel_np = markov_mask(T, 0.03, 8, g)
+    sel_np[0] = True
+    q = (torch.randn(T, hq, d, generator=g) * 0.5).to(torch.bfloat16)
+    k = (torch.randn(T, h, d, generator=g) * 0.5).to(torch.bfloat16)
+    v = (torch.randn(T, h, d, generator=g) * 0.5).to(torch.bfloat16)
+    do = torch.randn(T, hq, d, generator=g).to(torch.bfloat16)
+    print(f"long sequence T={T} hq={hq} h={h} d={d}: {int(sel_np.sum())} rows", flush=True)
+    qg, kg, vg = (x.to(gpu)[None].requires_grad_() for x in (q, k, v))
+    selg = torch.from_numpy(sel_np).to(gpu)[None]
+    cu = torch.tensor([0, T], dtype=torch.int32, device=gpu)
+    o = sq_full_attn(qg, kg, vg, selg, cu_seqlens=cu)
+    dq, dk, dv = torch.autograd.grad(o, (qg, kg, vg), do.to(gpu)[None])
+    torch.cuda.synchronize()
+    ro, (rdq, rdk, rdv) = torch_sq_attn(q.to(gpu), k.to(gpu), v.to(gpu), selg[0], cu.cpu(), do=do.to(gpu),
+                                        row_chunk=1024)
+    assert_within("o T=256K", o[0], ro)
+    assert_within("dq T=256K", dq[0], rdq)
+    assert_within("dk T=256K", dk[0], rdk)
+    assert_within("dv T=256K", dv[0], rdv)
+    unsel = ~selg[0]
+    assert int(o[0][unsel].count_nonzero()) == 0 and int(dq[0][unsel].count_nonzero()) == 0
