@@ -197,7 +197,9 @@ def swa_cfg4_measurement(q, k, v, do, iters=10):
     [1, 4 x 8192, 16, 128] (four packed sequences), forward alone and
     forward + backward through swa_attn.  Bandwidths are algorithmic bytes:
     forward q, k, v read and o written; backward q, k, v, o, dO read and dq,
-    dk, dv written (bf16), over the backward's share of the time."""
+    dk, dv written (bf16), over the backward's share of the time; beside
+    them, the rate of a plain device-to-device copy of the forward's bytes
+    (``copy_gbs``, half read and half written)."""
     from logo_amd.ops import swa_attn
     N4, H, D = 4 * 8192, q.shape[2], q.shape[3]
     dev = q.device
@@ -211,8 +213,17 @@ def swa_cfg4_measurement(q, k, v, do, iters=10):
         torch.autograd.grad(o, (q4, k4, v4), do[:, :N4])
     tsb = _time_ms(swa_fb, max(iters // 2, 1))
     io = 4 * N4 * H * D * 2
+    # a device-to-device copy of the forward's bytes (half read, half written),
+    # the read + write rate the part delivers in practice
+    src = torch.empty(io // 4, dtype=torch.bfloat16, device=dev)
+    dst = torch.empty_like(src)
+    tcp = _time_ms(lambda: dst.copy_(src), iters)
+    copy_gbs = io / tcp / 1e6
+    del src, dst
     return {"fwd_ms": round(tsf, 4), "fwd_gbs": round(io / tsf / 1e6, 1), "fwd_bwd_ms": round(tsb, 4),
-            "bwd_ms": round(tsb - tsf, 4), "bwd_gbs": round(2 * io / (tsb - tsf) / 1e6, 1)}
+            "bwd_ms": round(tsb - tsf, 4), "bwd_gbs": round(2 * io / (tsb - tsf) / 1e6, 1),
+            "copy_gbs": round(copy_gbs, 1), "fwd_of_copy": round(io / tsf / 1e6 / copy_gbs, 3),
+            "bwd_of_copy": round(2 * io / (tsb - tsf) / 1e6 / copy_gbs, 3)}
 
 
 def generic_measurement(dev, gen):
