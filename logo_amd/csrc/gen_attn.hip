@@ -44,29 +44,36 @@ namespace logo {
 namespace gen {
 
 // ---------------------------------------------------------------------------
-// MFMA per element type: 16x16 output, 16-deep k step, 4 elements per lane
+// MFMA per element type: 16x16 output tiles, a k step of KSTEP, NE = KSTEP / 4
+// elements per lane (lane group G holds elements NE G .. NE G + NE - 1 of the
+// step for both A and B, so they pair up whatever order the unit sums in)
 // ---------------------------------------------------------------------------
 template <typename T>
 struct Mma;
 template <>
 struct Mma<bf16> {
-  using Op = bf16x4;
+  static constexpr int KSTEP = 32, NE = 8;
+  using Op = bf16x8;
+  using V4 = bf16x4;
   __device__ __forceinline__ static f32x4 mma(Op a, Op b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
   }
 };
 template <>
 struct Mma<f16> {
-  using Op = f16x4;
+  static constexpr int KSTEP = 32, NE = 8;
+  using Op = f16x8;
+  using V4 = f16x4;
   __device__ __forceinline__ static f32x4 mma(Op a, Op b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
   }
 };
 template <>
 struct Mma<float> {
+  static constexpr int KSTEP = 16, NE = 4;
   using Op = f32x4;
-  // k slot G of MFMA s is element s of lane group G: k = 4 G + s, the same
-  // k as the 16-bit forms' element s of lane group G.
+  using V4 = f32x4;
+  // k slot G of instruction s is element s of lane group G: k = 4 G + s
   __device__ __forceinline__ static f32x4 mma(Op a, Op b, f32x4 c) {
 #pragma unroll
     for (int s = 0; s < 4; ++s) c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s], b[s], c, 0, 0, 0);
@@ -74,13 +81,16 @@ struct Mma<float> {
   }
 };
 
-// Four accumulator values as an operand of type T (the reference's
-// `.to(q.dtype)` before a product; exact for fp32).
+// The k-step operand made of accumulators: items of the 16-row accumulator
+// tiles acc[0 .. KSTEP / 16), as the input type (the reference's
+// `.to(q.dtype)` before a product; exact for fp32).  Element e of lane group
+// G is row 16 (e / 4) + 4 G + e % 4 of the step, the order GTile::trk reads
+// the matching operand in.
 template <typename T>
-__device__ __forceinline__ typename Mma<T>::Op to_op(const f32x4 v) {
+__device__ __forceinline__ typename Mma<T>::Op to_opk(const f32x4* acc) {
   typename Mma<T>::Op r;
 #pragma unroll
-  for (int e = 0; e < 4; ++e) r[e] = (T)v[e];
+  for (int e = 0; e < Mma<T>::NE; ++e) r[e] = (T)acc[e >> 2][e & 3];
   return r;
 }
 
@@ -89,34 +99,40 @@ __device__ __forceinline__ typename Mma<T>::Op to_op(const f32x4 v) {
 // ---------------------------------------------------------------------------
 template <typename T, int D>
 struct GTile {
-  using Op = typename Mma<T>::Op;
+  using M = Mma<T>;
+  using Op = typename M::Op;
   static constexpr int RB = D * (int)sizeof(T);  // bytes per row (>= 128)
   static constexpr int CH = RB / 16;             // 16-byte chunks per row
   static constexpr int SW = CH < 16 ? CH - 1 : 15;
   __device__ __forceinline__ static int off(int r, int ch) { return r * RB + 16 * (ch ^ (r & SW)); }
-  // byte offset of element (r, c); four elements from c = 4m stay in one chunk
+  // byte offset of element (r, c); 16 bytes from c a multiple of 16 / sizeof(T) stay in one chunk
   __device__ __forceinline__ static int eoff(int r, int c) {
     const int b = c * (int)sizeof(T);
     return off(r, b >> 4) + (b & 15);
   }
-  // Row operand: lane (i, G) gets elements 16 ks + 4 G .. + 3 of row r.
-  // (LDS reads go through the restrict wrappers of common.hpp, so the
-  // compiler does not make them wait for the next tile's copy in flight.)
+  // Row operand: lane (i, G) gets elements KSTEP ks + NE G .. + NE - 1 of row
+  // r (one 16-byte chunk).  (LDS reads go through the restrict wrappers of
+  // common.hpp, so the compiler does not make them wait for the next tile's
+  // copy in flight.)
   __device__ __forceinline__ static Op row(const char* t, int r, int ks, int G) {
-    return lds_load(reinterpret_cast<const Op*>(t + eoff(r, 16 * ks + 4 * G)));
+    return lds_load(reinterpret_cast<const Op*>(t + eoff(r, M::KSTEP * ks + M::NE * G)));
   }
-  // Transposed operand: lane l = 16 G + i gets column c0 + i of rows
-  // rb + 4 G .. rb + 4 G + 3 (c0 a multiple of 16).
-  __device__ __forceinline__ static Op tr(const char* t, int rb, int c0, int l) {
+  // Transposed operand of the k step whose rows start at rb: lane l = 16 G + i
+  // gets column c0 + i of rows rb + 16 (e / 4) + 4 G + e % 4 (c0 a multiple
+  // of 16), the order to_opk builds the other operand in.
+  __device__ __forceinline__ static Op trk(const char* t, int rb, int c0, int l) {
     const int G = l >> 4, i = l & 15;
     if constexpr (sizeof(T) == 2) {
       // ds_read_b64_tr_b16: lane 16G + 4a + b receives element b of the
       // 8-byte chunks addressed by lanes 16G + a + 4e (e = 0..3) as its
-      // elements e.  Lane 16G + j addresses row rb + 4G + j/4 at columns
-      // c0 + 4(j%4) .. + 3, so lane 16G + i receives rows rb + 4G + e of
-      // column c0 + i.
+      // elements e.  Lane 16G + j addresses row r0 + 4G + j/4 at columns
+      // c0 + 4(j%4) .. + 3, so lane 16G + i receives rows r0 + 4G + e of
+      // column c0 + i; two reads cover the step's two 16-row blocks.
       using L4 = std::conditional_t<Elem<T>::kHalf, lds_hf16x4, lds_bf16x4>;
-      return ds_read_tr((const L4*)(t + eoff(rb + 4 * G + (i >> 2), c0 + 4 * (i & 3))));
+      const int r = rb + 4 * G + (i >> 2), c = c0 + 4 * (i & 3);
+      const auto lo = ds_read_tr((const L4*)(t + eoff(r, c)));
+      const auto hi = ds_read_tr((const L4*)(t + eoff(r + 16, c)));
+      return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
     } else {
       Op v;
 #pragma unroll
@@ -187,7 +203,6 @@ __device__ __forceinline__ float col_max(float x) {
 constexpr int kRowsWG = 64;  // compacted rows per fwd / dq workgroup (half a kBQ tile)
 constexpr int kKT = 32;      // keys per K / V tile (fwd, dq)
 constexpr int kKeysWG = 64;  // keys per dk/dv workgroup (half a kBKV tile)
-constexpr int kQS = 16;      // query rows per dk/dv step
 
 // The rows of a fwd / dq workgroup: half (sub) of a kBQ-row tile of the
 // compaction's tile list.  qt describes the whole tile for the zero-row
@@ -249,7 +264,9 @@ __global__ __launch_bounds__(256) void gen_fwd_kernel(const AttnArgs a) {
   using M = Mma<T>;
   using Op = typename M::Op;
   using TL = GTile<T, D>;
-  constexpr int KS = D / 16;  // k steps over the head dim; also 16-column blocks of O
+  constexpr int KS = D / M::KSTEP;      // k steps over the head dim
+  constexpr int DT = D / 16;            // 16-column blocks of O
+  constexpr int KK = kKT / M::KSTEP;    // k steps over a tile's keys
   // two stages of [K tile][V tile], 32 keys each
   auto tK = [](int b) { return logo_smem + b * 2 * kKT * TL::RB; };
   auto tV = [](int b) { return logo_smem + (b * 2 + 1) * kKT * TL::RB; };
@@ -293,10 +310,10 @@ __global__ __launch_bounds__(256) void gen_fwd_kernel(const AttnArgs a) {
   Op qreg[KS];
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks)
-    qreg[ks] = valid ? *reinterpret_cast<const Op*>(q + (t * a.hq + hq) * D + 16 * ks + 4 * G) : Op{};
-  f32x4 oacc[KS];
+    qreg[ks] = valid ? *reinterpret_cast<const Op*>(q + (t * a.hq + hq) * D + M::KSTEP * ks + M::NE * G) : Op{};
+  f32x4 oacc[DT];
 #pragma unroll
-  for (int dt = 0; dt < KS; ++dt) oacc[dt] = f32x4{};
+  for (int dt = 0; dt < DT; ++dt) oacc[dt] = f32x4{};
   float m_run = -INFINITY, l_run = 0.f;
 
   for (int it = 0; it < ntl; ++it) {
@@ -343,12 +360,12 @@ __global__ __launch_bounds__(256) void gen_fwd_kernel(const AttnArgs a) {
     l_run = l_run * alpha + col_sum(ls);
     m_run = m_new;
 #pragma unroll
-    for (int dt = 0; dt < KS; ++dt) oacc[dt] *= alpha;
+    for (int dt = 0; dt < DT; ++dt) oacc[dt] *= alpha;
 #pragma unroll
-    for (int kb16 = 0; kb16 < kKT / 16; ++kb16) {
-      const Op pb = to_op<T>(sacc[kb16]);
+    for (int kk = 0; kk < KK; ++kk) {
+      const Op pb = to_opk<T>(&sacc[kk * (M::KSTEP / 16)]);
 #pragma unroll
-      for (int dt = 0; dt < KS; ++dt) oacc[dt] = M::mma(TL::tr(vb, 16 * kb16, 16 * dt, l), pb, oacc[dt]);
+      for (int dt = 0; dt < DT; ++dt) oacc[dt] = M::mma(TL::trk(vb, M::KSTEP * kk, 16 * dt, l), pb, oacc[dt]);
     }
   }
   if (!valid) return;
@@ -356,11 +373,11 @@ __global__ __launch_bounds__(256) void gen_fwd_kernel(const AttnArgs a) {
   if (G == 0) a.lse[(int64_t)hq * a.n + r] = m_run + log2f(l_run);
   T* orow = o + (t * a.hq + hq) * D + 4 * G;
 #pragma unroll
-  for (int dt = 0; dt < KS; ++dt) {
-    Op ov;
+  for (int dt = 0; dt < DT; ++dt) {
+    typename M::V4 ov;
 #pragma unroll
     for (int j = 0; j < 4; ++j) ov[j] = (T)(oacc[dt][j] * inv);
-    *reinterpret_cast<Op*>(orow + 16 * dt) = ov;
+    *reinterpret_cast<typename M::V4*>(orow + 16 * dt) = ov;
   }
 }
 
@@ -395,7 +412,7 @@ __global__ __launch_bounds__(256) void gen_dq_kernel(const AttnArgs a) {
   using M = Mma<T>;
   using Op = typename M::Op;
   using TL = GTile<T, D>;
-  constexpr int KS = D / 16;
+  constexpr int KS = D / M::KSTEP, DT = D / 16, KB = kKT / 16, KK = kKT / M::KSTEP;
   auto tK = [](int b) { return logo_smem + b * 2 * kKT * TL::RB; };
   auto tV = [](int b) { return logo_smem + (b * 2 + 1) * kKT * TL::RB; };
   const T* q = reinterpret_cast<const T*>(a.q);
@@ -441,13 +458,13 @@ __global__ __launch_bounds__(256) void gen_dq_kernel(const AttnArgs a) {
   Op qreg[KS], dreg[KS];
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) {
-    const int64_t off = (t * a.hq + hq) * D + 16 * ks + 4 * G;
+    const int64_t off = (t * a.hq + hq) * D + M::KSTEP * ks + M::NE * G;
     qreg[ks] = valid ? *reinterpret_cast<const Op*>(q + off) : Op{};
     dreg[ks] = valid ? *reinterpret_cast<const Op*>(dout + off) : Op{};
   }
-  f32x4 dqacc[KS];
+  f32x4 dqacc[DT];
 #pragma unroll
-  for (int dt = 0; dt < KS; ++dt) dqacc[dt] = f32x4{};
+  for (int dt = 0; dt < DT; ++dt) dqacc[dt] = f32x4{};
 
   for (int it = 0; it < ntl; ++it) {
     const int kt = kv_lo + kKT * it, b = it & 1;
@@ -457,35 +474,38 @@ __global__ __launch_bounds__(256) void gen_dq_kernel(const AttnArgs a) {
     if (!wave_active || kt > pw_hi || (win && kt + kKT - 1 < pw_lo - W)) continue;
     const char* kb = tK(b);
     const char* vb = tV(b);
+    f32x4 ds[KB];
 #pragma unroll
-    for (int kb16 = 0; kb16 < kKT / 16; ++kb16) {
+    for (int kb16 = 0; kb16 < KB; ++kb16) {
       f32x4 s = f32x4{}, dp = f32x4{};
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         s = M::mma(TL::row(kb, 16 * kb16 + i, ks, G), qreg[ks], s);
         dp = M::mma(TL::row(vb, 16 * kb16 + i, ks, G), dreg[ks], dp);
       }
-      f32x4 ds;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int key = kt + 16 * kb16 + 4 * G + j;
         const bool vis = key <= p && (!win || key >= p - W);
         const float pr = vis ? exp2f(s[j] * c - lse) : 0.f;
-        ds[j] = pr * (dp[j] - dlt);
+        ds[kb16][j] = pr * (dp[j] - dlt);
       }
-      const Op db = to_op<T>(ds);
+    }
 #pragma unroll
-      for (int dt = 0; dt < KS; ++dt) dqacc[dt] = M::mma(TL::tr(kb, 16 * kb16, 16 * dt, l), db, dqacc[dt]);
+    for (int kk = 0; kk < KK; ++kk) {
+      const Op db = to_opk<T>(&ds[kk * (M::KSTEP / 16)]);
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) dqacc[dt] = M::mma(TL::trk(kb, M::KSTEP * kk, 16 * dt, l), db, dqacc[dt]);
     }
   }
   if (!valid) return;
   T* drow = dq + (t * a.hq + hq) * D + 4 * G;
 #pragma unroll
-  for (int dt = 0; dt < KS; ++dt) {
-    Op dv;
+  for (int dt = 0; dt < DT; ++dt) {
+    typename M::V4 dv;
 #pragma unroll
     for (int j = 0; j < 4; ++j) dv[j] = (T)(dqacc[dt][j] * a.scale);
-    *reinterpret_cast<Op*>(drow + 16 * dt) = dv;
+    *reinterpret_cast<typename M::V4*>(drow + 16 * dt) = dv;
   }
 }
 
@@ -493,10 +513,14 @@ __global__ __launch_bounds__(256) void gen_dq_kernel(const AttnArgs a) {
 // dk / dv: S = Q K^T, P, dP = dO V^T, dS; dV^T += dO^T P, dK^T += Q^T dS,
 // summed over the query heads of the GQA group (:231-337, :444-445)
 // ---------------------------------------------------------------------------
-// LDS: two stages of [Q rows][dO rows][lse][delta][pos], kQS rows each.
+// Query rows per dk/dv step: one k step of the dV / dK products (whose k
+// index is the query row), 32 for 16-bit types and 16 for fp32.
+// LDS: two stages of [Q rows][dO rows][lse][delta][pos], that many rows each.
+template <typename T>
+constexpr int gen_qs() { return Mma<T>::KSTEP; }
 template <typename T, int D>
 constexpr size_t gen_dkv_stage() {
-  return (size_t)2 * kQS * GTile<T, D>::RB + 3 * kQS * sizeof(float);
+  return (size_t)2 * gen_qs<T>() * GTile<T, D>::RB + 3 * gen_qs<T>() * sizeof(float);
 }
 
 template <typename T, int D, bool SPARSE>
@@ -504,7 +528,8 @@ __global__ __launch_bounds__(256) void gen_dkv_kernel(const AttnArgs a) {
   using M = Mma<T>;
   using Op = typename M::Op;
   using TL = GTile<T, D>;
-  constexpr int KS = D / 16;
+  constexpr int KS = D / M::KSTEP, DT = D / 16;
+  constexpr int kQS = gen_qs<T>(), QB = kQS / 16;  // rows per step, 16-row blocks per step
   auto tQ = [](int b) { return logo_smem + b * gen_dkv_stage<T, D>(); };
   auto tO = [](int b) { return logo_smem + b * gen_dkv_stage<T, D>() + kQS * TL::RB; };
   auto sF = [](int b) { return reinterpret_cast<float*>(logo_smem + b * gen_dkv_stage<T, D>() + 2 * kQS * TL::RB); };
@@ -537,16 +562,16 @@ __global__ __launch_bounds__(256) void gen_dkv_kernel(const AttnArgs a) {
 
   Op kreg[KS], vreg[KS];
   {
-    const int64_t off = ((int64_t)(bos + key) * a.h + h) * D + 4 * G;
+    const int64_t off = ((int64_t)(bos + key) * a.h + h) * D + M::NE * G;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      kreg[ks] = valid_k ? *reinterpret_cast<const Op*>(k + off + 16 * ks) : Op{};
-      vreg[ks] = valid_k ? *reinterpret_cast<const Op*>(v + off + 16 * ks) : Op{};
+      kreg[ks] = valid_k ? *reinterpret_cast<const Op*>(k + off + M::KSTEP * ks) : Op{};
+      vreg[ks] = valid_k ? *reinterpret_cast<const Op*>(v + off + M::KSTEP * ks) : Op{};
     }
   }
-  f32x4 dkacc[KS], dvacc[KS];
+  f32x4 dkacc[DT], dvacc[DT];
 #pragma unroll
-  for (int dt = 0; dt < KS; ++dt) {
+  for (int dt = 0; dt < DT; ++dt) {
     dkacc[dt] = f32x4{};
     dvacc[dt] = f32x4{};
   }
@@ -605,27 +630,30 @@ __global__ __launch_bounds__(256) void gen_dkv_kernel(const AttnArgs a) {
         const float* sLse = sF(b);
         const float* sDelta = sLse + kQS;
         const int* sPos = reinterpret_cast<const int*>(sLse + 2 * kQS);
-        f32x4 sacc = f32x4{}, dpacc = f32x4{};
+        f32x4 pr[QB], ds[QB];
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-          sacc = M::mma(TL::row(qb, i, ks, G), kreg[ks], sacc);
-          dpacc = M::mma(TL::row(ob, i, ks, G), vreg[ks], dpacc);
+        for (int qb16 = 0; qb16 < QB; ++qb16) {
+          f32x4 sacc = f32x4{}, dpacc = f32x4{};
+#pragma unroll
+          for (int ks = 0; ks < KS; ++ks) {
+            sacc = M::mma(TL::row(qb, 16 * qb16 + i, ks, G), kreg[ks], sacc);
+            dpacc = M::mma(TL::row(ob, 16 * qb16 + i, ks, G), vreg[ks], dpacc);
+          }
+          // item j: query row rs + 16 qb16 + 4 G + j, key `key`
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int rj = 16 * qb16 + 4 * G + j;
+            const int pq = sPos[rj];
+            const bool vis = valid_k && key <= pq && (!win || key >= pq - W);
+            pr[qb16][j] = vis ? exp2f(sacc[j] * c - sLse[rj]) : 0.f;
+            ds[qb16][j] = pr[qb16][j] * (dpacc[j] - sDelta[rj]);
+          }
         }
-        // item j: query row rs + 4 G + j, key `key`
-        f32x4 pr, ds;
+        const Op pb = to_opk<T>(pr), db = to_opk<T>(ds);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int rj = 4 * G + j;
-          const int pq = sPos[rj];
-          const bool vis = valid_k && key <= pq && (!win || key >= pq - W);
-          pr[j] = vis ? exp2f(sacc[j] * c - sLse[rj]) : 0.f;
-          ds[j] = pr[j] * (dpacc[j] - sDelta[rj]);
-        }
-        const Op pb = to_op<T>(pr), db = to_op<T>(ds);
-#pragma unroll
-        for (int dt = 0; dt < KS; ++dt) {
-          dvacc[dt] = M::mma(TL::tr(ob, 0, 16 * dt, l), pb, dvacc[dt]);
-          dkacc[dt] = M::mma(TL::tr(qb, 0, 16 * dt, l), db, dkacc[dt]);
+        for (int dt = 0; dt < DT; ++dt) {
+          dvacc[dt] = M::mma(TL::trk(ob, 0, 16 * dt, l), pb, dvacc[dt]);
+          dkacc[dt] = M::mma(TL::trk(qb, 0, 16 * dt, l), db, dkacc[dt]);
         }
       }
       if (more) stash(b ^ 1);  // stage b ^ 1 was last read in the previous step
@@ -638,15 +666,15 @@ __global__ __launch_bounds__(256) void gen_dkv_kernel(const AttnArgs a) {
   T* dk = reinterpret_cast<T*>(a.dk) + off;
   T* dv = reinterpret_cast<T*>(a.dv) + off;
 #pragma unroll
-  for (int dt = 0; dt < KS; ++dt) {
-    Op kv, vv;
+  for (int dt = 0; dt < DT; ++dt) {
+    typename M::V4 kv, vv;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       kv[j] = (T)(dkacc[dt][j] * a.scale);
       vv[j] = (T)dvacc[dt][j];
     }
-    *reinterpret_cast<Op*>(dk + 16 * dt) = kv;
-    *reinterpret_cast<Op*>(dv + 16 * dt) = vv;
+    *reinterpret_cast<typename M::V4*>(dk + 16 * dt) = kv;
+    *reinterpret_cast<typename M::V4*>(dv + 16 * dt) = vv;
   }
 }
 
