@@ -131,3 +131,46 @@ def test_dense_and_window_branches_at_d256(gpu, window):
     ro, (rdq, rdk, rdv) = _oracle(q, k, v, None, cu, do, window=window)
     for name, x, r in (("o", o, ro), ("dq", qg.grad, rdq), ("dk", kg.grad, rdk), ("dv", vg.grad, rdv)):
         assert_within(f"{name} window={window}", x, r, max_abs=2e-2 * max(1.0, float(np.abs(r).max()) / 2))
+
+
+@pytest.mark.parametrize("dtype,d", [(torch.float32, 64), (torch.bfloat16, 256)])
+def test_generic_zero_rows_and_empty_lanes(gpu, dtype, d):
+    """The generic kernels' zero rows: an empty selection (every output and
+    gradient exactly zero except dk / dv, which are zero too since no row
+    sees any key), and a per-head selection where one head has no rows and
+    another one row, over packed segments with an empty one; against the
+    oracle where rows exist."""
+    n, hq, h = 300, 4, 2
+    g = gen(990 + d)
+    q, k, v = (torch.randn(n, x, d, generator=g).to(dtype) for x in (hq, h, h))
+    do = torch.randn(n, hq, d, generator=g).to(dtype)
+    cu = torch.tensor([0, 100, 100, 300], dtype=torch.int32)
+    none = torch.zeros(n, dtype=torch.bool)
+    o, (dq, dk, dv) = _run(q, k, v, none, cu, gpu, do)
+    for name, x in (("o", o), ("dq", dq), ("dk", dk), ("dv", dv)):
+        assert int(x.count_nonzero()) == 0, f"{name} not zero for an empty selection"
+    sel = torch.rand(n, hq, generator=g) < 0.5
+    sel[:, 1] = False          # a head without rows
+    sel[:, 2] = False
+    sel[150, 2] = True         # a head with one row
+    o, (dq, dk, dv) = _run(q, k, v, sel, cu, gpu, do)
+    ro, (rdq, rdk, rdv) = _oracle(q, k, v, sel, cu, do)
+    bound = (1e-3, 1e-4) if dtype == torch.float32 else (2e-2, 2e-3)
+    for name, x, r in (("o", o, ro), ("dq", dq, rdq), ("dk", dk, rdk), ("dv", dv, rdv)):
+        assert_within(f"{name} {dtype} d={d} empty lanes", x, r, max_abs=bound[0], mean_abs=bound[1])
+    assert int(o[:, 1].count_nonzero()) == 0 and int(dq[:, 1].count_nonzero()) == 0
+
+
+def test_fp32_value_dim_differs_from_key_dim(gpu):
+    """fp32 with K = 64, V = 48 (padded to 64 on the fp32 kernels), GQA."""
+    n, hq, h, K, V = 400, 4, 1, 64, 48
+    g = gen(995)
+    q, k = torch.randn(n, hq, K, generator=g), torch.randn(n, h, K, generator=g)
+    v, do = torch.randn(n, h, V, generator=g), torch.randn(n, hq, V, generator=g)
+    sel = torch.rand(n, generator=g) < 0.5
+    cu = torch.tensor([0, 400], dtype=torch.int32)
+    o, (dq, dk, dv) = _run(q, k, v, sel, cu, gpu, do)
+    assert o.shape == (n, hq, V) and dv.shape == v.shape and o.dtype == torch.float32
+    ro, (rdq, rdk, rdv) = _oracle(q, k, v, sel, cu, do)
+    for name, x, r in (("o", o, ro), ("dq", dq, rdq), ("dk", dk, rdk), ("dv", dv, rdv)):
+        assert_within(f"{name} fp32 K=64 V=48", x, r, max_abs=F32_MAX, mean_abs=F32_MEAN)
