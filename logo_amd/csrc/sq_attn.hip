@@ -5,7 +5,13 @@
 // their real position (:33-121); the backward recomputes P from the stored
 // log2-domain LSE (:141-228 dq, :231-337 dk/dv) with delta = rowsum(o * dO)
 // (:124-138); dk/dv of a GQA group are summed over its query heads (:444-445).
-// Differences in structure, not in results:
+// One difference in rounding: in sparse mode the query rows are pre-scaled
+// and rounded once, q' = bf16(-scale log2(e) q) (the forward's registers and
+// the backward's q_sel copies), where the reference scales the fp32 product
+// (:93).  That adds up to 2^-9 relative error per q element; measured against
+// float64 with scores up to +-43 in log2 units, o and the gradients stay
+// within 1.0-1.5x of the error of the reference's own rounding chain.
+// Differences in structure:
 //   * the forward gathers q rows and scatters o rows inside the kernel (the
 //     reference materialises q_sel / o_sel, :461 :469); the backward's delta
 //     pass writes compacted, head-major copies of q and dO ([HQ, N, D]) so the
