@@ -54,7 +54,7 @@ extern "C" {
 /* Message of the calling thread's last error ("" if none). */
 const char* logo_last_error(void);
 
-/* ABI version of this library (5: head dim 256, fp32, logo_sq_generic). */
+/* ABI version of this library (6: logo_head_linear_grad_acc; 5: head dim 256, fp32, logo_sq_generic). */
 int logo_abi_version(void);
 
 /*
@@ -386,6 +386,19 @@ size_t logo_head_linear_dw_workspace_bytes(int64_t n_tokens, int heads, int d);
  */
 int logo_head_linear_dw(const void* x, int64_t ldx, const void* dy, int64_t ldy, void* dw, void* workspace,
                         int64_t n_tokens, int heads, int d, int dtype, void* stream);
+
+/*
+ * Input gradient of logo_head_linear summed with another gradient of the same
+ * tensor: dx[n, h, :] = bf16(bf16(dy[n, h, :] W_h^T) + add[n, h, :]), the
+ * product rounded as logo_head_linear's and the sum as an eager bf16 add.
+ * Rows at dy + n * lddy, add + n * ldadd, dx + n * lddx (elements; dx may be
+ * add itself).  No counterpart in the reference: it folds autograd's
+ * accumulation of the two gradients of the layer's q, k and v (the local
+ * branch through RoPE, the global one through this map,
+ * logo/layers/logo.py:86-94, :121-158) into the map's backward.
+ */
+int logo_head_linear_grad_acc(const void* dy, int64_t lddy, const void* w, const void* add, int64_t ldadd, void* dx,
+                              int64_t lddx, int64_t n_tokens, int heads, int d, int dtype, void* stream);
 
 /*
  * Residual add + RMSNorm of the decoder: s_out = r + x (bf16, as the eager

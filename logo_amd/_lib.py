@@ -48,6 +48,7 @@ SIGNATURES = {
     "logo_head_linear": ([_P, _I64, _P, _P, _I64, _I64, _I, _I, _I, _I, _P], _I),
     "logo_head_linear_dw_workspace_bytes": ([_I64, _I, _I], _SZ),
     "logo_head_linear_dw": ([_P, _I64, _P, _I64, _P, _P, _I64, _I, _I, _I, _P], _I),
+    "logo_head_linear_grad_acc": ([_P, _I64, _P, _P, _I64, _P, _I64, _I64, _I, _I, _I, _P], _I),
     "logo_decode_fused_workspace_bytes": ([_I, _I, _I, _I], _SZ),
     "logo_decode_attn_fused": ([_P, _P, _P, _P, _I64, _I, _P, _P, _P, _P, _I64, _I, _P, _P, _I, _P, _P, _F, _P, _P, _I,
                                 _I, _I, _I, _F, _I, _P], _I),

@@ -12,6 +12,11 @@
 //     32x32x16 MFMA chain per 32 output columns), each wave loading its next
 //     pass's rows while it computes the current one; each wave's output tile
 //     goes through LDS so the stores are 16-byte row chunks.
+//     With an addend (ADD), each stored element is bf16(bf16(y) + a): the
+//     input gradient summed with the other gradient of the same tensor, with
+//     the two roundings of a bf16 product followed by an eager bf16 add, in
+//     place of a separate add pass (a may alias y: each lane reads its chunk
+//     of a before it writes the same chunk of y).
 //   * head_linear_dw_kernel: the weight gradient dW_h = X_h^T dY_h over a chunk
 //     of tokens per workgroup (64-token tiles of X_h and dY_h copied global ->
 //     LDS, both operands read transposed), fp32 partials per chunk, then
@@ -33,10 +38,12 @@ struct HlArgs {
   bf16* y;        // y[n * ldy + h * D + c]
   int64_t ldy;
   int64_t n;
+  const bf16* add;  // ADD: add[n * ldadd + h * D + c]
+  int64_t ldadd;
 };
 
-// TW = false: y = x W_h;  TW = true: y = x W_h^T.
-template <int D, bool TW>
+// TW = false: y = x W_h;  TW = true: y = x W_h^T.  ADD: y = bf16(bf16(y) + add).
+template <int D, bool TW, bool ADD = false>
 __global__ __launch_bounds__(256) void head_linear_kernel(const HlArgs a) {
   constexpr int RS = D + 8;  // padded LDS row (elements)
   constexpr int DS = D / 16, CT = D / 32;
@@ -93,8 +100,15 @@ __global__ __launch_bounds__(256) void head_linear_kernel(const HlArgs a) {
 #pragma unroll
     for (int it = 0; it < 32 * D / 8 / 64; ++it) {
       const int idx = it * 64 + l, rr = idx / (D / 8), c8 = (idx % (D / 8)) * 8;
-      const bf16x8 v = lds_load(reinterpret_cast<const bf16x8*>(yw + rr * RS + c8));
-      if (r0 + rr < a.n) *reinterpret_cast<bf16x8*>(a.y + (r0 + rr) * a.ldy + (int64_t)h * D + c8) = v;
+      bf16x8 v = lds_load(reinterpret_cast<const bf16x8*>(yw + rr * RS + c8));
+      if (r0 + rr < a.n) {
+        if constexpr (ADD) {
+          const bf16x8 ad = *reinterpret_cast<const bf16x8*>(a.add + (r0 + rr) * a.ldadd + (int64_t)h * D + c8);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) v[j] = (bf16)((float)v[j] + (float)ad[j]);
+        }
+        *reinterpret_cast<bf16x8*>(a.y + (r0 + rr) * a.ldy + (int64_t)h * D + c8) = v;
+      }
     }
   }
 }
@@ -188,8 +202,9 @@ using namespace logo;
 
 static constexpr size_t kHlDwSmem = (size_t)4 * 64 * 128 * sizeof(bf16);
 
-extern "C" int logo_head_linear(const void* x, int64_t ldx, const void* w, void* y, int64_t ldy, int64_t n_tokens,
-                                int heads, int d, int transpose_w, int dtype, void* stream) {
+static int head_linear_launch(const void* x, int64_t ldx, const void* w, const void* add, int64_t ldadd, void* y,
+                              int64_t ldy, int64_t n_tokens, int heads, int d, int transpose_w, int dtype,
+                              void* stream) {
   LOGO_REQUIRE(dtype == LOGO_DTYPE_BF16, "only bf16 tensors are supported");
   LOGO_REQUIRE(d == 64 || d == 128, "head dim %d unsupported (64 or 128)", d);
   LOGO_REQUIRE(n_tokens >= 0 && heads >= 1, "bad token / head counts");
@@ -197,6 +212,11 @@ extern "C" int logo_head_linear(const void* x, int64_t ldx, const void* w, void*
                "row strides must cover heads * d and be multiples of 8");
   LOGO_REQUIRE(x && w && y, "null pointer argument");
   LOGO_REQUIRE(((uintptr_t)x | (uintptr_t)w | (uintptr_t)y) % 16 == 0, "x, w, y must be 16-byte aligned");
+  if (add) {
+    LOGO_REQUIRE(ldadd >= (int64_t)heads * d && ldadd % 8 == 0 && (uintptr_t)add % 16 == 0,
+                 "the addend's row stride must cover heads * d and be a multiple of 8, the addend 16-byte aligned");
+    LOGO_REQUIRE(transpose_w, "the addend form is the input gradient (transpose_w = 1)");
+  }
   if (n_tokens == 0) return LOGO_OK;
   HlArgs a{};
   a.x = static_cast<const bf16*>(x);
@@ -205,20 +225,36 @@ extern "C" int logo_head_linear(const void* x, int64_t ldx, const void* w, void*
   a.y = static_cast<bf16*>(y);
   a.ldy = ldy;
   a.n = n_tokens;
+  a.add = static_cast<const bf16*>(add);
+  a.ldadd = ldadd;
   const int64_t per = (int64_t)kHlRows * kHlPasses;
   const int64_t nblk = (n_tokens + per - 1) / per;
   LOGO_REQUIRE(nblk < ((int64_t)1 << 31), "too many tokens");
   const dim3 grid((unsigned)nblk, (unsigned)heads);
   hipStream_t st = as_stream(stream);
   if (d == 128) {
-    if (transpose_w) hipLaunchKernelGGL((head_linear_kernel<128, true>), grid, dim3(256), 0, st, a);
+    if (add) hipLaunchKernelGGL((head_linear_kernel<128, true, true>), grid, dim3(256), 0, st, a);
+    else if (transpose_w) hipLaunchKernelGGL((head_linear_kernel<128, true>), grid, dim3(256), 0, st, a);
     else hipLaunchKernelGGL((head_linear_kernel<128, false>), grid, dim3(256), 0, st, a);
   } else {
-    if (transpose_w) hipLaunchKernelGGL((head_linear_kernel<64, true>), grid, dim3(256), 0, st, a);
+    if (add) hipLaunchKernelGGL((head_linear_kernel<64, true, true>), grid, dim3(256), 0, st, a);
+    else if (transpose_w) hipLaunchKernelGGL((head_linear_kernel<64, true>), grid, dim3(256), 0, st, a);
     else hipLaunchKernelGGL((head_linear_kernel<64, false>), grid, dim3(256), 0, st, a);
   }
   LOGO_LAUNCH_CHECK("head_linear_kernel");
   return LOGO_OK;
+}
+
+extern "C" int logo_head_linear(const void* x, int64_t ldx, const void* w, void* y, int64_t ldy, int64_t n_tokens,
+                                int heads, int d, int transpose_w, int dtype, void* stream) {
+  return head_linear_launch(x, ldx, w, nullptr, 0, y, ldy, n_tokens, heads, d, transpose_w, dtype, stream);
+}
+
+extern "C" int logo_head_linear_grad_acc(const void* dy, int64_t lddy, const void* w, const void* add,
+                                         int64_t ldadd, void* dx, int64_t lddx, int64_t n_tokens, int heads, int d,
+                                         int dtype, void* stream) {
+  LOGO_REQUIRE(add, "null pointer argument");
+  return head_linear_launch(dy, lddy, w, add, ldadd, dx, lddx, n_tokens, heads, d, 1, dtype, stream);
 }
 
 extern "C" size_t logo_head_linear_dw_workspace_bytes(int64_t n_tokens, int heads, int d) {

@@ -29,7 +29,7 @@ import torch.nn.functional as F
 
 from .ops.decode import LogoKVCache, decode_attn, decode_attn_fused, decode_qkv
 from .ops.epilogue import logo_epilogue
-from .ops.glue import head_linear, head_proj, rms_norm, rope, rope_apply_
+from .ops.glue import attn_inputs, head_linear, head_proj, rms_norm, rope, rope_apply_
 from .ops.sq_attn import dense_causal_attn, sq_full_attn, swa_attn
 
 __all__ = ["LoGoConfig", "LoGoAttention", "Attention", "RMSNorm", "rope_cos_sin", "apply_rope", "position_ids_for"]
@@ -311,6 +311,19 @@ class LoGoAttention(nn.Module):
         return (_per_head_linear(q, self.q_global_proj), _per_head_linear(k, self.k_global_proj),
                 _per_head_linear(v, self.v_global_proj))
 
+    def _fused_inputs_ok(self, hidden_states) -> bool:
+        """Training-size bf16 calls of the linear_proj form take the one-node
+        projections (q, k, v, gate) + global maps + RoPE (``attn_inputs``; cos
+        / sin must be ``[B, T, D]`` bf16 too): its backward sums the gradient
+        pairs of q, k, v and the four of h inside its own launches."""
+        if self.global_qk_param == "scale_offset" or not torch.is_grad_enabled():
+            return False
+        B, T, _ = hidden_states.shape
+        ws = (self.q_proj.weight, self.k_proj.weight, self.v_proj.weight, self.gate_proj.weight, self.q_global_proj,
+              self.k_global_proj, self.v_global_proj)
+        return (self.head_dim == 128 and B * T > 64
+                and all(t.is_cuda and t.dtype == torch.bfloat16 for t in (hidden_states, *ws)))
+
     def _fuse(self, local, glob, gate):
         """Context norms + gate mask + fusion; ``local/glob [B, T, H, D]``."""
         if self.use_context_norm:
@@ -388,15 +401,26 @@ class LoGoAttention(nn.Module):
                     self.global_token_count.add_((gate >= self.gate_thres).sum().float())
                     self.total_token_count.add_(gate.numel())
             return self.o_proj(out), None, past_key_value
-        q = self.q_proj(hidden_states).view(B, T, H, D)
-        k = self.k_proj(hidden_states).view(B, T, HK, D)
-        v = self.v_proj(hidden_states).view(B, T, HK, D)
-        gq, gk, gv = self._global_qkv(q, k, v)
-        gate = torch.sigmoid(self.gate_proj(hidden_states))  # [B, T, 1]
-
-        cos, sin = _cos_sin(self, B, T, hidden_states.device, q.dtype, position_ids, cu_seqlens, past_key_value,
-                            position_embeddings)
-        q, k, gq, gk = _rope_all((q, k, gq, gk), cos, sin)
+        cs = lambda dtype: _cos_sin(self, B, T, hidden_states.device, dtype, position_ids,  # noqa: E731
+                                    cu_seqlens, past_key_value, position_embeddings)
+        cos = sin = None
+        if self._fused_inputs_ok(hidden_states):
+            cos, sin = cs(hidden_states.dtype)
+        if cos is not None and all(t.is_cuda and t.dtype == torch.bfloat16 and tuple(t.shape) == (B, T, D)
+                                   for t in (cos, sin)):
+            q, k, v, gq, gk, gv, logit = attn_inputs(
+                hidden_states, self.q_proj, self.k_proj, self.v_proj, self.gate_proj,
+                (self.q_global_proj, self.k_global_proj, self.v_global_proj), cos, sin, H, HK)
+            gate = torch.sigmoid(logit)  # [B, T, 1]
+        else:
+            q = self.q_proj(hidden_states).view(B, T, H, D)
+            k = self.k_proj(hidden_states).view(B, T, HK, D)
+            v = self.v_proj(hidden_states).view(B, T, HK, D)
+            gq, gk, gv = self._global_qkv(q, k, v)
+            gate = torch.sigmoid(self.gate_proj(hidden_states))  # [B, T, 1]
+            if cos is None:
+                cos, sin = cs(q.dtype)
+            q, k, gq, gk = _rope_all((q, k, gq, gk), cos, sin)
 
         if past_key_value is not None and T == 1:
             out = self._decode(q, k, v, gq, gk, gv, gate, past_key_value)

@@ -10,11 +10,12 @@ tensors).
 """
 
 import torch
+import torch.nn.functional as F
 
 from .. import _lib
 
 __all__ = ["rope_apply_", "rope", "RopeFunction", "rms_norm", "head_proj", "add_rms_norm", "silu_mul",
-           "head_linear", "HeadLinearFunction"]
+           "head_linear", "HeadLinearFunction", "head_linear_grad_acc", "attn_inputs", "AttnInputsFunction"]
 
 
 def _rope_checked(tensors, cos, sin, what):
@@ -201,6 +202,43 @@ def _head_linear_launch(x, w, transpose_w: bool):
     return y.view(x.shape)
 
 
+def _head_linear_dw(x, dy):
+    """``dw[h] = sum_n x[n, h, :]^T dy[n, h, :]`` as bf16 ``[H, D, D]``."""
+    x2, n, ldx = _rows(x)
+    d2, _, ldy = _rows(dy)
+    H, D = x2.shape[1], x2.shape[2]
+    lib = _lib.lib()
+    ws = torch.empty((lib.logo_head_linear_dw_workspace_bytes(n, H, D) + 3) // 4, dtype=torch.float32,
+                     device=x.device)
+    dw = torch.empty(H, D, D, dtype=torch.bfloat16, device=x.device)
+    _lib.launch("logo_head_linear_dw", lib.logo_head_linear_dw, _lib.ptr(x2), ldx, _lib.ptr(d2), ldy,
+                _lib.ptr(dw), _lib.ptr(ws), n, H, D, _lib.DTYPE_BF16, _lib.stream_of(x2))
+    return dw
+
+
+def head_linear_grad_acc(dy, w, add, out):
+    """``out = bf16(bf16(dy @ w^T) + add)`` per head: the input gradient of
+    ``head_linear`` summed with another gradient ``add`` of the same tensor,
+    rounded exactly as the two-pass chain (the product, then an eager bf16
+    add).  ``dy``, ``add`` ``[N, H, D]`` bf16 with dense heads; ``out`` a
+    ``[N, H, D]`` view with dense heads and any 8-aligned row stride (for
+    instance a column slice of a wider buffer), or ``add`` itself."""
+    _lib.require_gpu(dy, w, add, out)
+    d2, n, lddy = _rows(dy)
+    a2, na, ldadd = _rows(add)
+    H, D = d2.shape[1], d2.shape[2]
+    if out.dim() != 3 or tuple(out.shape) != (n, H, D) or out.stride(2) != 1 or out.stride(1) != D \
+            or out.stride(0) % 8 or out.data_ptr() % 16 or out.dtype != torch.bfloat16:
+        raise ValueError("head_linear_grad_acc: out must be a bf16 [N, H, D] view with dense heads")
+    if na != n or a2.shape[1:] != d2.shape[1:] or tuple(w.shape) != (H, D, D):
+        raise ValueError("head_linear_grad_acc: dy, add and w shapes disagree")
+    lib = _lib.lib()
+    _lib.launch("logo_head_linear_grad_acc", lib.logo_head_linear_grad_acc, _lib.ptr(d2), lddy,
+                _lib.ptr(w), _lib.ptr(a2), ldadd, _lib.ptr(out), out.stride(0), n, H, D, _lib.DTYPE_BF16,
+                _lib.stream_of(d2))
+    return out
+
+
 class HeadLinearFunction(torch.autograd.Function):
     """``y[..., h, :] = x[..., h, :] @ w[h]`` with its gradients, every pass on
     the ``[..., H, D]`` layout in place (no head-major copies)."""
@@ -218,16 +256,7 @@ class HeadLinearFunction(torch.autograd.Function):
         if ctx.needs_input_grad[0]:
             dx = _head_linear_launch(dy, w, True)
         if ctx.needs_input_grad[1]:
-            x2, n, ldx = _rows(x)
-            d2, _, ldy = _rows(dy)
-            H, D = x2.shape[1], x2.shape[2]
-            lib = _lib.lib()
-            ws = torch.empty((lib.logo_head_linear_dw_workspace_bytes(n, H, D) + 3) // 4, dtype=torch.float32,
-                             device=x.device)
-            dw = torch.empty(H, D, D, dtype=torch.bfloat16, device=x.device)
-            _lib.launch("logo_head_linear_dw", lib.logo_head_linear_dw, _lib.ptr(x2), ldx, _lib.ptr(d2), ldy,
-                        _lib.ptr(dw), _lib.ptr(ws), n, H, D, _lib.DTYPE_BF16, _lib.stream_of(x2))
-            dw = dw.to(w.dtype)
+            dw = _head_linear_dw(x, dy).to(w.dtype)
         return dx, dw
 
 
@@ -241,3 +270,97 @@ def head_linear(x, w):
     if tuple(w.shape) != (H, D, D):
         raise ValueError(f"head_linear: weight {tuple(w.shape)} does not match heads {H}, dim {D}")
     return HeadLinearFunction.apply(x, w)
+
+
+class AttnInputsFunction(torch.autograd.Function):
+    """The attention inputs of a LoGo layer (linear_proj form) from its hidden
+    states, as one autograd node (logo/layers/logo.py:86-94, :112-158):
+
+        q, k, v    = h Wq^T + bq, h Wk^T + bk, h Wv^T + bv   (hipBLASLt GEMMs)
+        logit      = h wg^T + bg                            (the gate, before its sigmoid)
+        gq, gk, gv = per-head maps of q, k, v               (head_linear)
+        returns      rope(q), rope(k), v, rope(gq), rope(gk), gv, logit   (one RoPE launch)
+
+    The forward launches exactly the ops of the unfused chain.  The backward
+    differs in where sums happen, not in the products: q, k and v each feed
+    the local branch and their global map, and h feeds four projections, so
+    autograd would add gradient pairs in separate passes.  Here the RoPE
+    backward runs once over the four rotated gradients, the global maps' input
+    gradients are written by ``head_linear_grad_acc`` together with the local
+    gradients (the same bf16 values as the separate add) straight into one
+    ``[N, (H + 2 HK) D + 8]`` buffer whose last columns hold the gate logit's
+    gradient and seven zeros, and dh is one GEMM of that buffer with the
+    stacked projection weights (seven zero rows pad K to a multiple of 8).
+    dh is therefore summed in fp32 before one rounding, where the chain
+    rounds each projection's share first; the weight gradients are the
+    chain's products, read from the buffer's column slices."""
+
+    @staticmethod
+    def forward(ctx, h, wq, bq, wk, bk, wv, bv, wg, bg, gwq, gwk, gwv, cos, sin, heads, kv_heads):
+        B, T, C = h.shape
+        D = gwq.shape[-1]
+        q = F.linear(h, wq, bq).view(B, T, heads, D)
+        k = F.linear(h, wk, bk).view(B, T, kv_heads, D)
+        v = F.linear(h, wv, bv).view(B, T, kv_heads, D)
+        logit = F.linear(h, wg, bg)
+        gws = [w.contiguous() for w in (gwq, gwk, gwv)]
+        gq, gk, gv = (_head_linear_launch(x, w, False) for x, w in zip((q, k, v), gws))
+        cos, sin, n, _ = _rope_checked([q, k, gq, gk], cos, sin, "attn_inputs")
+        qr, kr, gqr, gkr = _rope_launch([q, k, gq, gk], cos, sin, n, D, inverse=False)
+        ctx.save_for_backward(h, wq, wk, wv, wg, q, k, v, *gws, cos, sin)
+        ctx.dims = (B, T, C, heads, kv_heads, D, n)
+        return qr, kr, v, gqr, gkr, gv, logit
+
+    @staticmethod
+    def backward(ctx, dqr, dkr, dv, dgqr, dgkr, dgv, dlogit):
+        h, wq, wk, wv, wg, q, k, v, gwq, gwk, gwv, cos, sin = ctx.saved_tensors
+        B, T, C, H, HK, D, n = ctx.dims
+        need = ctx.needs_input_grad
+        bf = lambda g: g.to(torch.bfloat16).contiguous()  # noqa: E731
+        dqr, dkr, dv, dgqr, dgkr, dgv = (bf(g) for g in (dqr, dkr, dv, dgqr, dgkr, dgv))
+        dqa, dka, dgq, dgk = _rope_launch([dqr, dkr, dgqr, dgkr], cos, sin, n, D, inverse=True)
+        cols = (H * D, HK * D, HK * D, 8)
+        dy = torch.empty(n, sum(cols), dtype=torch.bfloat16, device=h.device)
+        outs = dy.split(cols, dim=1)
+        for g, w, a, o, nh in zip((dgq, dgk, dgv), (gwq, gwk, gwv), (dqa, dka, dv), outs, (H, HK, HK)):
+            head_linear_grad_acc(g.view(n, nh, D), w, a.view(n, nh, D), o.view(n, nh, D))
+        outs[3].zero_()
+        outs[3][:, 0].copy_(dlogit.reshape(n))
+        dgw = [_head_linear_dw(x, g).to(w.dtype) if need[9 + i] else None
+               for i, (x, g, w) in enumerate(zip((q, k, v), (dgq, dgk, dgv), (gwq, gwk, gwv)))]
+        h2 = h.reshape(n, C)
+        dh = None
+        if need[0]:
+            wcat = torch.cat([wq, wk, wv, wg, wg.new_zeros(7, C)], dim=0)
+            dh = torch.mm(dy, wcat).view(B, T, C)
+        # weight gradients one GEMM per projection, each reading its column
+        # slice of dy in place (one stacked [(H + 2 HK) D + 8, C] product
+        # takes ~1.5x as long at these shapes)
+        dws = [torch.mm(o.t(), h2) if need[1 + 2 * i] else None for i, o in enumerate(outs[:3])]
+        dws.append(torch.mm(dlogit.reshape(n, 1).to(h2.dtype).t(), h2) if need[7] else None)
+        dbs = [None] * 4
+        if need[2] or need[4] or need[6] or need[8]:
+            dbs = [g if need[2 + 2 * i] else None for i, g in enumerate(dy.sum(0).split(cols))]
+            if dbs[3] is not None:
+                dbs[3] = dbs[3][:1]
+        return (dh, dws[0], dbs[0], dws[1], dbs[1], dws[2], dbs[2], dws[3], dbs[3], *dgw, None, None, None, None)
+
+
+def attn_inputs(h, q_proj, k_proj, v_proj, gate_proj, global_projs, cos, sin, heads, kv_heads):
+    """``(rope(q), rope(k), v, rope(gq), rope(gk), gv, gate_logit)`` of hidden
+    states ``h [B, T, C]`` through the ``nn.Linear`` projections (the gate's
+    with one output) and the per-head global maps ``global_projs = (Wgq, Wgk,
+    Wgv)`` (each ``[H_i, D, D]``), with ``cos/sin [B, T, D]``: ``[B, T, H_i,
+    D]`` tensors and the logit ``[B, T, 1]``; bf16 ROCm tensors, D = 128."""
+    _lib.require_gpu(h, cos, sin, *global_projs)
+    lins = (q_proj, k_proj, v_proj, gate_proj)
+    ws = (*(m.weight for m in lins), *global_projs)
+    if h.dtype != torch.bfloat16 or any(w.dtype != torch.bfloat16 for w in ws):
+        raise ValueError("attn_inputs takes bf16 tensors")
+    D = global_projs[0].shape[-1]
+    if D != 128 or tuple(global_projs[0].shape) != (heads, D, D) or tuple(global_projs[1].shape) != (kv_heads, D, D):
+        raise ValueError("attn_inputs: global maps must be [H, 128, 128] / [HK, 128, 128]")
+    if gate_proj.weight.shape[0] != 1:
+        raise ValueError("attn_inputs: the gate projection has one output")
+    args = [t for m in lins for t in (m.weight, m.bias)]
+    return AttnInputsFunction.apply(h, *args, *global_projs, cos, sin, heads, kv_heads)

@@ -22,7 +22,7 @@ def test_header_symbols_are_exported():
 
 def test_abi_version_and_workspace():
     lib = _lib.lib()
-    assert lib.logo_abi_version() == 5
+    assert lib.logo_abi_version() == 6
     # the generic kernels serve d = 256 and fp32; they never split
     assert [lib.logo_sq_generic(d, t) for d in (64, 128, 256) for t in (_lib.DTYPE_BF16, _lib.DTYPE_F16)] == \
         [0, 0, 0, 0, 1, 1]
@@ -83,6 +83,19 @@ def test_compact_rejects_bad_arguments():
     assert lib.logo_compact(p, -1, 1, p, 1, p, p, p, p, None) == 1
     assert lib.logo_compact(p, 16, 0, p, 1, p, p, p, p, None) == 1
     assert "lanes" in lib.logo_last_error().decode()
+
+
+def test_head_linear_grad_acc_rejects_bad_arguments():
+    """The addend form of the per-head map refuses a null addend, an
+    unaligned or too-short addend row stride and unsupported head dims, all
+    before any HIP call (pointers are placeholders)."""
+    lib = _lib.lib()
+    p = ctypes.c_void_p(256)
+    args = lambda add, ldadd, d: (p, 4 * d, p, add, ldadd, p, 4 * d, 100, 4, d, _lib.DTYPE_BF16, None)  # noqa: E731
+    for add, ldadd, d, msg in ((None, 512, 128, "null"), (p, 500, 128, "addend"), (p, 256, 128, "addend"),
+                               (p, 384, 96, "head dim")):
+        assert lib.logo_head_linear_grad_acc(*args(add, ldadd, d)) == 1
+        assert msg in lib.logo_last_error().decode()
 
 
 def test_ops_refuse_cpu_tensors():

@@ -2,6 +2,7 @@
 
 import pytest
 import torch
+import torch.nn.functional as F
 
 from logo_amd.layers import apply_rope, rope_cos_sin
 from logo_amd.ops.glue import rms_norm, rope, rope_apply_
@@ -151,3 +152,104 @@ def test_head_linear_fwd_bwd_matches_fp32(gpu, N, H, D, pad):
         assert close(wa.grad, wr.grad, 2.0 ** -7)
     y2 = head_linear(x, w)
     assert torch.equal(y2, y.detach())
+
+
+@pytest.mark.parametrize("N,H,D,layout", [(2500, 4, 128, "slice"), (77, 3, 64, "inplace"), (513, 2, 128, "dense")])
+def test_head_linear_grad_acc_equals_product_then_add(gpu, N, H, D, layout):
+    """``head_linear_grad_acc`` is bit-identical to the two-pass chain it
+    replaces (the input-gradient product, then an eager bf16 add), written
+    into a column slice of a wider buffer (the other columns untouched), in
+    place over the addend, or into a dense tensor; token counts off the
+    512-row workgroup grid."""
+    from logo_amd.ops.glue import _head_linear_launch, head_linear_grad_acc
+
+    g = gen(7 * N + H + D)
+    w = (torch.eye(D) + 0.05 * torch.randn(H, D, D, generator=g)).bfloat16().to(gpu)
+    dy = torch.randn(N, H, D, generator=g).bfloat16().to(gpu)
+    add = torch.randn(N, H, D, generator=g).bfloat16().to(gpu)
+    ref = (_head_linear_launch(dy, w, True).float() + add.float()).bfloat16()
+    assert torch.equal(ref, _head_linear_launch(dy, w, True) + add)  # the eager add rounds the same way
+    if layout == "slice":
+        buf = torch.full((N, 3 * H * D), 7.0, dtype=torch.bfloat16, device=gpu)
+        out = buf[:, H * D:2 * H * D].view(N, H, D)
+        head_linear_grad_acc(dy, w, add, out)
+        assert torch.equal(out, ref)
+        assert bool((buf[:, :H * D] == 7).all()) and bool((buf[:, 2 * H * D:] == 7).all())
+    elif layout == "inplace":
+        a2 = add.clone()
+        head_linear_grad_acc(dy, w, a2, a2)
+        assert torch.equal(a2, ref)
+    else:
+        out = torch.empty_like(dy)
+        head_linear_grad_acc(dy, w, add, out)
+        assert torch.equal(out, ref)
+
+
+def _attn_inputs_chain(h, lin, gws, cos, sin, H, HK):
+    """The unfused chain (separate projections, head_linear nodes, one RoPE
+    node): the autograd graph that sums gradient pairs in separate adds."""
+    from logo_amd.ops.glue import head_linear
+
+    B, T, _ = h.shape
+    q, k, v = (F.linear(h, m.weight, m.bias).view(B, T, n, 128) for m, n in zip(lin, (H, HK, HK)))
+    logit = F.linear(h, lin[3].weight, lin[3].bias)
+    gq, gk, gv = (head_linear(x, w) for x, w in zip((q, k, v), gws))
+    qr, kr, gqr, gkr = rope([q, k, gq, gk], cos, sin)
+    return qr, kr, v, gqr, gkr, gv, logit
+
+
+@pytest.mark.parametrize("bias", [False, True])
+def test_attn_inputs_matches_unfused_chain(gpu, bias):
+    """The one-node layer inputs (q, k, v and gate projections, global maps,
+    RoPE): forward outputs and the global maps' weight gradients
+    bit-identical to the unfused chain; dh (summed in fp32 before one
+    rounding, where the chain rounds each projection's share first) and the
+    projections' weight and bias gradients within bf16 rounding of an fp32
+    autograd reference, and at least as close to it as the chain's."""
+    from logo_amd.ops.glue import attn_inputs
+
+    torch.manual_seed(5)
+    B, T, C, H, HK = 2, 300, 512, 4, 2
+    g = gen(31 + bias)
+    lin = [torch.nn.Linear(C, n, bias=bias).to(gpu).bfloat16() for n in (H * 128, HK * 128, HK * 128, 1)]
+    gws = [(torch.eye(128) + 0.05 * torch.randn(n, 128, 128, generator=g)).bfloat16().to(gpu).requires_grad_()
+           for n in (H, HK, HK)]
+    pos = torch.randint(0, 8000, (B, T), generator=g).to(gpu)
+    cos, sin = rope_cos_sin(pos, 128, 10000.0, torch.bfloat16)
+    h = (torch.randn(B, T, C, generator=g) * 0.5).bfloat16().to(gpu).requires_grad_()
+    gos = [torch.randn(B, T, n, 128, generator=g).bfloat16().to(gpu) for n in (H, HK, HK, H, HK, HK)]
+    gos.append(torch.randn(B, T, 1, generator=g).bfloat16().to(gpu))
+    params = [h, *[p for m in lin for p in m.parameters()], *gws]
+
+    def grads(fn):
+        for p in params:
+            p.grad = None
+        outs = fn()
+        torch.autograd.backward(outs, gos)
+        return [o.detach() for o in outs], [p.grad.clone() for p in params]
+
+    fo, fg = grads(lambda: attn_inputs(h, *lin, gws, cos, sin, H, HK))
+    assert fo[6].shape == (B, T, 1)
+    co, cg = grads(lambda: _attn_inputs_chain(h, lin, gws, cos, sin, H, HK))
+    for a, b in zip(fo, co):
+        assert torch.equal(a, b)
+    for a, b in zip(fg[-3:], cg[-3:]):
+        assert torch.equal(a, b)
+    # fp32 reference of the same chain
+    hr = h.detach().float().requires_grad_()
+    lr = [(m.weight.detach().float().requires_grad_(), None if m.bias is None else m.bias.detach().float()
+           .requires_grad_()) for m in lin]
+    gr = [w.detach().float().requires_grad_() for w in gws]
+    q, k, v = (F.linear(hr, w, b).view(B, T, n, 128) for (w, b), n in zip(lr, (H, HK, HK)))
+    gq, gk, gv = (torch.einsum("bthd,hde->bthe", x, w) for x, w in zip((q, k, v), gr))
+    c32, s32 = cos.float(), sin.float()
+    outs = [apply_rope(q, c32, s32), apply_rope(k, c32, s32), v, apply_rope(gq, c32, s32), apply_rope(gk, c32, s32),
+            gv, F.linear(hr, *lr[3])]
+    torch.autograd.backward(outs, [x.float() for x in gos])
+    refs = [hr.grad, *[p.grad for wb in lr for p in wb if p is not None]]
+    for i, r in enumerate(refs):
+        f, c = fg[i].float(), cg[i].float()
+        scale = r.abs().max()
+        ef, ec = (f - r).abs().max() / scale, (c - r).abs().max() / scale
+        assert ef <= 2e-2, f"grad {i}: fused max rel err {ef:.3e}"
+        assert ef <= ec * 1.5 + 1e-3, f"grad {i}: fused {ef:.3e} vs chain {ec:.3e}"
