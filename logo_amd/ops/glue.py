@@ -290,10 +290,11 @@ class AttnInputsFunction(torch.autograd.Function):
     gradients (the same bf16 values as the separate add) straight into one
     ``[N, (H + 2 HK) D + 8]`` buffer whose last columns hold the gate logit's
     gradient and seven zeros, and dh is one GEMM of that buffer with the
-    stacked projection weights (seven zero rows pad K to a multiple of 8).
-    dh is therefore summed in fp32 before one rounding, where the chain
-    rounds each projection's share first; the weight gradients are the
-    chain's products, read from the buffer's column slices."""
+    stacked projection weights (seven zero rows pad K to a multiple of 8),
+    and the q / k / v weight gradients one GEMM of the buffer's first
+    columns with h.  dh is therefore summed in fp32 before one rounding,
+    where the chain rounds each projection's share first; each weight
+    gradient is the chain's product (same operands, one GEMM launch)."""
 
     @staticmethod
     def forward(ctx, h, wq, bq, wk, bk, wv, bv, wg, bg, gwq, gwk, gwv, cos, sin, heads, kv_heads):
@@ -333,10 +334,15 @@ class AttnInputsFunction(torch.autograd.Function):
         if need[0]:
             wcat = torch.cat([wq, wk, wv, wg, wg.new_zeros(7, C)], dim=0)
             dh = torch.mm(dy, wcat).view(B, T, C)
-        # weight gradients one GEMM per projection, each reading its column
-        # slice of dy in place (one stacked [(H + 2 HK) D + 8, C] product
-        # takes ~1.5x as long at these shapes)
-        dws = [torch.mm(o.t(), h2) if need[1 + 2 * i] else None for i, o in enumerate(outs[:3])]
+        # q / k / v weight gradients as one GEMM over the buffer's first
+        # (H + 2 HK) D columns (read in place), split into the three weights:
+        # at cfg4 ~725 us against 3 x ~280 us, where each 2048 x 2048 product
+        # fills half the GPU; the gate's column stays out of it (with it, M =
+        # 6152 takes ~1000 us) and is a GEMV of its own
+        if need[1] and need[3] and need[5]:
+            dws = list(torch.mm(dy[:, :sum(cols[:3])].t(), h2).split(cols[:3], dim=0))
+        else:
+            dws = [torch.mm(o.t(), h2) if need[1 + 2 * i] else None for i, o in enumerate(outs[:3])]
         dws.append(torch.mm(dlogit.reshape(n, 1).to(h2.dtype).t(), h2) if need[7] else None)
         dbs = [None] * 4
         if need[2] or need[4] or need[6] or need[8]:
