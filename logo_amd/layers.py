@@ -183,8 +183,10 @@ class VarlenPlan:
         return (flat if self.keep is None else flat.index_select(0, self.keep))[None]
 
     def unpack(self, y, B: int, T: int):
-        """``[1, N_kept, H, D]`` -> ``[B, T, H, D]``, dropped tokens zero (pad_input)."""
-        y = y[0]
+        """``[1, N_kept, H, D]`` -> ``[B, T, H, D]``, dropped tokens zero (pad_input).
+        A reshape, not ``y[0]``: the backward of an index allocates a zero
+        ``[1, N, H, D]`` gradient and copies into it."""
+        y = y.reshape(y.shape[1:])
         if self.keep is None:
             return y.view(B, T, y.shape[-2], y.shape[-1])
         out = y.new_zeros(B * T, y.shape[-2], y.shape[-1])
