@@ -8,7 +8,7 @@
 //   * head_linear_kernel: y[n, h, :] = x[n, h, :] W_h (or W_h^T for the input
 //     gradient), reading x rows with their head offset and writing y rows the
 //     same way.  A workgroup stages W_h in LDS once (rows padded, conflict-free
-//     16-byte reads) and runs kHlPasses passes of 128 tokens (32 per wave, one
+//     16-byte reads) and runs up to kHlMaxPasses passes of 128 tokens (32 per wave, one
 //     32x32x16 MFMA chain per 32 output columns), each wave loading its next
 //     pass's rows while it computes the current one; each wave's output tile
 //     goes through LDS so the stores are 16-byte row chunks.
@@ -27,8 +27,11 @@
 
 namespace logo {
 
-constexpr int kHlRows = 128;    // tokens per pass (4 waves x 32)
-constexpr int kHlPasses = 4;    // passes per workgroup (W_h staged once)
+int device_cus();  // sq_attn.hip
+
+constexpr int kHlRows = 128;     // tokens per pass (4 waves x 32)
+constexpr int kHlMaxPasses = 8;  // passes per workgroup (W_h staged once)
+constexpr int kHlWgsPerCu = 2;   // 66 KB of LDS per workgroup
 constexpr int kHlChunk = 1024;  // tokens per weight-gradient workgroup
 
 struct HlArgs {
@@ -40,6 +43,7 @@ struct HlArgs {
   int64_t n;
   const bf16* add;  // ADD: add[n * ldadd + h * D + c]
   int64_t ldadd;
+  int passes;       // 128-token passes per workgroup
 };
 
 // TW = false: y = x W_h;  TW = true: y = x W_h^T.  ADD: y = bf16(bf16(y) + add).
@@ -66,7 +70,7 @@ __global__ __launch_bounds__(256) void head_linear_kernel(const HlArgs a) {
   const int wave = threadIdx.x >> 6, l = threadIdx.x & 63, i = l & 31, g = l >> 5;
   bf16* yw = ys[wave];
   // rows past n read the last row; they are not stored
-  auto row_of = [&](int pass) { return ((int64_t)blockIdx.x * kHlPasses + pass) * kHlRows + 32 * wave; };
+  auto row_of = [&](int pass) { return ((int64_t)blockIdx.x * a.passes + pass) * kHlRows + 32 * wave; };
   auto load_x = [&](int64_t r0, bf16x8* dst) {
     const bf16* xr = a.x + (r0 + i < a.n ? r0 + i : a.n - 1) * a.ldx + (int64_t)h * D + 8 * g;
 #pragma unroll
@@ -74,13 +78,26 @@ __global__ __launch_bounds__(256) void head_linear_kernel(const HlArgs a) {
   };
   bf16x8 nx[DS];  // the next pass's rows, loaded while this pass computes
   if (row_of(0) < a.n) load_x(row_of(0), nx);
-  for (int pass = 0; pass < kHlPasses; ++pass) {
+  for (int pass = 0; pass < a.passes; ++pass) {
     const int64_t r0 = row_of(pass);
     if (r0 >= a.n) break;  // wave-uniform; no barrier follows
     bf16x8 av[DS];
 #pragma unroll
     for (int s = 0; s < DS; ++s) av[s] = nx[s];
-    if (pass + 1 < kHlPasses && row_of(pass + 1) < a.n) load_x(row_of(pass + 1), nx);
+    if (pass + 1 < a.passes && row_of(pass + 1) < a.n) load_x(row_of(pass + 1), nx);
+    // ADD: this pass's addend chunks (the ones this lane stores below), all
+    // loaded before the MFMAs; loaded in the store loop, each would wait out
+    // its own latency (y may alias add, so no load moves above a store)
+    constexpr int NIT = 32 * D / 8 / 64;
+    bf16x8 adv[ADD ? NIT : 1];
+    if constexpr (ADD) {
+#pragma unroll
+      for (int it = 0; it < NIT; ++it) {
+        const int idx = it * 64 + l, rr = idx / (D / 8), c8 = (idx % (D / 8)) * 8;
+        const int64_t row = r0 + rr < a.n ? r0 + rr : a.n - 1;
+        adv[it] = *reinterpret_cast<const bf16x8*>(a.add + row * a.ldadd + (int64_t)h * D + c8);
+      }
+    }
     f32x16 acc[CT];
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) {
@@ -98,14 +115,13 @@ __global__ __launch_bounds__(256) void head_linear_kernel(const HlArgs a) {
       for (int jj = 0; jj < 16; ++jj) yw[(8 * (jj / 4) + 4 * g + (jj % 4)) * RS + 32 * ct + i] = (bf16)acc[ct][jj];
     // each lane stores 16-byte chunks of the wave's 32 output rows
 #pragma unroll
-    for (int it = 0; it < 32 * D / 8 / 64; ++it) {
+    for (int it = 0; it < NIT; ++it) {
       const int idx = it * 64 + l, rr = idx / (D / 8), c8 = (idx % (D / 8)) * 8;
       bf16x8 v = lds_load(reinterpret_cast<const bf16x8*>(yw + rr * RS + c8));
       if (r0 + rr < a.n) {
         if constexpr (ADD) {
-          const bf16x8 ad = *reinterpret_cast<const bf16x8*>(a.add + (r0 + rr) * a.ldadd + (int64_t)h * D + c8);
 #pragma unroll
-          for (int j = 0; j < 8; ++j) v[j] = (bf16)((float)v[j] + (float)ad[j]);
+          for (int j = 0; j < 8; ++j) v[j] = (bf16)((float)v[j] + (float)adv[it][j]);
         }
         *reinterpret_cast<bf16x8*>(a.y + (r0 + rr) * a.ldy + (int64_t)h * D + c8) = v;
       }
@@ -227,7 +243,13 @@ static int head_linear_launch(const void* x, int64_t ldx, const void* w, const v
   a.n = n_tokens;
   a.add = static_cast<const bf16*>(add);
   a.ldadd = ldadd;
-  const int64_t per = (int64_t)kHlRows * kHlPasses;
+  // as many passes as fill every workgroup slot once (W_h staged fewer times:
+  // at 32K tokens x 16 heads, 8 passes took 54 / 49 / 96 us for the forward,
+  // input gradient and addend form against 58 / 55 / 108 us with 4)
+  const int cus = device_cus();
+  const int64_t fill = cus > 0 ? n_tokens * heads / ((int64_t)kHlRows * kHlWgsPerCu * cus) : 4;
+  a.passes = (int)std::min<int64_t>(kHlMaxPasses, std::max<int64_t>(1, fill));
+  const int64_t per = (int64_t)kHlRows * a.passes;
   const int64_t nblk = (n_tokens + per - 1) / per;
   LOGO_REQUIRE(nblk < ((int64_t)1 << 31), "too many tokens");
   const dim3 grid((unsigned)nblk, (unsigned)heads);
