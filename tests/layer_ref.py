@@ -146,9 +146,12 @@ def logo_layer_ref(h, p, cfg, sel_bt, cu=None, backend="hip", store_dtype=None, 
     h = R(h)  # the layer input is stored too: its gradient is rounded once summed
     B, T, C = h.shape
     H, HK, D = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
-    q = R(h @ p["q_proj.weight"].T).view(B, T, H, D)
-    k = R(h @ p["k_proj.weight"].T).view(B, T, HK, D)
-    v = R(h @ p["v_proj.weight"].T).view(B, T, HK, D)
+    # nn.Linear, with the bias when the config has one (attention_bias /
+    # attention_out_bias, logo/layers/logo.py:50-58)
+    lin = lambda x, name: x @ p[name + ".weight"].T + (p[name + ".bias"] if name + ".bias" in p else 0)  # noqa: E731
+    q = R(lin(h, "q_proj")).view(B, T, H, D)
+    k = R(lin(h, "k_proj")).view(B, T, HK, D)
+    v = R(lin(h, "v_proj")).view(B, T, HK, D)
     if cfg.global_qk_param == "linear_proj":
         gq = R(torch.einsum("bthd,hde->bthe", q, p["q_global_proj"]))
         gk = R(torch.einsum("bthd,hde->bthe", k, p["k_global_proj"]))
@@ -196,7 +199,7 @@ def logo_layer_ref(h, p, cfg, sel_bt, cu=None, backend="hip", store_dtype=None, 
     glob = _rmsnorm(glob, p["context_norm_global.weight"], cfg.rms_norm_eps, R).reshape(B, T, C)
     g = gate.masked_fill(~sel_bt.reshape(B, T, 1), 0.0)
     out = R(R(R(1 - g) * local) + R(g * glob))
-    return R(out @ p["o_proj.weight"].T)
+    return R(lin(out, "o_proj"))
 
 
 def plain_attn_layer_ref(h, p, cfg, cu=None):

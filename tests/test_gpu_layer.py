@@ -46,11 +46,18 @@ def _make(cfg, dev, seed):
     return layer.to(dev).to(torch.bfloat16)
 
 
-@pytest.mark.parametrize("backend,cu", [("hip", None), ("triton", [0, 100, 101, 300]), ("flash", None)])
-def test_layer_fwd_bwd(gpu, backend, cu):
+@pytest.mark.parametrize("backend,cu,bias", [("hip", None, False), ("triton", [0, 100, 101, 300], False),
+                                             ("flash", None, False), ("hip", None, True)])
+def test_layer_fwd_bwd(gpu, backend, cu, bias):
     cfg = LoGoConfig(hidden_size=512, num_attention_heads=4, num_hidden_layers=1,
-                     sparse_full_attn_backend=backend, gate_thres_init=0.5)
+                     sparse_full_attn_backend=backend, gate_thres_init=0.5, attention_bias=bias,
+                     attention_out_bias=bias)
     layer = _make(cfg, gpu, 0)
+    if bias:
+        with torch.no_grad():
+            for name, prm in layer.named_parameters():
+                if name.endswith(".bias"):
+                    prm.normal_(0, 0.1)
     layer.train()
     B, T = (2, 150) if cu is None else (1, 300)
     g = gen(1)
@@ -69,8 +76,11 @@ def test_layer_fwd_bwd(gpu, backend, cu):
     ref.backward(dout.double().cpu())
     _scaled("out", out, ref)
     _scaled("dh", h.grad, h64.grad)
-    for name in ("q_proj.weight", "k_proj.weight", "v_proj.weight", "o_proj.weight", "q_global_proj",
-                 "gate_proj.weight", "context_norm_local.weight", "context_norm_global.weight"):
+    names = ["q_proj.weight", "k_proj.weight", "v_proj.weight", "o_proj.weight", "q_global_proj",
+             "gate_proj.weight", "context_norm_local.weight", "context_norm_global.weight"]
+    if bias:
+        names += ["q_proj.bias", "k_proj.bias", "v_proj.bias", "o_proj.bias"]
+    for name in names:
         prm = dict(layer.named_parameters())[name]
         assert_close(name, params[name].grad, prm.grad.double().cpu(), 2e-2 if name == "gate_proj.weight" else 1e-2)
     assert layer.global_token_count.item() == sel.sum().item()
