@@ -15,7 +15,9 @@ namespace logo {
 // operands) and the dQ accumulators live in AGPRs; S and dP in VGPRs.
 // Keys are processed in 32-key halves; step (t, h) of key tile t runs
 //   X: the S^T / dP^T MFMAs of the next half ((t, 1) or (t + 1, 0)) while the
-//      VALU forms P = exp2(S c - lse) and dS = P (dP - delta) of half (t, h);
+//      VALU forms P = exp2(S c - lse) and dS = P (dP - delta) of half (t, h)
+//      (delta, and in sparse mode lse, enter as the accumulators' start
+//      values);
 //   Y: the dQ^T += K^T dS^T MFMAs of half (t, h).
 // K and V tiles (64 keys) sit in two LDS slots each (slot = tile & 1).
 // K(t + 1) is copied during step (t, 0), after K(t - 1)'s last read (step
@@ -73,15 +75,18 @@ __global__ __launch_bounds__(128) LOGO_OCC_DQ64 void sq_dq64_kernel(const AttnAr
   // Sparse mode reads the delta phase's copies q_sel = bf16(-c q) and
   // do_sel = -dO, so the S accumulators start from lse (a splat C operand,
   // fixed for the workgroup's rows): P = exp2(-S'); dP' = -dP gives the
-  // negated dS = P (dP' + delta), which leaves dQ negated.  (A delta splat
-  // as well would save the add but needs 32 more registers than the kernel
-  // has.)
+  // negated dS = P (dP' + delta), which leaves dQ negated.  The dP
+  // accumulators start from a delta splat in the same way (+delta in sparse
+  // mode, -delta in dense mode), so dS is one multiply per score.
   constexpr bool NEG = SPARSE;
-  f32x16 c_lse[2];
+  f32x16 c_lse[2], c_del[2];
 #pragma unroll
   for (int b = 0; b < 2; ++b)
 #pragma unroll
-    for (int j = 0; j < 16; ++j) c_lse[b][j] = NEG ? lse_q[b] : 0.f;
+    for (int j = 0; j < 16; ++j) {
+      c_lse[b][j] = NEG ? lse_q[b] : 0.f;
+      c_del[b][j] = NEG ? delta_q[b] : -delta_q[b];
+    }
   const float dq_mul = NEG ? -a.scale : a.scale;
 
   f32x16 dqacc[2][DT];  // AGPRs
@@ -171,7 +176,7 @@ __global__ __launch_bounds__(128) LOGO_OCC_DQ64 void sq_dq64_kernel(const AttnAr
             if constexpr (B == 1) __builtin_amdgcn_sched_barrier(0);
             if constexpr (DOX) {
               const E8 bop = KIND ? doreg[B][DSI] : qreg[B][DSI];
-              const f32x16 c0 = (NEG && !KIND) ? c_lse[B] : f32x16{};
+              const f32x16 c0 = KIND ? c_del[B] : (NEG ? c_lse[B] : f32x16{});
               sp[H ^ 1][B][KIND] = mfma32(o, bop, DSI == 0 ? c0 : sp[H ^ 1][B][KIND]);
             }
             if constexpr (DOV) {
@@ -187,7 +192,7 @@ __global__ __launch_bounds__(128) LOGO_OCC_DQ64 void sq_dq64_kernel(const AttnAr
                   if (WINDOW) vis = vis && off >= hi[B] - W;
                   if (!vis) pv = 0.f;
                 }
-                float dsv = NEG ? pv * (dpv + delta_q[B]) : pv * (dpv - delta_q[B]);
+                float dsv = pv * dpv;
                 pin(dsv);
                 sp[H][B][0][JJ] = pv;
                 sp[H][B][1][JJ] = dsv;
