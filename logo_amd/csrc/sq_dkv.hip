@@ -229,8 +229,7 @@ __global__ __launch_bounds__(256) LOGO_OCC_DKV void sq_dkv_kernel(const AttnArgs
         auto mfma_a = [&](auto u_c, auto a_c) {
           constexpr int U = decltype(u_c)::value, A = decltype(a_c)::value;
           constexpr int QQ = A / NS, KK = A % NS;
-          E8 op = opA[U * 2 * NS + A];
-          pin(op);
+          const E8 op = opA[U * 2 * NS + A];
           if constexpr (KK < DS) {
             const f32x16 c0 = NEG ? cat16(l4[U][QQ]) : f32x16{};
             sacc[QQ] = mfma32(op, kreg[KK], KK == 0 ? c0 : sacc[QQ]);
@@ -242,8 +241,7 @@ __global__ __launch_bounds__(256) LOGO_OCC_DKV void sq_dkv_kernel(const AttnArgs
         auto mfma_c = [&](auto u_c, auto c_c) {
           constexpr int U = decltype(u_c)::value, C = decltype(c_c)::value;
           constexpr int QQ = C / NS, KK = C % NS, HH = (KK % DS) / DT, DTI = KK % DT;
-          E8 op = opC[U * 2 * NS + C];
-          pin(op);
+          const E8 op = opC[U * 2 * NS + C];
           // D = 128: P and dS are packed at least four slots before their MFMAs
           // read them; D = 64 (four-slot blocks) keeps the leading wait states
           if constexpr (DS >= 8) {
@@ -255,13 +253,21 @@ __global__ __launch_bounds__(256) LOGO_OCC_DKV void sq_dkv_kernel(const AttnArgs
           }
         };
         // row item jj of half qq: items 4m..4m+3 are query rows 32qq + 8m + 4g + e.
-        // P items leave P in sacc (fp32) and pack pairs into pbf; dS items leave
-        // dS in pacc and pack pairs into dbf.
-        auto p_item = [&](auto u_c, int qq, auto jj_c) {
-          constexpr int U = decltype(u_c)::value, JJ = decltype(jj_c)::value;
-          constexpr int M = JJ / 4, E = JJ % 4;
+        // An item's inputs are anchored ahead of its slot's MFMA (which then
+        // separates the anchor from the VALU op that reads them), its
+        // arithmetic follows the MFMA, and pairs of items are packed to bf16
+        // one slot later: a VALU op right behind an anchor or an exp2 that
+        // wrote its input would cost an s_nop.  P items leave P in sacc
+        // (fp32), dS items leave dS in pacc.
+        auto p_pre = [&](int qq, auto jj_c) {
+          constexpr int JJ = decltype(jj_c)::value;
           float sv = sacc[qq][JJ];
           pin(sv);
+          return sv;
+        };
+        auto p_item = [&](auto u_c, int qq, auto jj_c, float sv) {
+          constexpr int U = decltype(u_c)::value, JJ = decltype(jj_c)::value;
+          constexpr int M = JJ / 4, E = JJ % 4;
           // NEG: sv = lse - c s, so P = exp2(-sv) (the negation is a source modifier)
           float pv = NEG ? fast_exp2(-sv) : fast_exp2(fmaf(sv, c, -l4[U][qq][M][E]));
           if constexpr (MASK) {
@@ -272,25 +278,39 @@ __global__ __launch_bounds__(256) LOGO_OCC_DKV void sq_dkv_kernel(const AttnArgs
           }
           pin(pv);
           sacc[qq][JJ] = pv;
+        };
+        auto p_pack = [&](int qq, auto jj_c) {
+          constexpr int JJ = decltype(jj_c)::value;
           if constexpr (JJ % 2 == 1) {
             pbf[qq][JJ / 8][JJ % 8 - 1] = (EL)sacc[qq][JJ - 1];
-            pbf[qq][JJ / 8][JJ % 8] = (EL)pv;
+            pbf[qq][JJ / 8][JJ % 8] = (EL)sacc[qq][JJ];
           }
+          // a finished group stays here: sunk to its MFMA, the packing would
+          // write the operand too close before it
+          if constexpr (JJ % 8 == 7) pin(pbf[qq][JJ / 8]);
         };
-        auto ds_item = [&](auto u_c, int qq, auto jj_c) {
-          constexpr int U = decltype(u_c)::value, JJ = decltype(jj_c)::value;
-          constexpr int M = JJ / 4, E = JJ % 4;
-          float pv = sacc[qq][JJ], dpv = pacc[qq][JJ];
+        auto ds_pre = [&](int qq, auto jj_c, float& pv, float& dpv) {
+          constexpr int JJ = decltype(jj_c)::value;
+          pv = sacc[qq][JJ];
+          dpv = pacc[qq][JJ];
           pin(pv);
           pin(dpv);
+        };
+        auto ds_item = [&](auto u_c, int qq, auto jj_c, float pv, float dpv) {
+          constexpr int U = decltype(u_c)::value, JJ = decltype(jj_c)::value;
+          constexpr int M = JJ / 4, E = JJ % 4;
           // NEG: dpv = delta - dP, and dS is kept negated (dO was negated too)
           float dsv = NEG ? pv * dpv : pv * (dpv - d4[U][qq][M][E]);
           pin(dsv);
           pacc[qq][JJ] = dsv;
+        };
+        auto ds_pack = [&](int qq, auto jj_c) {
+          constexpr int JJ = decltype(jj_c)::value;
           if constexpr (JJ % 2 == 1) {
             dbf[qq][JJ / 8][JJ % 8 - 1] = (EL)pacc[qq][JJ - 1];
-            dbf[qq][JJ / 8][JJ % 8] = (EL)dsv;
+            dbf[qq][JJ / 8][JJ % 8] = (EL)pacc[qq][JJ];
           }
+          if constexpr (JJ % 8 == 7) pin(dbf[qq][JJ / 8]);
         };
         // stats of (sub-tile u, half qq, group m) are read DS/2 slots before
         // the first item of group m needs them; the P items of half qq start at
@@ -319,6 +339,20 @@ __global__ __launch_bounds__(256) LOGO_OCC_DKV void sq_dkv_kernel(const AttnArgs
           constexpr int BLK = L / DS, K = L % DS;
           using UC = std::integral_constant<int, U>;
           __builtin_amdgcn_sched_barrier(0);
+          // the slot's P items (blocks 1, 2, 4, 5) and dS items (blocks 3, 6)
+          constexpr bool HASP = BLK == 1 || BLK == 2 || BLK == 4 || BLK == 5, HASD = BLK == 3 || BLK == 6;
+          constexpr int QP = BLK >= 4, JP = ((BLK - 1) % 3) * DS + K, QD = BLK == 6;
+          float sv[IPP], pv[IPD], dpv[IPD];
+          if constexpr (HASP)
+            static_for<IPP>([&](auto i_c) {
+              constexpr int I = decltype(i_c)::value;
+              sv[I] = p_pre(QP, std::integral_constant<int, JP * IPP + I>{});
+            });
+          if constexpr (HASD)
+            static_for<IPD>([&](auto i_c) {
+              constexpr int I = decltype(i_c)::value;
+              ds_pre(QD, std::integral_constant<int, K * IPD + I>{}, pv[I], dpv[I]);
+            });
           if constexpr (L < 2 * NS) mfma_a(UC{}, std::integral_constant<int, L>{});
           else mfma_c(UC{}, std::integral_constant<int, L - 2 * NS>{});
           if constexpr (S + PF < NSUB * SPT) load_for_slot(std::integral_constant<int, S + PF>{});
@@ -336,17 +370,29 @@ __global__ __launch_bounds__(256) LOGO_OCC_DKV void sq_dkv_kernel(const AttnArgs
                 if (!NEG && dstats_slot(u, qq, m) == S) load_dstats(u, qq, m);
               }
             }
-          if constexpr (BLK == 1 || BLK == 2 || BLK == 4 || BLK == 5) {
-            constexpr int QQ = BLK >= 4, J0 = ((BLK - 1) % 3) * DS + K;
+          if constexpr (HASP)
             static_for<IPP>([&](auto i_c) {
-              p_item(UC{}, QQ, std::integral_constant<int, J0 * IPP + decltype(i_c)::value>{});
+              constexpr int I = decltype(i_c)::value;
+              p_item(UC{}, QP, std::integral_constant<int, JP * IPP + I>{}, sv[I]);
             });
-          }
-          if constexpr (BLK == 3 || BLK == 6) {
-            constexpr int QQ = BLK == 6;
+          if constexpr (HASD)
             static_for<IPD>([&](auto i_c) {
-              ds_item(UC{}, QQ, std::integral_constant<int, K * IPD + decltype(i_c)::value>{});
+              constexpr int I = decltype(i_c)::value;
+              ds_item(UC{}, QD, std::integral_constant<int, K * IPD + I>{}, pv[I], dpv[I]);
             });
+          // the previous slot's items, packed (no item is formed in block 0 or
+          // 7, so a sub-tile's packs stay inside it; a group of eight is first
+          // read DT slots after its last pack at the earliest)
+          if constexpr (L >= 1) {
+            constexpr int LB = (L - 1) / DS, LK = (L - 1) % DS;
+            if constexpr (LB == 1 || LB == 2 || LB == 4 || LB == 5)
+              static_for<IPP>([&](auto i_c) {
+                p_pack(LB >= 4, std::integral_constant<int, (((LB - 1) % 3) * DS + LK) * IPP + decltype(i_c)::value>{});
+              });
+            if constexpr (LB == 3 || LB == 6)
+              static_for<IPD>([&](auto i_c) {
+                ds_pack(LB == 6, std::integral_constant<int, LK * IPD + decltype(i_c)::value>{});
+              });
           }
         });
         __builtin_amdgcn_sched_barrier(0);

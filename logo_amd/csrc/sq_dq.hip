@@ -162,18 +162,43 @@ __global__ __launch_bounds__(128) LOGO_OCC_DQ64 void sq_dq64_kernel(const AttnAr
       static_for<NX + NY>([&](auto s_c) {
         constexpr int S = decltype(s_c)::value;
         __builtin_amdgcn_sched_barrier(0);
+        // dS = P dP' of the items whose P was formed in slot s - 1: one slot
+        // after their exp2, so that no VALU op reads an exp2 result right
+        // behind it (a one-wait-state hazard, which would cost an s_nop)
+        auto ds_items = [&](auto b_c, auto s_c) {
+          constexpr int B = decltype(b_c)::value, SP = decltype(s_c)::value;
+          static_for<IX>([&](auto e_c) {
+            constexpr int JJ = SP * IX + decltype(e_c)::value;
+            float dsv = sp[H][B][0][JJ] * sp[H][B][1][JJ];
+            pin(dsv);
+            sp[H][B][1][JJ] = dsv;
+          });
+        };
+        // bf16 packing of a group of eight dS items, one slot after the dS of
+        // its last item (its P formed in slot s - 2)
+        auto pack = [&](auto b_c, auto s_c) {
+          constexpr int B = decltype(b_c)::value, SP = decltype(s_c)::value;
+          constexpr int LAST = SP * IX + IX - 1;
+          if constexpr (SP >= 0 && LAST % 8 == 7) dsb[B][LAST / 8] = acc_to<EL>(sp[H][B][1], LAST / 8);
+        };
         if constexpr (S < NX) {
           // one wave per SIMD issues in order: each MFMA is followed by the
           // VALU items of its row block, which run under it
           constexpr int DSI = S / 2, KIND = S % 2;
           E8 o;
-          if constexpr (DOX) {
-            o = op[S];
-            pin(o);
-          }
+          if constexpr (DOX) o = op[S];
           static_for<2>([&](auto b_c) {
             constexpr int B = decltype(b_c)::value;
             if constexpr (B == 1) __builtin_amdgcn_sched_barrier(0);
+            // the slot's scores, anchored ahead of the MFMA (which then
+            // separates the anchor from the exp2 that reads them)
+            float sv[IX];
+            if constexpr (DOV)
+              static_for<IX>([&](auto e_c) {
+                constexpr int E = decltype(e_c)::value;
+                sv[E] = sp[H][B][0][S * IX + E];
+                pin(sv[E]);
+              });
             if constexpr (DOX) {
               const E8 bop = KIND ? doreg[B][DSI] : qreg[B][DSI];
               const f32x16 c0 = KIND ? c_del[B] : (NEG ? c_lse[B] : f32x16{});
@@ -181,32 +206,36 @@ __global__ __launch_bounds__(128) LOGO_OCC_DQ64 void sq_dq64_kernel(const AttnAr
             }
             if constexpr (DOV) {
               static_for<IX>([&](auto e_c) {
-                constexpr int JJ = S * IX + decltype(e_c)::value;
-                float sv = sp[H][B][0][JJ], dpv = sp[H][B][1][JJ];
-                pin(sv);
-                pin(dpv);
-                float pv = NEG ? fast_exp2(-sv) : fast_exp2(fmaf(sv, c, -lse_q[B]));
+                constexpr int E = decltype(e_c)::value, JJ = S * IX + E;
+                float pv = NEG ? fast_exp2(-sv[E]) : fast_exp2(fmaf(sv[E], c, -lse_q[B]));
                 if constexpr (MASK) {
                   constexpr int off = 8 * (JJ / 4) + (JJ % 4);
                   bool vis = off <= hi[B];
                   if (WINDOW) vis = vis && off >= hi[B] - W;
                   if (!vis) pv = 0.f;
                 }
-                float dsv = pv * dpv;
-                pin(dsv);
                 sp[H][B][0][JJ] = pv;
-                sp[H][B][1][JJ] = dsv;
-                if constexpr (JJ % 8 == 7) dsb[B][JJ / 8] = acc_to<EL>(sp[H][B][1], JJ / 8);
               });
+              if constexpr (S >= 1) ds_items(b_c, std::integral_constant<int, S - 1>{});
+              pack(b_c, std::integral_constant<int, S - 2>{});
             }
           });
         } else {
           constexpr int Y = S - NX;
           if constexpr (DOV) {
             E8 o = op[S];
-            pin(o);
+            // the last slot's dS items under the first MFMA, their group's
+            // packing under the second (first read DT slots later)
             mfma32_agpr_ready(dqacc[0][Y % DT], o, dsb[0][Y / DT]);
+            if constexpr (Y == 0) {
+              ds_items(std::integral_constant<int, 0>{}, std::integral_constant<int, NX - 1>{});
+              ds_items(std::integral_constant<int, 1>{}, std::integral_constant<int, NX - 1>{});
+            }
             mfma32_agpr_ready(dqacc[1][Y % DT], o, dsb[1][Y / DT]);
+            if constexpr (Y == 0) {
+              pack(std::integral_constant<int, 0>{}, std::integral_constant<int, NX - 1>{});
+              pack(std::integral_constant<int, 1>{}, std::integral_constant<int, NX - 1>{});
+            }
           }
         }
         if constexpr (S + PF < NX + NY) load_op(std::integral_constant<int, S + PF>{});
