@@ -40,14 +40,21 @@ __global__ __launch_bounds__(64 * NW) LOGO_OCC_FWD void sq_fwd_pipe_kernel(const
   constexpr int NY = 4 * DT;   // PV MFMAs per tile (DT column blocks x 4 key steps)
   constexpr int IY = 32 / NY;  // mask / max items per Y slot
   // The 32 P items of a tile (per lane) are spread evenly over the X slots and
-  // the first three quarters of Y (the 8-wave form: the first half, measured
-  // 0.8% faster there; its 4-wave form would spill): PV runs key-step major
-  // (Y slot y: key step y / DT, column block y % DT), so pb[k] is first read at
-  // Y slot DT k, and the softmax work is split between both phases instead of
-  // crowding X.
-  constexpr int NPS = NX + (NW == 8 ? 2 : 3) * DT;  // slots that carry P items
+  // the first three quarters of Y less one slot (the 8-wave form: the first
+  // half less one, measured 0.8% faster there; its 4-wave form would spill):
+  // PV runs key-step major (Y slot y: key step y / DT, column block y % DT),
+  // so pb[k] is first read at Y slot DT k, and the softmax work is split
+  // between both phases instead of crowding X.  An item's exp2 runs in its
+  // slot, its row-sum add and its bf16 packing one slot later.
+  constexpr int NPS = NX + (NW == 8 ? 2 : 3) * DT - 1;  // slots that carry P items
   constexpr auto pslot = [](int it) constexpr { return it * NPS / 32; };
-  static_assert(pslot(7) < NX && pslot(15) < NX + DT && pslot(23) < NX + 2 * DT && pslot(31) < NX + 3 * DT,
+  // first item of slot s (items of slot s: [pfirst(s), pfirst(s + 1)))
+  constexpr auto pfirst = [](int s) constexpr { return (32 * s + NPS - 1) / NPS < 32 ? (32 * s + NPS - 1) / NPS : 32; };
+  constexpr int kMaxPerSlot = (32 + NPS - 1) / NPS;
+  static_assert(pfirst(NPS) == 32 && pslot(pfirst(1)) == 1 && pslot(pfirst(1) - 1) == 0, "slot ranges");
+  // a group is packed one slot after its last item
+  static_assert(pslot(7) + 1 < NX && pslot(15) + 1 < NX + DT && pslot(23) + 1 < NX + 2 * DT &&
+                    pslot(31) + 1 < NX + 3 * DT,
                 "each group of eight P items is packed before its PV MFMAs");
   constexpr int PF = 4;        // operand prefetch distance, in slots
   using GT = TileGeom<D, kSwz>;
@@ -151,18 +158,27 @@ __global__ __launch_bounds__(64 * NW) LOGO_OCC_FWD void sq_fwd_pipe_kernel(const
       static_for<NX + NY>([&](auto s_c) {
         constexpr int S = decltype(s_c)::value;
         __builtin_amdgcn_sched_barrier(0);
+        // the slot's P(t) scores (items [pfirst(S), pfirst(S + 1))), anchored
+        // ahead of its MFMA (which then separates the anchor from the exp2
+        // that reads them)
+        constexpr int I0 = pfirst(S), NI = pfirst(S + 1) - I0;
+        float spv[kMaxPerSlot];
+        if constexpr (DOPV)
+          static_for<NI>([&](auto i_c) {
+            constexpr int I = decltype(i_c)::value, IT = I0 + I;
+            spv[I] = sbuf[PAR][IT / 16][IT % 16];
+            pin(spv[I]);
+          });
         if constexpr (S < NX) {
           if constexpr (DOS) {
             constexpr int KK = S / DS, DSI = S % DS;
-            E8 o = op[S];
-            pin(o);
+            const E8 o = op[S];
             sbuf[PAR ^ 1][KK] = mfma32(o, qreg[DSI], DSI == 0 ? (NEG ? cbase : f32x16{}) : sbuf[PAR ^ 1][KK]);
           }
         } else {
           constexpr int Y = S - NX;
           if constexpr (DOPV) {
-            E8 o = op[S];
-            pin(o);
+            const E8 o = op[S];
             oacc[Y % DT] = mfma32(o, pb[Y / DT], oacc[Y % DT]);
           }
           if constexpr (DOS) {
@@ -188,22 +204,26 @@ __global__ __launch_bounds__(64 * NW) LOGO_OCC_FWD void sq_fwd_pipe_kernel(const
               mx = NEG ? min3_f32(mx, sv[e], sv[e + 1]) : max3_f32(mx, sv[e], sv[e + 1]);
           }
         }
-        // P(t) items assigned to this slot (X or Y)
+        // P(t) items assigned to this slot (X or Y); the row sum and the bf16
+        // packing of the previous slot's items, one slot after their exp2
+        // (a VALU op right behind an exp2 that wrote its input would cost an
+        // s_nop)
         if constexpr (DOPV) {
-          static_for<32>([&](auto it_c) {
-            constexpr int IT = decltype(it_c)::value;
-            if constexpr (pslot(IT) == S) {
-              constexpr int KK = IT / 16, JJ = IT % 16;
-              float sv = sbuf[PAR][KK][JJ];
-              pin(sv);
-              float pv = NEG ? fast_exp2(-sv) : fast_exp2(fmaf(sv, c, -base));
-              pin(pv);
-              sbuf[PAR][KK][JJ] = pv;
-              psum += pv;
-              pin(psum);
-              if constexpr (IT % 8 == 7) pb[IT / 8] = acc_to<EL>(sbuf[PAR][IT / 16], (IT / 8) & 1);
-            }
+          static_for<NI>([&](auto i_c) {
+            constexpr int I = decltype(i_c)::value, IT = I0 + I;
+            float pv = NEG ? fast_exp2(-spv[I]) : fast_exp2(fmaf(spv[I], c, -base));
+            pin(pv);
+            sbuf[PAR][IT / 16][IT % 16] = pv;
           });
+          if constexpr (S >= 1) {
+            constexpr int J0 = pfirst(S - 1), NJ = I0 - J0;
+            static_for<NJ>([&](auto i_c) {
+              constexpr int IT = J0 + decltype(i_c)::value;
+              psum += sbuf[PAR][IT / 16][IT % 16];
+              if constexpr (IT % 8 == 7) pb[IT / 8] = acc_to<EL>(sbuf[PAR][IT / 16], (IT / 8) & 1);
+            });
+            if constexpr (NJ > 0) pin(psum);
+          }
         }
         if constexpr (S + PF < NX + NY) load_op(std::integral_constant<int, S + PF>{});
       });
