@@ -308,6 +308,16 @@ __global__ __launch_bounds__(256) LOGO_OCC_DKV void swa_bwd_kernel(const AttnArg
     bf16x8 dbf[2][2] = {};  // dS of the halves as bf16 (zeros where not seen)
     if (see0 | see1) {
       const int key = K0 + i;
+      // Row p of item (half q, j) is R0 + 32 q + rowmap(g, j) and sees key
+      // iff key <= p <= min(key + W, seqlen - 1): with d = p - kb, one
+      // unsigned compare (unsigned) d <= lim.  A key past the segment end
+      // sees no row: kb then lies far above every row, so d wraps to a huge
+      // unsigned value, and lim is 0 (min(W, seqlen - 1 - key) would be
+      // negative, a huge unsigned bound).
+      const bool kin = key < b.seqlen;
+      const int kb = kin ? key : (1 << 30);
+      const unsigned lim = kin ? (unsigned)min(W, b.seqlen - 1 - key) : 0u;
+      const int d0 = R0 + 4 * g - kb;  // d of item (0, 0)
       const bf16* qb = ptr(L::q(B));
       const bf16* ob = ptr(L::dout(B));
       const f32x4* lb = reinterpret_cast<const f32x4*>(sm + L::lse(B));
@@ -329,38 +339,77 @@ __global__ __launch_bounds__(256) LOGO_OCC_DKV void swa_bwd_kernel(const AttnArg
           opA[T] = rd.tr((BLK % 2 == 0) ? ob : qb, 32 * QQ + 16 * HH, DTI);
         }
       };
-      auto p_item = [&](auto q_c, auto j_c) __attribute__((always_inline)) {
+      // An item's inputs are anchored ahead of its slot's MFMA (which then
+      // separates the anchor from the VALU op that reads them), its
+      // arithmetic follows the MFMA, and pairs are packed to bf16 one slot
+      // later: a VALU op right behind an anchor or an exp2 that wrote its
+      // input would cost an s_nop.
+      auto p_pre = [&](auto q_c, auto j_c) __attribute__((always_inline)) {
         constexpr int QQ = decltype(q_c)::value, JJ = decltype(j_c)::value;
-        const int p = R0 + 32 * QQ + rowmap(g, JJ);
-        const bool vis = (key <= p) & (key >= p - W) & (p < b.seqlen);  // no short circuit: no branch
         float sv = sacc[QQ][JJ];
         pin(sv);
-        float pv = fast_exp2(fmaf(sv, c, -l4[QQ][JJ / 4][JJ % 4]));
+        return sv;
+      };
+      auto p_item = [&](auto q_c, auto j_c, float sv) __attribute__((always_inline)) {
+        constexpr int QQ = decltype(q_c)::value, JJ = decltype(j_c)::value;
+        const bool vis = (unsigned)(d0 + (32 * QQ + 8 * (JJ / 4) + JJ % 4)) <= lim;
+        // masked before the exp2 (exp2(-inf) = 0), so no VALU op reads the
+        // exp2 result right behind it
+        const float x = fmaf(sv, c, -l4[QQ][JJ / 4][JJ % 4]);
+        float pv = fast_exp2(vis ? x : -INFINITY);
         pin(pv);
-        pv = vis ? pv : 0.f;
         sacc[QQ][JJ] = pv;
+      };
+      auto p_pack = [&](auto q_c, auto j_c) __attribute__((always_inline)) {
+        constexpr int QQ = decltype(q_c)::value, JJ = decltype(j_c)::value;
         if constexpr (JJ % 2 == 1) {
           pbf[QQ][JJ / 8][JJ % 8 - 1] = (bf16)sacc[QQ][JJ - 1];
-          pbf[QQ][JJ / 8][JJ % 8] = (bf16)pv;
+          pbf[QQ][JJ / 8][JJ % 8] = (bf16)sacc[QQ][JJ];
         }
+        // a finished group stays here: sunk to its MFMA, the packing would
+        // write the operand right before it
+        if constexpr (JJ % 8 == 7) pin(pbf[QQ][JJ / 8]);
       };
-      auto ds_item = [&](auto q_c, auto j_c) __attribute__((always_inline)) {
+      auto ds_pre = [&](auto q_c, auto j_c, float& pv, float& dpv) __attribute__((always_inline)) {
         constexpr int QQ = decltype(q_c)::value, JJ = decltype(j_c)::value;
-        float pv = sacc[QQ][JJ], dpv = pacc[QQ][JJ];
+        pv = sacc[QQ][JJ];
+        dpv = pacc[QQ][JJ];
         pin(pv);
         pin(dpv);
-        const float dsv = pv * (dpv - d4[QQ][JJ / 4][JJ % 4]);
+      };
+      auto ds_item = [&](auto q_c, auto j_c, float pv, float dpv) __attribute__((always_inline)) {
+        constexpr int QQ = decltype(q_c)::value, JJ = decltype(j_c)::value;
+        float dsv = pv * (dpv - d4[QQ][JJ / 4][JJ % 4]);
+        pin(dsv);
         pacc[QQ][JJ] = dsv;
+      };
+      auto ds_pack = [&](auto q_c, auto j_c) __attribute__((always_inline)) {
+        constexpr int QQ = decltype(q_c)::value, JJ = decltype(j_c)::value;
         if constexpr (JJ % 2 == 1) {
           dbf[QQ][JJ / 8][JJ % 8 - 1] = (bf16)pacc[QQ][JJ - 1];
-          dbf[QQ][JJ / 8][JJ % 8] = (bf16)dsv;
+          dbf[QQ][JJ / 8][JJ % 8] = (bf16)pacc[QQ][JJ];
         }
+        if constexpr (JJ % 8 == 7) pin(dbf[QQ][JJ / 8]);
       };
       static_for<PF>([&](auto t_c) __attribute__((always_inline)) { load_slot(t_c); });
       static_for<NSL>([&](auto s_c) __attribute__((always_inline)) {
         constexpr int S = decltype(s_c)::value, BLK = S / DS, K = S % DS;
         constexpr int HH = K / DT, DTI = K % DT;
         __builtin_amdgcn_sched_barrier(0);
+        // the slot's P items (blocks 1, 2, 4, 5) and dS items (blocks 3, 6)
+        constexpr bool HASP = BLK == 1 || BLK == 2 || BLK == 4 || BLK == 5, HASD = BLK == 3 || BLK == 6;
+        constexpr int QP = BLK >= 4, JP = HASP ? (S - DS * (1 + 3 * QP)) * IPP : 0, QD = BLK == 6, JD = K * IPD;
+        float sv[IPP], pv[IPD], dpv[IPD];
+        if constexpr (HASP)
+          static_for<IPP>([&](auto e_c) __attribute__((always_inline)) {
+            constexpr int E = decltype(e_c)::value;
+            sv[E] = p_pre(std::integral_constant<int, QP>{}, std::integral_constant<int, JP + E>{});
+          });
+        if constexpr (HASD)
+          static_for<IPD>([&](auto e_c) __attribute__((always_inline)) {
+            constexpr int E = decltype(e_c)::value;
+            ds_pre(std::integral_constant<int, QD>{}, std::integral_constant<int, JD + E>{}, pv[E], dpv[E]);
+          });
         if constexpr (BLK == 0 || BLK == 2) {
           constexpr int QQ = BLK / 2;
           sacc[QQ] = mfma32(opA[S], opB[QQ * DS + K], K == 0 ? f32x16{} : sacc[QQ]);
@@ -387,17 +436,30 @@ __global__ __launch_bounds__(256) LOGO_OCC_DKV void swa_bwd_kernel(const AttnArg
             if (S == DS * (1 + 3 * q) + 4 * m / IPP - 2) l4[q][m] = lds_load(lb + 8 * q + 2 * m + g);
             if (S == DS * (3 + 3 * q) + 4 * m / IPD - 2) d4[q][m] = lds_load(db + 8 * q + 2 * m + g);
           }
-        if constexpr (BLK == 1 || BLK == 2 || BLK == 4 || BLK == 5) {
-          constexpr int QQ = BLK >= 4, J0 = (S - DS * (1 + 3 * QQ)) * IPP;
+        if constexpr (HASP)
           static_for<IPP>([&](auto e_c) __attribute__((always_inline)) {
-            p_item(std::integral_constant<int, QQ>{}, std::integral_constant<int, J0 + decltype(e_c)::value>{});
+            constexpr int E = decltype(e_c)::value;
+            p_item(std::integral_constant<int, QP>{}, std::integral_constant<int, JP + E>{}, sv[E]);
           });
-        }
-        if constexpr (BLK == 3 || BLK == 6) {
-          constexpr int QQ = BLK == 6, J0 = K * IPD;
+        if constexpr (HASD)
           static_for<IPD>([&](auto e_c) __attribute__((always_inline)) {
-            ds_item(std::integral_constant<int, QQ>{}, std::integral_constant<int, J0 + decltype(e_c)::value>{});
+            constexpr int E = decltype(e_c)::value;
+            ds_item(std::integral_constant<int, QD>{}, std::integral_constant<int, JD + E>{}, pv[E], dpv[E]);
           });
+        // the previous slot's items, packed (no item is formed in block 0 or
+        // 7, so the packs stay inside the step)
+        if constexpr (S >= 1) {
+          constexpr int LS = S - 1, LB = LS / DS, LK = LS % DS;
+          if constexpr (LB == 1 || LB == 2 || LB == 4 || LB == 5)
+            static_for<IPP>([&](auto e_c) __attribute__((always_inline)) {
+              constexpr int LQ = LB >= 4;
+              p_pack(std::integral_constant<int, LQ>{},
+                     std::integral_constant<int, (LS - DS * (1 + 3 * LQ)) * IPP + decltype(e_c)::value>{});
+            });
+          if constexpr (LB == 3 || LB == 6)
+            static_for<IPD>([&](auto e_c) __attribute__((always_inline)) {
+              ds_pack(std::integral_constant<int, LB == 6>{}, std::integral_constant<int, LK * IPD + decltype(e_c)::value>{});
+            });
         }
       });
       __builtin_amdgcn_sched_barrier(0);
