@@ -416,14 +416,18 @@ __global__ __launch_bounds__(256) LOGO_OCC_DKV void swa_bwd_kernel(const AttnArg
         } else if constexpr (BLK == 1 || BLK == 3) {
           constexpr int QQ = BLK / 2;
           pacc[QQ] = mfma32(opA[S], vreg[K], K == 0 ? f32x16{} : pacc[QQ]);
-        } else if constexpr (BLK == 4) {
-          mfma32_agpr(dva[DTI], opA[S], pbf[0][HH]);
-        } else if constexpr (BLK == 5) {
-          mfma32_agpr(dka[DTI], opA[S], dbf[0][HH]);
-        } else if constexpr (BLK == 6) {
-          mfma32_agpr(dva[DTI], opA[S], pbf[1][HH]);
         } else {
-          mfma32_agpr(dka[DTI], opA[S], dbf[1][HH]);
+          // dV / dK: operands from LDS and P / dS packed at least DT slots
+          // earlier; D = 128 (DT = 4) needs no leading wait states, D = 64
+          // keeps them
+          auto acc_mfma = [&](f32x16& acc, const bf16x8& x, const bf16x8& y) __attribute__((always_inline)) {
+            if constexpr (DT >= 4) mfma32_agpr_ready(acc, x, y);
+            else mfma32_agpr(acc, x, y);
+          };
+          if constexpr (BLK == 4) acc_mfma(dva[DTI], opA[S], pbf[0][HH]);
+          else if constexpr (BLK == 5) acc_mfma(dka[DTI], opA[S], dbf[0][HH]);
+          else if constexpr (BLK == 6) acc_mfma(dva[DTI], opA[S], pbf[1][HH]);
+          else acc_mfma(dka[DTI], opA[S], dbf[1][HH]);
         }
         if constexpr (S + PF < NSL) load_slot(std::integral_constant<int, S + PF>{});
         // lse / delta of items 4m .. 4m+3 of a half, two slots before the
@@ -502,7 +506,7 @@ __global__ __launch_bounds__(256) LOGO_OCC_DKV void swa_bwd_kernel(const AttnArg
     static_for<NM>([&](auto m_c) __attribute__((always_inline)) {
       constexpr int M = decltype(m_c)::value, T = M < N0 ? 0 : 1;
       __builtin_amdgcn_sched_barrier(0);
-      mfma32_agpr(dqa[SET][T], ka[M], sb[M]);
+      mfma32_agpr_ready(dqa[SET][T], ka[M], sb[M]);  // operands straight from LDS
       if constexpr (M + PFQ < NM) load(std::integral_constant<int, M + PFQ>{});
     });
     __builtin_amdgcn_sched_barrier(0);

@@ -281,6 +281,8 @@ def test_window_backward_accumulators_are_drained_before_use(tmp_path):
         assert any(_ACC_DST.search(line) for line in lines), f"{name}: no AGPR-accumulator MFMA found"
         bad = check_accumulators_drained(lines)
         assert not bad, f"{name}: " + "; ".join(f"line {n}: {t[:100]}" for n, t in bad[:5])
+        bad = check_operand_distance(lines)
+        assert not bad, f"{name}: " + "; ".join(f"line {n}: {t[:100]}" for n, t in bad[:5])
 
 
 _GOOD = """\
