@@ -357,11 +357,13 @@ def extra_measurements(dev):
     bytes_active = (B5 // 2) * H * ctx * D * 2 * 2
     td_all = _time_ms(lambda: decode_attn(q5, kc, vc, lens5, max_len=ctx), 20)
     del kc, vc
-    ceiling = read_ceiling_gbs(dev, bytes_active)["best_gbs"]
+    rc = read_ceiling_gbs(dev, bytes_active)
+    ceiling = rc["best_gbs"]
     out["decode_global_cfg5_layer"] = {
         "active_rows": B5 // 2, "ms": round(td, 4), "gbs": round(bytes_active / td / 1e6, 1),
         "all_rows_ms": round(td_all, 4), "all_rows_gbs": round(2 * bytes_active / td_all / 1e6, 1),
         "hbm_peak_gbs": HBM_PEAK_GBS, "read_ceiling_gbs": ceiling,
+        "read_ceiling_ordinary_loads_gbs": rc["ordinary_loads_best_gbs"],
         "of_read_ceiling": round(bytes_active / td / 1e6 / ceiling, 4)}
     return out
 
@@ -471,20 +473,23 @@ def decode_layer_only(dev, calls=10):
 def read_ceiling_gbs(dev, nbytes, calls=10):
     """The read bandwidth this part delivers in practice: the library's
     streaming-read calibration kernel (logo_read_calibration) over a buffer
-    of ``nbytes``, at several grid sizes; best and per-grid GB/s."""
+    of ``nbytes``, at several grid sizes, with non-temporal loads (as the
+    decode kernel's cache reads) and with ordinary ones; best and per-grid
+    GB/s of the non-temporal reads, best of the ordinary ones."""
     from logo_amd import _lib
     lib = _lib.lib()
     buf = torch.ones(nbytes // 2, dtype=torch.bfloat16, device=dev)
     sink = torch.zeros(65536, dtype=torch.int32, device=dev)
     st = _lib.stream_of(buf)
-    per = {}
-    for grid in (2048, 8192, 16384):
-        def run():
-            _lib.check(lib.logo_read_calibration(_lib.ptr(buf), nbytes, _lib.ptr(sink), grid, st),
-                       "logo_read_calibration")
-        per[grid] = round(nbytes / _time_ms(run, calls) / 1e6, 1)
+    per = {0: {}, 1: {}}
+    for nt in (1, 0):
+        for grid in (2048, 8192, 16384):
+            def run():
+                _lib.check(lib.logo_read_calibration(_lib.ptr(buf), nbytes, _lib.ptr(sink), grid, nt, st),
+                           "logo_read_calibration")
+            per[nt][grid] = round(nbytes / _time_ms(run, calls) / 1e6, 1)
     del buf
-    return {"best_gbs": max(per.values()), "per_grid_gbs": per}
+    return {"best_gbs": max(per[1].values()), "per_grid_gbs": per[1], "ordinary_loads_best_gbs": max(per[0].values())}
 
 
 def decode_model_measurement(dev, batch=32, prompt=16384, steps=256, seed=4):

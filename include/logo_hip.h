@@ -54,7 +54,8 @@ extern "C" {
 /* Message of the calling thread's last error ("" if none). */
 const char* logo_last_error(void);
 
-/* ABI version of this library (6: logo_head_linear_grad_acc; 5: head dim 256, fp32, logo_sq_generic). */
+/* ABI version of this library (7: logo_read_calibration's nontemporal flag; 6: logo_head_linear_grad_acc;
+   5: head dim 256, fp32, logo_sq_generic). */
 int logo_abi_version(void);
 
 /*
@@ -62,10 +63,12 @@ int logo_abi_version(void);
  * (a multiple of 16) of the 16-byte aligned device buffer `buf` once with a
  * grid of `grid` 256-thread workgroups, for timing the read bandwidth the
  * part delivers in practice (the ceiling the decode kernel's bandwidth is
- * compared with).  `sink` is device memory of at least grid * 4 bytes, which
- * it leaves unchanged unless a workgroup's XOR of its words hits a sentinel.
+ * compared with); `nontemporal` != 0 uses non-temporal loads, as the decode
+ * kernel's cache reads do.  `sink` is device memory of at least grid * 4
+ * bytes, which it leaves unchanged unless a workgroup's XOR of its words hits
+ * a sentinel.
  */
-int logo_read_calibration(const void* buf, size_t bytes, void* sink, int grid, void* stream);
+int logo_read_calibration(const void* buf, size_t bytes, void* sink, int grid, int nontemporal, void* stream);
 
 /* Bytes of workspace logo_compact needs. */
 size_t logo_compact_workspace_bytes(int64_t n_tokens, int lanes);

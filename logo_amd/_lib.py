@@ -37,7 +37,7 @@ SIGNATURES = {
     "logo_sq_fwd": ([_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I, _I, _I, _I, _I, _I, _F, _I, _I, _P, _SZ, _P], _I),
     "logo_sq_workspace_bytes": ([_I64, _I, _I, _I], _SZ),
     "logo_sq_generic": ([_I, _I], _I),
-    "logo_read_calibration": ([_P, _SZ, _P, _I, _P], _I),
+    "logo_read_calibration": ([_P, _SZ, _P, _I, _I, _P], _I),
     "logo_sq_workspace_counter_bytes": ([], _SZ),
     "logo_epilogue_fwd": ([_P, _P, _P, _P, _I, _P, _P, _P, _I64, _I, _I, _F, _I, _P], _I),
     "logo_epilogue_bwd_workspace_bytes": ([_I64, _I, _I], _SZ),

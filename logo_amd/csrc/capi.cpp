@@ -18,4 +18,4 @@ void set_error(const char* fmt, ...) {
 
 extern "C" const char* logo_last_error(void) { return logo::g_last_error; }
 
-extern "C" int logo_abi_version(void) { return 6; }
+extern "C" int logo_abi_version(void) { return 7; }

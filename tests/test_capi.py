@@ -22,7 +22,7 @@ def test_header_symbols_are_exported():
 
 def test_abi_version_and_workspace():
     lib = _lib.lib()
-    assert lib.logo_abi_version() == 6
+    assert lib.logo_abi_version() == 7
     # the generic kernels serve d = 256 and fp32; they never split
     assert [lib.logo_sq_generic(d, t) for d in (64, 128, 256) for t in (_lib.DTYPE_BF16, _lib.DTYPE_F16)] == \
         [0, 0, 0, 0, 1, 1]
