@@ -152,6 +152,18 @@ __device__ __forceinline__ bf16x8 scale_bf16x8(const bf16x8 v, float s) { return
 template <typename T>
 __device__ __forceinline__ void pin(T& x) { asm volatile("" : "+v"(x)); }
 
+// Streaming 16-byte global accesses: non-temporal loads and stores, for data
+// a kernel reads or writes once and no kernel re-reads soon (they stream
+// faster than ordinary accesses on this part: a 1 GiB copy 5.9-6.1 against
+// 5.5 TB/s, a read 7.1 against 6.3 TB/s).  Used where they measured faster:
+// the decode cache reads, RoPE and the epilogue's backward; not where the
+// next kernel reads the data again (a store the next kernel reads, such as
+// the delta phase's copies or the epilogue's output, measured slower).
+template <typename V>
+__device__ __forceinline__ V ld_nt(const V* p) { return __builtin_nontemporal_load(p); }
+template <typename V>
+__device__ __forceinline__ void st_nt(V* p, V v) { __builtin_nontemporal_store(v, p); }
+
 // Calls f(std::integral_constant<int, I>{}) for I = 0 .. N-1 (compile-time
 // indices, so per-slot register arrays stay in registers).
 template <typename F, int... I>

@@ -85,9 +85,9 @@ __global__ __launch_bounds__(256) void epi_bwd_kernel(const EpiArgs a) {
     const bool ok = r < a.rows;
     bf16x8 lv{}, gv{}, dv{};
     if (ok) {
-      lv = *reinterpret_cast<const bf16x8*>(a.L + r * D + 8 * c);
-      gv = *reinterpret_cast<const bf16x8*>(a.G + r * D + 8 * c);
-      dv = *reinterpret_cast<const bf16x8*>(a.dout + r * D + 8 * c);
+      lv = ld_nt(reinterpret_cast<const bf16x8*>(a.L + r * D + 8 * c));
+      gv = ld_nt(reinterpret_cast<const bf16x8*>(a.G + r * D + 8 * c));
+      dv = ld_nt(reinterpret_cast<const bf16x8*>(a.dout + r * D + 8 * c));
     }
     float xl[8], xg[8], dy[8];
     float ssl = 0.f, ssg = 0.f;
@@ -131,8 +131,8 @@ __global__ __launch_bounds__(256) void epi_bwd_kernel(const EpiArgs a) {
         ol[e] = (bf16)(rl * (dnl[e] - nl[e] * dotl));
         og[e] = (bf16)(rgn * (dng[e] - ng[e] * dotg));
       }
-      *reinterpret_cast<bf16x8*>(a.dL + r * D + 8 * c) = ol;
-      *reinterpret_cast<bf16x8*>(a.dG + r * D + 8 * c) = og;
+      st_nt(reinterpret_cast<bf16x8*>(a.dL + r * D + 8 * c), ol);
+      st_nt(reinterpret_cast<bf16x8*>(a.dG + r * D + 8 * c), og);
       if (c == 0) a.dgate_part[r] = part;
     }
   }

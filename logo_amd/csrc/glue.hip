@@ -60,8 +60,8 @@ __global__ __launch_bounds__(256) void rope_kernel(const RopeArgs a, int64_t per
   const int64_t tok = row / H;
   const bf16* xr = a.x[ti] + row * D;
   bf16* yr = a.y[ti] + row * D;
-  const bf16x8 x1 = *reinterpret_cast<const bf16x8*>(xr + 8 * c);
-  const bf16x8 x2 = *reinterpret_cast<const bf16x8*>(xr + D / 2 + 8 * c);
+  const bf16x8 x1 = ld_nt(reinterpret_cast<const bf16x8*>(xr + 8 * c));
+  const bf16x8 x2 = ld_nt(reinterpret_cast<const bf16x8*>(xr + D / 2 + 8 * c));
   const bf16x8 c1 = *reinterpret_cast<const bf16x8*>(a.cos + tok * D + 8 * c);
   const bf16x8 c2 = *reinterpret_cast<const bf16x8*>(a.cos + tok * D + D / 2 + 8 * c);
   const bf16x8 s1 = *reinterpret_cast<const bf16x8*>(a.sin + tok * D + 8 * c);
@@ -87,8 +87,8 @@ __global__ __launch_bounds__(256) void rope_kernel(const RopeArgs a, int64_t per
       y2[e] = (bf16)(a2 + b2);
     }
   }
-  *reinterpret_cast<bf16x8*>(yr + 8 * c) = y1;
-  *reinterpret_cast<bf16x8*>(yr + D / 2 + 8 * c) = y2;
+  st_nt(reinterpret_cast<bf16x8*>(yr + 8 * c), y1);
+  st_nt(reinterpret_cast<bf16x8*>(yr + D / 2 + 8 * c), y2);
 }
 
 // One wave per row; rows of `cols` bf16 (a multiple of 8, at most 64 * 8 * 8).
