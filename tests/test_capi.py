@@ -98,6 +98,21 @@ def test_head_linear_grad_acc_rejects_bad_arguments():
         assert msg in lib.logo_last_error().decode()
 
 
+def test_read_calibration_rejects_bad_arguments():
+    """The streaming-read calibration refuses null pointers, an unaligned
+    buffer or size and grids outside [1, 65536], for either load kind, before
+    any HIP call (pointers are placeholders)."""
+    lib = _lib.lib()
+    p = ctypes.c_void_p(256)
+    for nt in (0, 1):
+        for buf, nbytes, sink, grid, msg in ((None, 1024, p, 8, "null"), (p, 1024, None, 8, "null"),
+                                             (ctypes.c_void_p(264), 1024, p, 8, "aligned"),
+                                             (p, 1000, p, 8, "aligned"), (p, 1024, p, 0, "grid"),
+                                             (p, 1024, p, 65537, "grid")):
+            assert lib.logo_read_calibration(buf, nbytes, sink, grid, nt, None) == 1
+            assert msg in lib.logo_last_error().decode()
+
+
 def test_ops_refuse_cpu_tensors():
     import torch
 
