@@ -179,9 +179,12 @@ def cpu_baseline(q, k, v, sel_np, cu, do, heads, flops_per_head):
 
 
 def _time_ms(fn, iters, warmup=2):
+    """Average GPU time of back-to-back calls: the start event is queued
+    behind the warm-up calls (no synchronisation in between), so the first
+    timed call's host-side launch latency is not counted as GPU time."""
+    torch.cuda.synchronize()
     for _ in range(warmup):
         fn()
-    torch.cuda.synchronize()
     a = torch.cuda.Event(enable_timing=True)
     b = torch.cuda.Event(enable_timing=True)
     a.record()
@@ -293,7 +296,7 @@ def extra_measurements(dev):
         def fb_sparse():
             o = sq_full_attn(q, k, v, sel, cu_seqlens=cu)
             torch.autograd.grad(o, (q, k, v), do)
-        t = _time_ms(fb_sparse, 3)
+        t = _time_ms(fb_sparse, 10)
         sweep[f"r{r}"] = {"ms": round(t, 3), "speedup": round(t_dense / t, 2), "ideal": round(1 / r, 2)}
     out["fwd_bwd_speedup_vs_dense_T32768"] = sweep
 
