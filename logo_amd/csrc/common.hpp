@@ -156,9 +156,10 @@ __device__ __forceinline__ void pin(T& x) { asm volatile("" : "+v"(x)); }
 // a kernel reads or writes once and no kernel re-reads soon (they stream
 // faster than ordinary accesses on this part: a 1 GiB copy 5.9-6.1 against
 // 5.5 TB/s, a read 7.1 against 6.3 TB/s).  Used where they measured faster:
-// the decode cache reads, RoPE and the epilogue's backward; not where the
-// next kernel reads the data again (a store the next kernel reads, such as
-// the delta phase's copies or the epilogue's output, measured slower).
+// the decode cache reads, RoPE, the epilogue's backward and the sparse
+// backward's outputs (dq, dk, dv and the zero rows); not where the next
+// kernel reads the data again (a store the next kernel reads, such as the
+// delta phase's copies or the epilogue's output, measured slower).
 template <typename V>
 __device__ __forceinline__ V ld_nt(const V* p) { return __builtin_nontemporal_load(p); }
 template <typename V>

@@ -342,7 +342,7 @@ __global__ __launch_bounds__(128) LOGO_OCC_DQ64 void sq_dq64_kernel(const AttnAr
     for (int r = threadIdx.x / CHR; r < nrow; r += RPP) {
       const int64_t tok = qt.rv.token(qt.r0 + r);
       const u32x4 v = *reinterpret_cast<const u32x4*>(smem + (r >> 6) * GT::ELEMS + GT::off(r & 63, ch));
-      *reinterpret_cast<u32x4*>(a.dq + (tok * a.hq + hq) * D + 8 * ch) = v;
+      st_nt(reinterpret_cast<u32x4*>(a.dq + (tok * a.hq + hq) * D + 8 * ch), v);  // not read back in the step
     }
   }
 }
