@@ -9,6 +9,7 @@ sliding-window branch (``swa_attn``) and the dense causal global branch
 """
 
 import functools
+import os
 from typing import Optional
 
 import torch
@@ -73,17 +74,64 @@ def _fwd(q, k, v, dsel: DeviceSelection, scale: float, window: int):
                             dsel.cu, dsel.lanes, float(scale), int(window))
 
 
+_side_streams = {}
+
+
+def _side_stream(dev: torch.device) -> torch.cuda.Stream:
+    """One extra stream per device, at the default priority, for the dk / dv
+    launch of packed backward calls."""
+    s = _side_streams.get(dev.index)
+    if s is None:
+        s = _side_streams[dev.index] = torch.cuda.Stream(device=dev)
+    return s
+
+
+def _overlap_dkv(dsel: DeviceSelection) -> bool:
+    """Whether dk / dv runs on the side stream beside dq: opt-in
+    (LOGO_BWD_OVERLAP=1), for calls that pack more than one sequence.  It
+    pays where sequences of unequal length leave the heaviest tiles of the
+    longest one running alone at the end of each kernel's grid (cfg3's four
+    sequences of 2.8K-12.5K tokens: fwd + bwd 1.49 -> 1.44 ms), and costs
+    where the grids are balanced (the cfg4 layer's four sequences of 8192
+    tokens: 7.33 -> 7.40 ms per step); the lengths are on the device, so the
+    choice is the caller's.  A single sequence keeps one stream either way
+    (its heaviest-first tile order balances each grid; T = 32K at r = 0.125,
+    0.25, 0.5 measured the same), and so does a backward traced by
+    torch.compile."""
+    return (dsel.cu.numel() > 2 and os.environ.get("LOGO_BWD_OVERLAP", "0") == "1"
+            and not torch.compiler.is_compiling())
+
+
 def _bwd(q, k, v, o, lse, do, dsel: DeviceSelection, scale: float, window: int):
     """dq (unselected rows zero), dk, dv: the delta phase (with the compacted
     q / dO copies of sparse mode), then dq and dk / dv as two launches, or
     as the one fused pass of the sliding-window branch (dense rows, window
     <= 128, HQ == H; the library picks the kernels, this only keeps the two
-    launches separately timed where they are separate)."""
+    launches separately timed where they are separate).
+
+    dq and dk / dv read only the delta phase's outputs and q, k, v, so with
+    the overlap switched on (``_overlap_dkv``) dk / dv is launched first, on
+    a side stream, and dq behind it on the caller's stream: dq's workgroups
+    take the CUs that dk / dv's tail leaves idle.  The caller's stream waits for the side
+    stream before returning (graph capture forks and joins the same way),
+    and dk / dv are marked as used on the caller's stream for the caching
+    allocator."""
     ops = _torch_ops.ops()
     args = (q, k, v, o, lse, do, dsel.q_idx, dsel.pos, dsel.meta, dsel.cu, dsel.lanes, float(scale), int(window))
     ws = _torch_ops.timed("logo_sq_bwd_delta", ops.sq_bwd_delta, *args)
     if dsel.q_idx is None and 0 <= window <= 128 and q.shape[1] == k.shape[1]:
         return _torch_ops.timed("logo_sq_bwd_dqkv", ops.sq_bwd_dqkv, *args, *ws)
+    if _overlap_dkv(dsel):
+        main = torch.cuda.current_stream(q.device)
+        side = _side_stream(q.device)
+        side.wait_stream(main)
+        with torch.cuda.stream(side):
+            dk, dv = _torch_ops.timed("logo_sq_bwd_dkv", ops.sq_bwd_dkv, *args, *ws)
+        dq = _torch_ops.timed("logo_sq_bwd_dq", ops.sq_bwd_dq, *args, *ws)
+        main.wait_stream(side)
+        dk.record_stream(main)
+        dv.record_stream(main)
+        return dq, dk, dv
     dq = _torch_ops.timed("logo_sq_bwd_dq", ops.sq_bwd_dq, *args, *ws)
     dk, dv = _torch_ops.timed("logo_sq_bwd_dkv", ops.sq_bwd_dkv, *args, *ws)
     return dq, dk, dv
