@@ -178,10 +178,12 @@ def cpu_baseline(q, k, v, sel_np, cu, do, heads, flops_per_head):
     }
 
 
-def _time_ms(fn, iters, warmup=2):
+def _time_ms(fn, iters, warmup=5):
     """Average GPU time of back-to-back calls: the start event is queued
     behind the warm-up calls (no synchronisation in between), so the first
-    timed call's host-side launch latency is not counted as GPU time."""
+    timed call's host-side launch latency is not counted as GPU time.  Five
+    warm-up calls: the first calls on new shapes (allocator growth, first
+    launches) ran slower for several calls (cfg3: 1.59 ms, then 1.49 ms)."""
     torch.cuda.synchronize()
     for _ in range(warmup):
         fn()
@@ -288,7 +290,7 @@ def extra_measurements(dev):
     def fb_dense():
         o = dense_causal_attn(q, k, v, cu)
         torch.autograd.grad(o, (q, k, v), do)
-    t_dense = _time_ms(fb_dense, 3)
+    t_dense = _time_ms(fb_dense, 5)
     sweep = {"dense_ms": round(t_dense, 3)}
     for r in (0.5, 0.25, 0.125):
         sel = torch.from_numpy(markov_mask(T, r, 8, gen)).to(dev)[None]
@@ -324,9 +326,7 @@ def extra_measurements(dev):
     def fb3():
         o = sq_full_attn(q3, k3, v3, sel3, cu_seqlens=cu3)
         torch.autograd.grad(o, (q3, k3, v3), do[:, :n3])
-    # steady state: the first calls on these new shapes ran ~7% slower for
-    # several calls past the usual two warm-up calls (1.59 against 1.49 ms)
-    t3 = _time_ms(fb3, 20, warmup=5)
+    t3 = _time_ms(fb3, 20)
     f3 = 3.5 * 4 * D * H * float((pos3 + 1).sum())
     out["cfg3_fwd_bwd_varlen"] = {"lens": lens, "ms": round(t3, 3), "tflops": round(f3 / t3 / 1e9, 1)}
 
