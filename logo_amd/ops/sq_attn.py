@@ -90,11 +90,12 @@ def _overlap_dkv(dsel: DeviceSelection) -> bool:
     """Whether dk / dv runs on the side stream beside dq: opt-in
     (LOGO_BWD_OVERLAP=1), for calls that pack more than one sequence.  It
     pays where sequences of unequal length leave the heaviest tiles of the
-    longest one running alone at the end of each kernel's grid (cfg3's four
-    sequences of 2.8K-12.5K tokens: fwd + bwd 1.49 -> 1.44 ms), and costs
-    where the grids are balanced (the cfg4 layer's four sequences of 8192
-    tokens: 7.33 -> 7.40 ms per step); the lengths are on the device, so the
-    choice is the caller's.  A single sequence keeps one stream either way
+    longest one running alone at the end of each kernel's grid (four packed
+    sequences of 2.8K-12.5K tokens, 16 heads, D = 128, r = 0.25: fwd + bwd
+    1.49 -> 1.44 ms), and costs where the grids are balanced (the LoGo
+    layer at B = 4, T = 8192, four sequences of 8192 tokens: 7.33 -> 7.40
+    ms per step); the lengths are on the device, so the choice is the
+    caller's.  A single sequence keeps one stream either way
     (its heaviest-first tile order balances each grid; T = 32K at r = 0.125,
     0.25, 0.5 measured the same), and so does a backward traced by
     torch.compile."""
@@ -112,10 +113,10 @@ def _bwd(q, k, v, o, lse, do, dsel: DeviceSelection, scale: float, window: int):
     dq and dk / dv read only the delta phase's outputs and q, k, v, so with
     the overlap switched on (``_overlap_dkv``) dk / dv is launched first, on
     a side stream, and dq behind it on the caller's stream: dq's workgroups
-    take the CUs that dk / dv's tail leaves idle.  The caller's stream waits for the side
-    stream before returning (graph capture forks and joins the same way),
-    and dk / dv are marked as used on the caller's stream for the caching
-    allocator."""
+    take the CUs that dk / dv's tail leaves idle.  The caller's stream waits
+    for the side stream before returning (graph capture forks and joins the
+    same way), and dk / dv are marked as used on the caller's stream for the
+    caching allocator."""
     ops = _torch_ops.ops()
     args = (q, k, v, o, lse, do, dsel.q_idx, dsel.pos, dsel.meta, dsel.cu, dsel.lanes, float(scale), int(window))
     ws = _torch_ops.timed("logo_sq_bwd_delta", ops.sq_bwd_delta, *args)
