@@ -64,3 +64,25 @@ def test_operators_refuse_cpu_tensors():
     cu = torch.tensor([0, 8], dtype=torch.int32)
     with pytest.raises((RuntimeError, NotImplementedError)):
         ops.dense_meta(cu, 8)
+
+
+@pytest.mark.parametrize("cu,env,want", [
+    ([0, 100], None, False), ([0, 100], "1", False),        # a single sequence keeps one stream
+    ([0, 40, 100], None, False), ([0, 40, 100], "0", False),  # off by default
+    ([0, 40, 100], "1", True), ([0, 0, 40, 100], "1", True),
+])
+def test_two_stream_backward_policy(cu, env, want, monkeypatch):
+    """The packed backward's dk / dv goes to a side stream only when
+    LOGO_BWD_OVERLAP=1 and the call packs more than one sequence (the GPU
+    side, bit-identical results included, is in tests/test_gpu_bwd_overlap.py)."""
+    from logo_amd.ops.common import DeviceSelection
+    from logo_amd.ops.sq_attn import _overlap_dkv
+
+    if env is None:
+        monkeypatch.delenv("LOGO_BWD_OVERLAP", raising=False)
+    else:
+        monkeypatch.setenv("LOGO_BWD_OVERLAP", env)
+    cu_t = torch.tensor(cu, dtype=torch.int32)
+    dsel = DeviceSelection(meta=torch.zeros(1, dtype=torch.int32), cu=cu_t, q_idx=None, pos=None,
+                           n_tokens=cu[-1], nseq=len(cu) - 1, lanes=1)
+    assert _overlap_dkv(dsel) is want
